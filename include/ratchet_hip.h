@@ -1,0 +1,214 @@
+/*
+ * ratchet_hip.h — C ABI of libratchet_hip.so, the gfx950 (MI355X) kernels of the
+ * ratchet-linear hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - Plain pointers to device memory, element strides (not bytes), int64 sizes.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream).
+ *     Work is enqueued on that stream; nothing synchronizes with the host.
+ *   - The library never allocates and never frees: the caller owns every buffer.
+ *   - Return value: RK_OK (0) or an RK_ERR_* code; the message of the last failure
+ *     on the calling thread is available from rk_last_error(). Nothing throws
+ *     across the ABI.
+ *   - dtype codes: RK_F32 = float32, RK_BF16 = bfloat16 (raw uint16 bits).
+ *
+ * Reference interfaces are cited as file:line in LoomNode/local-ai-training,
+ * src/local_ai_training/.
+ */
+#ifndef RATCHET_HIP_H
+#define RATCHET_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  RK_OK = 0,
+  RK_ERR_ARG = 1,         /* invalid shape, stride, dtype, null pointer, alignment  */
+  RK_ERR_LAUNCH = 2,      /* the HIP runtime reported an error at launch           */
+  RK_ERR_UNSUPPORTED = 3  /* a valid request this build does not implement         */
+};
+
+enum { RK_F32 = 0, RK_BF16 = 1 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+int rk_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rk_last_error(void);
+
+/*
+ * Per-token absmax int8 quantization of a 2-D tensor, optionally pre-scaled per
+ * column and optionally stochastically rounded.
+ *   x        [M, K] of dtype x_dtype, element strides (sxm, sxk)
+ *   col_scale[K] float32 or NULL
+ *   q        [M, K] int8, row stride ldq (unit column stride)
+ *   scale    [M]    float32
+ *   x_bf16   NULL, or [M, K] bf16 (row stride ld_xb) receiving bf16(x) (unscaled):
+ *            the cast that the BF16 grad_weight GEMM consumes, produced in the
+ *            same pass.
+ *   stochastic = 0: q = clamp(rint(x'/s), ±127); = 1: q = clamp(floor(x'/s + u), ±127)
+ *            with u = Philox4x32-10(counter = (uint32)(m*K + k), key = seed) mapped
+ *            to [0, 1); m counts rows from row_offset.
+ * Replaces: quantize_rows            int8_matmul.py:251-259
+ *           quantize_rows_colscaled  int8_matmul.py:262-277
+ *           _quantize_rows_fused / _quantize_rows_kernel  int8_matmul.py:106-150, 181-207
+ */
+int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                     int64_t sxk, const float* col_scale, int stochastic, uint64_t seed,
+                     int64_t row_offset, int8_t* q, int64_t ldq, float* scale,
+                     uint16_t* x_bf16, int64_t ld_xb, void* stream);
+
+/*
+ * Scaled int8 GEMM, "NT" form: C[m, n] = out( (float(sum_k A[m,k] * B[n,k]) * ls[m]) * rs[n] )
+ * with int32 accumulation. A int8 [M, K] (row stride lda, unit k stride); B int8
+ * [N, K] (row stride ldb, unit k stride). rs may be NULL (= ones). The product is
+ * rounded to bf16 (round-to-nearest-even); c_dtype RK_BF16 stores it as bf16,
+ * RK_F32 stores the same bf16 value widened to float32 (the reference's
+ * `.to(inputs.dtype)` cast, fused).
+ * Replaces: scaled_int8_mm  int8_matmul.py:289-343 (kernel 26-79) for a B operand
+ *           presented as the transposed view of an [N, K] matrix.
+ */
+int rk_int8_gemm_nt(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                    const float* ls, const float* rs, void* C, int c_dtype, int64_t ldc,
+                    int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * Same GEMM with B taken from the packed ratchet state: packed [N, K] uint8
+ * (row stride ldp), code = (byte & 15) - max_code decoded while staging tiles.
+ * Replaces: _RatchetMatmul.forward int8 branches  ratchet.py:46-53, 63-65, which
+ *           call scaled_int8_mm(q, code.t().contiguous(), s_x, scale) after
+ *           unpacking (ratchet.py:443-445, 195-199).
+ */
+int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* packed, int64_t ldp,
+                        int max_code, const float* ls, const float* rs, void* C,
+                        int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                        void* stream);
+
+/*
+ * Decode + transpose the packed state: codeT[k, n] = (packed[n, k] & 15) - max_code.
+ *   packed [N, K] (row stride ldp) -> codeT int8 [K, N] (row stride ldt).
+ * Feeds the int8 grad_input GEMM (contraction over the output features), replacing
+ * the `code` operand of scaled_int8_mm(grad_int8, code, ...)  ratchet.py:133-134.
+ */
+int rk_unpack_transpose(const uint8_t* packed, int64_t ldp, int max_code, int8_t* codeT,
+                        int64_t ldt, int64_t N, int64_t K, void* stream);
+
+/*
+ * Unpack the packed state into code / pressure int8 tensors (either may be NULL).
+ * Replaces: unpack_code_pressure  ratchet.py:195-199 (the .code / .pressure properties
+ * 443-449).
+ */
+int rk_unpack(const uint8_t* packed, int64_t n, int max_code, int8_t* code,
+              int8_t* pressure, void* stream);
+
+/*
+ * Effective BF16 weight: W[n, k] = bf16(code[n,k]) * bf16(scale[n]) rounded to bf16.
+ * Replaces: effective = code.to(bf16) * scale.to(bf16)[:, None]  ratchet.py:140, 61.
+ */
+int rk_effective_bf16(const uint8_t* packed, int64_t ldp, int max_code, const float* scale,
+                      uint16_t* W, int64_t ldw, int64_t N, int64_t K, void* stream);
+
+/*
+ * Dequantized BF16 activations: Xh[m, k] = bf16(q[m,k]) * bf16(s[m]) rounded to bf16.
+ * Replaces: quantized_inputs.to(bf16) * input_scale[:, None].to(bf16)  ratchet.py:73-75.
+ */
+int rk_dequant_bf16(const int8_t* q, int64_t ldq, const float* s, uint16_t* Xh, int64_t ldx,
+                    int64_t M, int64_t K, void* stream);
+
+/*
+ * Fused integer ratchet update on a normalized gradient z (float32 [rows, K], row
+ * stride ldz). packed [rows, K] (row stride ldp) is updated in place. counts[4]
+ * (int64) are INCREMENTED by (positive moves, negative moves, blocked positive,
+ * blocked negative); the caller zeroes them when it wants fresh sums.
+ * Replaces: _ratchet_update_core  ratchet.py:265-301 (+ bucket_pressure 248-262,
+ *           pack/unpack 185-199), as driven by apply_normalized_gradient 582-611.
+ */
+int rk_ratchet_update(uint8_t* packed, int64_t ldp, const float* z, int64_t ldz,
+                      int64_t rows, int64_t K, int max_code, int threshold, float low,
+                      float high, int64_t* counts, void* stream);
+
+/*
+ * Fused normalize + update from a raw weight gradient g ([rows, K], dtype g_dtype,
+ * row stride ldg), one wavefront per row:
+ *   ms = sum_k g^2 / K (fixed lane order), rms = sqrt(ms) or sqrt(EMA),
+ *   z = g / (rms + eps), then the integer update above.
+ * Optional outputs (NULL to skip):
+ *   rms_ema  [rows] float32, read and written (per-row EMA of ms; beta1 = beta,
+ *            beta2 = 1 - beta as float32; rows with ms == 0 keep their value)
+ *   row_rms  [rows] float32 <- sqrt(ms) (the instantaneous rms the stats sum)
+ *   grad_scale [rows] float32 <- sum_k g * code (pre-update code; trainable scale)
+ *   nonfinite int32 flag, set to 1 when a row holds a NaN/Inf; such rows are left
+ *            unchanged and do not contribute to counts.
+ * Replaces: _capture_weight_gradient  ratchet.py:487-537 (isfinite guard 501, stats
+ *           525-537), _normalize 539-556, apply_weight_gradient 558-580, and the
+ *           trainable-scale reduction ratchet.py:143-147, 167-169.
+ */
+int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* g, int g_dtype,
+                           int64_t ldg, int64_t rows, int64_t K, int max_code, int threshold,
+                           float low, float high, float eps, float* rms_ema, float beta1,
+                           float beta2, int64_t* counts, float* row_rms, float* grad_scale,
+                           int32_t* nonfinite, void* stream);
+
+/*
+ * Row normalization alone: z = g / (rms + eps) with rms = sqrt(sum_k g^2 / K) in the
+ * same fixed order as rk_ratchet_update_grad (or sqrt of the per-row EMA, which is
+ * updated in place when rms_ema is non-NULL). z float32 [rows, K] (row stride ldz);
+ * row_rms (may be NULL) receives the instantaneous rms.
+ * Replaces: DiscreteRatchetLinear._normalize  ratchet.py:539-556.
+ */
+int rk_normalize_rows(const void* g, int g_dtype, int64_t ldg, int64_t rows, int64_t K,
+                      float eps, float* rms_ema, float beta1, float beta2, float* z,
+                      int64_t ldz, float* row_rms, void* stream);
+
+/*
+ * Pressure leak: every nonzero pressure moves one unit toward zero.
+ * Replaces: _maybe_leak_pressure  ratchet.py:613-625 (the firing cadence stays in
+ * the host).
+ */
+int rk_pressure_leak(uint8_t* packed, int64_t n, int max_code, void* stream);
+
+/*
+ * State validation: flags[0] |= 1 if a code escapes [-max_code, max_code],
+ * flags[1] |= 1 if a pressure escapes [-7, 7], flags[2] |= 1 if a scale is not
+ * finite or <= 0 (scale may be NULL). flags is int32[3], caller-zeroed.
+ * Replaces: _validate_state  ratchet.py:672-679 (three host reductions).
+ */
+int rk_validate_state(const uint8_t* packed, int64_t n, int max_code, const float* scale,
+                      int64_t n_rows, int32_t* flags, void* stream);
+
+/*
+ * Fused RMSNorm + per-token absmax quantization:
+ *   y = x * rsqrt(mean_k x^2 + eps) * w;  (q, s) = quantize_rows(y).
+ * x [M, K] (dtype x_dtype, row stride ldx, unit k stride), w [K] float32.
+ * Replaces: fused_rmsnorm_quantize  int8_fused.py:14-56.
+ */
+int rk_rmsnorm_quantize(const void* x, int x_dtype, int64_t ldx, const float* w, float eps,
+                        int8_t* q, int64_t ldq, float* scale, int64_t M, int64_t K,
+                        void* stream);
+
+/*
+ * Fused tanh-GELU + per-token absmax quantization:
+ *   y = 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)));  (q, s) = quantize_rows(y).
+ * Replaces: fused_gelu_quantize  int8_fused.py:58-101.
+ */
+int rk_gelu_quantize(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                     float* scale, int64_t M, int64_t K, void* stream);
+
+/*
+ * Fused head-merge transpose + quantization: x [B, H, S, D] (element strides
+ * sb, sh, ss, sd) is read as rows [B*S, H*D] (row = b*S + s, col = h*D + d) and
+ * row-quantized.
+ * Replaces: fused_transpose_quantize  int8_fused.py:103-151.
+ */
+int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
+                          int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t sd,
+                          int8_t* q, int64_t ldq, float* scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RATCHET_HIP_H */

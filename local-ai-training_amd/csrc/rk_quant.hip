@@ -1,0 +1,380 @@
+// Per-token absmax int8 quantization kernels (gfx950).
+//
+// One 64-lane wavefront owns one row; a 256-thread block covers 4 rows. Lane l
+// handles 16-byte vectors at element offsets c*64*V + l*V (V = 4 fp32 / 8 bf16),
+// so every pass over a row is one fully coalesced sweep. Rows of up to
+// kMaxChunks*64*V elements stay in registers between the amax pass and the
+// quantize pass (HBM read once); longer rows are re-read (L2-resident).
+//
+// The same template serves four row sources:
+//   SRC_PLAIN     x[m, k] (+ optional per-column scale), int8_matmul.py:106-150
+//   SRC_RMSNORM   x * rsqrt(mean x^2 + eps) * w,          int8_fused.py:14-39
+//   SRC_GELU      tanh-GELU(x),                           int8_fused.py:58-84
+//   SRC_TRANSPOSE [B,H,S,D] read as [B*S, H*D],           int8_fused.py:103-131
+#include "rk_common.h"
+
+namespace rk {
+
+enum { SRC_PLAIN = 0, SRC_RMSNORM = 1, SRC_GELU = 2, SRC_TRANSPOSE = 3 };
+
+struct QuantArgs {
+  const void* x;
+  int64_t M, K;
+  int64_t sxm, sxk;           // plain / rmsnorm / gelu addressing
+  int64_t H, S, D;            // transpose addressing
+  int64_t sb, sh, ss, sd;
+  const float* col_scale;     // plain only, may be null
+  const float* w;             // rmsnorm weight
+  float eps;
+  uint32_t key0, key1;        // Philox key (SR only)
+  int64_t row_offset;         // SR counter row offset
+  int8_t* q;
+  int64_t ldq;
+  float* scale;
+  uint16_t* xb;               // plain only: bf16 side output, may be null
+  int64_t ldxb;
+  int vec_ok;                 // 16-byte vector loads are legal for every chunk
+};
+
+constexpr int kMaxChunks = 8;
+
+template <int DT, int SRC>
+__device__ __forceinline__ int64_t src_offset(const QuantArgs& a, int64_t row, int64_t e) {
+  if constexpr (SRC == SRC_TRANSPOSE) {
+    const int64_t b = row / a.S, s = row - b * a.S;
+    const int64_t h = e / a.D, d = e - h * a.D;
+    return b * a.sb + s * a.ss + h * a.sh + d * a.sd;
+  } else {
+    return row * a.sxm + e * a.sxk;
+  }
+}
+
+// Loads the raw chunk starting at element e0 (V elements; zeros past K).
+template <int DT, int SRC>
+__device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t row, int64_t e0,
+                                           float* v) {
+  constexpr int V = Vec<DT>::N;
+  if (a.vec_ok && e0 + V <= a.K) {
+    load_vec16<DT>(a.x, src_offset<DT, SRC>(a, row, e0), v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int64_t e = e0 + i;
+      v[i] = e < a.K ? load_elem<DT>(a.x, src_offset<DT, SRC>(a, row, e)) : 0.0f;
+    }
+  }
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), evaluated in the
+  // operation order of int8_fused.py:72-75.
+  const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float t = tanhf(inner);
+  return 0.5f * x * (1.0f + t);
+}
+
+// Row transform applied to a raw value at column e (row_factor = rsqrt for rmsnorm).
+template <int SRC>
+__device__ __forceinline__ float transform(const QuantArgs& a, float x, int64_t e,
+                                           float row_factor) {
+  if constexpr (SRC == SRC_PLAIN) {
+    return a.col_scale ? x * a.col_scale[e] : x;
+  } else if constexpr (SRC == SRC_RMSNORM) {
+    return x * row_factor * a.w[e];
+  } else if constexpr (SRC == SRC_GELU) {
+    return gelu_tanh(x);
+  } else {
+    return x;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_bf16_chunk(uint16_t* dst, int64_t e0, int64_t K,
+                                                 const float* v) {
+  constexpr int V = Vec<DT>::N;
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    if (e0 + i < K) dst[e0 + i] = f32_to_bf16(v[i]);
+}
+
+// Quantizes V transformed values y (row scale s) at columns e0.. and stores them.
+template <int DT, bool SR>
+__device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, int64_t row, int64_t e0,
+                                                  const float* y, float s, int8_t* qrow,
+                                                  bool vec_store) {
+  constexpr int V = Vec<DT>::N;
+  int8_t qv[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float t = y[i] / s;
+    float r;
+    if constexpr (SR) {
+      const uint64_t ctr =
+          static_cast<uint64_t>(a.row_offset + row) * static_cast<uint64_t>(a.K) +
+          static_cast<uint64_t>(e0 + i);
+      const float u =
+          uniform_from_word(philox_word0(static_cast<uint32_t>(ctr), a.key0, a.key1));
+      r = floorf(t + u);
+    } else {
+      r = __builtin_rintf(t);
+    }
+    r = fminf(fmaxf(r, -127.0f), 127.0f);
+    qv[i] = static_cast<int8_t>(static_cast<int>(r));
+  }
+  if (vec_store && e0 + V <= a.K) {
+    uint32_t w[V / 4];
+#pragma unroll
+    for (int j = 0; j < V / 4; ++j)
+      w[j] = (uint32_t)(uint8_t)qv[4 * j] | ((uint32_t)(uint8_t)qv[4 * j + 1] << 8) |
+             ((uint32_t)(uint8_t)qv[4 * j + 2] << 16) | ((uint32_t)(uint8_t)qv[4 * j + 3] << 24);
+    if constexpr (V == 8) {
+      *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(w[0], w[1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(qrow + e0) = w[0];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (e0 + i < a.K) qrow[e0 + i] = qv[i];
+  }
+}
+
+template <int DT, int SRC, bool SR, int NC>
+__global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
+  constexpr int V = Vec<DT>::N;
+  constexpr int SPAN = kWave * V;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const int64_t lane0 = static_cast<int64_t>(lane) * V;
+  const int64_t nchunks = (a.K + SPAN - 1) / SPAN;
+  int8_t* qrow = a.q + row * a.ldq;
+  const bool vec_store = (a.ldq % V) == 0 && ((reinterpret_cast<uintptr_t>(a.q) % V) == 0);
+  uint16_t* xbrow = (SRC == SRC_PLAIN && a.xb) ? a.xb + row * a.ldxb : nullptr;
+
+  if constexpr (NC > 0) {
+    // Register-resident row: one HBM read.
+    float xr[NC][V];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (c < nchunks) {
+        load_chunk<DT, SRC>(a, row, c * SPAN + lane0, xr[c]);
+        if (xbrow && c * SPAN + lane0 < a.K) store_bf16_chunk<DT>(xbrow, c * SPAN + lane0, a.K, xr[c]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
+      }
+    }
+    float row_factor = 1.0f;
+    if constexpr (SRC == SRC_RMSNORM) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc = acc + xr[c][i] * xr[c][i];
+      acc = wave_sum_butterfly(acc);
+      row_factor = 1.0f / sqrtf(acc / static_cast<float>(a.K) + a.eps);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const int64_t e = c * SPAN + lane0 + i;
+        if (e < a.K) {
+          xr[c][i] = transform<SRC>(a, xr[c][i], e, row_factor);
+          amax = fmaxf(amax, fabsf(xr[c][i]));
+        }
+      }
+    }
+    amax = wave_max(amax);
+    const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
+    if (lane == 0) a.scale[row] = s;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t e0 = c * SPAN + lane0;
+      if (c < nchunks && e0 < a.K) quant_store_chunk<DT, SR>(a, row, e0, xr[c], s, qrow, vec_store);
+    }
+  } else {
+    // Streaming row: re-read per pass (the row stays cache-resident).
+    float row_factor = 1.0f;
+    if constexpr (SRC == SRC_RMSNORM) {
+      float acc = 0.0f;
+      for (int64_t c = 0; c < nchunks; ++c) {
+        float v[V];
+        load_chunk<DT, SRC>(a, row, c * SPAN + lane0, v);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc = acc + v[i] * v[i];
+      }
+      acc = wave_sum_butterfly(acc);
+      row_factor = 1.0f / sqrtf(acc / static_cast<float>(a.K) + a.eps);
+    }
+    float amax = 0.0f;
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const int64_t e0 = c * SPAN + lane0;
+      float v[V];
+      load_chunk<DT, SRC>(a, row, e0, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        if (e0 + i < a.K) amax = fmaxf(amax, fabsf(transform<SRC>(a, v[i], e0 + i, row_factor)));
+    }
+    amax = wave_max(amax);
+    const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
+    if (lane == 0) a.scale[row] = s;
+    for (int64_t c = 0; c < nchunks; ++c) {
+      const int64_t e0 = c * SPAN + lane0;
+      if (e0 >= a.K) break;
+      float v[V], y[V];
+      load_chunk<DT, SRC>(a, row, e0, v);
+      if (xbrow) store_bf16_chunk<DT>(xbrow, e0, a.K, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        y[i] = (e0 + i < a.K) ? transform<SRC>(a, v[i], e0 + i, row_factor) : 0.0f;
+      quant_store_chunk<DT, SR>(a, row, e0, y, s, qrow, vec_store);
+    }
+  }
+}
+
+template <int DT, int SRC, bool SR>
+static int launch_quant(const QuantArgs& a, hipStream_t stream) {
+  constexpr int SPAN = kWave * Vec<DT>::N;
+  const int64_t nchunks = (a.K + SPAN - 1) / SPAN;
+  const dim3 grid(static_cast<unsigned>((a.M + 3) / 4));
+  const dim3 block(256);
+  if (nchunks <= 1) {
+    quant_rows_kernel<DT, SRC, SR, 1><<<grid, block, 0, stream>>>(a);
+  } else if (nchunks <= 2) {
+    quant_rows_kernel<DT, SRC, SR, 2><<<grid, block, 0, stream>>>(a);
+  } else if (nchunks <= 4) {
+    quant_rows_kernel<DT, SRC, SR, 4><<<grid, block, 0, stream>>>(a);
+  } else if (nchunks <= kMaxChunks) {
+    quant_rows_kernel<DT, SRC, SR, kMaxChunks><<<grid, block, 0, stream>>>(a);
+  } else {
+    quant_rows_kernel<DT, SRC, SR, 0><<<grid, block, 0, stream>>>(a);
+  }
+  return launch_status("quantize_rows");
+}
+
+template <int SRC, bool SR>
+static int dispatch_dtype(int dt, const QuantArgs& a, hipStream_t stream) {
+  if (dt == RK_F32) return launch_quant<RK_F32, SRC, SR>(a, stream);
+  return launch_quant<RK_BF16, SRC, SR>(a, stream);
+}
+
+static bool rows_vec_ok(const void* x, int dt, int64_t K, int64_t sxm, int64_t sxk) {
+  const int V = 16 / dtype_size(dt);
+  return sxk == 1 && aligned16(x) && (sxm % V) == 0 && (K % V) == 0;
+}
+
+static int check_common(const void* x, int dt, int64_t M, int64_t K, const int8_t* q,
+                        int64_t ldq, const float* scale) {
+  if (dt != RK_F32 && dt != RK_BF16) return fail(RK_ERR_ARG, "unsupported input dtype %d", dt);
+  if (M < 0 || K <= 0) return fail(RK_ERR_ARG, "invalid shape M=%lld K=%lld", (long long)M, (long long)K);
+  if (M > 0 && (!x || !q || !scale)) return fail(RK_ERR_ARG, "null pointer argument");
+  if (ldq < K) return fail(RK_ERR_ARG, "ldq (%lld) < K (%lld)", (long long)ldq, (long long)K);
+  if (M > (int64_t(1) << 33)) return fail(RK_ERR_ARG, "too many rows");
+  return RK_OK;
+}
+
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                                int64_t sxk, const float* col_scale, int stochastic,
+                                uint64_t seed, int64_t row_offset, int8_t* q, int64_t ldq,
+                                float* scale, uint16_t* x_bf16, int64_t ld_xb, void* stream) {
+  clear_error();
+  if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
+  if (x_bf16 && ld_xb < K) return fail(RK_ERR_ARG, "ld_xb < K");
+  if (M == 0) return RK_OK;
+  QuantArgs a{};
+  a.x = x;
+  a.M = M;
+  a.K = K;
+  a.sxm = sxm;
+  a.sxk = sxk;
+  a.col_scale = col_scale;
+  a.key0 = static_cast<uint32_t>(seed & 0xffffffffu);
+  a.key1 = static_cast<uint32_t>(seed >> 32);
+  a.row_offset = row_offset;
+  a.q = q;
+  a.ldq = ldq;
+  a.scale = scale;
+  a.xb = x_bf16;
+  a.ldxb = ld_xb;
+  a.vec_ok = rows_vec_ok(x, x_dtype, K, sxm, sxk) ? 1 : 0;
+  if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(x_dtype, a, as_stream(stream));
+  return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
+}
+
+extern "C" int rk_rmsnorm_quantize(const void* x, int x_dtype, int64_t ldx, const float* w,
+                                   float eps, int8_t* q, int64_t ldq, float* scale, int64_t M,
+                                   int64_t K, void* stream) {
+  clear_error();
+  if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
+  if (M > 0 && !w) return fail(RK_ERR_ARG, "null RMSNorm weight");
+  if (M == 0) return RK_OK;
+  QuantArgs a{};
+  a.x = x;
+  a.M = M;
+  a.K = K;
+  a.sxm = ldx;
+  a.sxk = 1;
+  a.w = w;
+  a.eps = eps;
+  a.q = q;
+  a.ldq = ldq;
+  a.scale = scale;
+  a.vec_ok = rows_vec_ok(x, x_dtype, K, ldx, 1) ? 1 : 0;
+  return dispatch_dtype<SRC_RMSNORM, false>(x_dtype, a, as_stream(stream));
+}
+
+extern "C" int rk_gelu_quantize(const void* x, int x_dtype, int64_t ldx, int8_t* q,
+                                int64_t ldq, float* scale, int64_t M, int64_t K, void* stream) {
+  clear_error();
+  if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
+  if (M == 0) return RK_OK;
+  QuantArgs a{};
+  a.x = x;
+  a.M = M;
+  a.K = K;
+  a.sxm = ldx;
+  a.sxk = 1;
+  a.q = q;
+  a.ldq = ldq;
+  a.scale = scale;
+  a.vec_ok = rows_vec_ok(x, x_dtype, K, ldx, 1) ? 1 : 0;
+  return dispatch_dtype<SRC_GELU, false>(x_dtype, a, as_stream(stream));
+}
+
+extern "C" int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int64_t H,
+                                     int64_t S, int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                     int64_t sd, int8_t* q, int64_t ldq, float* scale,
+                                     void* stream) {
+  clear_error();
+  if (B < 0 || H <= 0 || S < 0 || D <= 0) return fail(RK_ERR_ARG, "invalid [B,H,S,D] shape");
+  const int64_t M = B * S, K = H * D;
+  if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
+  if (M == 0) return RK_OK;
+  QuantArgs a{};
+  a.x = x;
+  a.M = M;
+  a.K = K;
+  a.H = H;
+  a.S = S;
+  a.D = D;
+  a.sb = sb;
+  a.sh = sh;
+  a.ss = ss;
+  a.sd = sd;
+  a.q = q;
+  a.ldq = ldq;
+  a.scale = scale;
+  const int V = 16 / dtype_size(x_dtype);
+  a.vec_ok = (sd == 1 && aligned16(x) && D % V == 0 && sb % V == 0 && sh % V == 0 &&
+              ss % V == 0)
+                 ? 1
+                 : 0;
+  return dispatch_dtype<SRC_TRANSPOSE, false>(x_dtype, a, as_stream(stream));
+}

@@ -1,0 +1,422 @@
+// Fused integer ratchet update (gfx950).
+//
+// Persistent state is one byte per weight: low nibble code + max_code, high nibble
+// pressure + 7 (ratchet.py:185-199). The update never materializes a float weight:
+// it reads the byte and the (normalized) gradient, writes the byte back, and
+// accumulates the four move counts. Everything is one HBM sweep:
+//   z path:    1 B packed read + 4 B z read + 1 B write per weight
+//   grad path: 1 B packed read + 2|4 B gradient read + 1 B write per weight,
+//              the row RMS normalization fused in (one wavefront per row).
+//
+// Row reduction order for mean(g^2) (fixed, reproduced by the oracle): lane l owns
+// 16-byte vectors at c*64*V + l*V; it accumulates acc = acc + g*g over chunks c
+// ascending and vector slots ascending (separately rounded fp32 ops); the 64 lane
+// sums are combined by the xor butterfly of wave_sum_butterfly.
+#include "rk_common.h"
+
+namespace rk {
+
+struct MoveCounts {
+  int pos = 0, neg = 0, bpos = 0, bneg = 0;
+};
+
+// One weight: ratchet.py:248-262 (bucket) and 277-294 (update + repack).
+__device__ __forceinline__ uint32_t ratchet_byte(uint32_t byte, float z, int mc, int T,
+                                                 float low, float high, MoveCounts& cnt) {
+  const float a = fabsf(z);
+  const int mag = a >= high ? 2 : (a >= low ? 1 : 0);
+  const int sgn = (z > 0.0f) - (z < 0.0f);
+  const int c = static_cast<int>(byte & 15u) - mc;
+  int p = static_cast<int>(byte >> 4) - 7 - sgn * mag;
+  const int pr = p >= T, nr = p <= -T;
+  const int pm = pr & (c < mc), nm = nr & (c > -mc);
+  p = p - pr * T + nr * T;
+  p = min(max(p, -128), 127);
+  cnt.pos += pm;
+  cnt.neg += nm;
+  cnt.bpos += pr & (pm ^ 1);
+  cnt.bneg += nr & (nm ^ 1);
+  const int cn = c + pm - nm;
+  return static_cast<uint32_t>((cn + mc) & 15) | (static_cast<uint32_t>((p + 7) & 15) << 4);
+}
+
+// Block-level count reduction and one 64-bit atomic per counter per block.
+__device__ __forceinline__ void flush_counts(MoveCounts cnt, int64_t* counts) {
+  __shared__ int sc[4];
+  if (threadIdx.x < 4) sc[threadIdx.x] = 0;
+  __syncthreads();
+  const int p = wave_sum_int(cnt.pos), n = wave_sum_int(cnt.neg);
+  const int bp = wave_sum_int(cnt.bpos), bn = wave_sum_int(cnt.bneg);
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(&sc[0], p);
+    atomicAdd(&sc[1], n);
+    atomicAdd(&sc[2], bp);
+    atomicAdd(&sc[3], bn);
+  }
+  __syncthreads();
+  if (threadIdx.x < 4 && counts) {
+    const int v = sc[threadIdx.x];
+    if (v) atomicAdd(reinterpret_cast<unsigned long long*>(counts) + threadIdx.x,
+                     static_cast<unsigned long long>(v));
+  }
+}
+
+__device__ __forceinline__ bool finite_f32(float x) {
+  return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u;
+}
+
+// Loads V packed bytes (zeros past K) into one word per 4 bytes.
+template <int V>
+__device__ __forceinline__ void load_bytes(const uint8_t* p, int64_t e0, int64_t K, bool vec,
+                                           uint32_t* w) {
+  if (vec && e0 + V <= K) {
+    if constexpr (V == 8) {
+      const uint2 t = *reinterpret_cast<const uint2*>(p + e0);
+      w[0] = t.x;
+      w[1] = t.y;
+    } else {
+      w[0] = *reinterpret_cast<const uint32_t*>(p + e0);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < V / 4; ++j) w[j] = 0;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (e0 + i < K) w[i >> 2] |= static_cast<uint32_t>(p[e0 + i]) << (8 * (i & 3));
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void store_bytes(uint8_t* p, int64_t e0, int64_t K, bool vec,
+                                            const uint32_t* w) {
+  if (vec && e0 + V <= K) {
+    if constexpr (V == 8) {
+      *reinterpret_cast<uint2*>(p + e0) = make_uint2(w[0], w[1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(p + e0) = w[0];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (e0 + i < K) p[e0 + i] = static_cast<uint8_t>(w[i >> 2] >> (8 * (i & 3)));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Update on a normalized gradient z (apply_normalized_gradient).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ratchet_update_z_kernel(
+    uint8_t* packed, int64_t ldp, const float* z, int64_t ldz, int64_t rows, int64_t K,
+    int mc, int T, float low, float high, int64_t* counts, int vec_z, int vec_p) {
+  constexpr int V = 4;
+  const int lane = threadIdx.x & 63;
+  MoveCounts cnt;
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < rows;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    uint8_t* prow = packed + row * ldp;
+    const float* zrow = z + row * ldz;
+    for (int64_t e0 = static_cast<int64_t>(lane) * V; e0 < K; e0 += 64 * V) {
+      float zv[V];
+      if (vec_z && e0 + V <= K) {
+        load_vec16<RK_F32>(zrow, e0, zv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) zv[i] = e0 + i < K ? zrow[e0 + i] : 0.0f;
+      }
+      uint32_t w[1];
+      load_bytes<V>(prow, e0, K, vec_p, w);
+      uint32_t out = 0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        if (e0 + i < K) {
+          out |= ratchet_byte((w[0] >> (8 * i)) & 0xffu, zv[i], mc, T, low, high, cnt) << (8 * i);
+        }
+      }
+      store_bytes<V>(prow, e0, K, vec_p, &out);
+    }
+  }
+  flush_counts(cnt, counts);
+}
+
+// ---------------------------------------------------------------------------
+// Fused normalize + update from the raw weight gradient (one wavefront per row).
+// NC > 0: the row's gradient stays in registers between the two passes.
+// ---------------------------------------------------------------------------
+struct GradUpdateArgs {
+  uint8_t* packed;
+  int64_t ldp;
+  const void* g;
+  int64_t ldg;
+  int64_t rows, K;
+  int mc, T;
+  float low, high, eps;
+  float* rms_ema;
+  float beta1, beta2;
+  int64_t* counts;
+  float* row_rms;
+  float* grad_scale;
+  int32_t* nonfinite;
+  float* z_out;  // normalize-only mode: z[row, k] (row stride ldz)
+  int64_t ldz;
+  int vec_g, vec_p;
+};
+
+// ZONLY = true: write z = g / (rms + eps) instead of updating (the reference's
+// _normalize, ratchet.py:539-556), with the identical reduction order.
+template <int DT, int NC, bool ZONLY>
+__global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs a) {
+  constexpr int V = Vec<DT>::N;
+  constexpr int SPAN = 64 * V;
+  constexpr int NW = V / 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t lane0 = static_cast<int64_t>(lane) * V;
+  const int64_t nchunks = (a.K + SPAN - 1) / SPAN;
+  MoveCounts cnt;
+
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    const char* grow =
+        static_cast<const char*>(a.g) + row * a.ldg * (DT == RK_F32 ? 4 : 2);
+    uint8_t* prow = a.packed + row * a.ldp;
+
+    auto load_g = [&](int64_t e0, float* v) {
+      if (a.vec_g && e0 + V <= a.K) {
+        load_vec16<DT>(grow, e0, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = e0 + i < a.K ? load_elem<DT>(grow, e0 + i) : 0.0f;
+      }
+    };
+
+    // Pass 1: sum of squares (fixed order) and the finiteness check.
+    float xr[NC > 0 ? NC : 1][V];
+    float acc = 0.0f;
+    int bad = 0;
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (c < nchunks) {
+          load_g(c * SPAN + lane0, xr[c]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          bad |= !finite_f32(xr[c][i]);
+          acc = acc + xr[c][i] * xr[c][i];
+        }
+      }
+    } else {
+      for (int64_t c = 0; c < nchunks; ++c) {
+        float v[V];
+        load_g(c * SPAN + lane0, v);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          bad |= !finite_f32(v[i]);
+          acc = acc + v[i] * v[i];
+        }
+      }
+    }
+    acc = wave_sum_butterfly(acc);
+    bad = wave_or_int(bad);
+
+    const float ms = acc / static_cast<float>(a.K);
+    const float rms_inst = sqrtf(ms);
+    float rms = rms_inst;
+    if (a.rms_ema) {
+      const float ema = a.rms_ema[row];
+      const float upd = ema == 0.0f ? ms : a.beta1 * ema + a.beta2 * ms;
+      const float ema_new = ms > 0.0f ? upd : ema;
+      rms = sqrtf(ema_new);
+      if ((ZONLY || !bad) && lane == 0) a.rms_ema[row] = ema_new;
+    }
+    if (a.row_rms && lane == 0) a.row_rms[row] = rms_inst;
+    if constexpr (ZONLY) {
+      const float dz = rms + a.eps;
+      float* zrow = a.z_out + row * a.ldz;
+      for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t e0 = c * SPAN + lane0;
+        if (e0 >= a.K) break;
+        float v[V];
+        if constexpr (NC > 0) {
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc)
+            if (cc == c) {
+#pragma unroll
+              for (int i = 0; i < V; ++i) v[i] = xr[cc][i];
+            }
+        } else {
+          load_g(e0, v);
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          if (e0 + i < a.K) zrow[e0 + i] = v[i] / dz;
+      }
+      continue;
+    }
+    if (bad) {
+      if (lane == 0 && a.nonfinite) a.nonfinite[0] = 1;
+      continue;
+    }
+    const float d = rms + a.eps;
+
+    // Pass 2: normalize, update, repack; optional sum_k g * code (pre-update code).
+    float gs = 0.0f;
+    auto do_chunk = [&](int64_t e0, const float* v) {
+      uint32_t w[NW], out[NW];
+      load_bytes<V>(prow, e0, a.K, a.vec_p, w);
+#pragma unroll
+      for (int j = 0; j < NW; ++j) out[j] = 0;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        if (a.grad_scale) gs = gs + v[i] * static_cast<float>(static_cast<int>(byte & 15u) - a.mc);
+        if (e0 + i < a.K) {
+          const float zz = v[i] / d;
+          out[i >> 2] |= ratchet_byte(byte, zz, a.mc, a.T, a.low, a.high, cnt) << (8 * (i & 3));
+        }
+      }
+      store_bytes<V>(prow, e0, a.K, a.vec_p, out);
+    };
+    if constexpr (NC > 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t e0 = c * SPAN + lane0;
+        if (c < nchunks && e0 < a.K) do_chunk(e0, xr[c]);
+      }
+    } else {
+      for (int64_t c = 0; c < nchunks; ++c) {
+        const int64_t e0 = c * SPAN + lane0;
+        if (e0 >= a.K) break;
+        float v[V];
+        load_g(e0, v);
+        do_chunk(e0, v);
+      }
+    }
+    if (a.grad_scale) {
+      gs = wave_sum_butterfly(gs);
+      if (lane == 0) a.grad_scale[row] = gs;
+    }
+  }
+  flush_counts(cnt, a.counts);
+}
+
+static unsigned row_grid(int64_t rows) {
+  // Enough blocks to fill 256 CUs several times over; rows beyond that loop.
+  const int64_t want = (rows + 3) / 4;
+  return static_cast<unsigned>(want < 4096 ? (want > 0 ? want : 1) : 4096);
+}
+
+static int check_update_common(const uint8_t* packed, int64_t ldp, int64_t rows, int64_t K,
+                               int mc, int T, float low, float high) {
+  if (rows < 0 || K <= 0) return fail(RK_ERR_ARG, "invalid update shape");
+  if (rows > 0 && !packed) return fail(RK_ERR_ARG, "null packed state");
+  if (ldp < K) return fail(RK_ERR_ARG, "ldp < K");
+  if (mc < 1 || mc > 7) return fail(RK_ERR_ARG, "max_code must be in 1..7");
+  if (T < 1 || T > 127) return fail(RK_ERR_ARG, "pressure_threshold must be in [1, 127]");
+  if (!(low >= 0.0f && low < high)) return fail(RK_ERR_ARG, "bucket thresholds must satisfy 0 <= low < high");
+  return RK_OK;
+}
+
+template <bool ZONLY>
+static int launch_grad_kernel(const GradUpdateArgs& a, int g_dtype, hipStream_t s) {
+  const int V = g_dtype == RK_F32 ? 4 : 8;
+  const int64_t nchunks = (a.K + 64 * V - 1) / (64 * V);
+  const dim3 grid(row_grid(a.rows)), block(256);
+  if (g_dtype == RK_F32) {
+    if (nchunks <= 2) ratchet_update_grad_kernel<RK_F32, 2, ZONLY><<<grid, block, 0, s>>>(a);
+    else if (nchunks <= 8) ratchet_update_grad_kernel<RK_F32, 8, ZONLY><<<grid, block, 0, s>>>(a);
+    else ratchet_update_grad_kernel<RK_F32, 0, ZONLY><<<grid, block, 0, s>>>(a);
+  } else {
+    if (nchunks <= 1) ratchet_update_grad_kernel<RK_BF16, 1, ZONLY><<<grid, block, 0, s>>>(a);
+    else if (nchunks <= 4) ratchet_update_grad_kernel<RK_BF16, 4, ZONLY><<<grid, block, 0, s>>>(a);
+    else if (nchunks <= 12) ratchet_update_grad_kernel<RK_BF16, 12, ZONLY><<<grid, block, 0, s>>>(a);
+    else ratchet_update_grad_kernel<RK_BF16, 0, ZONLY><<<grid, block, 0, s>>>(a);
+  }
+  return launch_status(ZONLY ? "normalize_rows" : "ratchet_update_grad");
+}
+
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" int rk_ratchet_update(uint8_t* packed, int64_t ldp, const float* z, int64_t ldz,
+                                 int64_t rows, int64_t K, int max_code, int threshold,
+                                 float low, float high, int64_t* counts, void* stream) {
+  clear_error();
+  if (int st = check_update_common(packed, ldp, rows, K, max_code, threshold, low, high)) return st;
+  if (rows == 0) return RK_OK;
+  if (!z) return fail(RK_ERR_ARG, "null gradient");
+  if (ldz < K) return fail(RK_ERR_ARG, "ldz < K");
+  const int vec_z = aligned16(z) && (ldz % 4) == 0 && (K % 4) == 0;
+  const int vec_p = (reinterpret_cast<uintptr_t>(packed) % 4) == 0 && (ldp % 4) == 0 && (K % 4) == 0;
+  ratchet_update_z_kernel<<<row_grid(rows), 256, 0, as_stream(stream)>>>(
+      packed, ldp, z, ldz, rows, K, max_code, threshold, low, high, counts, vec_z, vec_p);
+  return launch_status("ratchet_update");
+}
+
+extern "C" int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* g, int g_dtype,
+                                      int64_t ldg, int64_t rows, int64_t K, int max_code,
+                                      int threshold, float low, float high, float eps,
+                                      float* rms_ema, float beta1, float beta2, int64_t* counts,
+                                      float* row_rms, float* grad_scale, int32_t* nonfinite,
+                                      void* stream) {
+  clear_error();
+  if (int st = check_update_common(packed, ldp, rows, K, max_code, threshold, low, high)) return st;
+  if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
+  if (rows == 0) return RK_OK;
+  if (!g) return fail(RK_ERR_ARG, "null gradient");
+  if (ldg < K) return fail(RK_ERR_ARG, "ldg < K");
+  if (!(eps > 0.0f)) return fail(RK_ERR_ARG, "eps must be positive");
+  GradUpdateArgs a{};
+  a.packed = packed;
+  a.ldp = ldp;
+  a.g = g;
+  a.ldg = ldg;
+  a.rows = rows;
+  a.K = K;
+  a.mc = max_code;
+  a.T = threshold;
+  a.low = low;
+  a.high = high;
+  a.eps = eps;
+  a.rms_ema = rms_ema;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.counts = counts;
+  a.row_rms = row_rms;
+  a.grad_scale = grad_scale;
+  a.nonfinite = nonfinite;
+  const int V = g_dtype == RK_F32 ? 4 : 8;
+  a.vec_g = aligned16(g) && (ldg % V) == 0 && (K % V) == 0;
+  a.vec_p = (reinterpret_cast<uintptr_t>(packed) % V) == 0 && (ldp % V) == 0 && (K % V) == 0;
+  return launch_grad_kernel<false>(a, g_dtype, as_stream(stream));
+}
+
+extern "C" int rk_normalize_rows(const void* g, int g_dtype, int64_t ldg, int64_t rows, int64_t K,
+                                 float eps, float* rms_ema, float beta1, float beta2, float* z,
+                                 int64_t ldz, float* row_rms, void* stream) {
+  clear_error();
+  if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
+  if (rows < 0 || K <= 0) return fail(RK_ERR_ARG, "invalid normalize shape");
+  if (rows == 0) return RK_OK;
+  if (!g || !z) return fail(RK_ERR_ARG, "null pointer");
+  if (ldg < K || ldz < K) return fail(RK_ERR_ARG, "leading dimension too small");
+  if (!(eps > 0.0f)) return fail(RK_ERR_ARG, "eps must be positive");
+  GradUpdateArgs a{};
+  a.g = g;
+  a.ldg = ldg;
+  a.rows = rows;
+  a.K = K;
+  a.eps = eps;
+  a.rms_ema = rms_ema;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.row_rms = row_rms;
+  a.z_out = z;
+  a.ldz = ldz;
+  const int V = g_dtype == RK_F32 ? 4 : 8;
+  a.vec_g = aligned16(g) && (ldg % V) == 0 && (K % V) == 0;
+  return launch_grad_kernel<true>(a, g_dtype, as_stream(stream));
+}

@@ -1,0 +1,107 @@
+"""ctypes binding of libratchet_hip.so (the C ABI declared in include/ratchet_hip.h).
+
+The shared library is the only compute path of this package: if it is missing or
+fails to load, every GPU entry point raises. Tensors are passed as raw device
+pointers plus element strides; the stream is the caller's current torch stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libratchet_hip.so"
+LIB_PATH = Path(os.environ.get("RATCHET_HIP_LIB", Path(__file__).with_name(LIB_NAME)))
+
+RK_F32 = 0
+RK_BF16 = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_u64 = ctypes.c_uint64
+_f32 = ctypes.c_float
+_p = ctypes.c_void_p
+
+# name -> argument types (all return int status, except where noted)
+SIGNATURES: dict[str, list] = {
+    "rk_quantize_rows": [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _u64, _i64, _p, _i64, _p,
+                         _p, _i64, _p],
+    "rk_int8_gemm_nt": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p],
+    "rk_int8_gemm_packed": [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i64, _i64, _i64, _i64,
+                            _p],
+    "rk_unpack_transpose": [_p, _i64, _i32, _p, _i64, _i64, _i64, _p],
+    "rk_unpack": [_p, _i64, _i32, _p, _p, _p],
+    "rk_effective_bf16": [_p, _i64, _i32, _p, _p, _i64, _i64, _i64, _p],
+    "rk_dequant_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
+    "rk_ratchet_update": [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _f32, _f32, _p, _p],
+    "rk_ratchet_update_grad": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i32, _i32, _f32, _f32,
+                               _f32, _p, _f32, _f32, _p, _p, _p, _p, _p],
+    "rk_normalize_rows": [_p, _i32, _i64, _i64, _i64, _f32, _p, _f32, _f32, _p, _i64, _p, _p],
+    "rk_pressure_leak": [_p, _i64, _i32, _p],
+    "rk_validate_state": [_p, _i64, _i32, _p, _i64, _p, _p],
+    "rk_rmsnorm_quantize": [_p, _i32, _i64, _p, _f32, _p, _i64, _p, _i64, _i64, _p],
+    "rk_gelu_quantize": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _p],
+    "rk_transpose_quantize": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
+                              _i64, _p, _p],
+    "rk_version": [],
+    "rk_last_error": [],
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises RuntimeError if unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.is_file():
+        raise RuntimeError(
+            f"{LIB_NAME} not found at {LIB_PATH}; build it with "
+            "`python local-ai-training_amd/build.py` (the ratchet int8 path has no fallback)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "rk_last_error" else ctypes.c_int
+    _lib = lib
+    return lib
+
+
+class NativeError(RuntimeError):
+    """A libratchet_hip.so entry point returned a non-zero status."""
+
+
+def call(name: str, *args) -> None:
+    lib = load_library()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        message = lib.rk_last_error().decode(errors="replace")
+        raise NativeError(f"{name} failed (status {status}): {message}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return RK_F32
+    if dtype == torch.bfloat16:
+        return RK_BF16
+    raise TypeError(f"unsupported dtype {dtype}; expected float32 or bfloat16")
+
+
+def require_rocm(*tensors: torch.Tensor, what: str) -> None:
+    """The int8 ratchet path runs only on a ROCm GPU (torch device type 'cuda')."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{what} requires CUDA (a ROCm GPU); the int8 path is GPU-only")

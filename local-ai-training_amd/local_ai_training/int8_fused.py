@@ -1,0 +1,121 @@
+"""Fused per-token absmax-quant prologues on gfx950 (drop-in for ``int8_fused.py``).
+
+Each prologue computes its transform and the int8 row quantization in one HIP kernel
+(one wavefront per token row): RMSNorm+quant, tanh-GELU+quant and the attention
+head-merge transpose+quant (``int8_fused.py:14-151``). The autograd wrappers return
+the reference's third "dummy" output so gradient flows through the ratchet layer's
+``inputs`` argument (``int8_fused.py:153-201``).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _native as nat
+
+
+def _rowwise(x: Tensor) -> Tensor:
+    flat = x.flatten(0, -2)
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    if flat.dtype not in (torch.float32, torch.bfloat16):
+        flat = flat.float()
+    return flat
+
+
+def _ld(t: Tensor) -> int:
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+def fused_rmsnorm_quantize(x: Tensor, weight: Tensor, eps: float = 1e-5) -> tuple[Tensor, Tensor]:
+    if not x.is_cuda:
+        raise RuntimeError("CUDA required (a ROCm GPU)")
+    original_shape = x.shape
+    flat = _rowwise(x)
+    m, k = flat.shape
+    out = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    w = weight.detach().float().contiguous()
+    nat.call("rk_rmsnorm_quantize", flat.data_ptr(), nat.dtype_code(flat.dtype), _ld(flat),
+             w.data_ptr(), float(eps), out.data_ptr(), k, scale.data_ptr(), m, k,
+             nat.stream_handle(x.device))
+    return out.reshape(original_shape), scale.reshape(original_shape[:-1])
+
+
+def fused_gelu_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
+    if not x.is_cuda:
+        raise RuntimeError("CUDA required (a ROCm GPU)")
+    original_shape = x.shape
+    flat = _rowwise(x)
+    m, k = flat.shape
+    out = torch.empty((m, k), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    nat.call("rk_gelu_quantize", flat.data_ptr(), nat.dtype_code(flat.dtype), _ld(flat),
+             out.data_ptr(), k, scale.data_ptr(), m, k, nat.stream_handle(x.device))
+    return out.reshape(original_shape), scale.reshape(original_shape[:-1])
+
+
+def fused_transpose_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
+    """[B, H, S, D] (any strides) -> int8 rows [B*S, H*D] and float32 scales [B*S]."""
+    if not x.is_cuda:
+        raise RuntimeError("CUDA required (a ROCm GPU)")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    batch_size, n_head, seq_len, head_dim = x.shape
+    m, channels = batch_size * seq_len, n_head * head_dim
+    out = torch.empty((m, channels), device=x.device, dtype=torch.int8)
+    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
+    sb, sh, ss, sd = x.stride()
+    nat.call("rk_transpose_quantize", x.data_ptr(), nat.dtype_code(x.dtype), batch_size, n_head,
+             seq_len, head_dim, sb, sh, ss, sd, out.data_ptr(), channels, scale.data_ptr(),
+             nat.stream_handle(x.device))
+    return out, scale
+
+
+class FusedRMSNormQuantizeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, eps: float = 1e-5):
+        int8_out, scale_out = fused_rmsnorm_quantize(x, weight, eps)
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        return int8_out, scale_out, torch.empty_like(x)
+
+    @staticmethod
+    def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        x, weight = ctx.saved_tensors
+        from .int8_backward import rmsnorm_backward
+
+        grad_x, grad_w = rmsnorm_backward(grad_dummy, x, weight, ctx.eps)
+        return grad_x, grad_w, None
+
+
+class FusedGELUQuantizeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x: Tensor):
+        int8_out, scale_out = fused_gelu_quantize(x)
+        ctx.save_for_backward(x)
+        return int8_out, scale_out, torch.empty_like(x)
+
+    @staticmethod
+    def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        (x,) = ctx.saved_tensors
+        from .int8_backward import gelu_backward
+
+        return gelu_backward(grad_dummy, x)
+
+
+class FusedTransposeQuantizeFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, attended: Tensor):
+        int8_out, scale_out = fused_transpose_quantize(attended)
+        batch_size, n_head, seq_len, head_dim = attended.shape
+        ctx.shape = attended.shape
+        dummy = torch.empty((batch_size, seq_len, n_head * head_dim), device=attended.device,
+                            dtype=attended.dtype)
+        return int8_out, scale_out, dummy
+
+    @staticmethod
+    def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        batch_size, n_head, seq_len, head_dim = ctx.shape
+        return grad_dummy.view(batch_size, seq_len, n_head, head_dim).transpose(1, 2)

@@ -1,0 +1,252 @@
+"""Decoder-only ratchet GPT (drop-in for ``model.py``), the host caller of the int8 path.
+
+Same architecture and switches as the reference (``model.py:23-285``): sinusoidal
+positions, RMSNorm, causal SDPA, tanh-GELU FFN in int8 mode (erf-GELU otherwise),
+untied ratchet ``lm_head``, every dense matrix a ``DiscreteRatchetLinear`` with the
+update fused into backward. In ``matmul_mode="int8"`` the RMSNorm / GELU / head-merge
+prologues quantize on the GPU and hand int8 rows straight to the ratchet GEMMs.
+
+Additions: ``ffn_hidden`` (default ``4 * n_embd``, the reference's hard-coded width,
+``model.py:137``) so 1B-class shapes with FFN 5632 can be built.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from .int8_fused import FusedGELUQuantizeFn, FusedRMSNormQuantizeFn, FusedTransposeQuantizeFn
+from .ratchet import DiscreteRatchetLinear, RatchetEmbedding, RatchetUpdateStats
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    vocab_size: int
+    block_size: int = 128
+    n_layer: int = 2
+    n_head: int = 4
+    n_embd: int = 128
+    dropout: float = 0.0
+    pressure_threshold: int = 8
+    bucket_low: float = 0.5
+    bucket_high: float = 1.5
+    trainable_scale: bool = False
+    rms_ema_beta: float = 0.0
+    pressure_leak_period: int = 0
+    compile_update: bool = False
+    gradient_checkpointing: bool = False
+    matmul_mode: Literal["fp32", "bf16", "int8"] = "fp32"
+    int8_backward: bool = False
+    qat: bool = False
+    ratchet_embedding: bool = False
+    ffn_hidden: int | None = None
+
+    def __post_init__(self) -> None:
+        if min(self.vocab_size, self.block_size, self.n_layer, self.n_head, self.n_embd) <= 0:
+            raise ValueError("model dimensions must be positive")
+        if self.n_embd % self.n_head != 0:
+            raise ValueError("n_embd must be divisible by n_head")
+        if not 0 <= self.dropout < 1:
+            raise ValueError("dropout must be in [0, 1)")
+        if self.matmul_mode not in {"fp32", "bf16", "int8"}:
+            raise ValueError("matmul_mode must be fp32, bf16, or int8")
+        if self.ffn_hidden is not None and self.ffn_hidden <= 0:
+            raise ValueError("ffn_hidden must be positive")
+        if self.qat:
+            raise ValueError("the QAT control arm is not part of the ratchet-linear build")
+
+    @property
+    def hidden_size(self) -> int:
+        return self.ffn_hidden if self.ffn_hidden is not None else 4 * self.n_embd
+
+
+def _sinusoidal_positions(block_size: int, n_embd: int) -> Tensor:
+    positions = torch.arange(block_size, dtype=torch.float32)[:, None]
+    even = torch.arange(0, n_embd, 2, dtype=torch.float32)
+    frequencies = torch.exp(-math.log(10_000.0) * even / n_embd)
+    encoding = torch.zeros(block_size, n_embd, dtype=torch.float32)
+    encoding[:, 0::2] = torch.sin(positions * frequencies)
+    if n_embd > 1:
+        encoding[:, 1::2] = torch.cos(positions * frequencies[: encoding[:, 1::2].shape[1]])
+    return encoding
+
+
+def _linear(config: ModelConfig, in_features: int, out_features: int, max_code: int | None):
+    if max_code is None:
+        return nn.Linear(in_features, out_features, bias=False)
+    return DiscreteRatchetLinear(
+        in_features, out_features, max_code=max_code,
+        pressure_threshold=config.pressure_threshold, bucket_low=config.bucket_low,
+        bucket_high=config.bucket_high, trainable_scale=config.trainable_scale,
+        rms_ema_beta=config.rms_ema_beta, pressure_leak_period=config.pressure_leak_period,
+        compile_update=config.compile_update, matmul_mode=config.matmul_mode,
+        fuse_backward_update=True, int8_backward=config.int8_backward,
+    )
+
+
+def _is_int8(layer: nn.Module) -> bool:
+    return getattr(layer, "matmul_mode", "fp32") == "int8"
+
+
+class CausalSelfAttention(nn.Module):
+    def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
+        super().__init__()
+        self.qkv = _linear(config, config.n_embd, 3 * config.n_embd, max_code)
+        self.projection = _linear(config, config.n_embd, config.n_embd, max_code)
+        self.n_head = config.n_head
+        self.head_size = config.n_embd // config.n_head
+        self.dropout = config.dropout
+
+    def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
+                inputs_scale: Tensor | None = None) -> Tensor:
+        batch_size, sequence_length, channels = inputs.shape
+        if inputs_int8 is not None:
+            qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
+        else:
+            qkv = self.qkv(inputs)
+        query, key, value = qkv.chunk(3, dim=-1)
+
+        def heads(t: Tensor) -> Tensor:
+            return t.view(batch_size, sequence_length, self.n_head, self.head_size).transpose(1, 2)
+
+        q, k, v = heads(query), heads(key), heads(value)
+        dropout_p = self.dropout if self.training else 0.0
+        if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
+            # Fused attention kernels only: the math fallback runs 16-bit batched
+            # products on transposed views, which this path avoids.
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                attended = F.scaled_dot_product_attention(q, k, v, dropout_p=dropout_p,
+                                                          is_causal=True)
+        else:
+            attended = F.scaled_dot_product_attention(q, k, v, dropout_p=dropout_p,
+                                                      is_causal=True)
+        if _is_int8(self.projection):
+            attn_int8, attn_scale, dummy = FusedTransposeQuantizeFn.apply(attended)
+            return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale)
+        joined = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, channels)
+        return self.projection(joined)
+
+
+class FeedForward(nn.Module):
+    def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
+        super().__init__()
+        hidden = config.hidden_size
+        self.expand = _linear(config, config.n_embd, hidden, max_code)
+        self.contract = _linear(config, hidden, config.n_embd, max_code)
+        self.dropout = config.dropout
+
+    def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
+                inputs_scale: Tensor | None = None) -> Tensor:
+        if inputs_int8 is not None:
+            expanded = self.expand(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
+        else:
+            expanded = self.expand(inputs)
+        if _is_int8(self.contract):
+            gelu_int8, gelu_scale, dummy = FusedGELUQuantizeFn.apply(expanded)
+            contracted = self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale)
+        else:
+            contracted = self.contract(F.gelu(expanded))
+        return F.dropout(contracted, p=self.dropout, training=self.training)
+
+
+class TransformerBlock(nn.Module):
+    def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
+        super().__init__()
+        self.attention_norm = nn.RMSNorm(config.n_embd)
+        self.attention = CausalSelfAttention(config, max_code=max_code)
+        self.feed_forward_norm = nn.RMSNorm(config.n_embd)
+        self.feed_forward = FeedForward(config, max_code=max_code)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        if _is_int8(self.attention.qkv):
+            q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight, 1e-5)
+            inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s)
+        else:
+            inputs = inputs + self.attention(self.attention_norm(inputs))
+        if _is_int8(self.feed_forward.expand):
+            q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
+                                                       1e-5)
+            inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
+        else:
+            inputs = inputs + self.feed_forward(self.feed_forward_norm(inputs))
+        return inputs
+
+
+class RatchetGPT(nn.Module):
+    def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
+        super().__init__()
+        self.config = config
+        self.max_code = max_code
+        if max_code is not None and config.ratchet_embedding:
+            self.token_embedding = RatchetEmbedding(
+                config.vocab_size, config.n_embd, max_code=max_code,
+                pressure_threshold=config.pressure_threshold, bucket_low=config.bucket_low,
+                bucket_high=config.bucket_high, trainable_scale=config.trainable_scale,
+                compile_update=config.compile_update, rms_ema_beta=config.rms_ema_beta,
+                pressure_leak_period=config.pressure_leak_period,
+            )
+        else:
+            self.token_embedding = nn.Embedding(config.vocab_size, config.n_embd)
+        self.register_buffer(
+            "position_encoding", _sinusoidal_positions(config.block_size, config.n_embd)
+        )
+        self.blocks = nn.ModuleList(
+            TransformerBlock(config, max_code=max_code) for _ in range(config.n_layer)
+        )
+        self.final_norm = nn.RMSNorm(config.n_embd)
+        self.lm_head = _linear(config, config.n_embd, config.vocab_size, max_code)
+
+    def forward(self, tokens: Tensor, targets: Tensor | None = None
+                ) -> tuple[Tensor, Tensor | None]:
+        if tokens.ndim != 2:
+            raise ValueError("tokens must have shape (batch, sequence)")
+        sequence_length = tokens.shape[1]
+        if sequence_length > self.config.block_size:
+            raise ValueError("token sequence exceeds configured block_size")
+        hidden = self.token_embedding(tokens) + self.position_encoding[:sequence_length]
+        for block in self.blocks:
+            if self.config.gradient_checkpointing and self.training:
+                import torch.utils.checkpoint
+
+                hidden = torch.utils.checkpoint.checkpoint(block, hidden, use_reentrant=False)
+            else:
+                hidden = block(hidden)
+        logits = self.lm_head(self.final_norm(hidden))
+        loss = None
+        if targets is not None:
+            if targets.shape != tokens.shape:
+                raise ValueError("targets must have the same shape as tokens")
+            loss = F.cross_entropy(logits.flatten(0, 1), targets.flatten())
+        return logits, loss
+
+    def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
+        updates = [m.ratchet_update(validate=validate) for m in self.modules()
+                   if isinstance(m, DiscreteRatchetLinear)]
+        aggregated = RatchetUpdateStats(
+            total_weights=sum(u.total_weights for u in updates),
+            positive_moves=sum(u.positive_moves for u in updates),
+            negative_moves=sum(u.negative_moves for u in updates),
+            blocked_positive_moves=sum(u.blocked_positive_moves for u in updates),
+            blocked_negative_moves=sum(u.blocked_negative_moves for u in updates),
+            gradient_rms_mean=(sum(u.gradient_rms_mean for u in updates) / len(updates)
+                               if updates else 0.0),
+        )
+        return aggregated.materialize() if validate else aggregated
+
+    def discard_pending_gradients(self) -> None:
+        for module in self.modules():
+            if isinstance(module, DiscreteRatchetLinear):
+                module.discard_pending_gradient()
+
+
+def build_seeded_model(config: ModelConfig, *, max_code: int | None, seed: int) -> RatchetGPT:
+    """Build matched arms without changing the caller's global CPU RNG state."""
+    with torch.random.fork_rng(devices=[]):
+        torch.manual_seed(seed)
+        return RatchetGPT(config, max_code=max_code)

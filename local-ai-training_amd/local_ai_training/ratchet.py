@@ -1,0 +1,738 @@
+"""Master-weight-free discrete linear layers on MI355X (drop-in for ``ratchet.py``).
+
+Public surface kept from the reference (``ratchet.py:18-831``): ``DiscreteRatchetLinear``
+(same constructor arguments, buffers ``packed`` uint8 + ``_scale`` fp32 or parameter
+``log_scale``, ``code`` / ``pressure`` / ``scale`` properties, ``forward(x, *, inputs_int8,
+inputs_scale)``, ``apply_weight_gradient``, ``apply_normalized_gradient``,
+``ratchet_update``, ``discard_pending_gradient``), ``RatchetEmbedding``,
+``RatchetUpdateStats``, ``pack_code_pressure`` / ``unpack_code_pressure``,
+``bucket_pressure``, ``audit_no_master_weights`` and ``compare_persistent_footprint``.
+
+What changed underneath (behaviour is identical unless noted):
+
+* The int8 forward reads the packed state directly (nibble decode in the GEMM's tile
+  staging); no unpacked or transposed code copy is made (``ratchet.py:52``).
+* The int8 backward runs SR quantization, the int8 grad_input GEMM, the BF16
+  grad_weight GEMM and ONE fused normalize+update launch over all output rows. The
+  reference loops over 256-row tiles (``ratchet.py:150-169``); rows are independent,
+  so ``tile_size`` no longer changes any result.
+* Non-finite weight gradients in the fused path are detected on the device: the rows
+  holding them are left unchanged (which is what the reference's arithmetic does to
+  them too) and FloatingPointError is raised by the next validating
+  ``ratchet_update()`` instead of by a per-tile host sync (``ratchet.py:501``).
+* Every tensor computation of the ratchet path runs in libratchet_hip.so; CPU tensors
+  raise RuntimeError for the update and int8 paths.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+
+from . import _native as nat
+from .int8_matmul import (
+    _sr_seed,
+    dequant_bf16,
+    effective_bf16,
+    int8_mm_nt,
+    packed_int8_mm,
+    quantize_rows_into,
+    unpack_transpose,
+)
+
+
+# ---------------------------------------------------------------------------
+# Packed state helpers
+# ---------------------------------------------------------------------------
+def pack_code_pressure(code: Tensor, pressure: Tensor, max_code: int) -> Tensor:
+    """Pack signed code (low nibble) and pressure (high nibble) into one uint8.
+
+    Lossless for code in [-max_code, max_code] and pressure in [-7, 7]
+    (``ratchet.py:185-192``). Used at construction and by tests; the training path
+    writes the bytes inside the update kernel.
+    """
+    low = (code.to(torch.int16) + max_code) & 0x0F
+    high = (pressure.to(torch.int16) + 7) & 0x0F
+    return (low | (high << 4)).to(torch.uint8)
+
+
+def unpack_code_pressure(packed: Tensor, max_code: int) -> tuple[Tensor, Tensor]:
+    """(code, pressure) int8 tensors from the packed bytes (``ratchet.py:195-199``)."""
+    if packed.is_cuda:
+        flat = packed.contiguous()
+        code = torch.empty(flat.shape, dtype=torch.int8, device=flat.device)
+        pressure = torch.empty_like(code)
+        nat.call("rk_unpack", flat.data_ptr(), flat.numel(), max_code, code.data_ptr(),
+                 pressure.data_ptr(), nat.stream_handle(flat.device))
+        return code, pressure
+    value = packed.to(torch.int16)
+    return ((value & 0x0F) - max_code).to(torch.int8), ((value >> 4) - 7).to(torch.int8)
+
+
+def bucket_pressure(z: Tensor, *, low: float = 0.5, high: float = 1.5) -> Tensor:
+    """Normalized gradient -> integer pressure increment in the descent direction.
+
+    Semantics of ``ratchet.py:248-262``; the training path computes this inside the
+    update kernel, this function serves inspection and tests.
+    """
+    if not 0 <= low < high:
+        raise ValueError("pressure bucket thresholds must satisfy 0 <= low < high")
+    magnitude = z.abs()
+    bucket = (magnitude >= high).to(torch.int16) + (magnitude >= low).to(torch.int16)
+    return -torch.sign(z).nan_to_num(0.0).to(torch.int16) * bucket
+
+
+@dataclass(frozen=True)
+class RatchetUpdateStats:
+    total_weights: int
+    positive_moves: int
+    negative_moves: int
+    blocked_positive_moves: int
+    blocked_negative_moves: int
+    gradient_rms_mean: float
+
+    @property
+    def code_moves(self) -> int:
+        return self.positive_moves + self.negative_moves
+
+    @property
+    def blocked_moves(self) -> int:
+        return self.blocked_positive_moves + self.blocked_negative_moves
+
+    def materialize(self) -> RatchetUpdateStats:
+        """Copy with every field as a Python scalar (the one host sync of the stats)."""
+        values = [self.total_weights, self.positive_moves, self.negative_moves,
+                  self.blocked_positive_moves, self.blocked_negative_moves,
+                  self.gradient_rms_mean]
+        tensors = [v for v in values if isinstance(v, Tensor)]
+        if tensors:
+            host = torch.stack([t.detach().double().reshape(()) for t in tensors]).cpu().tolist()
+            it = iter(host)
+            values = [next(it) if isinstance(v, Tensor) else v for v in values]
+        return RatchetUpdateStats(
+            total_weights=int(values[0]),
+            positive_moves=int(values[1]),
+            negative_moves=int(values[2]),
+            blocked_positive_moves=int(values[3]),
+            blocked_negative_moves=int(values[4]),
+            gradient_rms_mean=float(values[5]),
+        )
+
+
+@dataclass(frozen=True)
+class RatchetAuditReport:
+    ratchet_layers: int
+    ratchet_weights: int
+    ratchet_state_bytes: int
+    support_parameter_bytes: int
+    violations: tuple[str, ...]
+
+
+# ---------------------------------------------------------------------------
+# Autograd function
+# ---------------------------------------------------------------------------
+class _RatchetMatmul(torch.autograd.Function):
+    """Ratchet matmul whose backward feeds the effective-weight gradient to the update.
+
+    Inputs: (inputs, inputs_int8, inputs_scale, packed, scale, layer). The packed state
+    is read in place (never unpacked); ``layer`` carries the mode switches and owns the
+    update (``ratchet.py:18-182``).
+    """
+
+    @staticmethod
+    def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer):
+        input_shape = inputs.shape
+        flat_inputs = inputs.flatten(0, -2)
+        mode = layer.matmul_mode
+        ctx.layer = layer
+        ctx.input_shape = input_shape
+        ctx.input_dtype = inputs.dtype
+        ctx.generation = layer._generation
+        out_features = packed.shape[0]
+        out_dtype = inputs.dtype if inputs.dtype in (torch.float32, torch.bfloat16) else None
+
+        if mode == "int8" and inputs_int8 is not None and inputs_scale is not None:
+            nat.require_rocm(inputs_int8, packed, what="int8 ratchet matmul")
+            q = inputs_int8.flatten(0, -2)
+            s = inputs_scale.flatten(0, -1).float()
+            if q.stride(-1) != 1:
+                q = q.contiguous()
+            ctx.save_for_backward(q, s, scale)
+            ctx.used_fused_int8 = True
+            output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
+                                    out_dtype or torch.bfloat16)
+        else:
+            ctx.save_for_backward(flat_inputs, scale)
+            ctx.used_fused_int8 = False
+            if mode == "fp32":
+                effective = layer._effective_weight_f32(scale)
+                output = flat_inputs.to(torch.float32) @ effective.t()
+            elif mode == "bf16":
+                effective = effective_bf16(packed, layer.max_code, scale.detach())
+                output = flat_inputs.to(torch.bfloat16) @ effective.t().contiguous()
+            else:
+                nat.require_rocm(flat_inputs, packed, what="int8 ratchet matmul")
+                m, k = flat_inputs.shape
+                q = torch.empty((m, k), device=flat_inputs.device, dtype=torch.int8)
+                s = torch.empty((m,), device=flat_inputs.device, dtype=torch.float32)
+                x = flat_inputs
+                if x.dtype not in (torch.float32, torch.bfloat16):
+                    x = x.float()
+                quantize_rows_into(x, q, s)
+                output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
+                                        out_dtype or torch.bfloat16)
+        output = output.reshape(*input_shape[:-1], out_features)
+        return output if output.dtype == inputs.dtype else output.to(inputs.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        layer = ctx.layer
+        if layer._generation != ctx.generation:
+            raise RuntimeError(
+                "ratchet state changed between this layer's forward and backward "
+                "(the layer was applied twice before backward; weight sharing is unsupported "
+                "with the fused update)"
+            )
+        packed = layer.packed
+        mode = layer.matmul_mode
+        if ctx.used_fused_int8:
+            q, s, scale = ctx.saved_tensors
+            inputs_bf16 = dequant_bf16(q, s)
+            inputs_fp32 = None
+        else:
+            flat_inputs, scale = ctx.saved_tensors
+            inputs_bf16 = flat_inputs.to(torch.bfloat16) if mode != "fp32" else None
+            inputs_fp32 = flat_inputs.to(torch.float32) if mode == "fp32" else None
+        flat_gradient = grad_output.flatten(0, -2)
+        scale_d = scale.detach()
+        needs_scale = ctx.needs_input_grad[4]
+
+        if not layer.fuse_backward_update:
+            if mode == "fp32":
+                gradient_fp32 = flat_gradient.to(torch.float32)
+                effective = layer._effective_weight_f32(scale_d)
+                grad_input = gradient_fp32 @ effective
+                grad_weight_fp32 = gradient_fp32.t() @ inputs_fp32
+            else:
+                gradient_bf16 = flat_gradient.to(torch.bfloat16)
+                effective = effective_bf16(packed, layer.max_code, scale_d)
+                grad_input = gradient_bf16 @ effective
+                grad_weight_fp32 = (gradient_bf16.t() @ inputs_bf16).float()
+            layer._capture_weight_gradient(grad_weight_fp32)
+            grad_scale = None
+            if needs_scale:
+                grad_scale = (grad_weight_fp32 * layer.code.float()).sum(dim=1)
+            return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
+                grad_scale, None
+
+        m, n = flat_gradient.shape
+        gradient_bf16 = None
+        if mode == "fp32":
+            gradient_fp32 = flat_gradient.to(torch.float32)
+            grad_input = gradient_fp32 @ layer._effective_weight_f32(scale_d)
+        elif layer.int8_backward and ctx.used_fused_int8:
+            # int8 grad_input: fold the per-row weight scale into the gradient, SR-quantize
+            # (Philox bits), GEMM against the pre-update codes (ratchet.py:125-134). The
+            # same pass writes the bf16 gradient the grad_weight GEMM consumes.
+            g = flat_gradient
+            if g.dtype not in (torch.float32, torch.bfloat16):
+                g = g.float()
+            grad_q = torch.empty((m, n), device=g.device, dtype=torch.int8)
+            grad_s = torch.empty((m,), device=g.device, dtype=torch.float32)
+            if g.dtype == torch.bfloat16:
+                gradient_bf16, side = g, None  # already the grad_weight operand
+            else:
+                gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
+                side = gradient_bf16
+            quantize_rows_into(g, grad_q, grad_s, col_scale=scale_d.float().contiguous(),
+                               stochastic=True, seed=_sr_seed(), bf16_out=side)
+            code_t = unpack_transpose(packed, layer.max_code)
+            out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
+                else torch.bfloat16
+            grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
+        else:
+            gradient_bf16 = flat_gradient.to(torch.bfloat16)
+            grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)
+
+        if mode == "fp32":
+            grad_weight = gradient_fp32.t() @ inputs_fp32
+        else:
+            if gradient_bf16 is None:
+                gradient_bf16 = flat_gradient.to(torch.bfloat16)
+            grad_weight = gradient_bf16.t() @ inputs_bf16
+        grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
+        return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
+            grad_scale, None
+
+
+# ---------------------------------------------------------------------------
+# Layer
+# ---------------------------------------------------------------------------
+class DiscreteRatchetLinear(nn.Module):
+    """Linear layer with integer codes and pressure, but no master weight parameter."""
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        *,
+        max_code: int,
+        pressure_threshold: int = 8,
+        bucket_low: float = 0.5,
+        bucket_high: float = 1.5,
+        eps: float = 1e-8,
+        rms_ema_beta: float = 0.0,
+        pressure_leak_period: int = 0,
+        trainable_scale: bool = False,
+        compile_update: bool = False,
+        matmul_mode: str = "fp32",
+        initial_weight: Tensor | None = None,
+        fuse_backward_update: bool = False,
+        int8_backward: bool = False,
+        tile_size: int = 256,
+    ) -> None:
+        super().__init__()
+        if in_features <= 0 or out_features <= 0:
+            raise ValueError("in_features and out_features must be positive")
+        if max_code not in (1, 2, 3, 4, 5, 6, 7):
+            raise ValueError(
+                "max_code must be in 1..7 (3..15 states); 7 is the 4-bit packing cap"
+            )
+        if pressure_threshold <= 0 or pressure_threshold > 127:
+            raise ValueError("pressure_threshold must be in [1, 127]")
+        if not 0 <= bucket_low < bucket_high:
+            raise ValueError("bucket thresholds must satisfy 0 <= low < high")
+        if eps <= 0:
+            raise ValueError("eps must be positive")
+        if not 0.0 <= rms_ema_beta < 1.0:
+            raise ValueError("rms_ema_beta must be in [0, 1)")
+        if pressure_leak_period < 0:
+            raise ValueError("pressure_leak_period must be a non-negative integer")
+        if matmul_mode not in ("fp32", "bf16", "int8"):
+            raise ValueError("matmul_mode must be fp32, bf16, or int8")
+
+        self.in_features = in_features
+        self.out_features = out_features
+        self.max_code = max_code
+        self.pressure_threshold = pressure_threshold
+        self.bucket_low = bucket_low
+        self.bucket_high = bucket_high
+        self.eps = eps
+        self.rms_ema_beta = rms_ema_beta
+        self.pressure_leak_period = pressure_leak_period
+        # The fused HIP update replaces both the eager and the torch.compile'd update
+        # (ratchet.py:328-330); the flag is kept for configuration compatibility.
+        self.compile_update = compile_update
+        self._update_count = 0
+        if rms_ema_beta > 0.0:
+            self.register_buffer("rms_ema", torch.zeros(out_features))
+        self.trainable_scale = trainable_scale
+        self.matmul_mode = matmul_mode
+        self.fuse_backward_update = fuse_backward_update
+        self.int8_backward = int8_backward
+        self.tile_size = tile_size
+
+        if initial_weight is None:
+            reference = torch.empty(out_features, in_features, dtype=torch.float32)
+            nn.init.kaiming_uniform_(reference, a=5**0.5)
+        else:
+            if initial_weight.shape != (out_features, in_features):
+                raise ValueError(
+                    f"initial_weight must have shape {(out_features, in_features)}, "
+                    f"got {tuple(initial_weight.shape)}"
+                )
+            reference = initial_weight.detach().to(dtype=torch.float32)
+        # Codes from a float matrix: per-row absmax scale, round, clamp
+        # (ratchet.py:380-386).
+        row_max = reference.abs().amax(dim=1)
+        scale = (row_max / max_code).clamp_min(torch.finfo(torch.float32).eps)
+        code = torch.round(reference / scale[:, None]).clamp(-max_code, max_code)
+        zero_pressure = torch.zeros_like(code, dtype=torch.int8)
+        self.register_buffer(
+            "packed", pack_code_pressure(code.to(torch.int8), zero_pressure, max_code)
+        )
+        if trainable_scale:
+            self.log_scale = nn.Parameter(scale.log())
+        else:
+            self.register_buffer("_scale", scale)
+
+        self._effective_weight: Tensor | None = None
+        self._pending_weight_gradient: Tensor | None = None
+        self._generation = 0
+        self._reset_pending_stats()
+
+    # -- state ----------------------------------------------------------------
+    def _reset_pending_stats(self) -> None:
+        self._pending_stats_total_weights = 0
+        self._pending_counts: Tensor | None = None
+        self._pending_stats_rms_sum: Tensor | float = 0.0
+        self._nonfinite: Tensor | None = None
+
+    @classmethod
+    def from_reference(cls, reference: Tensor, *, max_code: int, pressure_threshold: int = 8,
+                       bucket_low: float = 0.5, bucket_high: float = 1.5,
+                       eps: float = 1e-8) -> DiscreteRatchetLinear:
+        if reference.ndim != 2:
+            raise ValueError("reference weight must be a matrix")
+        return cls(reference.shape[1], reference.shape[0], max_code=max_code,
+                   pressure_threshold=pressure_threshold, bucket_low=bucket_low,
+                   bucket_high=bucket_high, eps=eps, initial_weight=reference)
+
+    @property
+    def has_pending_gradient(self) -> bool:
+        eager_pending = (
+            self._effective_weight is not None and self._effective_weight.grad is not None
+        )
+        return eager_pending or self._pending_weight_gradient is not None
+
+    @property
+    def persistent_state_bytes(self) -> int:
+        return (self.packed.numel() * self.packed.element_size()
+                + self.scale.numel() * self.scale.element_size())
+
+    @property
+    def code(self) -> Tensor:
+        return unpack_code_pressure(self.packed, self.max_code)[0]
+
+    @property
+    def pressure(self) -> Tensor:
+        return unpack_code_pressure(self.packed, self.max_code)[1]
+
+    @property
+    def scale(self) -> Tensor:
+        return self.log_scale.exp() if self.trainable_scale else self._scale
+
+    def effective_weight(self) -> Tensor:
+        return self.code.to(dtype=self.scale.dtype) * self.scale[:, None]
+
+    def _effective_weight_f32(self, scale: Tensor) -> Tensor:
+        return self.code.to(torch.float32) * scale.to(torch.float32)[:, None]
+
+    def _counts(self) -> Tensor:
+        if self._pending_counts is None:
+            self._pending_counts = torch.zeros(4, dtype=torch.int64, device=self.packed.device)
+        return self._pending_counts
+
+    def _nonfinite_flag(self) -> Tensor:
+        if self._nonfinite is None:
+            self._nonfinite = torch.zeros(1, dtype=torch.int32, device=self.packed.device)
+        return self._nonfinite
+
+    # -- forward --------------------------------------------------------------
+    def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
+                inputs_scale: Tensor | None = None) -> Tensor:
+        if self.matmul_mode != "fp32" or self.fuse_backward_update:
+            return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
+                                        self.scale, self)
+        effective = self.effective_weight().to(dtype=inputs.dtype)
+        if self.training and torch.is_grad_enabled():
+            if self.trainable_scale:
+                effective.retain_grad()
+            else:
+                effective = effective.detach().requires_grad_(True)
+            self._effective_weight = effective
+        return F.linear(inputs, effective)
+
+    # -- gradient capture and the fused update --------------------------------
+    def _capture_weight_gradient(self, gradient: Tensor) -> None:
+        """Non-fused modes: hold the effective-weight gradient until ratchet_update()."""
+        if self._pending_weight_gradient is not None:
+            raise RuntimeError(
+                "ratchet layer has multiple pending effective-weight gradients "
+                "(missing ratchet_update or unsupported weight sharing)"
+            )
+        self._pending_weight_gradient = gradient
+
+    def _launch_update(self, gradient: Tensor, counts: Tensor, row_rms: Tensor | None,
+                       grad_scale: Tensor | None, nonfinite: Tensor | None) -> None:
+        nat.require_rocm(gradient, self.packed, what="the ratchet update")
+        if gradient.dtype not in (torch.float32, torch.bfloat16):
+            gradient = gradient.float()
+        if gradient.stride(-1) != 1:
+            gradient = gradient.contiguous()
+        rows, k = gradient.shape
+        ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
+        beta = self.rms_ema_beta
+        nat.call(
+            "rk_ratchet_update_grad", self.packed.data_ptr(), self.packed.stride(0),
+            gradient.data_ptr(), nat.dtype_code(gradient.dtype),
+            gradient.stride(0) if rows > 1 else k, rows, k, self.max_code,
+            self.pressure_threshold, self.bucket_low, self.bucket_high, self.eps,
+            nat.ptr(ema), beta, 1.0 - beta, counts.data_ptr(), nat.ptr(row_rms),
+            nat.ptr(grad_scale), nat.ptr(nonfinite), nat.stream_handle(self.packed.device),
+        )
+        self._generation += 1
+
+    def _fused_update(self, grad_weight: Tensor, *, want_grad_scale: bool) -> Tensor | None:
+        """Normalize + update every output row in one launch (fused backward path)."""
+        if grad_weight.shape != (self.out_features, self.in_features):
+            raise ValueError("fused gradient shape mismatch")
+        row_rms = torch.empty(self.out_features, device=grad_weight.device, dtype=torch.float32)
+        grad_scale = (torch.empty(self.out_features, device=grad_weight.device,
+                                  dtype=torch.float32) if want_grad_scale else None)
+        self._launch_update(grad_weight, self._counts(), row_rms, grad_scale,
+                            self._nonfinite_flag())
+        self._pending_stats_total_weights += self.out_features * self.in_features
+        self._pending_stats_rms_sum = self._pending_stats_rms_sum + row_rms.sum()
+        return grad_scale
+
+    @torch.no_grad()
+    def _normalize(self, gradient: Tensor, row_start: int, row_end: int) -> Tensor:
+        """z = g / (row rms + eps) (or the per-row EMA rms), ``ratchet.py:539-556``."""
+        nat.require_rocm(gradient, what="ratchet normalization")
+        g = gradient if gradient.dtype in (torch.float32, torch.bfloat16) else gradient.float()
+        g = g.contiguous()
+        rows, k = g.shape
+        z = torch.empty((rows, k), device=g.device, dtype=torch.float32)
+        ema = None
+        if self.rms_ema_beta > 0.0:
+            ema = self.rms_ema[row_start:row_end]
+        nat.call("rk_normalize_rows", g.data_ptr(), nat.dtype_code(g.dtype), k, rows, k,
+                 self.eps, nat.ptr(ema), self.rms_ema_beta, 1.0 - self.rms_ema_beta,
+                 z.data_ptr(), k, None, nat.stream_handle(g.device))
+        return z
+
+    @torch.no_grad()
+    def apply_weight_gradient(self, gradient: Tensor, *,
+                              validate: bool = True) -> RatchetUpdateStats:
+        if gradient.shape != (self.out_features, self.in_features):
+            raise ValueError(
+                f"gradient must have shape {(self.out_features, self.in_features)}, "
+                f"got {tuple(gradient.shape)}"
+            )
+        if validate and not torch.isfinite(gradient).all():
+            raise FloatingPointError("ratchet gradient contains NaN or Inf")
+        counts = torch.zeros(4, dtype=torch.int64, device=self.packed.device)
+        row_rms = torch.empty(self.out_features, device=self.packed.device, dtype=torch.float32)
+        self._launch_update(gradient.to(self.packed.device), counts, row_rms, None, None)
+        if validate:
+            self._validate_state()
+        return RatchetUpdateStats(
+            total_weights=self.packed.numel(),
+            positive_moves=counts[0],
+            negative_moves=counts[1],
+            blocked_positive_moves=counts[2],
+            blocked_negative_moves=counts[3],
+            gradient_rms_mean=row_rms.mean(),
+        )
+
+    @torch.no_grad()
+    def apply_normalized_gradient(self, normalized: Tensor, *,
+                                  validate: bool = True) -> RatchetUpdateStats:
+        if normalized.shape != (self.out_features, self.in_features):
+            raise ValueError(
+                f"normalized gradient must have shape {(self.out_features, self.in_features)}, "
+                f"got {tuple(normalized.shape)}"
+            )
+        z = normalized.to(device=self.packed.device, dtype=torch.float32).contiguous()
+        nat.require_rocm(z, self.packed, what="the ratchet update")
+        counts = torch.zeros(4, dtype=torch.int64, device=self.packed.device)
+        rows, k = z.shape
+        nat.call("rk_ratchet_update", self.packed.data_ptr(), self.packed.stride(0),
+                 z.data_ptr(), k, rows, k, self.max_code, self.pressure_threshold,
+                 self.bucket_low, self.bucket_high, counts.data_ptr(),
+                 nat.stream_handle(z.device))
+        self._generation += 1
+        if validate:
+            self._validate_state()
+        return RatchetUpdateStats(
+            total_weights=self.packed.numel(),
+            positive_moves=counts[0],
+            negative_moves=counts[1],
+            blocked_positive_moves=counts[2],
+            blocked_negative_moves=counts[3],
+            gradient_rms_mean=0.0,
+        )
+
+    @torch.no_grad()
+    def _maybe_leak_pressure(self) -> None:
+        if self.pressure_leak_period <= 0:
+            return
+        self._update_count += 1
+        if self._update_count % self.pressure_leak_period != 0:
+            return
+        nat.require_rocm(self.packed, what="the pressure leak")
+        nat.call("rk_pressure_leak", self.packed.data_ptr(), self.packed.numel(), self.max_code,
+                 nat.stream_handle(self.packed.device))
+
+    def check_finite_gradients(self) -> None:
+        """Raise FloatingPointError if a fused update saw a NaN/Inf gradient (host sync)."""
+        if self._nonfinite is not None and int(self._nonfinite.item()):
+            self._nonfinite.zero_()
+            raise FloatingPointError("ratchet gradient contains NaN or Inf")
+
+    def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
+        if self.fuse_backward_update:
+            if validate:
+                self.check_finite_gradients()
+                self._validate_state()
+            counts = self._pending_counts
+            if counts is None:
+                pos = neg = bpos = bneg = 0
+            else:
+                pos, neg, bpos, bneg = counts[0], counts[1], counts[2], counts[3]
+            stats = RatchetUpdateStats(
+                total_weights=self._pending_stats_total_weights,
+                positive_moves=pos,
+                negative_moves=neg,
+                blocked_positive_moves=bpos,
+                blocked_negative_moves=bneg,
+                gradient_rms_mean=self._pending_stats_rms_sum / max(1, self.out_features),
+            )
+            nonfinite = self._nonfinite
+            self._reset_pending_stats()
+            self._nonfinite = nonfinite
+        elif self.matmul_mode != "fp32":
+            if self._pending_weight_gradient is None:
+                raise RuntimeError("ratchet layer has no pending effective-weight gradient")
+            try:
+                stats = self.apply_weight_gradient(self._pending_weight_gradient,
+                                                   validate=validate)
+            finally:
+                self._pending_weight_gradient = None
+        else:
+            if self._effective_weight is None or self._effective_weight.grad is None:
+                raise RuntimeError("ratchet layer has no pending effective-weight gradient")
+            try:
+                stats = self.apply_weight_gradient(self._effective_weight.grad,
+                                                   validate=validate)
+            finally:
+                self._effective_weight = None
+        self._maybe_leak_pressure()
+        return stats.materialize() if validate else stats
+
+    def discard_pending_gradient(self) -> None:
+        self._pending_weight_gradient = None
+        self._effective_weight = None
+
+    def _validate_state(self) -> None:
+        nat.require_rocm(self.packed, what="ratchet state validation")
+        flags = torch.zeros(3, dtype=torch.int32, device=self.packed.device)
+        scale = self.scale.detach().float().contiguous()
+        nat.call("rk_validate_state", self.packed.data_ptr(), self.packed.numel(),
+                 self.max_code, scale.data_ptr(), scale.numel(), flags.data_ptr(),
+                 nat.stream_handle(self.packed.device))
+        bad_code, bad_pressure, bad_scale = flags.tolist()
+        if bad_code:
+            raise RuntimeError("ratchet code escaped its allowed range")
+        if bad_pressure:
+            raise RuntimeError("ratchet pressure escaped the packed nibble range")
+        if bad_scale:
+            raise RuntimeError("ratchet row scales must remain positive and finite")
+
+    def extra_repr(self) -> str:
+        return (
+            f"in_features={self.in_features}, out_features={self.out_features}, "
+            f"states={2 * self.max_code + 1}, threshold={self.pressure_threshold}, bias=False"
+        )
+
+
+class RatchetEmbedding(DiscreteRatchetLinear):
+    """Master-weight-free token embedding (``ratchet.py:688-749``): a ratchet layer whose
+    forward is an embedding lookup; it joins every update/audit sweep."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, *, max_code: int,
+                 pressure_threshold: int = 8, bucket_low: float = 0.5,
+                 bucket_high: float = 1.5, eps: float = 1e-8, rms_ema_beta: float = 0.0,
+                 pressure_leak_period: int = 0, trainable_scale: bool = False,
+                 compile_update: bool = False, initial_weight: Tensor | None = None) -> None:
+        if initial_weight is None:
+            initial_weight = torch.randn(num_embeddings, embedding_dim)
+        super().__init__(
+            embedding_dim, num_embeddings, max_code=max_code,
+            pressure_threshold=pressure_threshold, bucket_low=bucket_low,
+            bucket_high=bucket_high, eps=eps, rms_ema_beta=rms_ema_beta,
+            pressure_leak_period=pressure_leak_period, trainable_scale=trainable_scale,
+            compile_update=compile_update, matmul_mode="fp32", initial_weight=initial_weight,
+        )
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+
+    def forward(self, token_ids: Tensor) -> Tensor:  # type: ignore[override]
+        effective = self.effective_weight()
+        if self.training and torch.is_grad_enabled():
+            effective = effective.detach().requires_grad_(True)
+            self._effective_weight = effective
+        return F.embedding(token_ids, effective)
+
+    def extra_repr(self) -> str:
+        return (
+            f"num_embeddings={self.num_embeddings}, embedding_dim={self.embedding_dim}, "
+            f"states={2 * self.max_code + 1}, threshold={self.pressure_threshold}"
+        )
+
+
+@dataclass(frozen=True)
+class PersistentFootprint:
+    """Persistent bytes of the trainable matrices: ratchet vs FP32 + AdamW."""
+
+    ratchet_weights: int
+    ratchet_matrix_bytes: int
+    fp32_master_bytes: int
+    fp32_optimizer_bytes: int
+
+    @property
+    def fp32_matrix_bytes(self) -> int:
+        return self.fp32_master_bytes + self.fp32_optimizer_bytes
+
+    @property
+    def reduction_ratio(self) -> float:
+        return self.fp32_matrix_bytes / max(self.ratchet_matrix_bytes, 1)
+
+
+def compare_persistent_footprint(model: nn.Module) -> PersistentFootprint:
+    weights = 0
+    ratchet_bytes = 0
+    for module in model.modules():
+        if isinstance(module, DiscreteRatchetLinear):
+            weights += module.packed.numel()
+            ratchet_bytes += module.persistent_state_bytes
+    return PersistentFootprint(ratchet_weights=weights, ratchet_matrix_bytes=ratchet_bytes,
+                               fp32_master_bytes=weights * 4, fp32_optimizer_bytes=weights * 8)
+
+
+def audit_no_master_weights(model: nn.Module, *,
+                            raise_on_violation: bool = False) -> RatchetAuditReport:
+    violations: list[str] = []
+    layers = weights = state_bytes = 0
+    for module_name, module in model.named_modules():
+        if not isinstance(module, DiscreteRatchetLinear):
+            continue
+        layers += 1
+        weights += module.packed.numel()
+        state_bytes += module.persistent_state_bytes
+        prefix = module_name or "<root>"
+        for parameter_name, parameter in module.named_parameters(recurse=False):
+            if parameter.is_floating_point() and parameter.ndim >= 2:
+                violations.append(f"{prefix}.{parameter_name}: floating matrix parameter")
+        if module.packed.dtype != torch.uint8:
+            violations.append(f"{prefix}.packed: expected uint8, got {module.packed.dtype}")
+        if module.scale.ndim != 1 or module.scale.shape[0] != module.out_features:
+            violations.append(f"{prefix}.scale: expected one scale per output row")
+    support_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    report = RatchetAuditReport(ratchet_layers=layers, ratchet_weights=weights,
+                                ratchet_state_bytes=state_bytes,
+                                support_parameter_bytes=support_bytes,
+                                violations=tuple(violations))
+    if raise_on_violation and violations:
+        raise RuntimeError("ratchet master-weight audit failed: " + "; ".join(violations))
+    return report
+
+
+def ratchet_layers(model: nn.Module) -> list[DiscreteRatchetLinear]:
+    return [m for m in model.modules() if isinstance(m, DiscreteRatchetLinear)]
+
+
+def persistent_bytes(model: nn.Module) -> int:
+    return sum(layer.persistent_state_bytes for layer in ratchet_layers(model))
+
+
+__all__ = [
+    "DiscreteRatchetLinear", "RatchetEmbedding", "RatchetUpdateStats", "RatchetAuditReport",
+    "PersistentFootprint", "pack_code_pressure", "unpack_code_pressure", "bucket_pressure",
+    "audit_no_master_weights", "compare_persistent_footprint", "ratchet_layers",
+    "persistent_bytes",
+]

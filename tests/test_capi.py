@@ -1,0 +1,67 @@
+"""The C-ABI library loads and exports every entry point include/ratchet_hip.h declares.
+
+No compute call is made here (no GPU on the CPU runner); argument validation paths
+that return before touching the device are exercised.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from local_ai_training import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "ratchet_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rk_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not nat.LIB_PATH.is_file():
+        pytest.fail(f"{nat.LIB_PATH} is not built; run `python local-ai-training_amd/build.py`")
+    return nat.load_library()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_symbols()
+    assert "rk_int8_gemm_packed" in names and "rk_ratchet_update_grad" in names
+    assert len(names) >= 15
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [name for name in declared_symbols() if not hasattr(lib, name)]
+    assert missing == []
+
+
+def test_python_binding_covers_every_declared_symbol():
+    assert sorted(nat.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_empty_error(lib):
+    assert lib.rk_version() == 100
+    assert lib.rk_last_error() == b""
+
+
+def test_argument_errors_return_status_without_device_work(lib):
+    # Shape/argument validation happens before any launch.
+    status = lib.rk_quantize_rows(None, 0, 4, 0, 1, 1, None, 0, 0, 0, None, 1, None, None, 0, None)
+    assert status == 1
+    assert b"invalid shape" in lib.rk_last_error()
+    status = lib.rk_ratchet_update(None, 4, None, 4, 0, 4, 9, 8, ctypes.c_float(0.5),
+                                   ctypes.c_float(1.5), None, None)
+    assert status == 1 and b"max_code" in lib.rk_last_error()
+    status = lib.rk_int8_gemm_packed(None, 8, None, 8, 2, None, None, None, 1, 8, 4, 4,
+                                     1 << 20, None)
+    assert status == 1 and b"K too large" in lib.rk_last_error()
+
+
+def test_zero_sized_calls_are_no_ops(lib):
+    assert lib.rk_int8_gemm_nt(None, 1, None, 1, None, None, None, 1, 1, 0, 5, 5, None) == 0
+    assert lib.rk_unpack(None, 0, 2, None, None, None) == 0
+    assert lib.rk_pressure_leak(None, 0, 2, None) == 0

@@ -1,0 +1,360 @@
+"""Kernel-level parity: every HIP entry point against the numpy oracle, bit for bit.
+
+Integer / byte / index outputs (int8 codes, int32 accumulators, packed bytes, move
+counts) and the IEEE-defined float outputs (quant scales, bf16 GEMM outputs, row rms,
+normalized gradients) must be identical. Inputs are seeded; shapes cover the reference
+tests' ragged cases, the BASELINE op shape (M=16384, K=512, N=2048) and 1B-class rows.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import synthetic_state
+from local_ai_training import _native as nat
+from local_ai_training.int8_matmul import (
+    dequant_bf16,
+    effective_bf16,
+    int8_mm_nt,
+    packed_int8_mm,
+    quantize_columns,
+    quantize_rows,
+    quantize_rows_colscaled,
+    quantize_rows_into,
+    scaled_int8_mm,
+    unpack_transpose,
+)
+from oracle import gemm as ogemm
+from oracle import quant as oquant
+from oracle import update as oupd
+from oracle.numerics import f32_to_bf16_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def f32bits(a) -> np.ndarray:
+    a = a.cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ---------------------------------------------------------------------------
+# Row quantization
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(67, 35), (128, 256), (1, 513), (255, 1), (300, 2048),
+                                   (7, 5632), (16384, 512)])
+def test_quantize_rows_bit_exact(cuda, shape, dtype):
+    values = (torch.randn(shape, generator=gen(7)) * 3.0).to(dtype)
+    q, s = quantize_rows(values.to(cuda))
+    q_ref, s_ref = oquant.quantize_rows(values.float().numpy())
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(f32bits(s), f32bits(s_ref))
+
+
+def test_quantize_rows_noncontiguous_and_zero_rows(cuda):
+    base = (torch.randn(70, 48, generator=gen(11)) * 2.0).to(torch.bfloat16)
+    view = base.to(cuda).t()
+    q, s = quantize_rows(view)
+    q_ref, s_ref = oquant.quantize_rows(base.t().float().numpy())
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(f32bits(s), f32bits(s_ref))
+    zq, zs = quantize_rows(torch.zeros(3, 5, device=cuda, dtype=torch.bfloat16))
+    assert int(torch.count_nonzero(zq)) == 0
+    assert torch.all(zs == torch.finfo(torch.float32).tiny)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(67, 35), (128, 256), (1, 255), (300, 1), (64, 2048)])
+def test_quantize_rows_colscaled_bit_exact(cuda, shape, dtype):
+    g = (torch.randn(shape, generator=gen(21)) * 3.0).to(dtype)
+    col = torch.rand(shape[1], generator=gen(22)) + 0.01
+    q, s = quantize_rows_colscaled(g.to(cuda), col.to(cuda))
+    q_ref, s_ref = oquant.quantize_rows(g.float().numpy(), col.numpy())
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(f32bits(s), f32bits(s_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(8, 64), (67, 35), (33, 2048), (3, 5632)])
+def test_stochastic_rounding_bit_exact_given_seed(cuda, shape, dtype):
+    g = (torch.randn(shape, generator=gen(31)) * 1e-2).to(dtype)
+    col = torch.rand(shape[1], generator=gen(32)) * 0.08 + 0.02
+    gd = g.to(cuda)
+    for seed in (0, 1, 123456789, 2**31 - 2):
+        q = torch.empty(shape, dtype=torch.int8, device=cuda)
+        s = torch.empty(shape[0], dtype=torch.float32, device=cuda)
+        quantize_rows_into(gd, q, s, col_scale=col.to(cuda), stochastic=True, seed=seed)
+        q_ref, s_ref = oquant.quantize_rows_sr(g.float().numpy(), col.numpy(), seed)
+        assert np.array_equal(q.cpu().numpy(), q_ref), f"seed {seed}"
+        assert np.array_equal(f32bits(s), f32bits(s_ref))
+
+
+def test_public_sr_draws_its_seed_from_the_cpu_generator(cuda):
+    # int8_matmul.py:200: one torch.randint draw per stochastic call.
+    g = torch.randn(16, 96, generator=gen(41))
+    col = torch.rand(96, generator=gen(42)) + 0.01
+    torch.manual_seed(5)
+    seed = int(torch.randint(0, 2**31 - 1, (1,)).item())
+    after_ref = torch.rand(3)
+    torch.manual_seed(5)
+    q, _ = quantize_rows_colscaled(g.to(cuda), col.to(cuda), stochastic=True)
+    assert torch.equal(torch.rand(3), after_ref)  # CPU RNG stream advanced identically
+    q_ref, _ = oquant.quantize_rows_sr(g.numpy(), col.numpy(), seed)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_sr_quant_full_op_shape_sampled_rows_and_bf16_side_output(cuda):
+    m, n = 16384, 2048
+    g = (torch.randn(m, n, generator=gen(51)) * 1e-2).to(torch.bfloat16)
+    col = torch.rand(n, generator=gen(52)) * 0.08 + 0.02
+    gd = g.to(cuda)
+    q = torch.empty(m, n, dtype=torch.int8, device=cuda)
+    s = torch.empty(m, dtype=torch.float32, device=cuda)
+    side = torch.empty(m, n, dtype=torch.bfloat16, device=cuda)
+    quantize_rows_into(gd, q, s, col_scale=col.to(cuda), stochastic=True, seed=987654,
+                       bf16_out=side)
+    assert torch.equal(side, gd)
+    qc, sc = q.cpu().numpy(), s.cpu().numpy()
+    rows = np.random.default_rng(0).choice(m, 256, replace=False)
+    for r0 in rows:
+        q_ref, s_ref = oquant.quantize_rows_sr(g[r0:r0 + 1].float().numpy(), col.numpy(),
+                                               987654, row_start=int(r0))
+        assert np.array_equal(qc[r0:r0 + 1], q_ref) and sc[r0] == s_ref[0]
+
+
+def test_f32_gradient_side_output_is_rne_bf16(cuda):
+    g = torch.randn(64, 512, generator=gen(53))
+    q = torch.empty(64, 512, dtype=torch.int8, device=cuda)
+    s = torch.empty(64, dtype=torch.float32, device=cuda)
+    side = torch.empty(64, 512, dtype=torch.bfloat16, device=cuda)
+    quantize_rows_into(g.to(cuda), q, s, stochastic=True, seed=3, bf16_out=side)
+    assert np.array_equal(bits16(side), f32_to_bf16_bits(g.numpy()))
+
+
+def test_quantize_columns_matches_transposed_rows(cuda):
+    x = torch.randn(384, 200, generator=gen(13)) * 2.0
+    q, s = quantize_columns(x.to(cuda))
+    q_ref, s_ref = oquant.quantize_columns(x.numpy())
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(f32bits(s), f32bits(s_ref))
+
+
+# ---------------------------------------------------------------------------
+# int8 GEMM
+# ---------------------------------------------------------------------------
+GEMM_SHAPES = [(67, 35, 53), (48, 40, 53), (1, 64, 1), (128, 128, 64), (130, 200, 129),
+               (256, 384, 512), (1000, 1536, 512)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_int8_gemm_nt_bit_exact(cuda, m, n, k):
+    g = gen(m * 7 + n)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    ls = torch.rand(m, generator=g) + 0.01
+    rs = torch.rand(n, generator=g) + 0.01
+    out = int8_mm_nt(a.to(cuda), b.to(cuda), ls.to(cuda), rs.to(cuda))
+    ref = ogemm.scaled_int8_mm(a.numpy(), b.numpy().T, ls.numpy(), rs.numpy())
+    assert np.array_equal(bits16(out), ref)
+    out1 = int8_mm_nt(a.to(cuda), b.to(cuda), ls.to(cuda), None, torch.float32)
+    ref1 = ogemm.scaled_int8_mm(a.numpy(), b.numpy().T, ls.numpy(), None)
+    assert np.array_equal(f32bits(out1), f32bits(np.float32(ref1.astype(np.uint32) << 16)))
+
+
+@pytest.mark.parametrize("max_code", [1, 2, 3, 7])
+@pytest.mark.parametrize("m,n,k", [(67, 53, 35), (512, 1536, 512), (257, 130, 192)])
+def test_packed_gemm_bit_exact(cuda, m, n, k, max_code):
+    packed, scale = synthetic_state(n, k, max_code, seed=m + n + k)
+    code, _ = oupd.unpack(packed, max_code)
+    q = torch.randint(-127, 128, (m, k), generator=gen(m), dtype=torch.int8)
+    ls = torch.rand(m, generator=gen(m + 1)) * 0.05 + 1e-3
+    out = packed_int8_mm(q.to(cuda), torch.from_numpy(packed).to(cuda), max_code,
+                         ls.to(cuda), torch.from_numpy(scale).to(cuda))
+    ref = ogemm.scaled_int8_mm(q.numpy(), code.T, ls.numpy(), scale)
+    assert np.array_equal(bits16(out), ref)
+
+
+def test_forward_gemm_full_op_shape_bit_exact(cuda):
+    # BASELINE op: M=16384 tokens, K=512, N=2048, quinary codes, scales U[0.02, 0.1].
+    m, n, k, mc = 16384, 2048, 512, 2
+    packed, scale = synthetic_state(n, k, mc, seed=2048, random_pressure=False)
+    x = torch.randn(m, k, generator=gen(1)).to(torch.bfloat16)
+    q, s = quantize_rows(x.to(cuda))
+    out = packed_int8_mm(q, torch.from_numpy(packed).to(cuda), mc, s,
+                         torch.from_numpy(scale).to(cuda))
+    code, _ = oupd.unpack(packed, mc)
+    ref = ogemm.scaled_int8_mm(q.cpu().numpy(), code.T, s.cpu().numpy(), scale)
+    assert np.array_equal(bits16(out), ref)
+
+
+def test_grad_input_gemm_full_op_shape_bit_exact(cuda):
+    # int8 grad_input: A = SR-quantized gradient [M, N_out], B = code^T [K_in, N_out].
+    m, n_out, k_in, mc = 16384, 2048, 512, 2
+    packed, _ = synthetic_state(n_out, k_in, mc, seed=77)
+    gq = torch.randint(-127, 128, (m, n_out), generator=gen(2), dtype=torch.int8)
+    gs = torch.rand(m, generator=gen(3)) * 1e-3 + 1e-5
+    code_t = unpack_transpose(torch.from_numpy(packed).to(cuda), mc)
+    code, _ = oupd.unpack(packed, mc)
+    assert np.array_equal(code_t.cpu().numpy(), code.T)
+    out = int8_mm_nt(gq.to(cuda), code_t, gs.to(cuda), None, torch.float32)
+    ref = ogemm.scaled_int8_mm(gq.numpy(), code, gs.numpy(), None)
+    assert np.array_equal(f32bits(out), f32bits(np.float32(ref.astype(np.uint32) << 16)))
+
+
+def test_scaled_int8_mm_public_api_strided_and_errors(cuda):
+    # tests/test_int8_matmul.py:172-207
+    g = gen(5)
+    lhs = torch.randint(-20, 21, (48, 40), generator=g, dtype=torch.int8).to(cuda)
+    weight = torch.randint(-8, 9, (53, 40), generator=g, dtype=torch.int8).to(cuda)
+    ls = (torch.rand(48, generator=g) + 0.01).to(cuda)
+    rs = (torch.rand(53, generator=g) + 0.01).to(cuda)
+    strided = scaled_int8_mm(lhs, weight.t(), ls, rs)
+    contiguous = scaled_int8_mm(lhs, weight.t().contiguous(), ls, rs)
+    assert strided.dtype == torch.bfloat16 and torch.equal(strided, contiguous)
+    expected = ((lhs.float() @ weight.t().float()) * ls[:, None] * rs[None, :]).to(torch.bfloat16)
+    assert torch.equal(strided, expected)
+    with pytest.raises(ValueError, match="finite and positive"):
+        scaled_int8_mm(lhs, weight.t(), -ls, rs)
+    with pytest.raises(TypeError):
+        scaled_int8_mm(lhs.float(), weight.t(), ls, rs)
+    with pytest.raises(ValueError, match="inner dimensions"):
+        scaled_int8_mm(lhs, weight, ls, rs)
+
+
+def test_effective_and_dequant_bf16_match_torch_formula(cuda):
+    packed, scale = synthetic_state(53, 35, 3, seed=9)
+    code, _ = oupd.unpack(packed, 3)
+    eff = effective_bf16(torch.from_numpy(packed).to(cuda), 3, torch.from_numpy(scale).to(cuda))
+    ref = torch.from_numpy(code).to(torch.bfloat16) * torch.from_numpy(scale).to(torch.bfloat16)[:, None]
+    assert torch.equal(eff.cpu(), ref)
+    q = torch.randint(-127, 128, (40, 32), generator=gen(8), dtype=torch.int8)
+    s = torch.rand(40, generator=gen(9)) * 0.1
+    xh = dequant_bf16(q.to(cuda), s.to(cuda))
+    assert torch.equal(xh.cpu(), q.to(torch.bfloat16) * s[:, None].to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# Ratchet update
+# ---------------------------------------------------------------------------
+def _update_z(packed: torch.Tensor, z: torch.Tensor, mc: int, T: int, low=0.5, high=1.5):
+    counts = torch.zeros(4, dtype=torch.int64, device=packed.device)
+    rows, k = z.shape
+    nat.call("rk_ratchet_update", packed.data_ptr(), packed.stride(0), z.data_ptr(), k, rows, k,
+             mc, T, low, high, counts.data_ptr(), nat.stream_handle(packed.device))
+    return counts
+
+
+@pytest.mark.parametrize("max_code,threshold", [(1, 1), (2, 2), (2, 8), (3, 4), (4, 8), (7, 3)])
+@pytest.mark.parametrize("rows,k", [(6, 8), (48, 32), (37, 1001), (2048, 512)])
+def test_update_from_normalized_gradient_bit_exact(cuda, rows, k, max_code, threshold):
+    packed, _ = synthetic_state(rows, k, max_code, seed=rows * k + max_code)
+    if threshold < 8:  # stored |pressure| < threshold for a reachable state
+        _, p = oupd.unpack(packed, max_code)
+        c, _ = oupd.unpack(packed, max_code)
+        packed = oupd.pack(c, np.clip(p, -(threshold - 1), threshold - 1), max_code)
+    z = torch.randn(rows, k, generator=gen(rows + k)) * 2.0
+    pd = torch.from_numpy(packed).to(cuda)
+    counts = _update_z(pd, z.to(cuda), max_code, threshold)
+    ref, ref_counts = oupd.update_core(packed, z.numpy(), max_code, threshold)
+    assert np.array_equal(pd.cpu().numpy(), ref)
+    assert counts.cpu().tolist() == ref_counts.tolist()
+
+
+def _update_grad(packed, g, mc, T, eps=1e-8, ema=None, beta=0.0, want_scale=True):
+    dev = packed.device
+    rows, k = g.shape
+    counts = torch.zeros(4, dtype=torch.int64, device=dev)
+    row_rms = torch.empty(rows, device=dev)
+    gscale = torch.empty(rows, device=dev) if want_scale else None
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    nat.call("rk_ratchet_update_grad", packed.data_ptr(), packed.stride(0), g.data_ptr(),
+             nat.dtype_code(g.dtype), g.stride(0), rows, k, mc, T, 0.5, 1.5, eps, nat.ptr(ema),
+             beta, 1.0 - beta, counts.data_ptr(), row_rms.data_ptr(), nat.ptr(gscale),
+             flag.data_ptr(), nat.stream_handle(dev))
+    return counts, row_rms, gscale, flag
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,k", [(6, 8), (37, 1001), (2048, 512), (512, 2048), (64, 5632),
+                                    (16, 12000)])
+def test_fused_normalize_update_bit_exact(cuda, rows, k, dtype):
+    mc, T = 2, 8
+    packed, _ = synthetic_state(rows, k, mc, seed=rows + 3 * k)
+    g = (torch.randn(rows, k, generator=gen(rows * 5 + k)) * 1e-3).to(dtype)
+    pd = torch.from_numpy(packed).to(cuda)
+    counts, row_rms, gscale, flag = _update_grad(pd, g.to(cuda), mc, T)
+    vec = oupd.vec_for_dtype("f32" if dtype == torch.float32 else "bf16")
+    ref = oupd.update_from_gradient(packed, g.float().numpy(), mc, T, 0.5, 1.5, 1e-8, vec)
+    assert np.array_equal(pd.cpu().numpy(), ref["packed"])
+    assert counts.cpu().tolist() == ref["counts"].tolist()
+    assert np.array_equal(f32bits(row_rms), f32bits(ref["row_rms"]))
+    assert np.array_equal(f32bits(gscale), f32bits(ref["grad_scale"]))
+    assert int(flag.item()) == 0
+
+
+def test_fused_update_rms_ema_bit_exact(cuda):
+    rows, k, mc, beta = 64, 512, 3, 0.9
+    packed, _ = synthetic_state(rows, k, mc, seed=5)
+    ema = np.zeros(rows, np.float32)
+    pd = torch.from_numpy(packed).to(cuda)
+    ema_d = torch.from_numpy(ema.copy()).to(cuda)
+    for step in range(3):
+        g = torch.randn(rows, k, generator=gen(step)) * (step + 1)
+        if step == 2:
+            g[5] = 0.0  # a row without gradient keeps its EMA
+        _update_grad(pd, g.to(cuda), mc, 8, ema=ema_d, beta=beta, want_scale=False)
+        ref = oupd.update_from_gradient(packed, g.numpy(), mc, 8, 0.5, 1.5, 1e-8, 4,
+                                        rms_ema=ema, beta=beta)
+        packed, ema = ref["packed"], ref["rms_ema"]
+        assert np.array_equal(pd.cpu().numpy(), packed)
+        assert np.array_equal(f32bits(ema_d), f32bits(ema))
+
+
+def test_fused_update_nonfinite_rows_unchanged_and_flagged(cuda):
+    rows, k, mc = 8, 256, 2
+    packed, _ = synthetic_state(rows, k, mc, seed=6)
+    g = torch.randn(rows, k, generator=gen(6))
+    g[2, 17] = float("nan")
+    g[5, 0] = float("inf")
+    pd = torch.from_numpy(packed).to(cuda)
+    counts, _, _, flag = _update_grad(pd, g.to(cuda), mc, 2)
+    ref = oupd.update_from_gradient(packed, g.numpy(), mc, 2, 0.5, 1.5, 1e-8, 4)
+    assert int(flag.item()) == 1 and ref["nonfinite"] == 1
+    assert np.array_equal(pd.cpu().numpy(), ref["packed"])
+    assert counts.cpu().tolist() == ref["counts"].tolist()
+
+
+def test_normalize_rows_matches_oracle(cuda):
+    g = torch.randn(100, 700, generator=gen(12)) * 3.0
+    z = torch.empty(100, 700, device=cuda)
+    gd = g.to(cuda)
+    nat.call("rk_normalize_rows", gd.data_ptr(), nat.RK_F32, 700, 100, 700, 1e-8, None, 0.0,
+             1.0, z.data_ptr(), 700, None, nat.stream_handle(gd.device))
+    ref, _, _ = oupd.normalize_rows(g.numpy(), 1e-8, 4)
+    assert np.array_equal(f32bits(z), f32bits(ref))
+
+
+def test_unpack_leak_and_validate(cuda):
+    packed, _ = synthetic_state(33, 65, 3, seed=4)
+    pd = torch.from_numpy(packed).to(cuda)
+    code = torch.empty(packed.shape, dtype=torch.int8, device=cuda)
+    pres = torch.empty_like(code)
+    nat.call("rk_unpack", pd.data_ptr(), pd.numel(), 3, code.data_ptr(), pres.data_ptr(),
+             nat.stream_handle(pd.device))
+    c_ref, p_ref = oupd.unpack(packed, 3)
+    assert np.array_equal(code.cpu().numpy(), c_ref) and np.array_equal(pres.cpu().numpy(), p_ref)
+    nat.call("rk_pressure_leak", pd.data_ptr(), pd.numel(), 3, nat.stream_handle(pd.device))
+    assert np.array_equal(pd.cpu().numpy(), oupd.pressure_leak(packed, 3))
+    flags = torch.zeros(3, dtype=torch.int32, device=cuda)
+    scale = torch.tensor([0.5, float("nan")], device=cuda)
+    bad = torch.tensor([0x0F, 0x00], dtype=torch.uint8, device=cuda)  # code 12 > 3; p = -7
+    nat.call("rk_validate_state", bad.data_ptr(), 2, 3, scale.data_ptr(), 2, flags.data_ptr(),
+             nat.stream_handle(bad.device))
+    assert flags.cpu().tolist() == [1, 0, 1]

@@ -1,0 +1,122 @@
+"""The ratchet GPT on the GPU: forward/backward/fused update in every matmul mode,
+and the fused int8 prologues against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from local_ai_training.int8_fused import (
+    fused_gelu_quantize,
+    fused_rmsnorm_quantize,
+    fused_transpose_quantize,
+)
+from local_ai_training.model import ModelConfig, build_seeded_model
+from local_ai_training.ratchet import DiscreteRatchetLinear
+from oracle import quant as oquant
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny_config(**kw) -> ModelConfig:
+    return ModelConfig(vocab_size=11, block_size=8, n_layer=2, n_head=2, n_embd=16, **kw)
+
+
+@pytest.mark.parametrize("mode,int8_backward", [("fp32", False), ("bf16", False),
+                                                ("int8", False), ("int8", True)])
+def test_forward_backward_and_ratchet_update_clear_all_temporary_weights(cuda, mode,
+                                                                        int8_backward):
+    # tests/test_model.py:42-56 in each matmul mode.
+    config = tiny_config(matmul_mode=mode, int8_backward=int8_backward)
+    model = build_seeded_model(config, max_code=3, seed=5).to(cuda).train()
+    tokens = torch.randint(0, config.vocab_size, (3, config.block_size)).to(cuda)
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        logits, loss = model(tokens, tokens)
+    assert logits.shape == (3, config.block_size, config.vocab_size)
+    assert torch.isfinite(loss)
+    loss.backward()
+    stats = model.ratchet_update()
+    layers = [m for m in model.modules() if isinstance(m, DiscreteRatchetLinear)]
+    assert stats.total_weights == sum(layer.packed.numel() for layer in layers)
+    assert all(not layer.has_pending_gradient for layer in layers)
+    for layer in layers:
+        assert int(layer.code.abs().max()) <= 3 and int(layer.pressure.abs().max()) <= 7
+
+
+def test_int8_training_moves_codes_and_lowers_loss(cuda):
+    torch.manual_seed(0)
+    config = ModelConfig(vocab_size=16, block_size=32, n_layer=2, n_head=4, n_embd=64,
+                         matmul_mode="int8", int8_backward=True)
+    model = build_seeded_model(config, max_code=2, seed=1337).to(cuda).train()
+    optimizer = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.0)
+    pattern = torch.arange(33) % 4  # a learnable periodic sequence
+    batch = torch.stack([torch.roll(pattern, s) for s in range(16)]).to(cuda)
+    inputs, targets = batch[:, :32], batch[:, 1:]
+    losses, moves = [], 0
+    for _ in range(60):
+        optimizer.zero_grad(set_to_none=True)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            _, loss = model(inputs, targets)
+        loss.backward()
+        stats = model.ratchet_update(validate=False)
+        optimizer.step()
+        losses.append(float(loss))
+        moves += int(stats.code_moves)
+    assert moves > 0
+    assert np.mean(losses[-10:]) < np.mean(losses[:10]) - 0.1
+
+
+def _rms_norm_f64(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = x.astype(np.float64)
+    return x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * w.astype(np.float64)
+
+
+def _gelu_tanh_f64(x: np.ndarray) -> np.ndarray:
+    x = x.astype(np.float64)
+    return 0.5 * x * (1.0 + np.tanh(0.7978845608028654 * (x + 0.044715 * x ** 3)))
+
+
+def _assert_quant_close(q, s, y_ref):
+    # Transcendentals / reduction order make the float transform differ in the last ulp,
+    # so codes on a rounding boundary may differ by one (the reference's own fused
+    # prologues are only checked against torch ops the same way).
+    q_ref, s_ref = oquant.quantize_rows(y_ref.astype(np.float32))
+    q = q.cpu().numpy().reshape(q_ref.shape)
+    s = s.cpu().numpy().reshape(s_ref.shape)
+    assert np.allclose(s, s_ref, rtol=1e-5, atol=0)
+    diff = np.abs(q.astype(np.int32) - q_ref.astype(np.int32))
+    assert diff.max() <= 1
+    assert (diff > 0).mean() < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(33, 64), (1024, 512), (7, 2048)])
+def test_fused_rmsnorm_quantize(cuda, shape, dtype):
+    g = torch.Generator().manual_seed(shape[0])
+    x = (torch.randn(shape, generator=g) * 2.0).to(dtype)
+    w = torch.rand(shape[1], generator=g) + 0.5
+    q, s = fused_rmsnorm_quantize(x.to(cuda), w.to(cuda), 1e-5)
+    _assert_quant_close(q, s, _rms_norm_f64(x.float().numpy(), w.numpy(), 1e-5))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(33, 64), (1024, 2048)])
+def test_fused_gelu_quantize(cuda, shape, dtype):
+    x = (torch.randn(shape, generator=torch.Generator().manual_seed(3)) * 2.0).to(dtype)
+    q, s = fused_gelu_quantize(x.to(cuda))
+    _assert_quant_close(q, s, _gelu_tanh_f64(x.float().numpy()))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_transpose_quantize_is_exact(cuda, dtype):
+    b, h, s_len, d = 3, 4, 10, 16
+    x = torch.randn(b, h, s_len, d, generator=torch.Generator().manual_seed(4)).to(dtype)
+    q, s = fused_transpose_quantize(x.to(cuda))
+    rows = x.transpose(1, 2).reshape(b * s_len, h * d).float().numpy()
+    q_ref, s_ref = oquant.quantize_rows(rows)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+    # a strided (non-contiguous) producer layout
+    xt = x.to(cuda).transpose(2, 3).contiguous().transpose(2, 3)
+    q2, s2 = fused_transpose_quantize(xt)
+    assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(s2.cpu(), s.cpu())
