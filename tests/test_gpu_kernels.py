@@ -165,7 +165,7 @@ def test_int8_gemm_nt_bit_exact(cuda, m, n, k):
     assert np.array_equal(bits16(out), ref)
     out1 = int8_mm_nt(a.to(cuda), b.to(cuda), ls.to(cuda), None, torch.float32)
     ref1 = ogemm.scaled_int8_mm(a.numpy(), b.numpy().T, ls.numpy(), None)
-    assert np.array_equal(f32bits(out1), f32bits(np.float32(ref1.astype(np.uint32) << 16)))
+    assert np.array_equal(f32bits(out1), (ref1.astype(np.uint32) << 16))
 
 
 @pytest.mark.parametrize("max_code", [1, 2, 3, 7])
@@ -205,7 +205,7 @@ def test_grad_input_gemm_full_op_shape_bit_exact(cuda):
     assert np.array_equal(code_t.cpu().numpy(), code.T)
     out = int8_mm_nt(gq.to(cuda), code_t, gs.to(cuda), None, torch.float32)
     ref = ogemm.scaled_int8_mm(gq.numpy(), code, gs.numpy(), None)
-    assert np.array_equal(f32bits(out), f32bits(np.float32(ref.astype(np.uint32) << 16)))
+    assert np.array_equal(f32bits(out), (ref.astype(np.uint32) << 16))
 
 
 def test_scaled_int8_mm_public_api_strided_and_errors(cuda):
