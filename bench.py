@@ -111,10 +111,11 @@ def kernel_breakdown(layer, x, g, iters: int):
 
     from local_ai_training import _native as nat
     from local_ai_training.int8_matmul import (
-        dequant_bf16,
+        dequant_transpose_bf16,
         int8_mm_nt,
         packed_int8_mm,
         quantize_rows_into,
+        transpose_bf16,
         unpack_transpose,
     )
 
@@ -147,8 +148,9 @@ def kernel_breakdown(layer, x, g, iters: int):
         ("unpack_transpose", lambda: holder.__setitem__("ct", unpack_transpose(packed,
                                                                                MAX_CODE))),
         ("grad_input_gemm", lambda: int8_mm_nt(gq, holder["ct"], gs, None, out=gin)),
-        ("dequant_bf16", lambda: holder.__setitem__("xh", dequant_bf16(q, s))),
-        ("grad_weight_gemm_blas", lambda: torch.mm(g.t(), holder["xh"], out=gw)),
+        ("transpose_grad_bf16", lambda: holder.__setitem__("gt", transpose_bf16(g))),
+        ("dequant_transpose_bf16", lambda: holder.__setitem__("xt", dequant_transpose_bf16(q, s))),
+        ("grad_weight_gemm_blas", lambda: torch.mm(holder["gt"], holder["xt"].t(), out=gw)),
         ("ratchet_update_grad", update),
     ]
     for _, fn in stages:  # warm
@@ -173,7 +175,8 @@ def kernel_breakdown(layer, x, g, iters: int):
         "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
         "unpack_transpose": ("bytes", 2 * n * k),
         "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
-        "dequant_bf16": ("bytes", m * k + m * 4 + m * k * 2),
+        "transpose_grad_bf16": ("bytes", m * n * g.element_size() + m * n * 2),
+        "dequant_transpose_bf16": ("bytes", m * k + m * 4 + m * k * 2),
         "grad_weight_gemm_blas": ("flops", mnk2, m * n * 2 + m * k * 2 + n * k * 2),
         "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
     }

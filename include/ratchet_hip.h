@@ -119,6 +119,23 @@ int rk_dequant_bf16(const int8_t* q, int64_t ldq, const float* s, uint16_t* Xh, 
                     int64_t M, int64_t K, void* stream);
 
 /*
+ * Transposed bf16 copy: T[n, m] = bf16_RNE(X[m, n]); X [M, N] of dtype x_dtype (row
+ * stride ldx), T [N, M] bf16 (row stride ldt). Lays the upstream gradient out as the
+ * K-contiguous operand of the BF16 grad_weight GEMM (grad_out_tile.to(bf16) in
+ * ratchet.py:162, transposed so the GEMM runs in its fast NT form).
+ */
+int rk_transpose_bf16(const void* x, int x_dtype, int64_t ldx, uint16_t* t, int64_t ldt,
+                      int64_t M, int64_t N, void* stream);
+
+/*
+ * Dequantize + transpose: T[k, m] = bf16(q[m,k]) * bf16(scale[m]) rounded to bf16.
+ * The dequantized activations of ratchet.py:73-75, laid out [K, M] for the NT
+ * grad_weight GEMM.
+ */
+int rk_dequant_transpose_bf16(const int8_t* q, int64_t ldq, const float* scale, uint16_t* t,
+                              int64_t ldt, int64_t M, int64_t K, void* stream);
+
+/*
  * Fused integer ratchet update on a normalized gradient z (float32 [rows, K], row
  * stride ldz). packed [rows, K] (row stride ldp) is updated in place. counts[4]
  * (int64) are INCREMENTED by (positive moves, negative moves, blocked positive,

@@ -19,6 +19,8 @@
 //
 // Block order is XCD-aware: consecutive tile indices (which share an A row panel)
 // are kept on one XCD's L2.
+#include <type_traits>
+
 #include "rk_common.h"
 
 namespace rk {
@@ -222,12 +224,296 @@ __global__ __launch_bounds__(256) void int8_gemm_nt_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel for aligned shapes (K % 64 == 0, 16-byte aligned rows, N % 8 == 0).
+//
+//  * Block tile 128 x BN (BN = 128 or 256), 4 wavefronts in 2 x 2, wave tile 64 x BN/2.
+//  * Global -> register ring of S stages (S k-steps of 64 bytes in flight per thread),
+//    register -> LDS ping-pong tiles; one barrier per k-step. The hardware keeps the
+//    S stages' loads in flight while the MFMAs of the current step run.
+//  * LDS tiles are unpadded 64-byte rows with the 16-byte segment index XOR-swizzled
+//    by swz(row) = ((row >> 1) ^ (row >> 3)) & 3, so the fragment reads of any 8 or 16
+//    consecutive rows touch disjoint banks (32- or 64-bank LDS).
+//  * Packed codes are decoded after the LDS read, just before the MFMA.
+//  * Epilogue: accumulators -> bf16/fp32 in an XOR-swizzled LDS staging tile, then
+//    every lane stores 16 contiguous bytes, so each wave writes whole 256-byte rows.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int seg_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// Staging registers of one k-step (one slot of the register ring).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NA, int NB>
+struct RingSlot {
+  u32x4 a[NA];
+  u32x4 b[NB];
+};
+
+template <int NA, int NB>
+__device__ __forceinline__ void ring_load(RingSlot<NA, NB>& r, const uint8_t* const (&a_src)[NA],
+                                          const uint8_t* const (&b_src)[NB], int64_t off) {
+#pragma unroll
+  for (int j = 0; j < NA; ++j) r.a[j] = *reinterpret_cast<const u32x4*>(a_src[j] + off);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) r.b[j] = *reinterpret_cast<const u32x4*>(b_src[j] + off);
+  // Keep ring slots in issue order: a slot's loads must not be scheduled behind later
+  // slots' loads, or waiting for this slot would wait for everything in flight.
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int NA, int NB>
+__device__ __forceinline__ void ring_store(const RingSlot<NA, NB>& r, uint8_t* at, uint8_t* bt,
+                                           const int (&a_dst)[NA], const int (&b_dst)[NB]) {
+#pragma unroll
+  for (int j = 0; j < NA; ++j) *reinterpret_cast<u32x4*>(at + a_dst[j]) = r.a[j];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) *reinterpret_cast<u32x4*>(bt + b_dst[j]) = r.b[j];
+}
+
+// MFMAs of one k-step from the LDS tiles (wave tile 64 x 16*NI).
+template <int KIND, int MI, int NI, int BK>
+__device__ __forceinline__ void tile_mfma(v4i (&acc)[MI][NI], const uint8_t* at,
+                                          const uint8_t* bt, int arow0, int brow0, int r16,
+                                          int g4, uint32_t mc4) {
+  v4i fa[MI], fb[NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int row = arow0 + i * 16 + r16;
+    fa[i] = *reinterpret_cast<const v4i*>(at + row * BK + 16 * (g4 ^ seg_swz(row)));
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int row = brow0 + j * 16 + r16;
+    v4i v = *reinterpret_cast<const v4i*>(bt + row * BK + 16 * (g4 ^ seg_swz(row)));
+    if constexpr (KIND == B_PACKED) {
+      v.x = static_cast<int>(decode4(static_cast<uint32_t>(v.x), mc4));
+      v.y = static_cast<int>(decode4(static_cast<uint32_t>(v.y), mc4));
+      v.z = static_cast<int>(decode4(static_cast<uint32_t>(v.z), mc4));
+      v.w = static_cast<int>(decode4(static_cast<uint32_t>(v.w), mc4));
+    }
+    fb[j] = v;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined kernel for aligned shapes (K % 64 == 0, 16-byte aligned rows, N % 8 == 0).
+//
+//  * Block tile 128 x BN (BN = 128 or 256), 4 wavefronts in 2 x 2, wave tile 64 x BN/2.
+//  * Global -> register ring of S stages (S k-steps of 64 bytes in flight per thread),
+//    register -> LDS ping-pong tiles; one barrier per k-step. The hardware keeps the
+//    S stages' loads in flight while the MFMAs of the current step run.
+//  * LDS tiles are unpadded 64-byte rows with the 16-byte segment index XOR-swizzled
+//    by swz(row) = ((row >> 1) ^ (row >> 3)) & 3, so the fragment reads of any 8 or 16
+//    consecutive rows touch disjoint banks (32- or 64-bank LDS).
+//  * Packed codes are decoded after the LDS read, just before the MFMA.
+//  * Epilogue: accumulators -> bf16/fp32 in an XOR-swizzled LDS staging tile, then
+//    every lane stores 16 contiguous bytes, so each wave writes whole 256-byte rows.
+// ---------------------------------------------------------------------------
+template <int KIND, int CDT, int BN, int S>
+__global__ __launch_bounds__(256) void int8_gemm_pipe_kernel(GemmArgs g) {
+  constexpr int BM = 128, BK = 64;
+  constexpr int WN = BN / 2;
+  constexpr int NI = WN / 16;
+  constexpr int MI = 4;
+  constexpr int A_SEGS = BM * BK / 16 / 256;
+  constexpr int B_SEGS = BN * BK / 16 / 256;
+  constexpr int TILE_BYTES = 2 * (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[TILE_BYTES];
+  uint8_t* As = smem;                      // [2][BM * BK]
+  uint8_t* Bs = smem + 2 * BM * BK;        // [2][BN * BK]
+
+  const int64_t tiles_n = (g.N + BN - 1) / BN;
+  int64_t b = blockIdx.x;
+  const int64_t nb = gridDim.x;
+  if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
+  const int64_t m0 = (b / tiles_n) * BM;
+  const int64_t n0 = (b % tiles_n) * BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int g4 = lane >> 4, r16 = lane & 15;
+
+  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
+  // Staging segments of this thread (rows past the edge are clamped: they only feed
+  // outputs that are never stored).
+  const uint8_t* a_src[A_SEGS];
+  const uint8_t* b_src[B_SEGS];
+  int a_dst[A_SEGS], b_dst[B_SEGS];
+  // Staging: 4 consecutive lanes cover one 64-byte row segment (coalesced global
+  // loads); the LDS slot of segment seg of row `row` is seg ^ seg_swz(row).
+#pragma unroll
+  for (int j = 0; j < A_SEGS; ++j) {
+    const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
+    const int64_t gr = min(m0 + row, g.M - 1);
+    a_src[j] = Ab + gr * g.lda + 16 * seg;
+    a_dst[j] = row * BK + 16 * (seg ^ seg_swz(row));
+  }
+#pragma unroll
+  for (int j = 0; j < B_SEGS; ++j) {
+    const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
+    const int64_t gr = min(n0 + row, g.N - 1);
+    b_src[j] = g.B + gr * g.ldb + 16 * seg;
+    b_dst[j] = row * BK + 16 * (seg ^ seg_swz(row));
+  }
+
+  v4i acc[MI][NI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  const int nk = static_cast<int>(g.K / BK);
+  RingSlot<A_SEGS, B_SEGS> r0, r1, r2, r3;
+  // Loads and LDS stores are unconditional (tail k-steps re-read the last stage via a
+  // clamped offset) so the compiler's outstanding-load count is the same on every path
+  // and each ring slot waits only for its own loads; only the MFMAs are predicated.
+  const int last = nk - 1;
+  ring_load(r0, a_src, b_src, 0);
+  if constexpr (S > 1) ring_load(r1, a_src, b_src, static_cast<int64_t>(min(1, last)) * BK);
+  if constexpr (S > 2) ring_load(r2, a_src, b_src, static_cast<int64_t>(min(2, last)) * BK);
+  if constexpr (S > 3) ring_load(r3, a_src, b_src, static_cast<int64_t>(min(3, last)) * BK);
+
+  const int arow0 = wm * 64, brow0 = wn * WN;
+#define RK_PIPE_STEP(R, KT)                                                              \
+  {                                                                                      \
+    const int kt_ = (KT);                                                                \
+    const int buf_ = kt_ & 1;                                                            \
+    ring_store(R, As + buf_ * BM * BK, Bs + buf_ * BN * BK, a_dst, b_dst);               \
+    ring_load(R, a_src, b_src, static_cast<int64_t>(min(kt_ + S, last)) * BK);           \
+    __syncthreads();                                                                     \
+    if (kt_ < nk)                                                                        \
+      tile_mfma<KIND, MI, NI, BK>(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0,   \
+                                  brow0, r16, g4, g.mc4);                                \
+  }
+  for (int kb = 0; kb < nk; kb += S) {
+    RK_PIPE_STEP(r0, kb)
+    if constexpr (S > 1) RK_PIPE_STEP(r1, kb + 1)
+    if constexpr (S > 2) RK_PIPE_STEP(r2, kb + 2)
+    if constexpr (S > 3) RK_PIPE_STEP(r3, kb + 3)
+  }
+#undef RK_PIPE_STEP
+  __syncthreads();  // all fragment reads done: the tiles become the staging buffer
+
+  // Epilogue. Staging row pitch = BN * esize bytes, 16-byte chunks XOR-swizzled by
+  // (row & 15) so both the 8-byte fragment writes and the 16-byte row reads are
+  // conflict-free. fp32 output stages 64 rows per pass.
+  constexpr int ES = CDT == RK_BF16 ? 2 : 4;
+  constexpr int PITCH = BN * ES;
+  constexpr int CHUNKS = PITCH / 16;
+  constexpr int ROWS_PER_PASS = (TILE_BYTES / PITCH) >= BM ? BM : 64;
+  constexpr int PASSES = BM / ROWS_PER_PASS;
+  static_assert(ROWS_PER_PASS * PITCH <= TILE_BYTES, "staging tile does not fit");
+  float lsv[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int64_t m = m0 + wm * 64 + i * 16 + r16;
+    lsv[i] = m < g.M ? g.ls[m] : 0.0f;
+  }
+  float rsv[NI][4];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + wn * WN + j * 16 + 4 * g4 + r;
+      rsv[j][r] = g.rs ? (n < g.N ? g.rs[n] : 0.0f) : 1.0f;
+    }
+  const bool has_rs = g.rs != nullptr;
+
+#pragma unroll
+  for (int pass = 0; pass < PASSES; ++pass) {
+    if (PASSES == 1 || wm == pass) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int row = (PASSES == 1 ? wm * 64 : 0) + i * 16 + r16;  // row in the staging tile
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int col = wn * WN + j * 16 + 4 * g4;  // first of 4 output columns
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = static_cast<float>(acc[i][j][r]) * lsv[i];
+            if (has_rs) t = t * rsv[j][r];
+            v[r] = t;
+          }
+          const int byte = col * ES;
+          const int chunk = (byte >> 4) ^ (row & 15);
+          uint8_t* dst = smem + row * PITCH + chunk * 16 + (byte & 15);
+          if constexpr (CDT == RK_BF16) {
+            uint2 pk;
+            pk.x = static_cast<uint32_t>(f32_to_bf16(v[0])) |
+                   (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+            pk.y = static_cast<uint32_t>(f32_to_bf16(v[2])) |
+                   (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+            *reinterpret_cast<uint2*>(dst) = pk;
+          } else {
+            *reinterpret_cast<float4*>(dst) =
+                make_float4(round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3]));
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // Coalesced copy-out: each lane moves one 16-byte chunk.
+    constexpr int TOTAL = ROWS_PER_PASS * CHUNKS;
+    const int64_t row_base = m0 + (PASSES == 1 ? 0 : pass * 64);
+#pragma unroll
+    for (int c = tid; c < TOTAL; c += 256) {
+      const int row = c / CHUNKS, ch = c % CHUNKS;
+      const int64_t m = row_base + row;
+      const int64_t n = n0 + (ch * 16) / ES;
+      if (m < g.M && n < g.N) {
+        const uint4 val = *reinterpret_cast<const uint4*>(smem + row * PITCH +
+                                                           ((ch ^ (row & 15)) * 16));
+        char* out = static_cast<char*>(g.C) + (m * g.ldc + n) * ES;
+        *reinterpret_cast<uint4*>(out) = val;
+      }
+    }
+    if (PASSES > 1) __syncthreads();
+  }
+}
+
+static int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v ? atoi(v) : dflt;
+}
+
 template <int KIND, int CDT>
 static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
-  const int64_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
-  if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
   const bool fast = (g.K % kBK) == 0 && (g.lda % 16) == 0 && (g.ldb % 16) == 0 &&
                     aligned16(g.A) && aligned16(g.B);
+  const int es = CDT == RK_BF16 ? 2 : 4;
+  const bool aligned_out = fast && (g.N % 8) == 0 && ((g.ldc * es) % 16) == 0 && aligned16(g.C);
+  if (aligned_out) {
+    // Tuning knobs (every config gives identical results): RK_GEMM_BN (128 or 256),
+    // RK_GEMM_STAGES (register-ring depth, 2..4).
+    static const int bn_env = env_int("RK_GEMM_BN", 128);
+    static const int st_env = env_int("RK_GEMM_STAGES", 3);
+    const int stages = (st_env >= 2 && st_env <= 4) ? st_env : 3;
+    const int bn = (bn_env == 256 && CDT == RK_BF16) ? 256 : 128;
+    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + bn - 1) / bn);
+    const dim3 grid(static_cast<unsigned>(tiles)), block(256);
+    if (bn == 256) {
+      if constexpr (CDT == RK_BF16) {
+        if (stages == 2) int8_gemm_pipe_kernel<KIND, CDT, 256, 2><<<grid, block, 0, stream>>>(g);
+        else if (stages == 4) int8_gemm_pipe_kernel<KIND, CDT, 256, 4><<<grid, block, 0, stream>>>(g);
+        else int8_gemm_pipe_kernel<KIND, CDT, 256, 3><<<grid, block, 0, stream>>>(g);
+      }
+    } else {
+      if (stages == 2) int8_gemm_pipe_kernel<KIND, CDT, 128, 2><<<grid, block, 0, stream>>>(g);
+      else if (stages == 4) int8_gemm_pipe_kernel<KIND, CDT, 128, 4><<<grid, block, 0, stream>>>(g);
+      else int8_gemm_pipe_kernel<KIND, CDT, 128, 3><<<grid, block, 0, stream>>>(g);
+    }
+    return launch_status("int8_gemm");
+  }
+  const int64_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);
+  if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
   const dim3 grid(static_cast<unsigned>(tiles)), block(256);
   if (fast) {
     int8_gemm_nt_kernel<KIND, true, CDT><<<grid, block, 0, stream>>>(g);

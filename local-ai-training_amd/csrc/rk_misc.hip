@@ -86,6 +86,41 @@ __global__ void dequant_bf16_kernel(const int8_t* q, int64_t ldq, const float* s
   }
 }
 
+// 64 x 64 tiles through LDS: X[m, n] (f32 or bf16, row stride ldx) -> T[n, m] bf16
+// (row stride ldt), each element rounded to bf16 (RNE) on the way. With DEQUANT the
+// source is int8 q[m, n] and the value is bf16(q) * bf16(s[m]) rounded to bf16.
+// Reads and writes are both row-contiguous 128-byte (or wider) wave accesses.
+template <int DT, bool DEQUANT>
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const void* X, int64_t ldx,
+                                                             const float* s, uint16_t* T,
+                                                             int64_t ldt, int64_t M, int64_t N) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t tiles_n = (N + 63) / 64;
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) / tiles_n) * 64;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) % tiles_n) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t m = m0 + r, n = n0 + tx;
+    uint16_t v = 0;
+    if (m < M && n < N) {
+      if constexpr (DEQUANT) {
+        const int8_t q = static_cast<const int8_t*>(X)[m * ldx + n];
+        v = f32_to_bf16(static_cast<float>(q) * round_bf16(s[m]));
+      } else if constexpr (DT == RK_F32) {
+        v = f32_to_bf16(static_cast<const float*>(X)[m * ldx + n]);
+      } else {
+        v = static_cast<const uint16_t*>(X)[m * ldx + n];
+      }
+    }
+    tile[r][tx] = v;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t n = n0 + r, m = m0 + tx;
+    if (n < N && m < M) T[n * ldt + m] = tile[tx][r];
+  }
+}
+
 __global__ void pressure_leak_kernel(uint8_t* packed, int64_t n, int mc) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -204,4 +239,37 @@ extern "C" int rk_validate_state(const uint8_t* packed, int64_t n, int max_code,
   validate_kernel<<<flat_grid(work > 0 ? work : 1, 1), 256, 0, as_stream(stream)>>>(
       packed, n, max_code, scale, n_rows, flags);
   return launch_status("validate_state");
+}
+
+extern "C" int rk_transpose_bf16(const void* x, int x_dtype, int64_t ldx, uint16_t* t,
+                                 int64_t ldt, int64_t M, int64_t N, void* stream) {
+  clear_error();
+  if (x_dtype != RK_F32 && x_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported dtype");
+  if (M < 0 || N < 0) return fail(RK_ERR_ARG, "negative size");
+  if (M == 0 || N == 0) return RK_OK;
+  if (!x || !t) return fail(RK_ERR_ARG, "null pointer");
+  if (ldx < N || ldt < M) return fail(RK_ERR_ARG, "leading dimension too small");
+  const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
+  hipStream_t s = as_stream(stream);
+  if (x_dtype == RK_F32)
+    transpose_bf16_kernel<RK_F32, false><<<static_cast<unsigned>(tiles), 256, 0, s>>>(x, ldx, nullptr, t, ldt, M, N);
+  else
+    transpose_bf16_kernel<RK_BF16, false><<<static_cast<unsigned>(tiles), 256, 0, s>>>(x, ldx, nullptr, t, ldt, M, N);
+  return launch_status("transpose_bf16");
+}
+
+extern "C" int rk_dequant_transpose_bf16(const int8_t* q, int64_t ldq, const float* scale,
+                                         uint16_t* t, int64_t ldt, int64_t M, int64_t K,
+                                         void* stream) {
+  clear_error();
+  if (M < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
+  if (M == 0 || K == 0) return RK_OK;
+  if (!q || !scale || !t) return fail(RK_ERR_ARG, "null pointer");
+  if (ldq < K || ldt < M) return fail(RK_ERR_ARG, "leading dimension too small");
+  const int64_t tiles = ((M + 63) / 64) * ((K + 63) / 64);
+  if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
+  transpose_bf16_kernel<RK_BF16, true><<<static_cast<unsigned>(tiles), 256, 0, as_stream(stream)>>>(
+      q, ldq, scale, t, ldt, M, K);
+  return launch_status("dequant_transpose_bf16");
 }

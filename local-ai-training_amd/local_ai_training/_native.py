@@ -36,6 +36,8 @@ SIGNATURES: dict[str, list] = {
     "rk_unpack": [_p, _i64, _i32, _p, _p, _p],
     "rk_effective_bf16": [_p, _i64, _i32, _p, _p, _i64, _i64, _i64, _p],
     "rk_dequant_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
+    "rk_transpose_bf16": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p],
+    "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_ratchet_update": [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _f32, _f32, _p, _p],
     "rk_ratchet_update_grad": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i32, _i32, _f32, _f32,
                                _f32, _p, _f32, _f32, _p, _p, _p, _p, _p],

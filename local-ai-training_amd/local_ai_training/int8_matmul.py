@@ -190,3 +190,23 @@ def dequant_bf16(q: Tensor, s: Tensor) -> Tensor:
     nat.call("rk_dequant_bf16", q.data_ptr(), _ld(q), s.data_ptr(), out.data_ptr(), _ld(out),
              m, k, nat.stream_handle(q.device))
     return out
+
+
+def transpose_bf16(x: Tensor) -> Tensor:
+    """bf16 transposed copy of a 2-D float32/bfloat16 tensor (unit column stride)."""
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    m, n = x.shape
+    out = torch.empty((n, m), device=x.device, dtype=torch.bfloat16)
+    nat.call("rk_transpose_bf16", x.data_ptr(), nat.dtype_code(x.dtype), _ld(x), out.data_ptr(),
+             _ld(out), m, n, nat.stream_handle(x.device))
+    return out
+
+
+def dequant_transpose_bf16(q: Tensor, s: Tensor) -> Tensor:
+    """(bf16(q) * bf16(s)[:, None])^T as a contiguous bf16 [K, M] tensor."""
+    m, k = q.shape
+    out = torch.empty((k, m), device=q.device, dtype=torch.bfloat16)
+    nat.call("rk_dequant_transpose_bf16", q.data_ptr(), _ld(q), s.data_ptr(), out.data_ptr(),
+             _ld(out), m, k, nat.stream_handle(q.device))
+    return out

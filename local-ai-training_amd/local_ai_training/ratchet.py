@@ -36,10 +36,12 @@ from . import _native as nat
 from .int8_matmul import (
     _sr_seed,
     dequant_bf16,
+    dequant_transpose_bf16,
     effective_bf16,
     int8_mm_nt,
     packed_int8_mm,
     quantize_rows_into,
+    transpose_bf16,
     unpack_transpose,
 )
 
@@ -200,7 +202,7 @@ class _RatchetMatmul(torch.autograd.Function):
         mode = layer.matmul_mode
         if ctx.used_fused_int8:
             q, s, scale = ctx.saved_tensors
-            inputs_bf16 = dequant_bf16(q, s)
+            inputs_bf16 = dequant_bf16(q, s) if not layer.fuse_backward_update else None
             inputs_fp32 = None
         else:
             flat_inputs, scale = ctx.saved_tensors
@@ -235,20 +237,14 @@ class _RatchetMatmul(torch.autograd.Function):
             grad_input = gradient_fp32 @ layer._effective_weight_f32(scale_d)
         elif layer.int8_backward and ctx.used_fused_int8:
             # int8 grad_input: fold the per-row weight scale into the gradient, SR-quantize
-            # (Philox bits), GEMM against the pre-update codes (ratchet.py:125-134). The
-            # same pass writes the bf16 gradient the grad_weight GEMM consumes.
+            # (Philox bits), GEMM against the pre-update codes (ratchet.py:125-134).
             g = flat_gradient
             if g.dtype not in (torch.float32, torch.bfloat16):
                 g = g.float()
             grad_q = torch.empty((m, n), device=g.device, dtype=torch.int8)
             grad_s = torch.empty((m,), device=g.device, dtype=torch.float32)
-            if g.dtype == torch.bfloat16:
-                gradient_bf16, side = g, None  # already the grad_weight operand
-            else:
-                gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
-                side = gradient_bf16
             quantize_rows_into(g, grad_q, grad_s, col_scale=scale_d.float().contiguous(),
-                               stochastic=True, seed=_sr_seed(), bf16_out=side)
+                               stochastic=True, seed=_sr_seed())
             code_t = unpack_transpose(packed, layer.max_code)
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
@@ -260,9 +256,16 @@ class _RatchetMatmul(torch.autograd.Function):
         if mode == "fp32":
             grad_weight = gradient_fp32.t() @ inputs_fp32
         else:
-            if gradient_bf16 is None:
-                gradient_bf16 = flat_gradient.to(torch.bfloat16)
-            grad_weight = gradient_bf16.t() @ inputs_bf16
+            # BF16 grad_weight [N, K] = bf16(g)^T @ bf16(x) (ratchet.py:159-163), run as an
+            # NT GEMM on transposed bf16 copies (both operands contiguous along tokens).
+            g = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
+                else flat_gradient.float()
+            grad_t = transpose_bf16(g)
+            if ctx.used_fused_int8:
+                inputs_t = dequant_transpose_bf16(q, s)
+            else:
+                inputs_t = transpose_bf16(inputs_bf16)
+            grad_weight = grad_t @ inputs_t.t()
         grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
             grad_scale, None

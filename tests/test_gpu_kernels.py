@@ -16,6 +16,7 @@ from helpers import synthetic_state
 from local_ai_training import _native as nat
 from local_ai_training.int8_matmul import (
     dequant_bf16,
+    dequant_transpose_bf16,
     effective_bf16,
     int8_mm_nt,
     packed_int8_mm,
@@ -24,6 +25,7 @@ from local_ai_training.int8_matmul import (
     quantize_rows_colscaled,
     quantize_rows_into,
     scaled_int8_mm,
+    transpose_bf16,
     unpack_transpose,
 )
 from oracle import gemm as ogemm
@@ -238,6 +240,35 @@ def test_effective_and_dequant_bf16_match_torch_formula(cuda):
     s = torch.rand(40, generator=gen(9)) * 0.1
     xh = dequant_bf16(q.to(cuda), s.to(cuda))
     assert torch.equal(xh.cpu(), q.to(torch.bfloat16) * s[:, None].to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(1, 1), (63, 65), (64, 64), (130, 7), (257, 300),
+                                   (16384, 2048)])
+def test_transpose_bf16_is_rne_cast_then_transpose(cuda, shape, dtype):
+    m, n = shape
+    x = (torch.randn(m, n, generator=gen(m * 7 + n)) * 3).to(dtype)
+    t = transpose_bf16(x.to(cuda))
+    assert t.shape == (n, m) and t.is_contiguous()
+    assert np.array_equal(bits16(t), bits16(x.to(torch.bfloat16).t().contiguous()))
+
+
+def test_transpose_bf16_of_strided_rows(cuda):
+    base = torch.randn(70, 96, generator=gen(5)).to(cuda)
+    view = base[:, 8:72]
+    t = transpose_bf16(view)
+    assert np.array_equal(bits16(t), bits16(view.cpu().to(torch.bfloat16).t().contiguous()))
+
+
+@pytest.mark.parametrize("shape", [(1, 64), (40, 32), (129, 257), (16384, 512)])
+def test_dequant_transpose_matches_dequant_then_transpose(cuda, shape):
+    m, k = shape
+    q = torch.randint(-127, 128, (m, k), generator=gen(m + k), dtype=torch.int8)
+    s = torch.rand(m, generator=gen(k)) * 0.1
+    xt = dequant_transpose_bf16(q.to(cuda), s.to(cuda))
+    ref = (q.to(torch.bfloat16) * s[:, None].to(torch.bfloat16)).t().contiguous()
+    assert xt.shape == (k, m)
+    assert np.array_equal(bits16(xt), bits16(ref))
 
 
 # ---------------------------------------------------------------------------

@@ -344,6 +344,11 @@ def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
         assert np.array_equal(gin, gin_ref), f"grad_input differs at step {step}"
         gw = captured["gw"]
         assert gw.dtype == torch.bfloat16
+        # grad_weight = bf16(g)^T @ bf16(x_hat) in fp32, bf16 output: rel 1e-2 / abs 1e-3.
+        xh = (torch.from_numpy(q_ref).to(torch.bfloat16)
+              * torch.from_numpy(s_ref).to(torch.bfloat16)[:, None]).float()
+        gw_ref = gout.float().t() @ xh
+        torch.testing.assert_close(gw.float().cpu(), gw_ref, rtol=1e-2, atol=1e-3)
         ref = oupd.update_from_gradient(packed_ref, gw.float().cpu().numpy(), mc, 8, 0.5, 1.5,
                                         1e-8, oupd.vec_for_dtype("bf16"))
         packed_ref = ref["packed"]
