@@ -62,6 +62,15 @@ int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t s
                      uint16_t* x_bf16, int64_t ld_xb, void* stream);
 
 /*
+ * Random words of the stochastic rounding: out[i] = first output word of
+ * Philox4x32-10 for counter ((counter0 + i) mod 2^32, 0, 0, 0) and key
+ * (seed & 0xffffffff, seed >> 32), exactly the words rk_quantize_rows(stochastic=1)
+ * draws for counters m*K + k.
+ * Replaces: tl.randint(seed, offsets) behind tl.rand, int8_matmul.py:143-144.
+ */
+int rk_philox_word0(uint64_t seed, uint32_t counter0, int64_t n, uint32_t* out, void* stream);
+
+/*
  * Scaled int8 GEMM, "NT" form: C[m, n] = out( (float(sum_k A[m,k] * B[n,k]) * ls[m]) * rs[n] )
  * with int32 accumulation. A int8 [M, K] (row stride lda, unit k stride); B int8
  * [N, K] (row stride ldb, unit k stride). rs may be NULL (= ones). The product is

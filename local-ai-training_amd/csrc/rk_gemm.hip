@@ -1,4 +1,4 @@
-// Scaled int8 GEMM on gfx950 int8 MFMA (v_mfma_i32_16x16x64_i8).
+// Scaled int8 GEMM on gfx950 int8 MFMA.
 //
 //   C[m, n] = bf16_RNE( (float(sum_k A[m,k] * B[n,k]) * ls[m]) * rs[n] )
 //
@@ -8,15 +8,12 @@
 // persistent codes are stored (packed[n, k]), so the forward GEMM needs no
 // transposed copy of the weights (the reference makes one, ratchet.py:52).
 //
-// Tiling: 256 threads (4 wavefronts, 2x2), block tile 128x128, k-step 64 bytes.
-// Each wavefront owns a 64x64 sub-tile = 4x4 MFMA 16x16 tiles (64 int32
-// accumulators per lane). Tiles are double-buffered in LDS with rows padded to
-// 80 bytes so the 16-byte fragment reads of 8 consecutive rows hit disjoint banks.
-//
-// MFMA operand roles are swapped (the B tile feeds the MFMA "A" operand) so that
-// the accumulator layout gives every lane 4 consecutive output columns n of one
-// row m: the epilogue stores 8 bytes (bf16) or 16 bytes (f32) per lane.
-//
+// Two kernels:
+//  * int8_gemm_m32_kernel, for aligned shapes (K % 64 == 0, 16-byte aligned rows and
+//    scales, N % 8 == 0): v_mfma_i32_32x32x32_i8, 128 x 128 block tiles, register
+//    ring + LDS ping-pong, LDS-staged coalesced epilogue;
+//  * int8_gemm_nt_kernel, any shape and stride (ragged K, unaligned rows):
+//    v_mfma_i32_16x16x64_i8 with bounds-checked staging.
 // Block order is XCD-aware: consecutive tile indices (which share an A row panel)
 // are kept on one XCD's L2.
 #include <type_traits>
@@ -26,6 +23,7 @@
 namespace rk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 128;
 constexpr int kBN = 128;
@@ -224,25 +222,16 @@ __global__ __launch_bounds__(256) void int8_gemm_nt_kernel(GemmArgs g) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Pipelined kernel for aligned shapes (K % 64 == 0, 16-byte aligned rows, N % 8 == 0).
-//
-//  * Block tile 128 x BN (BN = 128 or 256), 4 wavefronts in 2 x 2, wave tile 64 x BN/2.
-//  * Global -> register ring of S stages (S k-steps of 64 bytes in flight per thread),
-//    register -> LDS ping-pong tiles; one barrier per k-step. The hardware keeps the
-//    S stages' loads in flight while the MFMAs of the current step run.
-//  * LDS tiles are unpadded 64-byte rows with the 16-byte segment index XOR-swizzled
-//    by swz(row) = ((row >> 1) ^ (row >> 3)) & 3, so the fragment reads of any 8 or 16
-//    consecutive rows touch disjoint banks (32- or 64-bank LDS).
-//  * Packed codes are decoded after the LDS read, just before the MFMA.
-//  * Epilogue: accumulators -> bf16/fp32 in an XOR-swizzled LDS staging tile, then
-//    every lane stores 16 contiguous bytes, so each wave writes whole 256-byte rows.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int seg_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> packed bf16 pair (low half = lo), round-to-nearest-even.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // Staging registers of one k-step (one slot of the register ring).
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
 template <int NA, int NB>
 struct RingSlot {
   u32x4 a[NA];
@@ -261,71 +250,73 @@ __device__ __forceinline__ void ring_load(RingSlot<NA, NB>& r, const uint8_t* co
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NA, int NB>
+template <int KIND, int NA, int NB>
 __device__ __forceinline__ void ring_store(const RingSlot<NA, NB>& r, uint8_t* at, uint8_t* bt,
-                                           const int (&a_dst)[NA], const int (&b_dst)[NB]) {
+                                           const int (&a_dst)[NA], const int (&b_dst)[NB],
+                                           uint32_t mc4) {
 #pragma unroll
   for (int j = 0; j < NA; ++j) *reinterpret_cast<u32x4*>(at + a_dst[j]) = r.a[j];
 #pragma unroll
-  for (int j = 0; j < NB; ++j) *reinterpret_cast<u32x4*>(bt + b_dst[j]) = r.b[j];
-}
-
-// MFMAs of one k-step from the LDS tiles (wave tile 64 x 16*NI).
-template <int KIND, int MI, int NI, int BK>
-__device__ __forceinline__ void tile_mfma(v4i (&acc)[MI][NI], const uint8_t* at,
-                                          const uint8_t* bt, int arow0, int brow0, int r16,
-                                          int g4, uint32_t mc4) {
-  v4i fa[MI], fb[NI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int row = arow0 + i * 16 + r16;
-    fa[i] = *reinterpret_cast<const v4i*>(at + row * BK + 16 * (g4 ^ seg_swz(row)));
-  }
-#pragma unroll
-  for (int j = 0; j < NI; ++j) {
-    const int row = brow0 + j * 16 + r16;
-    v4i v = *reinterpret_cast<const v4i*>(bt + row * BK + 16 * (g4 ^ seg_swz(row)));
+  for (int j = 0; j < NB; ++j) {
+    u32x4 v = r.b[j];
     if constexpr (KIND == B_PACKED) {
-      v.x = static_cast<int>(decode4(static_cast<uint32_t>(v.x), mc4));
-      v.y = static_cast<int>(decode4(static_cast<uint32_t>(v.y), mc4));
-      v.z = static_cast<int>(decode4(static_cast<uint32_t>(v.z), mc4));
-      v.w = static_cast<int>(decode4(static_cast<uint32_t>(v.w), mc4));
+      v.x = decode4(v.x, mc4);
+      v.y = decode4(v.y, mc4);
+      v.z = decode4(v.z, mc4);
+      v.w = decode4(v.w, mc4);
     }
-    fb[j] = v;
+    *reinterpret_cast<u32x4*>(bt + b_dst[j]) = v;
   }
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel for aligned shapes (K % 64 == 0, 16-byte aligned rows, N % 8 == 0).
+// 32x32x32 MFMA kernel (aligned shapes): block tile 128 x 128, 4 wavefronts in 2 x 2,
+// wave tile 64 x 64 = 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (two per 64-byte k-step),
+// register ring of S k-steps, LDS ping-pong, one barrier per k-step.
 //
-//  * Block tile 128 x BN (BN = 128 or 256), 4 wavefronts in 2 x 2, wave tile 64 x BN/2.
-//  * Global -> register ring of S stages (S k-steps of 64 bytes in flight per thread),
-//    register -> LDS ping-pong tiles; one barrier per k-step. The hardware keeps the
-//    S stages' loads in flight while the MFMAs of the current step run.
-//  * LDS tiles are unpadded 64-byte rows with the 16-byte segment index XOR-swizzled
-//    by swz(row) = ((row >> 1) ^ (row >> 3)) & 3, so the fragment reads of any 8 or 16
-//    consecutive rows touch disjoint banks (32- or 64-bank LDS).
-//  * Packed codes are decoded after the LDS read, just before the MFMA.
-//  * Epilogue: accumulators -> bf16/fp32 in an XOR-swizzled LDS staging tile, then
-//    every lane stores 16 contiguous bytes, so each wave writes whole 256-byte rows.
+// The 32x32x32 form issues half as many MFMAs per MAC as 16x16x64 and sustained
+// 4.3-4.5 POP/s in register-resident MFMA chains on MI355X (16x16x64: at most ~3.4).
+// Fragment layout: lane l holds row (l & 31), k bytes 16 (l >> 5) .. +15 of a 32-byte
+// k half. LDS rows are 64 bytes with the 16-byte segment XOR-swizzled by
+// (row >> 2) & 3, which keeps these 32-row fragment reads free of bank conflicts.
+// Operands are swapped (B rows feed the MFMA's first operand) so the accumulator gives
+// each lane 4 consecutive output columns n for one row m:
+//   acc[e], e = 0..15: n = 8 (e / 4) + 4 (l >> 5) + (e % 4), m = l & 31.
 // ---------------------------------------------------------------------------
-template <int KIND, int CDT, int BN, int S>
-__global__ __launch_bounds__(256) void int8_gemm_pipe_kernel(GemmArgs g) {
-  constexpr int BM = 128, BK = 64;
-  constexpr int WN = BN / 2;
-  constexpr int NI = WN / 16;
-  constexpr int MI = 4;
+__device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
+
+__device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at,
+                                            const uint8_t* bt, int arow0, int brow0, int lane) {
+  const int r32 = lane & 31, h = lane >> 5;
+  v4i fa[2][2], fb[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra = arow0 + i * 32 + r32;
+    const int rb = brow0 + i * 32 + r32;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      fa[i][kh] = *reinterpret_cast<const v4i*>(at + ra * 64 + 16 * ((h + 2 * kh) ^ swz32(ra)));
+      fb[i][kh] = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
+    }
+  }
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j][kh], fa[i][kh], acc[i][j], 0, 0, 0);
+}
+
+template <int KIND, int CDT, int S, bool HAS_RS>
+__global__ __launch_bounds__(256) void int8_gemm_m32_kernel(GemmArgs g) {
+  constexpr int BM = 128, BN = 128, BK = 64;
   constexpr int A_SEGS = BM * BK / 16 / 256;
   constexpr int B_SEGS = BN * BK / 16 / 256;
-  constexpr int TILE_BYTES = 2 * (BM + BN) * BK;
+  constexpr int TILE_BYTES = 2 * (BM + BN) * BK;  // 32 KB ping-pong operand tiles
   __shared__ __attribute__((aligned(16))) uint8_t smem[TILE_BYTES];
-  uint8_t* As = smem;                      // [2][BM * BK]
-  uint8_t* Bs = smem + 2 * BM * BK;        // [2][BN * BK]
+  uint8_t* As = smem;
+  uint8_t* Bs = smem + 2 * BM * BK;
 
   const int64_t tiles_n = (g.N + BN - 1) / BN;
   int64_t b = blockIdx.x;
@@ -338,145 +329,125 @@ __global__ __launch_bounds__(256) void int8_gemm_pipe_kernel(GemmArgs g) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  const int g4 = lane >> 4, r16 = lane & 15;
+  const int arow0 = wm * 64, brow0 = wn * 64;
 
   const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
-  // Staging segments of this thread (rows past the edge are clamped: they only feed
-  // outputs that are never stored).
   const uint8_t* a_src[A_SEGS];
   const uint8_t* b_src[B_SEGS];
   int a_dst[A_SEGS], b_dst[B_SEGS];
-  // Staging: 4 consecutive lanes cover one 64-byte row segment (coalesced global
-  // loads); the LDS slot of segment seg of row `row` is seg ^ seg_swz(row).
 #pragma unroll
   for (int j = 0; j < A_SEGS; ++j) {
     const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
-    const int64_t gr = min(m0 + row, g.M - 1);
-    a_src[j] = Ab + gr * g.lda + 16 * seg;
-    a_dst[j] = row * BK + 16 * (seg ^ seg_swz(row));
+    a_src[j] = Ab + min(m0 + row, g.M - 1) * g.lda + 16 * seg;
+    a_dst[j] = row * BK + 16 * (seg ^ swz32(row));
   }
 #pragma unroll
   for (int j = 0; j < B_SEGS; ++j) {
     const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
-    const int64_t gr = min(n0 + row, g.N - 1);
-    b_src[j] = g.B + gr * g.ldb + 16 * seg;
-    b_dst[j] = row * BK + 16 * (seg ^ seg_swz(row));
+    b_src[j] = g.B + min(n0 + row, g.N - 1) * g.ldb + 16 * seg;
+    b_dst[j] = row * BK + 16 * (seg ^ swz32(row));
   }
 
-  v4i acc[MI][NI];
+  v16i acc[2][2];
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NI; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
 
   const int nk = static_cast<int>(g.K / BK);
-  RingSlot<A_SEGS, B_SEGS> r0, r1, r2, r3;
-  // Loads and LDS stores are unconditional (tail k-steps re-read the last stage via a
-  // clamped offset) so the compiler's outstanding-load count is the same on every path
-  // and each ring slot waits only for its own loads; only the MFMAs are predicated.
   const int last = nk - 1;
+  RingSlot<A_SEGS, B_SEGS> r0, r1, r2, r3;
   ring_load(r0, a_src, b_src, 0);
   if constexpr (S > 1) ring_load(r1, a_src, b_src, static_cast<int64_t>(min(1, last)) * BK);
   if constexpr (S > 2) ring_load(r2, a_src, b_src, static_cast<int64_t>(min(2, last)) * BK);
   if constexpr (S > 3) ring_load(r3, a_src, b_src, static_cast<int64_t>(min(3, last)) * BK);
 
-  const int arow0 = wm * 64, brow0 = wn * WN;
-#define RK_PIPE_STEP(R, KT)                                                              \
-  {                                                                                      \
-    const int kt_ = (KT);                                                                \
-    const int buf_ = kt_ & 1;                                                            \
-    ring_store(R, As + buf_ * BM * BK, Bs + buf_ * BN * BK, a_dst, b_dst);               \
-    ring_load(R, a_src, b_src, static_cast<int64_t>(min(kt_ + S, last)) * BK);           \
-    __syncthreads();                                                                     \
-    if (kt_ < nk)                                                                        \
-      tile_mfma<KIND, MI, NI, BK>(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0,   \
-                                  brow0, r16, g4, g.mc4);                                \
+#define RK_M32_STEP(R, KT)                                                                  \
+  {                                                                                         \
+    const int kt_ = (KT);                                                                   \
+    const int buf_ = kt_ & 1;                                                               \
+    ring_store<KIND>(R, As + buf_ * BM * BK, Bs + buf_ * BN * BK, a_dst, b_dst, g.mc4);     \
+    ring_load(R, a_src, b_src, static_cast<int64_t>(min(kt_ + S, last)) * BK);              \
+    __syncthreads();                                                                        \
+    if (kt_ < nk) mfma32_step(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0, brow0, lane); \
   }
   for (int kb = 0; kb < nk; kb += S) {
-    RK_PIPE_STEP(r0, kb)
-    if constexpr (S > 1) RK_PIPE_STEP(r1, kb + 1)
-    if constexpr (S > 2) RK_PIPE_STEP(r2, kb + 2)
-    if constexpr (S > 3) RK_PIPE_STEP(r3, kb + 3)
+    RK_M32_STEP(r0, kb)
+    if constexpr (S > 1) RK_M32_STEP(r1, kb + 1)
+    if constexpr (S > 2) RK_M32_STEP(r2, kb + 2)
+    if constexpr (S > 3) RK_M32_STEP(r3, kb + 3)
   }
-#undef RK_PIPE_STEP
+#undef RK_M32_STEP
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer
 
-  // Epilogue. Staging row pitch = BN * esize bytes, 16-byte chunks XOR-swizzled by
-  // (row & 15) so both the 8-byte fragment writes and the 16-byte row reads are
-  // conflict-free. fp32 output stages 64 rows per pass.
-  constexpr int ES = CDT == RK_BF16 ? 2 : 4;
-  constexpr int PITCH = BN * ES;
-  constexpr int CHUNKS = PITCH / 16;
-  constexpr int ROWS_PER_PASS = (TILE_BYTES / PITCH) >= BM ? BM : 64;
-  constexpr int PASSES = BM / ROWS_PER_PASS;
-  static_assert(ROWS_PER_PASS * PITCH <= TILE_BYTES, "staging tile does not fit");
-  float lsv[MI];
+  // Epilogue: (acc * ls) * rs -> bf16 into a [128][128] bf16 staging tile (32 KB) whose
+  // 8-byte units are XOR-swizzled by (row & 31) (conflict-free 32-row writes), then
+  // 16-byte coalesced copy-out (a lane re-orders the two 8-byte halves of its chunk
+  // when the row's swizzle flips unit parity). fp32 output widens the bf16 value.
+  constexpr int PITCH = BN * 2;       // bytes per staged row
+  constexpr int UNITS = PITCH / 8;    // 8-byte units per row (32)
+  const int r32 = lane & 31, hh = lane >> 5;
+  float lsv[2];
 #pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int64_t m = m0 + wm * 64 + i * 16 + r16;
-    lsv[i] = m < g.M ? g.ls[m] : 0.0f;
-  }
-  float rsv[NI][4];
+  for (int i = 0; i < 2; ++i) lsv[i] = g.ls[min(m0 + arow0 + i * 32 + r32, g.M - 1)];
 #pragma unroll
-  for (int j = 0; j < NI; ++j)
+  for (int j = 0; j < 2; ++j) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t n = n0 + wn * WN + j * 16 + 4 * g4 + r;
-      rsv[j][r] = g.rs ? (n < g.N ? g.rs[n] : 0.0f) : 1.0f;
-    }
-  const bool has_rs = g.rs != nullptr;
-
+    for (int q = 0; q < 4; ++q) {
+      const int col = brow0 + j * 32 + 8 * q + 4 * hh;  // first of 4 columns
+      float4 rs4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+      if constexpr (HAS_RS) rs4 = *reinterpret_cast<const float4*>(g.rs + min(n0 + col, g.N - 4));
 #pragma unroll
-  for (int pass = 0; pass < PASSES; ++pass) {
-    if (PASSES == 1 || wm == pass) {
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int row = (PASSES == 1 ? wm * 64 : 0) + i * 16 + r16;  // row in the staging tile
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int col = wn * WN + j * 16 + 4 * g4;  // first of 4 output columns
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = static_cast<float>(acc[i][j][r]) * lsv[i];
-            if (has_rs) t = t * rsv[j][r];
-            v[r] = t;
-          }
-          const int byte = col * ES;
-          const int chunk = (byte >> 4) ^ (row & 15);
-          uint8_t* dst = smem + row * PITCH + chunk * 16 + (byte & 15);
-          if constexpr (CDT == RK_BF16) {
-            uint2 pk;
-            pk.x = static_cast<uint32_t>(f32_to_bf16(v[0])) |
-                   (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-            pk.y = static_cast<uint32_t>(f32_to_bf16(v[2])) |
-                   (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-            *reinterpret_cast<uint2*>(dst) = pk;
-          } else {
-            *reinterpret_cast<float4*>(dst) =
-                make_float4(round_bf16(v[0]), round_bf16(v[1]), round_bf16(v[2]), round_bf16(v[3]));
-          }
+      for (int i = 0; i < 2; ++i) {
+        const int row = arow0 + i * 32 + r32;
+        float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
+        float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
+        float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
+        float v3 = static_cast<float>(acc[i][j][4 * q + 3]) * lsv[i];
+        if constexpr (HAS_RS) {
+          v0 = v0 * rs4.x;
+          v1 = v1 * rs4.y;
+          v2 = v2 * rs4.z;
+          v3 = v3 * rs4.w;
         }
+        const int unit = (col >> 2) ^ (row & 31);
+        *reinterpret_cast<uint2*>(smem + row * PITCH + unit * 8) =
+            make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
       }
     }
-    __syncthreads();
-    // Coalesced copy-out: each lane moves one 16-byte chunk.
-    constexpr int TOTAL = ROWS_PER_PASS * CHUNKS;
-    const int64_t row_base = m0 + (PASSES == 1 ? 0 : pass * 64);
-#pragma unroll
-    for (int c = tid; c < TOTAL; c += 256) {
-      const int row = c / CHUNKS, ch = c % CHUNKS;
-      const int64_t m = row_base + row;
-      const int64_t n = n0 + (ch * 16) / ES;
-      if (m < g.M && n < g.N) {
-        const uint4 val = *reinterpret_cast<const uint4*>(smem + row * PITCH +
-                                                           ((ch ^ (row & 15)) * 16));
-        char* out = static_cast<char*>(g.C) + (m * g.ldc + n) * ES;
-        *reinterpret_cast<uint4*>(out) = val;
-      }
-    }
-    if (PASSES > 1) __syncthreads();
   }
+  __syncthreads();
+  constexpr int CHUNKS = PITCH / 16;
+#pragma unroll
+  for (int c = tid; c < BM * CHUNKS; c += 256) {
+    const int row = c / CHUNKS, ch = c % CHUNKS;
+    const int64_t m = m0 + row;
+    const int64_t n = n0 + ch * 8;
+    if (m < g.M && n < g.N) {
+      const int u0 = (2 * ch) ^ (row & 31);  // staged unit of columns 8 ch .. 8 ch + 3
+      uint4 v = *reinterpret_cast<const uint4*>(smem + row * PITCH + (u0 & ~1) * 8);
+      if (u0 & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+      if constexpr (CDT == RK_BF16) {
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.C) + m * g.ldc + n) = v;
+      } else {
+        float* out = static_cast<float*>(g.C) + m * g.ldc + n;
+        *reinterpret_cast<uint4*>(out) = make_uint4(v.x << 16, v.x & 0xffff0000u,
+                                                    v.y << 16, v.y & 0xffff0000u);
+        *reinterpret_cast<uint4*>(out + 4) = make_uint4(v.z << 16, v.z & 0xffff0000u,
+                                                        v.w << 16, v.w & 0xffff0000u);
+      }
+    }
+  }
+  (void)UNITS;
+}
+
+template <int KIND, int CDT, bool HAS_RS>
+static void launch_m32(const GemmArgs& g, int stages, hipStream_t stream) {
+  const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(256);
+  if (stages == 3) int8_gemm_m32_kernel<KIND, CDT, 3, HAS_RS><<<grid, block, 0, stream>>>(g);
+  else if (stages == 4) int8_gemm_m32_kernel<KIND, CDT, 4, HAS_RS><<<grid, block, 0, stream>>>(g);
+  else int8_gemm_m32_kernel<KIND, CDT, 2, HAS_RS><<<grid, block, 0, stream>>>(g);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -489,27 +460,15 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const bool fast = (g.K % kBK) == 0 && (g.lda % 16) == 0 && (g.ldb % 16) == 0 &&
                     aligned16(g.A) && aligned16(g.B);
   const int es = CDT == RK_BF16 ? 2 : 4;
-  const bool aligned_out = fast && (g.N % 8) == 0 && ((g.ldc * es) % 16) == 0 && aligned16(g.C);
+  const bool aligned_out = fast && (g.N % 8) == 0 && ((g.ldc * es) % 16) == 0 &&
+                           aligned16(g.C) && (g.rs == nullptr || aligned16(g.rs));
   if (aligned_out) {
-    // Tuning knobs (every config gives identical results): RK_GEMM_BN (128 or 256),
-    // RK_GEMM_STAGES (register-ring depth, 2..4).
-    static const int bn_env = env_int("RK_GEMM_BN", 128);
-    static const int st_env = env_int("RK_GEMM_STAGES", 3);
-    const int stages = (st_env >= 2 && st_env <= 4) ? st_env : 3;
-    const int bn = (bn_env == 256 && CDT == RK_BF16) ? 256 : 128;
-    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + bn - 1) / bn);
-    const dim3 grid(static_cast<unsigned>(tiles)), block(256);
-    if (bn == 256) {
-      if constexpr (CDT == RK_BF16) {
-        if (stages == 2) int8_gemm_pipe_kernel<KIND, CDT, 256, 2><<<grid, block, 0, stream>>>(g);
-        else if (stages == 4) int8_gemm_pipe_kernel<KIND, CDT, 256, 4><<<grid, block, 0, stream>>>(g);
-        else int8_gemm_pipe_kernel<KIND, CDT, 256, 3><<<grid, block, 0, stream>>>(g);
-      }
-    } else {
-      if (stages == 2) int8_gemm_pipe_kernel<KIND, CDT, 128, 2><<<grid, block, 0, stream>>>(g);
-      else if (stages == 4) int8_gemm_pipe_kernel<KIND, CDT, 128, 4><<<grid, block, 0, stream>>>(g);
-      else int8_gemm_pipe_kernel<KIND, CDT, 128, 3><<<grid, block, 0, stream>>>(g);
-    }
+    // Register-ring depth (2..4); every setting gives identical results.
+    static const int st_env = env_int("RK_GEMM_STAGES", 2);
+    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+    if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
+    if (g.rs) launch_m32<KIND, CDT, true>(g, st_env, stream);
+    else launch_m32<KIND, CDT, false>(g, st_env, stream);
     return launch_status("int8_gemm");
   }
   const int64_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);

@@ -49,12 +49,13 @@ __device__ __forceinline__ int64_t src_offset(const QuantArgs& a, int64_t row, i
   }
 }
 
-// Loads the raw chunk starting at element e0 (V elements; zeros past K).
-template <int DT, int SRC>
+// Loads the raw chunk starting at element e0 (V elements; zeros past K). VEC: the
+// chunk is inside the row and 16-byte vector loads are legal.
+template <int DT, int SRC, bool VEC>
 __device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t row, int64_t e0,
                                            float* v) {
   constexpr int V = Vec<DT>::N;
-  if (a.vec_ok && e0 + V <= a.K) {
+  if (VEC || (a.vec_ok && e0 + V <= a.K)) {
     load_vec16<DT>(a.x, src_offset<DT, SRC>(a, row, e0), v);
   } else {
 #pragma unroll
@@ -97,31 +98,59 @@ __device__ __forceinline__ void store_bf16_chunk(uint16_t* dst, int64_t e0, int6
     if (e0 + i < K) dst[e0 + i] = f32_to_bf16(v[i]);
 }
 
-// Quantizes V transformed values y (row scale s) at columns e0.. and stores them.
-template <int DT, bool SR>
-__device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, int64_t row, int64_t e0,
-                                                  const float* y, float s, int8_t* qrow,
-                                                  bool vec_store) {
+// Margin of the reciprocal fast path (2^-12). With r = RN(1/s) and |x/s| <= 127.00002,
+// ya = RN(x * r) differs from x/s by at most |x/s| * 2^-23 < 2^-16, and the correctly
+// rounded quotient Y = RN(x / s) by at most 2^-16 + 2^-18 < 2^-15. For stochastic
+// rounding the sums RN(Y + u) and RN(ya + u) then differ by less than 2^-14 (each add
+// rounds by at most half an ulp of a value below 128). So whenever ya (or ya + u) lies
+// more than the margin away from a rounding boundary (a half-integer for rint, an
+// integer for floor), the fast result equals the one computed from Y; otherwise, and
+// for non-finite inputs, the lane takes the IEEE division x / s (int8_matmul.py:142,
+// div_rn) and rounds that.
+constexpr float kAmbiguity = 0.000244140625f;
+
+template <bool SR>
+__device__ __forceinline__ float round_quotient(float y, float s, float r, float u) {
+  const float ya = y * r;
+  if constexpr (SR) {
+    const float v = ya + u;
+    const float f = floorf(v);
+    const float d = v - f;
+    if (!(fabsf(ya) <= 128.0f) || d < kAmbiguity || d > 1.0f - kAmbiguity) {
+      return floorf(y / s + u);
+    }
+    return f;
+  } else {
+    const float t = __builtin_rintf(ya);
+    if (!(fabsf(ya) <= 128.0f) || fabsf(ya - t) > 0.5f - kAmbiguity) {
+      return __builtin_rintf(y / s);
+    }
+    return t;
+  }
+}
+
+// Quantizes V transformed values y (row scale s, r = 1/s) at columns e0.. and stores
+// them. ALL: every one of the V columns is inside the row (no per-element checks).
+template <int DT, bool SR, bool ALL>
+__device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, uint32_t ctr_row,
+                                                  const PhiloxKey& key, int64_t e0,
+                                                  const float* y, float s, float r,
+                                                  int8_t* qrow, bool vec_store) {
   constexpr int V = Vec<DT>::N;
   int8_t qv[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    const float t = y[i] / s;
-    float r;
+    float u = 0.0f;
     if constexpr (SR) {
-      const uint64_t ctr =
-          static_cast<uint64_t>(a.row_offset + row) * static_cast<uint64_t>(a.K) +
-          static_cast<uint64_t>(e0 + i);
-      const float u =
-          uniform_from_word(philox_word0(static_cast<uint32_t>(ctr), a.key0, a.key1));
-      r = floorf(t + u);
-    } else {
-      r = __builtin_rintf(t);
+      // counter = (row_offset + m) * K + k, wrapped to 32 bits like the int32 offsets
+      // of int8_matmul.py:143
+      u = uniform_from_word(philox_word0(ctr_row + static_cast<uint32_t>(e0 + i), key));
     }
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    qv[i] = static_cast<int8_t>(static_cast<int>(r));
+    float t = round_quotient<SR>(y[i], s, r, u);
+    t = fminf(fmaxf(t, -127.0f), 127.0f);
+    qv[i] = static_cast<int8_t>(static_cast<int>(t));
   }
-  if (vec_store && e0 + V <= a.K) {
+  if (vec_store && (ALL || e0 + V <= a.K)) {
     uint32_t w[V / 4];
 #pragma unroll
     for (int j = 0; j < V / 4; ++j)
@@ -139,7 +168,31 @@ __device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, int64_t ro
   }
 }
 
-template <int DT, int SRC, bool SR, int NC>
+// Transformed values of one chunk (VEC: the whole chunk is inside the row and the
+// per-column scale, if any, is 16-byte aligned).
+template <int DT, int SRC, bool VEC>
+__device__ __forceinline__ void transform_chunk(const QuantArgs& a, int64_t e0, float* v,
+                                                float row_factor) {
+  constexpr int V = Vec<DT>::N;
+  if constexpr (VEC && SRC == SRC_PLAIN) {
+    if (a.col_scale) {
+#pragma unroll
+      for (int j = 0; j < V / 4; ++j) {
+        const float4 cs = *reinterpret_cast<const float4*>(a.col_scale + e0 + 4 * j);
+        v[4 * j] = v[4 * j] * cs.x;
+        v[4 * j + 1] = v[4 * j + 1] * cs.y;
+        v[4 * j + 2] = v[4 * j + 2] * cs.z;
+        v[4 * j + 3] = v[4 * j + 3] * cs.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      v[i] = (VEC || e0 + i < a.K) ? transform<SRC>(a, v[i], e0 + i, row_factor) : 0.0f;
+  }
+}
+
+template <int DT, int SRC, bool SR, int NC, bool VEC>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
   constexpr int V = Vec<DT>::N;
   constexpr int SPAN = kWave * V;
@@ -151,15 +204,20 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
   int8_t* qrow = a.q + row * a.ldq;
   const bool vec_store = (a.ldq % V) == 0 && ((reinterpret_cast<uintptr_t>(a.q) % V) == 0);
   uint16_t* xbrow = (SRC == SRC_PLAIN && a.xb) ? a.xb + row * a.ldxb : nullptr;
+  PhiloxKey key{};
+  if constexpr (SR) key = philox_key(a.key0, a.key1);
+  const uint32_t ctr_row =
+      static_cast<uint32_t>(a.row_offset + row) * static_cast<uint32_t>(a.K);
 
   if constexpr (NC > 0) {
     // Register-resident row: one HBM read.
     float xr[NC][V];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      if (c < nchunks) {
-        load_chunk<DT, SRC>(a, row, c * SPAN + lane0, xr[c]);
-        if (xbrow && c * SPAN + lane0 < a.K) store_bf16_chunk<DT>(xbrow, c * SPAN + lane0, a.K, xr[c]);
+      const int64_t e0 = c * SPAN + lane0;
+      if (c < nchunks && (!VEC || e0 < a.K)) {
+        load_chunk<DT, SRC, VEC>(a, row, e0, xr[c]);
+        if (xbrow && e0 < a.K) store_bf16_chunk<DT>(xbrow, e0, a.K, xr[c]);
       } else {
 #pragma unroll
         for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
@@ -178,22 +236,22 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
+      const int64_t e0 = c * SPAN + lane0;
+      if (c < nchunks && e0 < a.K) {
+        transform_chunk<DT, SRC, VEC>(a, e0, xr[c], row_factor);
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const int64_t e = c * SPAN + lane0 + i;
-        if (e < a.K) {
-          xr[c][i] = transform<SRC>(a, xr[c][i], e, row_factor);
-          amax = fmaxf(amax, fabsf(xr[c][i]));
-        }
+        for (int i = 0; i < V; ++i) amax = fmaxf(amax, fabsf(xr[c][i]));
       }
     }
     amax = wave_max(amax);
     const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
+    const float r = 1.0f / s;
     if (lane == 0) a.scale[row] = s;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t e0 = c * SPAN + lane0;
-      if (c < nchunks && e0 < a.K) quant_store_chunk<DT, SR>(a, row, e0, xr[c], s, qrow, vec_store);
+      if (c < nchunks && e0 < a.K)
+        quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, xr[c], s, r, qrow, vec_store);
     }
   } else {
     // Streaming row: re-read per pass (the row stays cache-resident).
@@ -202,7 +260,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
       float acc = 0.0f;
       for (int64_t c = 0; c < nchunks; ++c) {
         float v[V];
-        load_chunk<DT, SRC>(a, row, c * SPAN + lane0, v);
+        load_chunk<DT, SRC, VEC>(a, row, c * SPAN + lane0, v);
 #pragma unroll
         for (int i = 0; i < V; ++i) acc = acc + v[i] * v[i];
       }
@@ -212,26 +270,35 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     float amax = 0.0f;
     for (int64_t c = 0; c < nchunks; ++c) {
       const int64_t e0 = c * SPAN + lane0;
+      if (e0 >= a.K) break;
       float v[V];
-      load_chunk<DT, SRC>(a, row, e0, v);
+      load_chunk<DT, SRC, VEC>(a, row, e0, v);
+      transform_chunk<DT, SRC, VEC>(a, e0, v, row_factor);
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        if (e0 + i < a.K) amax = fmaxf(amax, fabsf(transform<SRC>(a, v[i], e0 + i, row_factor)));
+      for (int i = 0; i < V; ++i) amax = fmaxf(amax, fabsf(v[i]));
     }
     amax = wave_max(amax);
     const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
+    const float r = 1.0f / s;
     if (lane == 0) a.scale[row] = s;
     for (int64_t c = 0; c < nchunks; ++c) {
       const int64_t e0 = c * SPAN + lane0;
       if (e0 >= a.K) break;
-      float v[V], y[V];
-      load_chunk<DT, SRC>(a, row, e0, v);
+      float v[V];
+      load_chunk<DT, SRC, VEC>(a, row, e0, v);
       if (xbrow) store_bf16_chunk<DT>(xbrow, e0, a.K, v);
-#pragma unroll
-      for (int i = 0; i < V; ++i)
-        y[i] = (e0 + i < a.K) ? transform<SRC>(a, v[i], e0 + i, row_factor) : 0.0f;
-      quant_store_chunk<DT, SR>(a, row, e0, y, s, qrow, vec_store);
+      transform_chunk<DT, SRC, VEC>(a, e0, v, row_factor);
+      quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, v, s, r, qrow, vec_store);
     }
+  }
+}
+
+template <int DT, int SRC, bool SR, int NC>
+static void launch_quant_nc(const QuantArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  if (a.vec_ok) {
+    quant_rows_kernel<DT, SRC, SR, NC, true><<<grid, block, 0, stream>>>(a);
+  } else {
+    quant_rows_kernel<DT, SRC, SR, NC, false><<<grid, block, 0, stream>>>(a);
   }
 }
 
@@ -242,15 +309,15 @@ static int launch_quant(const QuantArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((a.M + 3) / 4));
   const dim3 block(256);
   if (nchunks <= 1) {
-    quant_rows_kernel<DT, SRC, SR, 1><<<grid, block, 0, stream>>>(a);
+    launch_quant_nc<DT, SRC, SR, 1>(a, grid, block, stream);
   } else if (nchunks <= 2) {
-    quant_rows_kernel<DT, SRC, SR, 2><<<grid, block, 0, stream>>>(a);
+    launch_quant_nc<DT, SRC, SR, 2>(a, grid, block, stream);
   } else if (nchunks <= 4) {
-    quant_rows_kernel<DT, SRC, SR, 4><<<grid, block, 0, stream>>>(a);
+    launch_quant_nc<DT, SRC, SR, 4>(a, grid, block, stream);
   } else if (nchunks <= kMaxChunks) {
-    quant_rows_kernel<DT, SRC, SR, kMaxChunks><<<grid, block, 0, stream>>>(a);
+    launch_quant_nc<DT, SRC, SR, kMaxChunks>(a, grid, block, stream);
   } else {
-    quant_rows_kernel<DT, SRC, SR, 0><<<grid, block, 0, stream>>>(a);
+    launch_quant_nc<DT, SRC, SR, 0>(a, grid, block, stream);
   }
   return launch_status("quantize_rows");
 }
@@ -303,7 +370,7 @@ extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K
   a.scale = scale;
   a.xb = x_bf16;
   a.ldxb = ld_xb;
-  a.vec_ok = rows_vec_ok(x, x_dtype, K, sxm, sxk) ? 1 : 0;
+  a.vec_ok = (rows_vec_ok(x, x_dtype, K, sxm, sxk) && (!col_scale || aligned16(col_scale))) ? 1 : 0;
   if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(x_dtype, a, as_stream(stream));
   return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
 }
@@ -377,4 +444,32 @@ extern "C" int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int6
                  ? 1
                  : 0;
   return dispatch_dtype<SRC_TRANSPOSE, false>(x_dtype, a, as_stream(stream));
+}
+
+namespace rk {
+
+__global__ __launch_bounds__(256) void philox_word0_kernel(uint32_t key0, uint32_t key1,
+                                                           uint32_t counter0, int64_t n,
+                                                           uint32_t* out) {
+  const PhiloxKey key = philox_key(key0, key1);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    out[i] = philox_word0(counter0 + static_cast<uint32_t>(i), key);
+  }
+}
+
+}  // namespace rk
+
+extern "C" int rk_philox_word0(uint64_t seed, uint32_t counter0, int64_t n, uint32_t* out,
+                               void* stream) {
+  clear_error();
+  if (n < 0) return fail(RK_ERR_ARG, "negative count");
+  if (n == 0) return RK_OK;
+  if (!out) return fail(RK_ERR_ARG, "null output");
+  const int64_t blocks = (n + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(blocks < 8192 ? blocks : 8192);
+  philox_word0_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+      static_cast<uint32_t>(seed & 0xffffffffu), static_cast<uint32_t>(seed >> 32), counter0, n,
+      out);
+  return launch_status("philox_word0");
 }

@@ -29,6 +29,7 @@ _p = ctypes.c_void_p
 SIGNATURES: dict[str, list] = {
     "rk_quantize_rows": [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _u64, _i64, _p, _i64, _p,
                          _p, _i64, _p],
+    "rk_philox_word0": [_u64, ctypes.c_uint32, _i64, _p, _p],
     "rk_int8_gemm_nt": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p],
     "rk_int8_gemm_packed": [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i64, _i64, _i64, _i64,
                             _p],

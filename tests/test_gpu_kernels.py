@@ -99,6 +99,70 @@ def test_stochastic_rounding_bit_exact_given_seed(cuda, shape, dtype):
         assert np.array_equal(f32bits(s), f32bits(s_ref))
 
 
+def philox_words(cuda, seed: int, counter0: int, n: int) -> np.ndarray:
+    out = torch.empty(n, dtype=torch.int32, device=cuda)
+    nat.call("rk_philox_word0", seed, counter0, n, out.data_ptr(), nat.stream_handle(cuda))
+    return out.cpu().numpy().view(np.uint32)
+
+
+def test_philox_words_match_random123_kat_and_oracle(cuda, golden):
+    # Random123 KAT: counter 0, key 0 -> first word 6627e8d5 (the only published vector
+    # whose counter has the (x, 0, 0, 0) form the stochastic rounding uses).
+    kat = golden["philox4x32_10"]["vectors"][0]
+    assert kat["ctr"] == ["00000000"] * 4 and kat["key"] == ["00000000"] * 2
+    assert philox_words(cuda, 0, 0, 1)[0] == int(kat["out"][0], 16)
+    from oracle import philox as ophilox
+    for seed, c0, n in ((0, 0, 4096), (1234567, 17, 100_003), (2**31 - 2, 2**32 - 5000, 10_000),
+                        ((7 << 32) | 99, 123, 50_000)):
+        got = philox_words(cuda, seed, c0, n)
+        offsets = (np.arange(n, dtype=np.uint64) + np.uint64(c0)) & np.uint64(0xFFFFFFFF)
+        ref = ophilox.randint(seed, offsets.astype(np.uint32))
+        assert np.array_equal(got, ref), f"seed {seed} counter0 {c0}"
+
+
+def near_boundary_rows(rows: int, cols: int, seed: int, sr_seed: int | None):
+    """Rows whose quotients x / s sit on or within a few ulps of the rounding boundaries
+    (half-integers for rint; for SR, the integers minus the element's own uniform u), so
+    the kernels' reciprocal fast path must defer to the IEEE division."""
+    from oracle import philox as ophilox
+    rng = np.random.default_rng(seed)
+    amax = rng.uniform(0.5, 3.0, size=rows).astype(np.float32)
+    s = np.maximum(amax / np.float32(127.0), np.float32(np.finfo(np.float32).tiny))
+    k = rng.integers(-126, 126, size=(rows, cols)).astype(np.float32)
+    if sr_seed is None:
+        target = k + np.float32(0.5)
+    else:
+        u = ophilox.rand(sr_seed, ophilox.sr_offsets(rows, cols)).reshape(rows, cols)
+        target = k - u
+    x = (target * s[:, None]).astype(np.float32)
+    ulps = rng.integers(-3, 4, size=(rows, cols)).astype(np.int32)
+    x = (x.view(np.int32) + ulps).view(np.float32)
+    x[:, 0] = amax  # pins the row absmax, so s is exactly amax / 127
+    x[:, 1] = -amax
+    return np.clip(x, -amax[:, None], amax[:, None])
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 512), (5, 2048), (33, 40)])
+def test_quantize_rows_near_half_integer_quotients(cuda, rows, cols):
+    x = near_boundary_rows(rows, cols, 3, None)
+    q, s = quantize_rows(torch.from_numpy(x).to(cuda))
+    q_ref, s_ref = oquant.quantize_rows(x)
+    assert np.array_equal(f32bits(s), f32bits(s_ref))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 512), (5, 2048), (33, 40)])
+def test_stochastic_rounding_near_integer_sums(cuda, rows, cols):
+    seed = 4242
+    x = near_boundary_rows(rows, cols, 5, seed)
+    q = torch.empty(rows, cols, dtype=torch.int8, device=cuda)
+    s = torch.empty(rows, dtype=torch.float32, device=cuda)
+    quantize_rows_into(torch.from_numpy(x).to(cuda), q, s, stochastic=True, seed=seed)
+    q_ref, s_ref = oquant.quantize_rows_sr(x, None, seed)
+    assert np.array_equal(f32bits(s), f32bits(s_ref))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
 def test_public_sr_draws_its_seed_from_the_cpu_generator(cuda):
     # int8_matmul.py:200: one torch.randint draw per stochastic call.
     g = torch.randn(16, 96, generator=gen(41))
@@ -151,8 +215,12 @@ def test_quantize_columns_matches_transposed_rows(cuda):
 # ---------------------------------------------------------------------------
 # int8 GEMM
 # ---------------------------------------------------------------------------
+# Covers the generic kernel (ragged K or N), the ping-pong kernel (K = 64) and the
+# persistent cross-tile kernel (K % 128 == 0, N % 8 == 0): ragged last row/column tiles,
+# several tiles per block, and the fewest k-steps it accepts (K = 128).
 GEMM_SHAPES = [(67, 35, 53), (48, 40, 53), (1, 64, 1), (128, 128, 64), (130, 200, 129),
-               (256, 384, 512), (1000, 1536, 512)]
+               (256, 384, 512), (1000, 1536, 512), (300, 200, 256), (129, 8, 128),
+               (2500, 1032, 1024), (1, 16, 128)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
