@@ -57,6 +57,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the eager autograd step instead of its HIP-graph replay")
     return ap.parse_args()
 
 
@@ -94,15 +96,36 @@ def op_bench(args, device):
         x.grad = None
         layer.ratchet_update(validate=False)
 
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
+    eager_s = timed(step, args.steps)
+    if args.no_graph:
+        return eager_s, eager_s, layer, x.detach(), g
+    # The whole step (quant, forward, backward, fused update) captured once into a HIP
+    # graph and replayed: every replay launches the same kernels on the same buffers, so
+    # the host-side autograd and launch overhead of the eager step disappears. The SR
+    # seed drawn on the host at capture time is part of the graph (same work per step).
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
         step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    return elapsed / args.steps, layer, x.detach(), g
+    for _ in range(args.warmup):
+        graph.replay()
+    graph_s = timed(graph.replay, args.steps)
+    return graph_s, eager_s, layer, x.detach(), g
 
 
 def kernel_breakdown(layer, x, g, iters: int):
@@ -111,11 +134,11 @@ def kernel_breakdown(layer, x, g, iters: int):
 
     from local_ai_training import _native as nat
     from local_ai_training.int8_matmul import (
-        dequant_transpose_bf16,
+        grad_weight_bf16,
+        grad_weight_splits,
         int8_mm_nt,
         packed_int8_mm,
         quantize_rows_into,
-        transpose_bf16,
         unpack_transpose,
     )
 
@@ -130,6 +153,8 @@ def kernel_breakdown(layer, x, g, iters: int):
     gs = torch.empty(m, dtype=torch.float32, device=dev)
     gin = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
     gw = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+    splits = grad_weight_splits(m, n, k)
+    gw_work = torch.empty(splits, n, k, dtype=torch.float32, device=dev)
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
     row_rms = torch.empty(n, dtype=torch.float32, device=dev)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -148,9 +173,7 @@ def kernel_breakdown(layer, x, g, iters: int):
         ("unpack_transpose", lambda: holder.__setitem__("ct", unpack_transpose(packed,
                                                                                MAX_CODE))),
         ("grad_input_gemm", lambda: int8_mm_nt(gq, holder["ct"], gs, None, out=gin)),
-        ("transpose_grad_bf16", lambda: holder.__setitem__("gt", transpose_bf16(g))),
-        ("dequant_transpose_bf16", lambda: holder.__setitem__("xt", dequant_transpose_bf16(q, s))),
-        ("grad_weight_gemm_blas", lambda: torch.mm(holder["gt"], holder["xt"].t(), out=gw)),
+        ("grad_weight_bf16", lambda: grad_weight_bf16(g, q, s, splits, out=gw, work=gw_work)),
         ("ratchet_update_grad", update),
     ]
     for _, fn in stages:  # warm
@@ -175,9 +198,8 @@ def kernel_breakdown(layer, x, g, iters: int):
         "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
         "unpack_transpose": ("bytes", 2 * n * k),
         "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
-        "transpose_grad_bf16": ("bytes", m * n * g.element_size() + m * n * 2),
-        "dequant_transpose_bf16": ("bytes", m * k + m * 4 + m * k * 2),
-        "grad_weight_gemm_blas": ("flops", mnk2, m * n * 2 + m * k * 2 + n * k * 2),
+        "grad_weight_bf16": ("flops", mnk2, m * n * g.element_size() + m * k + m * 4
+                             + n * k * 2),
         "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
     }
     report = {}
@@ -310,10 +332,11 @@ def main() -> int:
         return 1
     device = torch.device("cuda:0")
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
-    step_s, layer, x, g = op_bench(args, device)
+    step_s, eager_s, layer, x, g = op_bench(args, device)
     ops = 3 * 2.0 * M_TOK * N_OUT * K_IN
     tops = ops / step_s / 1e12
-    log(f"op step {step_s * 1e3:.3f} ms -> {tops:.1f} TOPS")
+    log(f"op step {step_s * 1e3:.3f} ms -> {tops:.1f} TOPS (eager autograd step "
+        f"{eager_s * 1e3:.3f} ms)")
     kernels = kernel_breakdown(layer, x, g, args.kernel_iters)
     for name, e in kernels.items():
         log(f"  {name}: {e}")
@@ -325,6 +348,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_s * 1e3, 4),
+        "eager_ms_per_step": round(eager_s * 1e3, 4),
+        "step_mode": "eager" if args.no_graph else "hip_graph",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -145,6 +145,25 @@ int rk_dequant_transpose_bf16(const int8_t* q, int64_t ldq, const float* scale, 
                               int64_t ldt, int64_t M, int64_t K, void* stream);
 
 /*
+ * BF16 weight gradient from the saved int8 activations, without transposed copies:
+ *   Gw[n, k] = bf16( sum_m bf16(g[m, n]) * bf16(bf16(q[m, k]) * bf16(s[m])) )
+ *   g  [M, N] float32 or bfloat16 (row stride ldg), q [M, K] int8 (row stride ldq),
+ *   s  [M] float32, out [N, K] bf16 (row stride ldo).
+ * The token axis is split into nsplit ranges (rk_grad_weight_splits gives the default);
+ * workspace is float32 [nsplit, N, K] (caller-allocated, fully overwritten). Partial
+ * sums are added in split order, so the result is reproducible. Requires N % 8 == 0,
+ * K % 16 == 0 and 16-byte aligned rows (RK_ERR_UNSUPPORTED otherwise).
+ * Replaces: grad_weight_tile = grad_out_tile.to(bf16) @ inputs_bf16 over the 256-row
+ *           tiles of ratchet.py:148-163, with inputs_bf16 from ratchet.py:71-76.
+ */
+int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, const int8_t* q, int64_t ldq,
+                        const float* s, int64_t M, int64_t N, int64_t K, float* workspace,
+                        int nsplit, uint16_t* out, int64_t ldo, void* stream);
+
+/* Default token-range split count of rk_grad_weight_bf16 for an [M] x [N, K] problem. */
+int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K);
+
+/*
  * Fused integer ratchet update on a normalized gradient z (float32 [rows, K], row
  * stride ldz). packed [rows, K] (row stride ldp) is updated in place. counts[4]
  * (int64) are INCREMENTED by (positive moves, negative moves, blocked positive,

@@ -39,6 +39,9 @@ SIGNATURES: dict[str, list] = {
     "rk_dequant_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_transpose_bf16": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p],
     "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
+    "rk_grad_weight_bf16": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i32, _p,
+                            _i64, _p],
+    "rk_grad_weight_splits": [_i64, _i64, _i64],
     "rk_ratchet_update": [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _f32, _f32, _p, _p],
     "rk_ratchet_update_grad": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i32, _i32, _f32, _f32,
                                _f32, _p, _f32, _f32, _p, _p, _p, _p, _p],
@@ -91,7 +94,15 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
+    """Raw handle of the caller's current stream on ``device`` (a capture stream inside
+    CUDA-graph capture, so launches through the library are captured too)."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

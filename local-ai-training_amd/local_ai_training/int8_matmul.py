@@ -210,3 +210,34 @@ def dequant_transpose_bf16(q: Tensor, s: Tensor) -> Tensor:
     nat.call("rk_dequant_transpose_bf16", q.data_ptr(), _ld(q), s.data_ptr(), out.data_ptr(),
              _ld(out), m, k, nat.stream_handle(q.device))
     return out
+
+
+def grad_weight_splits(m: int, n: int, k: int) -> int:
+    """Token-range split count rk_grad_weight_bf16 uses by default."""
+    return int(nat.load_library().rk_grad_weight_splits(m, n, k))
+
+
+def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = None, *,
+                     out: Tensor | None = None, work: Tensor | None = None) -> Tensor:
+    """Gw = bf16(bf16(grad)^T @ bf16(bf16(q) * bf16(s)[:, None])) as [N, K] bf16.
+
+    The BF16 weight gradient of ratchet.py:148-163 computed straight from the saved int8
+    activations (q [M, K], s [M]) and the upstream gradient grad [M, N] (float32 or
+    bfloat16), with no transposed copies. ``work`` (float32 [nsplit, N, K]) and ``out``
+    may be passed preallocated.
+    """
+    m, n = grad.shape
+    k = q.shape[1]
+    if grad.stride(-1) != 1:
+        grad = grad.contiguous()
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
+    if work is None:
+        work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
+    if out is None:
+        out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
+    nat.call("rk_grad_weight_bf16", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
+             q.data_ptr(), _ld(q), s.contiguous().data_ptr(), m, n, k, work.data_ptr(), splits,
+             out.data_ptr(), _ld(out), nat.stream_handle(grad.device))
+    return out

@@ -38,6 +38,7 @@ from .int8_matmul import (
     dequant_bf16,
     dequant_transpose_bf16,
     effective_bf16,
+    grad_weight_bf16,
     int8_mm_nt,
     packed_int8_mm,
     quantize_rows_into,
@@ -131,6 +132,14 @@ class RatchetAuditReport:
     ratchet_state_bytes: int
     support_parameter_bytes: int
     violations: tuple[str, ...]
+
+
+def _grad_weight_supported(g: Tensor, q: Tensor) -> bool:
+    """Shapes the direct int8-activation grad_weight kernel takes (rk_grad_weight_bf16)."""
+    n, k = g.shape[1], q.shape[1]
+    return (n % 8 == 0 and k % 16 == 0 and g.stride(-1) == 1 and q.stride(-1) == 1
+            and (g.stride(0) * g.element_size()) % 16 == 0 and q.stride(0) % 16 == 0
+            and g.data_ptr() % 16 == 0 and q.data_ptr() % 16 == 0)
 
 
 # ---------------------------------------------------------------------------
@@ -256,16 +265,20 @@ class _RatchetMatmul(torch.autograd.Function):
         if mode == "fp32":
             grad_weight = gradient_fp32.t() @ inputs_fp32
         else:
-            # BF16 grad_weight [N, K] = bf16(g)^T @ bf16(x) (ratchet.py:159-163), run as an
-            # NT GEMM on transposed bf16 copies (both operands contiguous along tokens).
+            # BF16 grad_weight [N, K] = bf16(g)^T @ bf16(x) (ratchet.py:159-163).
             g = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
                 else flat_gradient.float()
-            grad_t = transpose_bf16(g)
-            if ctx.used_fused_int8:
-                inputs_t = dequant_transpose_bf16(q, s)
+            if ctx.used_fused_int8 and _grad_weight_supported(g, q):
+                # straight from the saved int8 activations, no transposed copies
+                grad_weight = grad_weight_bf16(g, q, s)
             else:
-                inputs_t = transpose_bf16(inputs_bf16)
-            grad_weight = grad_t @ inputs_t.t()
+                # NT GEMM on transposed bf16 copies (both operands contiguous along tokens)
+                grad_t = transpose_bf16(g)
+                if ctx.used_fused_int8:
+                    inputs_t = dequant_transpose_bf16(q, s)
+                else:
+                    inputs_t = transpose_bf16(inputs_bf16)
+                grad_weight = grad_t @ inputs_t.t()
         grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
             grad_scale, None

@@ -18,6 +18,7 @@ from local_ai_training.int8_matmul import (
     dequant_bf16,
     dequant_transpose_bf16,
     effective_bf16,
+    grad_weight_bf16,
     int8_mm_nt,
     packed_int8_mm,
     quantize_columns,
@@ -31,7 +32,7 @@ from local_ai_training.int8_matmul import (
 from oracle import gemm as ogemm
 from oracle import quant as oquant
 from oracle import update as oupd
-from oracle.numerics import f32_to_bf16_bits
+from oracle.numerics import f32_to_bf16_bits, round_to_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -457,3 +458,58 @@ def test_unpack_leak_and_validate(cuda):
     nat.call("rk_validate_state", bad.data_ptr(), 2, 3, scale.data_ptr(), 2, flags.data_ptr(),
              nat.stream_handle(bad.device))
     assert flags.cpu().tolist() == [1, 0, 1]
+
+
+# ---------------------------------------------------------------------------
+# BF16 grad_weight from int8 activations (TN product, no transposed copies)
+# ---------------------------------------------------------------------------
+def _xhat(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """bf16(bf16(q) * bf16(s)[:, None]) as float32 (ratchet.py:73-75)."""
+    return round_to_bf16(q.astype(np.float32) * round_to_bf16(s.astype(np.float32))[:, None])
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("m,n,k", [(4096, 256, 128), (1000, 136, 48), (16384, 2048, 512),
+                                   (31, 8, 16)])
+def test_grad_weight_bit_exact_when_every_sum_is_exact(cuda, m, n, k, gdtype):
+    # g = small integers * 2^-4, q integers, s = 2^-7: every product and every partial sum
+    # is exactly representable in fp32, so the result is order-free and must equal the
+    # bf16 rounding of the exact float64 sum bit for bit (pins indexing and layouts).
+    rng = np.random.default_rng(m + n + k)
+    g = (rng.integers(-8, 9, size=(m, n)) / 16.0).astype(np.float32)
+    q = rng.integers(-127, 128, size=(m, k)).astype(np.int8)
+    s = np.full(m, 2.0**-7, np.float32)
+    gd = torch.from_numpy(g).to(cuda).to(gdtype)
+    out = grad_weight_bf16(gd, torch.from_numpy(q).to(cuda), torch.from_numpy(s).to(cuda))
+    exact = g.astype(np.float64).T @ _xhat(q, s).astype(np.float64)
+    assert np.array_equal(bits16(out), f32_to_bf16_bits(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_grad_weight_op_shape_within_tolerance_and_deterministic(cuda, gdtype):
+    # Op shape: M=16384 tokens, N=2048, K=512; gradient N(0, 1e-2), activations N(0, 1)
+    # quantized per token. Tolerance rel 1e-2 / abs 1e-3 against an fp32 product of the
+    # same bf16 operands.
+    m, n, k = 16384, 2048, 512
+    g = (torch.randn(m, n, generator=gen(61)) * 1e-2).to(gdtype)
+    x = torch.randn(m, k, generator=gen(62))
+    q, s = quantize_rows(x.to(cuda))
+    gd = g.to(cuda)
+    out = grad_weight_bf16(gd, q, s)
+    ref = gd.to(torch.bfloat16).float().t() @ torch.from_numpy(
+        _xhat(q.cpu().numpy(), s.cpu().numpy())).to(cuda)
+    err = (out.float() - ref).abs()
+    assert bool((err <= 1e-3 + 1e-2 * ref.abs()).all()), float(err.max())
+    again = grad_weight_bf16(gd, q, s)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    # the split count changes the summation grouping only within the tolerance
+    one = grad_weight_bf16(gd, q, s, nsplit=1)
+    assert bool(((one.float() - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
+
+
+def test_grad_weight_rejects_unaligned_shapes(cuda):
+    g = torch.randn(64, 12, device=cuda)
+    q = torch.zeros(64, 16, dtype=torch.int8, device=cuda)
+    s = torch.ones(64, device=cuda)
+    with pytest.raises(nat.NativeError, match="N % 8 == 0"):
+        grad_weight_bf16(g, q, s)

@@ -313,13 +313,15 @@ def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
     packed_ref = layer.packed.cpu().numpy().copy()
     scale = layer.scale.float().cpu().numpy()
     captured = {}
-    original = layer._fused_update
+    original = layer._launch_update
 
-    def capture(grad_weight, *, want_grad_scale):
-        captured["gw"] = grad_weight.detach().clone()
-        return original(grad_weight, want_grad_scale=want_grad_scale)
+    def capture(gradient, counts, row_rms, grad_scale, nonfinite):
+        # the weight gradient the update consumes (the one float producer shared with
+        # the oracle); runs on whichever stream the update is enqueued on
+        captured["gw"] = gradient.detach().clone()
+        return original(gradient, counts, row_rms, grad_scale, nonfinite)
 
-    layer._fused_update = capture
+    layer._launch_update = capture
     data = torch.Generator().manual_seed(99)
     for step in range(100):
         x = torch.randn(m, k, generator=data).to(torch.bfloat16)
