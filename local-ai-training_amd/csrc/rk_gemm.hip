@@ -308,11 +308,8 @@ __device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j][kh], fa[i][kh], acc[i][j], 0, 0, 0);
 }
 
-#ifndef RK_M32_WAVES
-#define RK_M32_WAVES 2
-#endif
 template <int KIND, int CDT, int S, bool HAS_RS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RK_M32_WAVES, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void int8_gemm_m32_kernel(GemmArgs g) {
   constexpr int BM = 128, BN = 128, BK = 64;
   constexpr int A_SEGS = BM * BK / 16 / 256;

@@ -72,11 +72,8 @@ __device__ __forceinline__ v8bf gw_fragment(const uint8_t* tile, int tok0, int c
   return f;
 }
 
-#ifndef RK_GW_WAVES
-#define RK_GW_WAVES 2
-#endif
 template <int GDT, int S>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(RK_GW_WAVES, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void grad_weight_partial_kernel(GwArgs a) {
   constexpr int GV = GDT == RK_F32 ? 4 : 2;  // 16-byte g loads per thread per step
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * GW_TILE];
@@ -284,18 +281,21 @@ extern "C" int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, cons
   const int64_t blocks = tiles * nsplit;
   if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
   hipStream_t st = as_stream(stream);
+  // Ring depth: 4 steps for a bf16 gradient, 2 for float32 (its wider staging would
+  // drop the kernel to one wave per SIMD at depth 4). RK_GW_RING overrides (2, 4, 6).
   static const int ring_env = [] {
     const char* v = getenv("RK_GW_RING");
-    return v ? atoi(v) : 4;
+    return v ? atoi(v) : 0;
   }();
+  const int ring = ring_env ? ring_env : (g_dtype == RK_F32 ? 2 : 4);
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
   if (g_dtype == RK_F32) {
-    if (ring_env == 2) grad_weight_partial_kernel<RK_F32, 2><<<grid, block, 0, st>>>(a);
-    else if (ring_env == 6) grad_weight_partial_kernel<RK_F32, 6><<<grid, block, 0, st>>>(a);
-    else grad_weight_partial_kernel<RK_F32, 4><<<grid, block, 0, st>>>(a);
+    if (ring == 4) grad_weight_partial_kernel<RK_F32, 4><<<grid, block, 0, st>>>(a);
+    else if (ring == 6) grad_weight_partial_kernel<RK_F32, 6><<<grid, block, 0, st>>>(a);
+    else grad_weight_partial_kernel<RK_F32, 2><<<grid, block, 0, st>>>(a);
   } else {
-    if (ring_env == 2) grad_weight_partial_kernel<RK_BF16, 2><<<grid, block, 0, st>>>(a);
-    else if (ring_env == 6) grad_weight_partial_kernel<RK_BF16, 6><<<grid, block, 0, st>>>(a);
+    if (ring == 2) grad_weight_partial_kernel<RK_BF16, 2><<<grid, block, 0, st>>>(a);
+    else if (ring == 6) grad_weight_partial_kernel<RK_BF16, 6><<<grid, block, 0, st>>>(a);
     else grad_weight_partial_kernel<RK_BF16, 4><<<grid, block, 0, st>>>(a);
   }
   if (int e = launch_status("grad_weight_partial")) return e;
