@@ -160,6 +160,19 @@ int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, const int8_t* q
                         const float* s, int64_t M, int64_t N, int64_t K, float* workspace,
                         int nsplit, uint16_t* out, int64_t ldo, void* stream);
 
+/*
+ * The same BF16 weight gradient with the activation operand given directly:
+ *   Gw[n, k] = bf16( sum_m bf16(g[m, n]) * bf16(x[m, k]) )
+ *   x  [M, K] float32 or bfloat16 (x_dtype, row stride ldx); other arguments and
+ *   requirements as rk_grad_weight_bf16.
+ * Replaces: grad_out_tile.to(bf16) @ flat_inputs.to(bf16)  ratchet.py:159-163 (and the
+ *           non-fused bf16 grad_weight, ratchet.py:95-106), with x the dequantized
+ *           activations (rk_dequant_bf16) or the layer inputs.
+ */
+int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x, int x_dtype,
+                          int64_t ldx, int64_t M, int64_t N, int64_t K, float* workspace,
+                          int nsplit, uint16_t* out, int64_t ldo, void* stream);
+
 /* Default token-range split count of rk_grad_weight_bf16 for an [M] x [N, K] problem. */
 int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K);
 
@@ -251,6 +264,36 @@ int rk_gelu_quantize(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t
 int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
                           int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t sd,
                           int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * Backward of the RMSNorm prologue, per row of x [M, K] and grad_y [M, K]:
+ *   rsqrt = 1 / sqrt(sum(x^2) / K + eps);  dvar = sum(grad_y * w * x) * -0.5 * rsqrt^3
+ *   grad_x = bf16(grad_y * w * rsqrt + dvar * 2 * x / K)   (stored in x_dtype)
+ *   grad_w[k] = sum over rows of grad_y * x * rsqrt         (float32)
+ * grad_w is summed in a fixed order (per-block partials in `workspace`, then a
+ * reduction in block order), so it is identical run to run. `workspace` holds at
+ * least rk_rmsnorm_backward_parts(M) * K floats. K <= 4096 (RK_ERR_UNSUPPORTED
+ * otherwise); grad_x has row stride ldgx and the dtype of x.
+ * Replaces: rmsnorm_backward  int8_backward.py:7-51.
+ */
+int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
+                        int x_dtype, int64_t ldx, const float* w, float eps, int64_t M,
+                        int64_t K, void* grad_x, int64_t ldgx, float* grad_w, float* workspace,
+                        int64_t workspace_floats, void* stream);
+
+/* Number of grad_w partial rows rk_rmsnorm_backward uses for M rows (0 for M <= 0, at most 512). */
+int rk_rmsnorm_backward_parts(int64_t M);
+
+/*
+ * Backward of the tanh-GELU prologue, elementwise over x [M, K]:
+ *   t = tanh(0.7978845608 (x + 0.044715 x^3))
+ *   grad_x = bf16(grad_y * (0.5 (1 + t) + 0.5 x (1 - t^2) 0.7978845608 (1 + 0.134145 x^2)))
+ * stored in x_dtype with row stride ldgx.
+ * Replaces: gelu_backward  int8_backward.py:53-89.
+ */
+int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x, int x_dtype,
+                     int64_t ldx, int64_t M, int64_t K, void* grad_x, int64_t ldgx,
+                     void* stream);
 
 #ifdef __cplusplus
 }

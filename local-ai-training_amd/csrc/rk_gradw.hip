@@ -1,16 +1,21 @@
 // BF16 grad_weight of the ratchet backward on gfx950 (the "TN" product):
 //
-//   Gw[n, k] = bf16_RNE( sum_m bf16(g[m, n]) * xh[m, k] ),
-//   xh[m, k] = bf16_RNE( bf16(q[m, k]) * bf16_RNE(s[m]) )        (ratchet.py:73-75, 159-163)
+//   Gw[n, k] = bf16_RNE( sum_m bf16(g[m, n]) * X[m, k] )                 (ratchet.py:159-163)
 //
-// g is the upstream gradient [M, N] (float32 or bfloat16, row-major), q / s the saved
-// per-token int8 activations and scales. Both operands are read in their natural
-// token-major layout: no transposed copies are made. Tiles are staged in LDS as
-// [32 tokens][128 features] bf16 (xh is dequantized during staging) and the MFMA
-// fragments, which need 8 consecutive tokens of one feature per lane, are gathered with
-// gfx950's transposing LDS read ds_read_b64_tr_b16: within each 16-lane group, source
-// lane s points at token row (s >> 2), features 4 (s & 3) .. +3, and lane l receives
-// feature l of the four token rows.
+// g is the upstream gradient [M, N] (float32 or bfloat16, row-major). The activation
+// operand X [M, K] comes in one of three forms:
+//   int8 q + scale s : X = bf16_RNE(bf16(q) * bf16_RNE(s[m]))  (the dequantized saved
+//                      activations of the fused int8 forward, ratchet.py:73-75),
+//                      dequantized while staging;
+//   bfloat16         : X as given (e.g. that dequantized copy, or bf16(inputs) of the
+//                      non-fused forward, ratchet.py:161);
+//   float32          : X = bf16_RNE(x), converted while staging.
+// Both operands are read in their natural token-major layout: no transposed copies are
+// made. Tiles are staged in LDS as [BM tokens][128 features] bf16 and the MFMA fragments,
+// which need 8 consecutive tokens of one feature per lane, are gathered with gfx950's
+// transposing LDS read ds_read_b64_tr_b16: within each 16-lane group, source lane s
+// points at token row (s >> 2), features 4 (s & 3) .. +3, and lane l receives feature l
+// of the four token rows.
 //
 // The token (contraction) axis is split into `nsplit` ranges; each block writes fp32
 // partial sums of one 128 x 128 output tile for one range, and a second kernel adds the
@@ -25,23 +30,31 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 typedef unsigned int gw_u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
+// Forms of the activation operand X.
+enum { GW_X_Q8 = 0, GW_X_BF16 = 1, GW_X_F32 = 2 };
+
 struct GwArgs {
   const void* g;
   int64_t ldg;
-  const int8_t* q;
-  int64_t ldq;
-  const float* s;
-  float* part;  // [nsplit][N][K] fp32
+  const void* x;    // int8 q, bf16 or f32 activations [M, K]
+  int64_t ldx;
+  const float* s;   // per-token scale (int8 form only)
+  float* part;      // [nsplit][N][K] fp32
   int64_t M, N, K;
-  int64_t m_chunk;  // tokens per split, a multiple of 32
+  int64_t m_chunk;  // tokens per split, a multiple of GW_BM
   int nsplit;
 };
 
 constexpr int GW_BN = 128;                 // output rows (n) per block
 constexpr int GW_BK = 128;                 // output columns (k) per block
 constexpr int GW_BM = 32;                  // tokens per pipeline step
-constexpr int GW_PITCH = GW_BN * 2 + 32;   // LDS row pitch in bytes (conflict-free tr reads)
-constexpr int GW_TILE = GW_BM * GW_PITCH;  // one staged operand tile
+// LDS row pitch: 320 bytes = 80 dwords, so consecutive token rows start 16 banks apart.
+// A transposing read serves 32 lanes per pass (rows r..r+3, two 32-byte column halves):
+// rows start at banks 0, 16, 32, 48 and the second half adds 8, so the eight 8-bank
+// segments are disjoint.
+constexpr int GW_PITCH = GW_BN * 2 + 64;
+constexpr int kGwBufferWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (32-bit data)
+constexpr int kGwMaxRing = 6;
 
 __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
@@ -49,12 +62,50 @@ __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Global data of one pipeline step held in registers (ring slot): the g tile piece
-// (GV 16-byte loads) and the q tile piece (one 16-byte load) of this thread.
-template <int GV>
+// Raw buffer descriptor (stride 0) over [base, base + bytes). The inputs are made
+// wave-uniform explicitly: the 64-bit arithmetic that produces them runs on the vector
+// unit, and a descriptor left in vector registers turns every load into a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gw_buffer(const void* base, int64_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, n, kGwBufferWord3);
+}
+
+// A [BM tokens][128 features] tile of an operand with ES-byte elements is read as
+// 16-byte pieces: 8 * ES pieces per token row, 16 / ES elements each, 256 threads,
+// BM * ES / 32 pieces per thread (piece c = tid + 256 j).
+template <int ES, int BM>
+struct GwPieces {
+  static constexpr int kPerRow = 8 * ES;
+  static constexpr int kElems = 16 / ES;
+  static constexpr int kPerThread = BM * ES / 32;
+  __device__ static int row(int c) { return c / kPerRow; }
+  __device__ static int col(int c) { return (c % kPerRow) * kElems; }
+};
+
+// Writes one 16-byte piece of a float32 (4 values) or bfloat16 (8 values) operand into
+// the bf16 LDS tile.
+template <int ES>
+__device__ __forceinline__ void gw_store_piece(uint8_t* dst, const gw_u32x4& v) {
+  if constexpr (ES == 4) {
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(gw_pack_bf16x2(__uint_as_float(v.x), __uint_as_float(v.y)),
+                   gw_pack_bf16x2(__uint_as_float(v.z), __uint_as_float(v.w)));
+  } else {
+    *reinterpret_cast<gw_u32x4*>(dst) = v;
+  }
+}
+
+// Global data of one pipeline step held in registers (ring slot): the g and X tile
+// pieces of this thread, and (int8 form) the scales of its X rows.
+template <int GV, int XV>
 struct GwSlot {
   gw_u32x4 g[GV];
-  gw_u32x4 q;
+  gw_u32x4 x[XV];
+  float s[XV];
 };
 
 // Fragment of 8 consecutive tokens for feature column `col0 + lane % 16` (+16 for the
@@ -72,11 +123,16 @@ __device__ __forceinline__ v8bf gw_fragment(const uint8_t* tile, int tok0, int c
   return f;
 }
 
-template <int GDT, int S>
+template <int GDT, int XK, int S, int BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void grad_weight_partial_kernel(GwArgs a) {
-  constexpr int GV = GDT == RK_F32 ? 4 : 2;  // 16-byte g loads per thread per step
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * GW_TILE];
+  constexpr int GE = GDT == RK_F32 ? 4 : 2;                          // g element bytes
+  constexpr int XE = XK == GW_X_Q8 ? 1 : (XK == GW_X_BF16 ? 2 : 4);  // X element bytes
+  using GP = GwPieces<GE, BM>;
+  using XP = GwPieces<XE, BM>;
+  constexpr int GV = GP::kPerThread, XV = XP::kPerThread;
+  constexpr int TILE = BM * GW_PITCH;  // one staged operand tile
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * TILE];
 
   const int64_t tiles_k = (a.K + GW_BK - 1) / GW_BK;
   const int64_t tiles = ((a.N + GW_BN - 1) / GW_BN) * tiles_k;
@@ -88,72 +144,97 @@ void grad_weight_partial_kernel(GwArgs a) {
   const int64_t n0 = (t / tiles_k) * GW_BN, k0 = (t % tiles_k) * GW_BK;
   const int64_t m_begin = split * a.m_chunk;
   const int64_t m_end = min(a.M, m_begin + a.m_chunk);
-  const int steps = m_end > m_begin ? static_cast<int>((m_end - m_begin + GW_BM - 1) / GW_BM) : 0;
+  const int steps = m_end > m_begin ? static_cast<int>((m_end - m_begin + BM - 1) / BM) : 0;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wk = wave >> 1;
 
-  // Staging geometry. g: 16-byte pieces of 8 bf16 (or 4 f32 -> 4 bf16 = 8 bytes) along n.
-  // q: one 16-byte piece (16 tokens' ... 16 features of one token) per thread.
-  int g_row[GV], g_col[GV];  // token row in the step, first feature column in the tile
+  // Buffer descriptors over this block's token range. num_records ends at the last valid
+  // byte (row m_end - 1, column N - 1 / K - 1), so every load past the range - token rows
+  // of padded steps, feature columns past N or K in the last row - returns zeros without
+  // a branch or a select. Loads stay unconditional, so the compiler counts outstanding
+  // loads exactly and waits only for the ring slot it consumes. Per-thread offsets are
+  // fixed; the step advances a scalar offset. The host guarantees offsets < 2^31.
+  const int64_t rows = m_end - m_begin;
+  const __amdgpu_buffer_rsrc_t g_rsrc = gw_buffer(
+      static_cast<const char*>(a.g) + (m_begin * a.ldg + n0) * GE,
+      rows > 0 ? ((rows - 1) * a.ldg + (a.N - n0)) * GE : 0);
+  const __amdgpu_buffer_rsrc_t x_rsrc = gw_buffer(
+      static_cast<const char*>(a.x) + (m_begin * a.ldx + k0) * XE,
+      rows > 0 ? ((rows - 1) * a.ldx + (a.K - k0)) * XE : 0);
+  const __amdgpu_buffer_rsrc_t s_rsrc =
+      gw_buffer(XK == GW_X_Q8 ? a.s + m_begin : a.s, XK == GW_X_Q8 && rows > 0 ? rows * 4 : 0);
+  int g_voff[GV], g_lds[GV], x_voff[XV], x_lds[XV], s_voff[XV];
 #pragma unroll
   for (int j = 0; j < GV; ++j) {
     const int c = tid + 256 * j;
-    if constexpr (GDT == RK_F32) {
-      g_row[j] = c >> 5;         // 32 pieces of 4 floats per 128-feature row
-      g_col[j] = 4 * (c & 31);
-    } else {
-      g_row[j] = c >> 4;         // 16 pieces of 8 bf16 per row
-      g_col[j] = 8 * (c & 15);
-    }
+    g_voff[j] = (GP::row(c) * static_cast<int>(a.ldg) + GP::col(c)) * GE;
+    g_lds[j] = GP::row(c) * GW_PITCH + GP::col(c) * 2;
   }
-  const int q_row = tid >> 3, q_col = 16 * (tid & 7);
-  const int es = GDT == RK_F32 ? 4 : 2;
-  const char* gbase = static_cast<const char*>(a.g);
+#pragma unroll
+  for (int j = 0; j < XV; ++j) {
+    const int c = tid + 256 * j;
+    x_voff[j] = (XP::row(c) * static_cast<int>(a.ldx) + XP::col(c)) * XE;
+    x_lds[j] = TILE + XP::row(c) * GW_PITCH + XP::col(c) * 2;
+    s_voff[j] = XP::row(c) * 4;
+  }
+  const int g_step = BM * static_cast<int>(a.ldg) * GE;
+  const int x_step = BM * static_cast<int>(a.ldx) * XE;
 
-  auto load_slot = [&](GwSlot<GV>& r, int step) {
-    const int64_t m_base = m_begin + static_cast<int64_t>(step) * GW_BM;
+  auto load_slot = [&](GwSlot<GV, XV>& r, int step) {
 #pragma unroll
-    for (int j = 0; j < GV; ++j) {
-      const int64_t m = m_base + g_row[j], n = n0 + g_col[j];
-      r.g[j] = gw_u32x4{0, 0, 0, 0};
-      if (m < m_end && n < a.N)
-        r.g[j] = *reinterpret_cast<const gw_u32x4*>(gbase + (m * a.ldg + n) * es);
+    for (int j = 0; j < GV; ++j)
+      r.g[j] = __builtin_bit_cast(
+          gw_u32x4, __builtin_amdgcn_raw_buffer_load_b128(g_rsrc, g_voff[j], step * g_step, 0));
+#pragma unroll
+    for (int j = 0; j < XV; ++j)
+      r.x[j] = __builtin_bit_cast(
+          gw_u32x4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, x_voff[j], step * x_step, 0));
+    if constexpr (XK == GW_X_Q8) {
+#pragma unroll
+      for (int j = 0; j < XV; ++j)
+        r.s[j] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, s_voff[j], step * BM * 4, 0));
     }
-    const int64_t m = m_base + q_row, k = k0 + q_col;
-    r.q = gw_u32x4{0, 0, 0, 0};
-    if (m < m_end && k < a.K) r.q = *reinterpret_cast<const gw_u32x4*>(a.q + m * a.ldq + k);
   };
-  auto store_slot = [&](const GwSlot<GV>& r, int step, uint8_t* gt, uint8_t* xt) {
+  // `tile` is the g tile of one LDS buffer; the X tile follows it.
+  auto store_slot = [&](GwSlot<GV, XV>& r, uint8_t* tile) {
+    // Pin the slot's registers here: without this the compiler computes the conversions
+    // of every slot as soon as its load is issued, which makes it wait for the whole
+    // ring instead of the one slot being stored.
 #pragma unroll
-    for (int j = 0; j < GV; ++j) {
-      uint8_t* dst = gt + g_row[j] * GW_PITCH + g_col[j] * 2;
-      if constexpr (GDT == RK_F32) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(
-            gw_pack_bf16x2(__uint_as_float(r.g[j].x), __uint_as_float(r.g[j].y)),
-            gw_pack_bf16x2(__uint_as_float(r.g[j].z), __uint_as_float(r.g[j].w)));
-      } else {
-        *reinterpret_cast<gw_u32x4*>(dst) = r.g[j];
+    for (int j = 0; j < GV; ++j) asm volatile("" : "+v"(r.g[j]));
+#pragma unroll
+    for (int j = 0; j < XV; ++j) asm volatile("" : "+v"(r.x[j]));
+#pragma unroll
+    for (int j = 0; j < GV; ++j) gw_store_piece<GE>(tile + g_lds[j], r.g[j]);
+    if constexpr (XK == GW_X_Q8) {
+      // X = bf16(bf16(q) * bf16(s)): q is exact in bf16, so this is one fp32 multiply of
+      // q by the bf16-rounded scale (a positive finite value, so the hardware
+      // conversion's round-to-nearest-even is the reference's cast), rounded to bf16.
+      // Rows past the range load q = 0 and s = 0.
+#pragma unroll
+      for (int j = 0; j < XV; ++j) {
+        asm volatile("" : "+v"(r.s[j]));
+        const float sm = static_cast<float>(static_cast<__bf16>(r.s[j]));
+        const uint32_t w[4] = {r.x[j].x, r.x[j].y, r.x[j].z, r.x[j].w};
+        uint32_t o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v0 = static_cast<float>(static_cast<int8_t>(w[i] & 0xff)) * sm;
+          const float v1 = static_cast<float>(static_cast<int8_t>((w[i] >> 8) & 0xff)) * sm;
+          const float v2 = static_cast<float>(static_cast<int8_t>((w[i] >> 16) & 0xff)) * sm;
+          const float v3 = static_cast<float>(static_cast<int8_t>(w[i] >> 24)) * sm;
+          o[2 * i] = gw_pack_bf16x2(v0, v1);
+          o[2 * i + 1] = gw_pack_bf16x2(v2, v3);
+        }
+        *reinterpret_cast<gw_u32x4*>(tile + x_lds[j]) = gw_u32x4{o[0], o[1], o[2], o[3]};
+        *reinterpret_cast<gw_u32x4*>(tile + x_lds[j] + 16) = gw_u32x4{o[4], o[5], o[6], o[7]};
       }
-    }
-    // xh = bf16(bf16(q) * bf16(s)): q is exact in bf16, so this is one fp32 multiply
-    // of q by the bf16-rounded scale, rounded to bf16.
-    const int64_t m = m_begin + static_cast<int64_t>(step) * GW_BM + q_row;
-    const float sm = m < m_end ? round_bf16(a.s[m]) : 0.0f;
-    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-    uint32_t o[8];
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v0 = static_cast<float>(static_cast<int8_t>(w[i] & 0xff)) * sm;
-      const float v1 = static_cast<float>(static_cast<int8_t>((w[i] >> 8) & 0xff)) * sm;
-      const float v2 = static_cast<float>(static_cast<int8_t>((w[i] >> 16) & 0xff)) * sm;
-      const float v3 = static_cast<float>(static_cast<int8_t>(w[i] >> 24)) * sm;
-      o[2 * i] = gw_pack_bf16x2(v0, v1);
-      o[2 * i + 1] = gw_pack_bf16x2(v2, v3);
+      for (int j = 0; j < XV; ++j) gw_store_piece<XE>(tile + x_lds[j], r.x[j]);
     }
-    uint8_t* dst = xt + q_row * GW_PITCH + q_col * 2;
-    *reinterpret_cast<gw_u32x4*>(dst) = gw_u32x4{o[0], o[1], o[2], o[3]};
-    *reinterpret_cast<gw_u32x4*>(dst + 16) = gw_u32x4{o[4], o[5], o[6], o[7]};
   };
 
   v16f acc[2][2];
@@ -163,23 +244,36 @@ void grad_weight_partial_kernel(GwArgs a) {
     for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
   // Register ring of S steps: the global loads of step st + S are issued right after
-  // step st is written to LDS, so S steps of g and q stream in while the MFMAs run.
-  GwSlot<GV> ring[S];
+  // step st is written to LDS, so S steps of g and X stream in while the MFMAs run. The
+  // step count is padded to a multiple of S (even, so a slot's LDS buffer is fixed);
+  // padded steps stage zeros.
+  static_assert(S % 2 == 0 && S <= kGwMaxRing, "ring depth must be even and <= 6");
+  if (steps > 0) {
+    const int steps_pad = ((steps + S - 1) / S) * S;
+    GwSlot<GV, XV> ring[S];
+    // Issue the first S steps in slot order (the scheduler barrier keeps them so): the
+    // loop body waits for slot i with S - 1 slots still in flight only if slot i's loads
+    // are older than those of the later slots on every path into the loop.
 #pragma unroll
-  for (int i = 0; i < S; ++i)
-    if (i < steps) load_slot(ring[i], i);
-  for (int st = 0; st < steps; st += S) {
+    for (int i = 0; i < S; ++i) {
+      load_slot(ring[i], i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int st = 0; st < steps_pad; st += S) {
 #pragma unroll
-    for (int slot = 0; slot < S; ++slot) {
-      const int step = st + slot;
-      if (step < steps) {
-        uint8_t* gt = smem + (step & 1) * 2 * GW_TILE;
-        uint8_t* xt = gt + GW_TILE;
-        store_slot(ring[slot], step, gt, xt);
-        if (step + S < steps) load_slot(ring[slot], step + S);
+      for (int slot = 0; slot < S; ++slot) {
+        const int step = st + slot;
+        uint8_t* gt = smem + (slot & 1) * 2 * TILE;
+        uint8_t* xt = gt + TILE;
+        store_slot(ring[slot], gt);
+        load_slot(ring[slot], step + S);
         __syncthreads();
+        // No branch for padded steps: their tiles are zeros, and adding +0 products to
+        // an accumulator that started at +0 leaves it bit-for-bit unchanged. One basic
+        // block per step lets the scheduler overlap these MFMAs with the next step's
+        // staging.
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < BM / 16; ++u) {
           v8bf fa[2], fb[2];
 #pragma unroll
           for (int i = 0; i < 2; ++i) fa[i] = gw_fragment(gt, 16 * u, wn * 64 + 32 * i, lane);
@@ -189,7 +283,8 @@ void grad_weight_partial_kernel(GwArgs a) {
           for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+              acc[i][j] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
       }
     }
@@ -233,6 +328,67 @@ __global__ __launch_bounds__(256) void grad_weight_reduce_kernel(const float* pa
   }
 }
 
+// Ring depth 2 and 32-token steps: ring depths 4 and 6 and 64-token steps (BM = 64, 80 KB
+// of LDS) measure the same or slower on MI355X at the op and model shapes.
+template <int XK>
+void launch_partial_g(const GwArgs& a, int g_dtype, dim3 grid, hipStream_t st) {
+  if (g_dtype == RK_F32) grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM><<<grid, 256, 0, st>>>(a);
+  else grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM><<<grid, 256, 0, st>>>(a);
+}
+
+// Shared validation and launch of both entry points; x_kind is a GW_X_* form.
+int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, int x_kind,
+                       int64_t ldx, const float* s, int64_t M, int64_t N, int64_t K,
+                       float* workspace, int nsplit, uint16_t* out, int64_t ldo, void* stream) {
+  if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
+  if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
+  if (N == 0 || K == 0) return RK_OK;
+  if (!g || !x || (x_kind == GW_X_Q8 && !s) || !workspace || !out)
+    return fail(RK_ERR_ARG, "null pointer");
+  if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
+  if (ldg < N || ldx < K || ldo < K) return fail(RK_ERR_ARG, "leading dimension too small");
+  const int ge = g_dtype == RK_F32 ? 4 : 2;
+  const int xe = x_kind == GW_X_Q8 ? 1 : (x_kind == GW_X_BF16 ? 2 : 4);
+  if ((N % 8) != 0 || (K % 16) != 0 || ((ldg * ge) % 16) != 0 || ((ldx * xe) % 16) != 0 ||
+      (ldo % 4) != 0 || !aligned16(g) || !aligned16(x) || !aligned16(workspace) ||
+      (reinterpret_cast<uintptr_t>(out) % 8) != 0)
+    return fail(RK_ERR_UNSUPPORTED,
+                "grad_weight needs N %% 8 == 0, K %% 16 == 0 and 16-byte aligned rows");
+  const int64_t tiles = ((N + GW_BN - 1) / GW_BN) * ((K + GW_BK - 1) / GW_BK);
+  const int64_t chunk = ((M + nsplit - 1) / nsplit + GW_BM - 1) / GW_BM * GW_BM;
+  // Buffer offsets are 32-bit: the furthest load of a block (ring padding and prefetch
+  // included) must stay below 2^31 bytes from the block's first row.
+  const int64_t reach = chunk + (2 * kGwMaxRing + 1) * GW_BM;
+  if (reach * ldg * ge >= (int64_t{1} << 31) || reach * ldx * xe >= (int64_t{1} << 31))
+    return fail(RK_ERR_UNSUPPORTED,
+                "grad_weight token range too large for 32-bit offsets; raise nsplit");
+  GwArgs a{};
+  a.g = g;
+  a.ldg = ldg;
+  a.x = x;
+  a.ldx = ldx;
+  a.s = s;
+  a.part = workspace;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.m_chunk = chunk > 0 ? chunk : GW_BM;
+  a.nsplit = nsplit;
+  const int64_t blocks = tiles * nsplit;
+  if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
+  hipStream_t st = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8>(a, g_dtype, grid, st);
+  else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16>(a, g_dtype, grid, st);
+  else launch_partial_g<GW_X_F32>(a, g_dtype, grid, st);
+  if (int e = launch_status("grad_weight_partial")) return e;
+  const int64_t total4 = N * K / 4;
+  const int64_t rblocks = (total4 + 255) / 256;
+  grad_weight_reduce_kernel<<<static_cast<unsigned>(rblocks < 4096 ? rblocks : 4096), 256, 0, st>>>(
+      workspace, nsplit, N, K, out, ldo);
+  return launch_status("grad_weight_reduce");
+}
+
 }  // namespace rk
 
 using namespace rk;
@@ -252,56 +408,16 @@ extern "C" int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, cons
                                    float* workspace, int nsplit, uint16_t* out, int64_t ldo,
                                    void* stream) {
   clear_error();
-  if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
-  if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
-  if (N == 0 || K == 0) return RK_OK;
-  if (!g || !q || !s || !workspace || !out) return fail(RK_ERR_ARG, "null pointer");
-  if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
-  if (ldg < N || ldq < K || ldo < K) return fail(RK_ERR_ARG, "leading dimension too small");
-  const int ge = g_dtype == RK_F32 ? 4 : 2;
-  if ((N % 8) != 0 || (K % 16) != 0 || ((ldg * ge) % 16) != 0 || (ldq % 16) != 0 ||
-      (ldo % 4) != 0 || !aligned16(g) || !aligned16(q) || !aligned16(workspace) ||
-      (reinterpret_cast<uintptr_t>(out) % 8) != 0)
-    return fail(RK_ERR_UNSUPPORTED,
-                "grad_weight needs N %% 8 == 0, K %% 16 == 0 and 16-byte aligned rows");
-  const int64_t tiles = ((N + GW_BN - 1) / GW_BN) * ((K + GW_BK - 1) / GW_BK);
-  const int64_t chunk = ((M + nsplit - 1) / nsplit + GW_BM - 1) / GW_BM * GW_BM;
-  GwArgs a{};
-  a.g = g;
-  a.ldg = ldg;
-  a.q = q;
-  a.ldq = ldq;
-  a.s = s;
-  a.part = workspace;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  a.m_chunk = chunk > 0 ? chunk : GW_BM;
-  a.nsplit = nsplit;
-  const int64_t blocks = tiles * nsplit;
-  if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
-  hipStream_t st = as_stream(stream);
-  // Ring depth: 4 steps for a bf16 gradient, 2 for float32 (its wider staging would
-  // drop the kernel to one wave per SIMD at depth 4). RK_GW_RING overrides (2, 4, 6).
-  static const int ring_env = [] {
-    const char* v = getenv("RK_GW_RING");
-    return v ? atoi(v) : 0;
-  }();
-  const int ring = ring_env ? ring_env : (g_dtype == RK_F32 ? 2 : 4);
-  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
-  if (g_dtype == RK_F32) {
-    if (ring == 4) grad_weight_partial_kernel<RK_F32, 4><<<grid, block, 0, st>>>(a);
-    else if (ring == 6) grad_weight_partial_kernel<RK_F32, 6><<<grid, block, 0, st>>>(a);
-    else grad_weight_partial_kernel<RK_F32, 2><<<grid, block, 0, st>>>(a);
-  } else {
-    if (ring == 2) grad_weight_partial_kernel<RK_BF16, 2><<<grid, block, 0, st>>>(a);
-    else if (ring == 6) grad_weight_partial_kernel<RK_BF16, 6><<<grid, block, 0, st>>>(a);
-    else grad_weight_partial_kernel<RK_BF16, 4><<<grid, block, 0, st>>>(a);
-  }
-  if (int e = launch_status("grad_weight_partial")) return e;
-  const int64_t total4 = N * K / 4;
-  const int64_t rblocks = (total4 + 255) / 256;
-  grad_weight_reduce_kernel<<<static_cast<unsigned>(rblocks < 4096 ? rblocks : 4096), 256, 0, st>>>(
-      workspace, nsplit, N, K, out, ldo);
-  return launch_status("grad_weight_reduce");
+  return grad_weight_launch(g, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, workspace, nsplit,
+                            out, ldo, stream);
+}
+
+extern "C" int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x,
+                                     int x_dtype, int64_t ldx, int64_t M, int64_t N, int64_t K,
+                                     float* workspace, int nsplit, uint16_t* out, int64_t ldo,
+                                     void* stream) {
+  clear_error();
+  if (x_dtype != RK_F32 && x_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported x dtype");
+  return grad_weight_launch(g, g_dtype, ldg, x, x_dtype == RK_F32 ? GW_X_F32 : GW_X_BF16, ldx,
+                            nullptr, M, N, K, workspace, nsplit, out, ldo, stream);
 }

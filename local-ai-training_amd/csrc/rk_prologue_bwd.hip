@@ -1,0 +1,374 @@
+// Backward of the fused int8 prologues (RMSNorm+quant and tanh-GELU+quant).
+//
+// rmsnorm_backward, int8_backward.py:7-51, per row of x[M, K] and grad_y[M, K]:
+//   variance = sum(x * x) / K;           rsqrt = 1 / sqrt(variance + eps)
+//   dx_hat   = grad_y * w;               dvar  = sum(dx_hat * x) * -0.5 * rsqrt^3
+//   dx       = dx_hat * rsqrt + dvar * 2 * x / K   -> rounded to bf16, stored in x's dtype
+// and grad_w[k] = sum over rows of grad_y * x * rsqrt (float32).
+//
+// gelu_backward, int8_backward.py:53-89, elementwise:
+//   t  = tanh(sqrt(2/pi) * (x + 0.044715 * x * x^2))
+//   dx = grad_y * (0.5 * (1 + t) + 0.5 * x * (1 - t^2) * sqrt(2/pi) * (1 + 0.134145 * x^2))
+//   -> rounded to bf16, stored in x's dtype.
+//
+// Both are HBM-bound streams. The RMSNorm kernel keeps a whole row in registers (one
+// wavefront per row, 4 columns per lane per 256-column chunk, K <= 4096), so x and
+// grad_y are read once, dx is written once, and grad_w is accumulated per lane over
+// the block's rows. Each block writes its grad_w partial; a second kernel sums the
+// partials in block order, so grad_w is reproducible run to run (no float atomics).
+#include "rk_common.h"
+
+namespace rk {
+namespace {
+
+constexpr int kBwdV = 4;                   // columns per lane per chunk
+constexpr int kBwdSpan = kWave * kBwdV;    // 256 columns per chunk
+constexpr int kBwdMaxChunks = 16;          // K <= 4096 on the register-resident path
+constexpr int kBwdTargetBlocks = 512;      // grid size the row split aims for
+
+// Valid columns (0..4) of the 4-column group starting at e0 in a row of K.
+__device__ __forceinline__ int quad_valid(int64_t K, int64_t e0) {
+  const int64_t n = K - e0;
+  return n <= 0 ? 0 : (n >= kBwdV ? kBwdV : static_cast<int>(n));
+}
+
+// Loads n (0..4) elements at base[idx..], zero-filling the rest; VEC: n == 4 and the
+// address is 4-element aligned, so one 16-byte (f32) or 8-byte (bf16) load is used.
+template <int DT>
+__device__ __forceinline__ void load4(const void* base, int64_t idx, int n, bool vec,
+                                      float* v) {
+  if (vec && n == 4) {
+    if constexpr (DT == RK_F32) {
+      const float4 r = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+      v[0] = r.x; v[1] = r.y; v[2] = r.z; v[3] = r.w;
+    } else {
+      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
+      v[0] = __uint_as_float(r.x << 16);
+      v[1] = __uint_as_float(r.x & 0xffff0000u);
+      v[2] = __uint_as_float(r.y << 16);
+      v[3] = __uint_as_float(r.y & 0xffff0000u);
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = i < n ? load_elem<DT>(base, idx + i) : 0.0f;
+}
+
+// Stores n (0..4) values rounded to bf16, in dtype DT (an f32 destination holds the
+// bf16 value widened, as `dx.to(bfloat16)` stored into a float32 buffer).
+template <int DT>
+__device__ __forceinline__ void store4_bf16(void* base, int64_t idx, int n, bool vec,
+                                            const float* v) {
+  uint16_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) h[i] = f32_to_bf16(v[i]);
+  if constexpr (DT == RK_F32) {
+    float* p = static_cast<float*>(base) + idx;
+    if (vec && n == 4) {
+      *reinterpret_cast<float4*>(p) =
+          make_float4(bf16_to_f32(h[0]), bf16_to_f32(h[1]), bf16_to_f32(h[2]), bf16_to_f32(h[3]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < n) p[i] = bf16_to_f32(h[i]);
+    }
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(base) + idx;
+    if (vec && n == 4) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16),
+                                                h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < n) p[i] = h[i];
+    }
+  }
+}
+
+struct NormBwdArgs {
+  const void* gy;
+  int64_t ldg;
+  const void* x;
+  int64_t ldx;
+  const float* w;
+  float eps;
+  int64_t M, K;
+  void* gx;
+  int64_t ldgx;
+  float* part;             // [gridDim.x][K] grad_w partial of each block
+  int64_t rows_per_block;  // a multiple of 4
+  int vec;                 // 4-element vector access is legal for x, grad_y, grad_x and w
+};
+
+template <int GDT, int XDT, int NC>
+__device__ __forceinline__ void norm_load_row(const NormBwdArgs& a, int64_t row, int lane,
+                                              float (&xv)[NC][kBwdV], float (&gv)[NC][kBwdV]) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+    const int n = quad_valid(a.K, e0);
+    load4<XDT>(a.x, row * a.ldx + e0, n, a.vec, xv[c]);
+    load4<GDT>(a.gy, row * a.ldg + e0, n, a.vec, gv[c]);
+  }
+}
+
+// One block = 4 wavefronts = rows [blockIdx.x * rows_per_block, +rows_per_block); wave w
+// takes rows w, w + 4, ... of that range. PREFETCH issues the next row's loads before
+// the current row's reductions (small NC only: it doubles the row registers).
+template <int GDT, int XDT, int NC, bool PREFETCH>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
+  __shared__ __attribute__((aligned(16))) float red[4][NC * kBwdSpan];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_block;
+  const int64_t r1 = r0 + a.rows_per_block < a.M ? r0 + a.rows_per_block : a.M;
+  const float kf = static_cast<float>(a.K);
+
+  float wv[NC][kBwdV], gw[NC][kBwdV];
+  int nv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+    nv[c] = quad_valid(a.K, e0);
+    load4<RK_F32>(a.w, e0, nv[c], a.vec, wv[c]);
+#pragma unroll
+    for (int i = 0; i < kBwdV; ++i) gw[c][i] = 0.0f;
+  }
+
+  int64_t row = r0 + wave;
+  float xv[NC][kBwdV], gv[NC][kBwdV];
+  if (row < r1) norm_load_row<GDT, XDT, NC>(a, row, lane, xv, gv);
+  while (row < r1) {
+    const int64_t next = row + 4;
+    float xn[NC][kBwdV], gn[NC][kBwdV];
+    if constexpr (PREFETCH) {
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xn, gn);
+    }
+    float sxx = 0.0f, sgx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int i = 0; i < kBwdV; ++i) {
+        sxx = sxx + xv[c][i] * xv[c][i];
+        sgx = sgx + (gv[c][i] * wv[c][i]) * xv[c][i];
+      }
+    sxx = wave_sum_butterfly(sxx);
+    sgx = wave_sum_butterfly(sgx);
+    const float rs = 1.0f / sqrtf(sxx / kf + a.eps);
+    const float dvar = sgx * -0.5f * (rs * rs * rs);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float dx[kBwdV];
+#pragma unroll
+      for (int i = 0; i < kBwdV; ++i) {
+        dx[i] = (gv[c][i] * wv[c][i]) * rs + dvar * 2.0f * xv[c][i] / kf;
+        gw[c][i] = gw[c][i] + gv[c][i] * xv[c][i] * rs;
+      }
+      const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+      if (nv[c] > 0) store4_bf16<XDT>(a.gx, row * a.ldgx + e0, nv[c], a.vec, dx);
+    }
+    if constexpr (PREFETCH) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int i = 0; i < kBwdV; ++i) {
+          xv[c][i] = xn[c][i];
+          gv[c][i] = gn[c][i];
+        }
+    } else {
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xv, gv);
+    }
+    row = next;
+  }
+
+  // Block partial: the four waves' column sums, added in wave order.
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    *reinterpret_cast<float4*>(&red[wave][c * kBwdSpan + lane * kBwdV]) =
+        make_float4(gw[c][0], gw[c][1], gw[c][2], gw[c][3]);
+  __syncthreads();
+  float* out = a.part + static_cast<int64_t>(blockIdx.x) * a.K;
+  for (int64_t col = threadIdx.x; col < a.K; col += 256)
+    out[col] = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
+}
+
+// grad_w[k] = sum of part[p][k] over p: 16 columns x 16 part-groups per block; group g
+// sums parts g, g + 16, ... and the 16 group sums are then added in group order.
+__global__ __launch_bounds__(256) void rmsnorm_gw_reduce_kernel(const float* part,
+                                                                int64_t nparts, int64_t K,
+                                                                float* gw) {
+  __shared__ float s[16][17];
+  const int cl = threadIdx.x & 15, g = threadIdx.x >> 4;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 16 + cl;
+  float acc = 0.0f;
+  if (col < K) {
+#pragma unroll 8
+    for (int64_t p = g; p < nparts; p += 16) acc = acc + part[p * K + col];
+  }
+  s[g][cl] = acc;
+  __syncthreads();
+  if (threadIdx.x < 16 && col < K) {
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t = t + s[i][threadIdx.x];
+    gw[col] = t;
+  }
+}
+
+struct GeluBwdArgs {
+  const void* gy;
+  int64_t ldg;
+  const void* x;
+  int64_t ldx;
+  void* gx;
+  int64_t ldgx;
+  int64_t M, K;
+  int64_t quads;  // ceil(K / 4) column groups per row
+  int vec;
+};
+
+// The derivative of the tanh-GELU, evaluated in the operation order of
+// int8_backward.py:65-72.
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float k = 0.7978845608028654f;
+  const float x_sq = x * x;
+  const float inner = k * (x + 0.044715f * x * x_sq);
+  const float t = tanhf(inner);
+  const float term1 = 0.5f * (1.0f + t);
+  const float term2 = 0.5f * x * (1.0f - t * t) * k * (1.0f + 0.134145f * x_sq);
+  return term1 + term2;
+}
+
+// One thread = 4 consecutive columns of one row; grid-stride over M * quads groups.
+template <int GDT, int XDT>
+__global__ __launch_bounds__(256) void gelu_bwd_kernel(GeluBwdArgs a) {
+  const int64_t total = a.M * a.quads;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
+       u += stride) {
+    const int64_t row = u / a.quads;
+    const int64_t e0 = (u - row * a.quads) * kBwdV;
+    const int n = quad_valid(a.K, e0);
+    float xv[kBwdV], gv[kBwdV], dx[kBwdV];
+    load4<XDT>(a.x, row * a.ldx + e0, n, a.vec, xv);
+    load4<GDT>(a.gy, row * a.ldg + e0, n, a.vec, gv);
+#pragma unroll
+    for (int i = 0; i < kBwdV; ++i) dx[i] = gv[i] * gelu_tanh_grad(xv[i]);
+    store4_bf16<XDT>(a.gx, row * a.ldgx + e0, n, a.vec, dx);
+  }
+}
+
+bool vec4_ok(const void* p, int dt, int64_t ld, int64_t K) {
+  const uintptr_t align = static_cast<uintptr_t>(dtype_size(dt)) * 4;
+  return (reinterpret_cast<uintptr_t>(p) % align) == 0 && ld % 4 == 0 && K % 4 == 0;
+}
+
+template <int GDT, int XDT, int NC>
+void launch_norm_nc(const NormBwdArgs& a, dim3 grid, hipStream_t st) {
+  constexpr bool kPrefetch = NC <= 4;
+  rmsnorm_bwd_kernel<GDT, XDT, NC, kPrefetch><<<grid, dim3(256), 0, st>>>(a);
+}
+
+template <int GDT, int XDT>
+int launch_norm(const NormBwdArgs& a, dim3 grid, hipStream_t st) {
+  const int64_t nc = (a.K + kBwdSpan - 1) / kBwdSpan;
+  if (nc <= 1) launch_norm_nc<GDT, XDT, 1>(a, grid, st);
+  else if (nc <= 2) launch_norm_nc<GDT, XDT, 2>(a, grid, st);
+  else if (nc <= 4) launch_norm_nc<GDT, XDT, 4>(a, grid, st);
+  else if (nc <= 8) launch_norm_nc<GDT, XDT, 8>(a, grid, st);
+  else launch_norm_nc<GDT, XDT, 16>(a, grid, st);
+  return launch_status("rmsnorm_backward");
+}
+
+int64_t norm_rows_per_block(int64_t M) {
+  const int64_t per = (M + kBwdTargetBlocks - 1) / kBwdTargetBlocks;
+  return ((per + 3) / 4) * 4;
+}
+
+}  // namespace
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" int rk_rmsnorm_backward_parts(int64_t M) {
+  if (M <= 0) return 0;
+  const int64_t rpb = norm_rows_per_block(M);
+  return static_cast<int>((M + rpb - 1) / rpb);  // <= kBwdTargetBlocks
+}
+
+extern "C" int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
+                                   int x_dtype, int64_t ldx, const float* w, float eps, int64_t M,
+                                   int64_t K, void* grad_x, int64_t ldgx, float* grad_w,
+                                   float* workspace, int64_t workspace_floats, void* stream) {
+  clear_error();
+  if (M < 0 || K < 0) return fail(RK_ERR_ARG, "negative size M=%lld K=%lld", (long long)M,
+                                  (long long)K);
+  if (dtype_size(gy_dtype) == 0 || dtype_size(x_dtype) == 0)
+    return fail(RK_ERR_ARG, "grad_y/x dtype must be RK_F32 or RK_BF16");
+  if (K > static_cast<int64_t>(kBwdMaxChunks) * kBwdSpan)
+    return fail(RK_ERR_UNSUPPORTED, "rmsnorm_backward supports K <= %d (got %lld)",
+                kBwdMaxChunks * kBwdSpan, (long long)K);
+  if (K == 0) return RK_OK;
+  if (!grad_w || !w) return fail(RK_ERR_ARG, "null w or grad_w");
+  hipStream_t st = as_stream(stream);
+  const dim3 reduce_grid(static_cast<unsigned>((K + 15) / 16));
+  if (M == 0) {  // grad_w = 0: the reduce over zero partials writes zeros
+    rmsnorm_gw_reduce_kernel<<<reduce_grid, dim3(256), 0, st>>>(nullptr, 0, K, grad_w);
+    return launch_status("rmsnorm_backward_reduce");
+  }
+  if (!grad_y || !x || !grad_x || !workspace) return fail(RK_ERR_ARG, "null pointer");
+  if (ldg < K || ldx < K || ldgx < K) return fail(RK_ERR_ARG, "leading dimension below K");
+  const int64_t nparts = rk_rmsnorm_backward_parts(M);
+  if (workspace_floats < nparts * K)
+    return fail(RK_ERR_ARG, "workspace holds %lld floats, needs %lld",
+                (long long)workspace_floats, (long long)(nparts * K));
+  NormBwdArgs a{};
+  a.gy = grad_y; a.ldg = ldg; a.x = x; a.ldx = ldx; a.w = w; a.eps = eps;
+  a.M = M; a.K = K; a.gx = grad_x; a.ldgx = ldgx; a.part = workspace;
+  a.rows_per_block = norm_rows_per_block(M);
+  a.vec = vec4_ok(grad_y, gy_dtype, ldg, K) && vec4_ok(x, x_dtype, ldx, K) &&
+          vec4_ok(grad_x, x_dtype, ldgx, K) && vec4_ok(w, RK_F32, K, K);
+  const dim3 grid(static_cast<unsigned>(nparts));
+  int e;
+  if (gy_dtype == RK_F32) {
+    e = x_dtype == RK_F32 ? launch_norm<RK_F32, RK_F32>(a, grid, st)
+                          : launch_norm<RK_F32, RK_BF16>(a, grid, st);
+  } else {
+    e = x_dtype == RK_F32 ? launch_norm<RK_BF16, RK_F32>(a, grid, st)
+                          : launch_norm<RK_BF16, RK_BF16>(a, grid, st);
+  }
+  if (e) return e;
+  rmsnorm_gw_reduce_kernel<<<reduce_grid, dim3(256), 0, st>>>(workspace, nparts, K, grad_w);
+  return launch_status("rmsnorm_backward_reduce");
+}
+
+extern "C" int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
+                                int x_dtype, int64_t ldx, int64_t M, int64_t K, void* grad_x,
+                                int64_t ldgx, void* stream) {
+  clear_error();
+  if (M < 0 || K < 0) return fail(RK_ERR_ARG, "negative size M=%lld K=%lld", (long long)M,
+                                  (long long)K);
+  if (dtype_size(gy_dtype) == 0 || dtype_size(x_dtype) == 0)
+    return fail(RK_ERR_ARG, "grad_y/x dtype must be RK_F32 or RK_BF16");
+  if (M == 0 || K == 0) return RK_OK;
+  if (!grad_y || !x || !grad_x) return fail(RK_ERR_ARG, "null pointer");
+  if (ldg < K || ldx < K || ldgx < K) return fail(RK_ERR_ARG, "leading dimension below K");
+  GeluBwdArgs a{};
+  a.gy = grad_y; a.ldg = ldg; a.x = x; a.ldx = ldx; a.gx = grad_x; a.ldgx = ldgx;
+  a.M = M; a.K = K; a.quads = (K + kBwdV - 1) / kBwdV;
+  a.vec = vec4_ok(grad_y, gy_dtype, ldg, K) && vec4_ok(x, x_dtype, ldx, K) &&
+          vec4_ok(grad_x, x_dtype, ldgx, K);
+  const int64_t total = M * a.quads;
+  const int64_t want = (total + 255) / 256;
+  const int64_t blocks = want < (int64_t{1} << 20) ? want : (int64_t{1} << 20);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  hipStream_t st = as_stream(stream);
+  if (gy_dtype == RK_F32) {
+    if (x_dtype == RK_F32) gelu_bwd_kernel<RK_F32, RK_F32><<<grid, block, 0, st>>>(a);
+    else gelu_bwd_kernel<RK_F32, RK_BF16><<<grid, block, 0, st>>>(a);
+  } else {
+    if (x_dtype == RK_F32) gelu_bwd_kernel<RK_BF16, RK_F32><<<grid, block, 0, st>>>(a);
+    else gelu_bwd_kernel<RK_BF16, RK_BF16><<<grid, block, 0, st>>>(a);
+  }
+  return launch_status("gelu_backward");
+}

@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
     "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_grad_weight_bf16": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i32, _p,
                             _i64, _p],
+    "rk_grad_weight_bf16_x": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _p,
+                              _i64, _p],
     "rk_grad_weight_splits": [_i64, _i64, _i64],
     "rk_ratchet_update": [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _f32, _f32, _p, _p],
     "rk_ratchet_update_grad": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i32, _i32, _f32, _f32,
@@ -52,6 +54,10 @@ SIGNATURES: dict[str, list] = {
     "rk_gelu_quantize": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _p],
     "rk_transpose_quantize": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                               _i64, _p, _p],
+    "rk_rmsnorm_backward": [_p, _i32, _i64, _p, _i32, _i64, _p, _f32, _i64, _i64, _p, _i64, _p,
+                            _p, _i64, _p],
+    "rk_rmsnorm_backward_parts": [_i64],
+    "rk_gelu_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "rk_version": [],
     "rk_last_error": [],
 }

@@ -1,9 +1,12 @@
 """Backward of the fused int8 prologues (drop-in for ``int8_backward.py``).
 
-The reference computes these in Triton (``int8_backward.py:7-89``) and stores dx
-rounded to bf16 into a buffer of the input dtype (``int8_backward.py:27``, ``74``).
-They are not part of the ratchet-linear arithmetic; here they are plain tensor
-expressions with the same formulas and the same bf16 rounding of dx.
+Same functions, arguments and results as the reference (``int8_backward.py:7-89``):
+``rmsnorm_backward(grad_y, x, w, eps) -> (grad_x, grad_w)`` and
+``gelu_backward(grad_y, x) -> grad_x``. grad_x is rounded to bf16 and stored in x's
+dtype (``int8_backward.py:27, 74``); grad_w is summed in float32 and returned in w's
+dtype (``int8_backward.py:45-51``). Both run as gfx950 HIP kernels
+(``rk_rmsnorm_backward`` / ``rk_gelu_backward``). RMSNorm rows wider than 4096 columns
+run as the same formulas in torch tensor ops on the GPU.
 """
 
 from __future__ import annotations
@@ -11,34 +14,69 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
+from . import _native as nat
+
 _SQRT_2_OVER_PI = 0.7978845608028654
+_MAX_NORM_K = 4096
+
+
+def _rows(t: Tensor) -> Tensor:
+    """[..., K] -> [M, K] with unit column stride (a view when possible)."""
+    flat = t.reshape(-1, t.shape[-1])
+    if flat.stride(-1) != 1:
+        flat = flat.contiguous()
+    return flat
+
+
+def _float_or_bf16(t: Tensor) -> Tensor:
+    return t if t.dtype in (torch.float32, torch.bfloat16) else t.float()
+
+
+def _rmsnorm_backward_torch(gy: Tensor, x_flat: Tensor, w: Tensor, eps: float
+                            ) -> tuple[Tensor, Tensor]:
+    xf, gf, wf = x_flat.float(), gy.float(), w.float()
+    k = xf.shape[1]
+    rsqrt = torch.rsqrt((xf * xf).sum(dim=1, keepdim=True) / k + eps)
+    dx_hat = gf * wf
+    dvar = (dx_hat * xf).sum(dim=1, keepdim=True) * (-0.5) * (rsqrt * rsqrt * rsqrt)
+    dx = dx_hat * rsqrt + dvar * 2.0 * xf / k
+    return dx.to(torch.bfloat16).to(x_flat.dtype), (gf * xf * rsqrt).sum(dim=0)
 
 
 def rmsnorm_backward(grad_y: Tensor, x: Tensor, w: Tensor, eps: float = 1e-5
                      ) -> tuple[Tensor, Tensor]:
     if not x.is_cuda:
         raise RuntimeError("CUDA required (a ROCm GPU)")
-    x_flat = x.flatten(0, -2).float()
-    gy = grad_y.flatten(0, -2).float()
-    k = x_flat.shape[1]
-    wf = w.float()
-    variance = (x_flat * x_flat).sum(dim=1, keepdim=True) / k
-    rsqrt = torch.rsqrt(variance + eps)
-    dx_hat = gy * wf
-    dvar = (dx_hat * x_flat).sum(dim=1, keepdim=True) * (-0.5) * (rsqrt * rsqrt * rsqrt)
-    dx = dx_hat * rsqrt + dvar * 2.0 * x_flat / k
-    grad_x = dx.to(torch.bfloat16).to(x.dtype).reshape(x.shape)
-    grad_w = (gy * x_flat * rsqrt).sum(dim=0)
-    return grad_x, grad_w.to(w.dtype)
+    x_flat = _rows(_float_or_bf16(x))
+    gy = _rows(_float_or_bf16(grad_y))
+    m, k = x_flat.shape
+    if gy.shape != x_flat.shape:
+        raise ValueError(f"grad_y {tuple(grad_y.shape)} does not match x {tuple(x.shape)}")
+    wf = w.float().contiguous()
+    if k > _MAX_NORM_K:
+        grad_x, grad_w = _rmsnorm_backward_torch(gy, x_flat, wf, eps)
+    else:
+        grad_x = torch.empty((m, k), device=x.device, dtype=x_flat.dtype)
+        grad_w = torch.empty((k,), device=x.device, dtype=torch.float32)
+        parts = int(nat.load_library().rk_rmsnorm_backward_parts(m))
+        work = torch.empty((max(parts, 1), k), device=x.device, dtype=torch.float32)
+        nat.call("rk_rmsnorm_backward", gy.data_ptr(), nat.dtype_code(gy.dtype), gy.stride(0),
+                 x_flat.data_ptr(), nat.dtype_code(x_flat.dtype), x_flat.stride(0),
+                 wf.data_ptr(), float(eps), m, k, grad_x.data_ptr(), grad_x.stride(0),
+                 grad_w.data_ptr(), work.data_ptr(), work.numel(), nat.stream_handle(x.device))
+    return grad_x.to(x.dtype).reshape(x.shape), grad_w.to(w.dtype)
 
 
 def gelu_backward(grad_y: Tensor, x: Tensor) -> Tensor:
     if not x.is_cuda:
         raise RuntimeError("CUDA required (a ROCm GPU)")
-    xf = x.float()
-    gy = grad_y.float()
-    x_sq = xf * xf
-    t = torch.tanh(_SQRT_2_OVER_PI * (xf + 0.044715 * xf * x_sq))
-    term1 = 0.5 * (1.0 + t)
-    term2 = 0.5 * xf * (1.0 - t * t) * _SQRT_2_OVER_PI * (1.0 + 0.134145 * x_sq)
-    return (gy * (term1 + term2)).to(torch.bfloat16).to(x.dtype)
+    x_flat = _rows(_float_or_bf16(x))
+    gy = _rows(_float_or_bf16(grad_y))
+    if gy.shape != x_flat.shape:
+        raise ValueError(f"grad_y {tuple(grad_y.shape)} does not match x {tuple(x.shape)}")
+    m, k = x_flat.shape
+    grad_x = torch.empty((m, k), device=x.device, dtype=x_flat.dtype)
+    nat.call("rk_gelu_backward", gy.data_ptr(), nat.dtype_code(gy.dtype), gy.stride(0),
+             x_flat.data_ptr(), nat.dtype_code(x_flat.dtype), x_flat.stride(0), m, k,
+             grad_x.data_ptr(), grad_x.stride(0), nat.stream_handle(x.device))
+    return grad_x.to(x.dtype).reshape(x.shape)

@@ -241,3 +241,26 @@ def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = No
              q.data_ptr(), _ld(q), s.contiguous().data_ptr(), m, n, k, work.data_ptr(), splits,
              out.data_ptr(), _ld(out), nat.stream_handle(grad.device))
     return out
+
+
+def grad_weight_bf16_x(grad: Tensor, x: Tensor, nsplit: int | None = None, *,
+                       out: Tensor | None = None, work: Tensor | None = None) -> Tensor:
+    """Gw = bf16(bf16(grad)^T @ bf16(x)) as [N, K] bf16, for activations x [M, K] given
+    directly (float32 or bfloat16): the non-fused BF16 grad_weight of ratchet.py:159-163
+    (``grad_out_tile.to(bf16) @ flat_inputs.to(bf16)``), or the fused one on a
+    dequantized copy (dequant_bf16). ``work`` / ``out`` as in grad_weight_bf16."""
+    m, n = grad.shape
+    k = x.shape[1]
+    if grad.stride(-1) != 1:
+        grad = grad.contiguous()
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
+    if work is None:
+        work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
+    if out is None:
+        out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
+    nat.call("rk_grad_weight_bf16_x", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
+             x.data_ptr(), nat.dtype_code(x.dtype), _ld(x), m, n, k, work.data_ptr(), splits,
+             out.data_ptr(), _ld(out), nat.stream_handle(grad.device))
+    return out

@@ -39,6 +39,7 @@ from .int8_matmul import (
     dequant_transpose_bf16,
     effective_bf16,
     grad_weight_bf16,
+    grad_weight_bf16_x,
     int8_mm_nt,
     packed_int8_mm,
     quantize_rows_into,
@@ -134,12 +135,14 @@ class RatchetAuditReport:
     violations: tuple[str, ...]
 
 
-def _grad_weight_supported(g: Tensor, q: Tensor) -> bool:
-    """Shapes the direct int8-activation grad_weight kernel takes (rk_grad_weight_bf16)."""
-    n, k = g.shape[1], q.shape[1]
-    return (n % 8 == 0 and k % 16 == 0 and g.stride(-1) == 1 and q.stride(-1) == 1
-            and (g.stride(0) * g.element_size()) % 16 == 0 and q.stride(0) % 16 == 0
-            and g.data_ptr() % 16 == 0 and q.data_ptr() % 16 == 0)
+def _grad_weight_supported(g: Tensor, x: Tensor) -> bool:
+    """Shapes the direct grad_weight kernels take (rk_grad_weight_bf16 on int8
+    activations, rk_grad_weight_bf16_x on float32 / bfloat16 ones)."""
+    n, k = g.shape[1], x.shape[1]
+    return (n % 8 == 0 and k % 16 == 0 and g.stride(-1) == 1 and x.stride(-1) == 1
+            and (g.stride(0) * g.element_size()) % 16 == 0
+            and (x.stride(0) * x.element_size()) % 16 == 0
+            and g.data_ptr() % 16 == 0 and x.data_ptr() % 16 == 0)
 
 
 # ---------------------------------------------------------------------------
@@ -215,7 +218,7 @@ class _RatchetMatmul(torch.autograd.Function):
             inputs_fp32 = None
         else:
             flat_inputs, scale = ctx.saved_tensors
-            inputs_bf16 = flat_inputs.to(torch.bfloat16) if mode != "fp32" else None
+            inputs_bf16 = None  # bf16(inputs), made only where a path needs the copy
             inputs_fp32 = flat_inputs.to(torch.float32) if mode == "fp32" else None
         flat_gradient = grad_output.flatten(0, -2)
         scale_d = scale.detach()
@@ -228,6 +231,8 @@ class _RatchetMatmul(torch.autograd.Function):
                 grad_input = gradient_fp32 @ effective
                 grad_weight_fp32 = gradient_fp32.t() @ inputs_fp32
             else:
+                if inputs_bf16 is None:
+                    inputs_bf16 = flat_inputs.to(torch.bfloat16)
                 gradient_bf16 = flat_gradient.to(torch.bfloat16)
                 effective = effective_bf16(packed, layer.max_code, scale_d)
                 grad_input = gradient_bf16 @ effective
@@ -252,8 +257,13 @@ class _RatchetMatmul(torch.autograd.Function):
                 g = g.float()
             grad_q = torch.empty((m, n), device=g.device, dtype=torch.int8)
             grad_s = torch.empty((m,), device=g.device, dtype=torch.float32)
+            if g.dtype == torch.float32 and _grad_weight_supported(g, ctx.saved_tensors[0]):
+                # The same pass writes bf16(g), the grad_weight GEMM's gradient operand
+                # (grad_out_tile.to(bf16), ratchet.py:162), so that GEMM reads 2-byte
+                # values instead of converting float32 ones.
+                gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
             quantize_rows_into(g, grad_q, grad_s, col_scale=scale_d.float().contiguous(),
-                               stochastic=True, seed=_sr_seed())
+                               stochastic=True, seed=_sr_seed(), bf16_out=gradient_bf16)
             code_t = unpack_transpose(packed, layer.max_code)
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
@@ -268,16 +278,25 @@ class _RatchetMatmul(torch.autograd.Function):
             # BF16 grad_weight [N, K] = bf16(g)^T @ bf16(x) (ratchet.py:159-163).
             g = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
                 else flat_gradient.float()
+            if gradient_bf16 is not None:
+                g = gradient_bf16  # the bf16 copy this backward already made
+            x_direct = None
+            if not ctx.used_fused_int8:
+                x_direct = flat_inputs if flat_inputs.dtype in (torch.float32, torch.bfloat16) \
+                    else flat_inputs.to(torch.bfloat16)
             if ctx.used_fused_int8 and _grad_weight_supported(g, q):
                 # straight from the saved int8 activations, no transposed copies
                 grad_weight = grad_weight_bf16(g, q, s)
+            elif x_direct is not None and _grad_weight_supported(g, x_direct):
+                # straight from the saved inputs (bf16 cast while staging)
+                grad_weight = grad_weight_bf16_x(g, x_direct)
             else:
                 # NT GEMM on transposed bf16 copies (both operands contiguous along tokens)
                 grad_t = transpose_bf16(g)
                 if ctx.used_fused_int8:
                     inputs_t = dequant_transpose_bf16(q, s)
                 else:
-                    inputs_t = transpose_bf16(inputs_bf16)
+                    inputs_t = transpose_bf16(x_direct)
                 grad_weight = grad_t @ inputs_t.t()
         grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \

@@ -19,6 +19,7 @@ from local_ai_training.int8_matmul import (
     dequant_transpose_bf16,
     effective_bf16,
     grad_weight_bf16,
+    grad_weight_bf16_x,
     int8_mm_nt,
     packed_int8_mm,
     quantize_columns,
@@ -505,6 +506,44 @@ def test_grad_weight_op_shape_within_tolerance_and_deterministic(cuda, gdtype):
     # the split count changes the summation grouping only within the tolerance
     one = grad_weight_bf16(gd, q, s, nsplit=1)
     assert bool(((one.float() - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 256, 128), (1000, 136, 48), (31, 8, 16)])
+@pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
+def test_grad_weight_x_bit_exact_when_every_sum_is_exact(cuda, m, n, k, xdtype):
+    # Activations given directly: x = integers * 2^-6 (exact in bf16), g = integers / 16,
+    # so every partial sum is exact and the result is the bf16 of the float64 sum.
+    rng = np.random.default_rng(m * 3 + n + k)
+    g = (rng.integers(-8, 9, size=(m, n)) / 16.0).astype(np.float32)
+    x = (rng.integers(-127, 128, size=(m, k)) / 64.0).astype(np.float32)
+    out = grad_weight_bf16_x(torch.from_numpy(g).to(cuda), torch.from_numpy(x).to(cuda).to(xdtype))
+    exact = g.astype(np.float64).T @ x.astype(np.float64)
+    assert np.array_equal(bits16(out), f32_to_bf16_bits(exact.astype(np.float32)))
+
+
+@pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
+def test_grad_weight_x_equals_the_int8_form_on_the_dequantized_copy(cuda, gdtype):
+    # Same operands, same tiling and summation order: the int8-activation entry point and
+    # the bf16-activation one on dequant_bf16(q, s) agree bit for bit at the op shape.
+    m, n, k = 16384, 2048, 512
+    g = (torch.randn(m, n, generator=gen(63)) * 1e-2).to(gdtype).to(cuda)
+    q, s = quantize_rows(torch.randn(m, k, generator=gen(64)).to(cuda))
+    fused = grad_weight_bf16(g, q, s)
+    direct = grad_weight_bf16_x(g, dequant_bf16(q, s))
+    assert torch.equal(fused.view(torch.int16), direct.view(torch.int16))
+
+
+def test_grad_weight_x_rounds_float32_activations_to_nearest_even(cuda):
+    # Float32 activations are rounded to bf16 while staging: identical to passing the
+    # RNE-cast bf16 copy, for values that are not bf16-representable.
+    m, n, k = 2048, 512, 256
+    g = (torch.randn(m, n, generator=gen(65)) * 1e-2).to(cuda)
+    x = torch.randn(m, k, generator=gen(66)).to(cuda)
+    a = grad_weight_bf16_x(g, x)
+    b = grad_weight_bf16_x(g, x.to(torch.bfloat16))
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    ref = g.to(torch.bfloat16).float().t() @ x.to(torch.bfloat16).float()
+    assert bool(((a.float() - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
 
 
 def test_grad_weight_rejects_unaligned_shapes(cuda):

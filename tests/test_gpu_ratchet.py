@@ -11,7 +11,7 @@ import pytest
 import torch
 from torch import nn
 
-from local_ai_training.int8_matmul import quantize_rows
+from local_ai_training.int8_matmul import grad_weight_bf16, grad_weight_bf16_x, quantize_rows
 from local_ai_training.ratchet import (
     DiscreteRatchetLinear,
     audit_no_master_weights,
@@ -297,6 +297,62 @@ def test_trainable_scale_receives_gradient_and_stays_master_weight_free(cuda):
     layer.ratchet_update()
     optimizer.step()
     assert not torch.equal(layer.scale.detach(), before) and torch.all(layer.scale > 0)
+
+
+def test_float32_gradient_grad_weight_from_the_quant_pass_bf16_copy(cuda):
+    """A float32 upstream gradient reaches grad_weight as the bf16 copy the SR-quant pass
+    writes; the update must receive exactly what the grad_weight kernel gives when it
+    converts the float32 gradient itself (both round to nearest even)."""
+    m, k, n = 1024, 512, 768
+    torch.manual_seed(5)
+    layer = DiscreteRatchetLinear(k, n, max_code=2, matmul_mode="int8", int8_backward=True,
+                                  fuse_backward_update=True).to(cuda).train()
+    captured = {}
+    original = layer._launch_update
+
+    def capture(gradient, *rest):
+        captured["gw"] = gradient.detach().clone()
+        return original(gradient, *rest)
+
+    layer._launch_update = capture
+    data = torch.Generator().manual_seed(8)
+    x = torch.randn(m, k, generator=data).to(cuda)
+    g = (torch.randn(m, n, generator=data) * 1e-2).to(cuda)
+    q, s = quantize_rows(x)
+    out = layer(x.clone().requires_grad_(True), inputs_int8=q, inputs_scale=s)
+    assert out.dtype == torch.float32
+    out.backward(g)
+    want = grad_weight_bf16(g, q, s)
+    assert torch.equal(captured["gw"].view(torch.int16), want.view(torch.int16))
+
+
+def test_unfused_int8_layer_grad_weight_reads_the_saved_inputs(cuda):
+    """Without pre-quantized inputs (the lm_head case) grad_weight is bf16(g)^T @ bf16(x)
+    on the saved float32 inputs (ratchet.py:159-163); the update must receive exactly the
+    direct-activation kernel's result, which matches an fp32 product of the same bf16
+    operands at rel 1e-2 / abs 1e-3."""
+    m, k, n = 2048, 512, 1024
+    torch.manual_seed(6)
+    layer = DiscreteRatchetLinear(k, n, max_code=2, matmul_mode="int8",
+                                  fuse_backward_update=True).to(cuda).train()
+    captured = {}
+    original = layer._launch_update
+
+    def capture(gradient, *rest):
+        captured["gw"] = gradient.detach().clone()
+        return original(gradient, *rest)
+
+    layer._launch_update = capture
+    data = torch.Generator().manual_seed(9)
+    x = torch.randn(m, k, generator=data).to(cuda)
+    g = torch.randn(m, n, generator=data).to(cuda) * 1e-2
+    out = layer(x.clone().requires_grad_(True))
+    out.backward(g)
+    want = grad_weight_bf16_x(g.to(torch.bfloat16), x)
+    assert torch.equal(captured["gw"].view(torch.int16), want.view(torch.int16))
+    ref = g.to(torch.bfloat16).float().t() @ x.to(torch.bfloat16).float()
+    got = captured["gw"].float()
+    assert bool(((got - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
 
 
 def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
