@@ -47,6 +47,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Four packed ratchet bytes -> four int8 codes: (byte & 15) - max_code per byte,
+// computed without inter-byte borrows (each byte biased by 0x80). mc4 = max_code *
+// 0x01010101.
+__device__ __forceinline__ uint32_t decode4(uint32_t w, uint32_t mc4) {
+  return (((w & 0x0F0F0F0Fu) | 0x80808080u) - mc4) ^ 0x80808080u;
+}
+
 // Elements per 16-byte vector for a dtype code.
 template <int DT>
 struct Vec;

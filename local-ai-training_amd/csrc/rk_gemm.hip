@@ -46,12 +46,6 @@ struct GemmArgs {
   int64_t M, N, K;
 };
 
-// Four packed bytes -> four int8 codes: byte - max_code on the low nibble,
-// computed without inter-byte borrows (each lane biased by 0x80).
-__device__ __forceinline__ uint32_t decode4(uint32_t w, uint32_t mc4) {
-  return (((w & 0x0F0F0F0Fu) | 0x80808080u) - mc4) ^ 0x80808080u;
-}
-
 // Loads the 16-byte segment (row, k0 .. k0+15) of an operand; zeros outside
 // [0, rows) x [0, K). FAST: K % 64 == 0, ld % 16 == 0, 16-byte aligned base.
 template <bool FAST, int KIND>
@@ -363,20 +357,32 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   if constexpr (S > 2) ring_load(r2, a_src, b_src, static_cast<int64_t>(min(2, last)) * BK);
   if constexpr (S > 3) ring_load(r3, a_src, b_src, static_cast<int64_t>(min(3, last)) * BK);
 
-#define RK_M32_STEP(R, KT)                                                                  \
+  // Full groups of S k-steps run without a branch around the MFMAs (one basic block per
+  // group, so the scheduler can overlap a step's MFMAs with the next step's staging);
+  // a final partial group (nk % S != 0) checks each step. Loads past the last k-step
+  // re-read the last tile and are never consumed.
+#define RK_M32_STEP(R, KT, GUARD)                                                           \
   {                                                                                         \
     const int kt_ = (KT);                                                                   \
     const int buf_ = kt_ & 1;                                                               \
     ring_store<KIND>(R, As + buf_ * BM * BK, Bs + buf_ * BN * BK, a_dst, b_dst, g.mc4);     \
     ring_load(R, a_src, b_src, static_cast<int64_t>(min(kt_ + S, last)) * BK);              \
     __syncthreads();                                                                        \
-    if (kt_ < nk) mfma32_step(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0, brow0, lane); \
+    if (!(GUARD) || kt_ < nk)                                                               \
+      mfma32_step(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0, brow0, lane);       \
   }
-  for (int kb = 0; kb < nk; kb += S) {
-    RK_M32_STEP(r0, kb)
-    if constexpr (S > 1) RK_M32_STEP(r1, kb + 1)
-    if constexpr (S > 2) RK_M32_STEP(r2, kb + 2)
-    if constexpr (S > 3) RK_M32_STEP(r3, kb + 3)
+  const int nk_full = nk - nk % S;
+  for (int kb = 0; kb < nk_full; kb += S) {
+    RK_M32_STEP(r0, kb, false)
+    if constexpr (S > 1) RK_M32_STEP(r1, kb + 1, false)
+    if constexpr (S > 2) RK_M32_STEP(r2, kb + 2, false)
+    if constexpr (S > 3) RK_M32_STEP(r3, kb + 3, false)
+  }
+  if (nk_full < nk) {
+    RK_M32_STEP(r0, nk_full, true)
+    if constexpr (S > 1) RK_M32_STEP(r1, nk_full + 1, true)
+    if constexpr (S > 2) RK_M32_STEP(r2, nk_full + 2, true)
+    if constexpr (S > 3) RK_M32_STEP(r3, nk_full + 3, true)
   }
 #undef RK_M32_STEP
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer

@@ -63,6 +63,53 @@ __global__ __launch_bounds__(256) void unpack_transpose_kernel(const uint8_t* pa
   }
 }
 
+// Aligned form (N % 16 == 0, K % 16 == 0, 16-byte aligned rows): a 64 x 64 tile per
+// block; each thread loads one 16-byte piece of a packed row (16 k values of one n),
+// decodes it four bytes at a time, and after the tile is in LDS gathers one 16-byte
+// piece of a codeT row (16 n values of one k). LDS rows are 68 bytes: the 16 rows a
+// wave gathers from at once (16 c + i, c = 0..3) then start 16 banks apart.
+__global__ __launch_bounds__(256) void unpack_transpose_vec_kernel(const uint8_t* packed,
+                                                                   int64_t ldp, uint32_t mc4,
+                                                                   int8_t* codeT, int64_t ldt,
+                                                                   int64_t N, int64_t K) {
+  constexpr int P = 68;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64 * P];
+  const int64_t tiles_k = (K + 63) / 64;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) / tiles_k) * 64;
+  const int64_t k0 = (static_cast<int64_t>(blockIdx.x) % tiles_k) * 64;
+  const int t = threadIdx.x;
+  {
+    const int r = t >> 2, seg = t & 3;
+    const int64_t n = n0 + r, k = k0 + 16 * seg;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (n < N && k < K) {
+      v = *reinterpret_cast<const uint4*>(packed + n * ldp + k);
+      v = make_uint4(decode4(v.x, mc4), decode4(v.y, mc4), decode4(v.z, mc4),
+                     decode4(v.w, mc4));
+    }
+    uint32_t* row = reinterpret_cast<uint32_t*>(tile + r * P + 16 * seg);
+    row[0] = v.x;
+    row[1] = v.y;
+    row[2] = v.z;
+    row[3] = v.w;
+  }
+  __syncthreads();
+  const int kk = t >> 2, c = t & 3;
+  const int64_t k = k0 + kk, n = n0 + 16 * c;
+  if (k < K && n < N) {
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        x |= static_cast<uint32_t>(tile[(16 * c + 4 * q + b) * P + kk]) << (8 * b);
+      w[q] = x;
+    }
+    *reinterpret_cast<uint4*>(codeT + k * ldt + n) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 __global__ void effective_bf16_kernel(const uint8_t* packed, int64_t ldp, int mc,
                                       const float* scale, uint16_t* W, int64_t ldw, int64_t N,
                                       int64_t K) {
@@ -189,8 +236,14 @@ extern "C" int rk_unpack_transpose(const uint8_t* packed, int64_t ldp, int max_c
   if (ldp < K || ldt < N) return fail(RK_ERR_ARG, "leading dimension too small");
   const int64_t tiles = ((N + 63) / 64) * ((K + 63) / 64);
   if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
-  unpack_transpose_kernel<<<static_cast<unsigned>(tiles), 256, 0, as_stream(stream)>>>(
-      packed, ldp, max_code, codeT, ldt, N, K);
+  if (N % 16 == 0 && K % 16 == 0 && ldp % 16 == 0 && ldt % 16 == 0 && aligned16(packed) &&
+      aligned16(codeT)) {
+    unpack_transpose_vec_kernel<<<static_cast<unsigned>(tiles), 256, 0, as_stream(stream)>>>(
+        packed, ldp, static_cast<uint32_t>(max_code) * 0x01010101u, codeT, ldt, N, K);
+  } else {
+    unpack_transpose_kernel<<<static_cast<unsigned>(tiles), 256, 0, as_stream(stream)>>>(
+        packed, ldp, max_code, codeT, ldt, N, K);
+  }
   return launch_status("unpack_transpose");
 }
 

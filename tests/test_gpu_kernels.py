@@ -266,6 +266,19 @@ def test_forward_gemm_full_op_shape_bit_exact(cuda):
     assert np.array_equal(bits16(out), ref)
 
 
+@pytest.mark.parametrize("n,k", [(2048, 512), (1040, 528), (64, 48), (16, 16), (37, 45),
+                                 (130, 64)])
+@pytest.mark.parametrize("mc", [1, 2, 3, 7])
+def test_unpack_transpose_matches_oracle(cuda, n, k, mc):
+    # Aligned shapes (n, k multiples of 16) take the 16-byte decode/gather kernel, partial
+    # 64 x 64 tiles included; the others the element-wise one.
+    packed, _ = synthetic_state(n, k, mc, seed=n + k + mc)
+    code_t = unpack_transpose(torch.from_numpy(packed).to(cuda), mc)
+    code, _ = oupd.unpack(packed, mc)
+    assert code_t.shape == (k, n)
+    assert np.array_equal(code_t.cpu().numpy(), code.T)
+
+
 def test_grad_input_gemm_full_op_shape_bit_exact(cuda):
     # int8 grad_input: A = SR-quantized gradient [M, N_out], B = code^T [K_in, N_out].
     m, n_out, k_in, mc = 16384, 2048, 512, 2
