@@ -47,6 +47,20 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Raw buffer descriptor (stride 0) over [base, base + bytes), gfx9 data format word.
+// Loads past `bytes` return zeros and stores past it are dropped, which replaces
+// per-lane bounds checks at tile edges. The inputs are made wave-uniform explicitly:
+// 64-bit address arithmetic runs on the vector unit, and a descriptor left in vector
+// registers turns every buffer access into a waterfall loop. bytes < 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buffer(const void* base, int64_t bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
+  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, n, 0x00020000);
+}
+
 // Four packed ratchet bytes -> four int8 codes: (byte & 15) - max_code per byte,
 // computed without inter-byte borrows (each byte biased by 0x80). mc4 = max_code *
 // 0x01010101.

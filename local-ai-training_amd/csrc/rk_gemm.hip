@@ -10,8 +10,8 @@
 //
 // Two kernels:
 //  * int8_gemm_m32_kernel, for aligned shapes (K % 64 == 0, 16-byte aligned rows and
-//    scales, N % 8 == 0): v_mfma_i32_32x32x32_i8, 128 x 128 block tiles, register
-//    ring + LDS ping-pong, LDS-staged coalesced epilogue;
+//    scales, N % 8 == 0): v_mfma_i32_32x32x32_i8, 128 x 128 block tiles, buffer
+//    addressing, register ring + LDS ping-pong, LDS-staged coalesced epilogue;
 //  * int8_gemm_nt_kernel, any shape and stride (ragged K, unaligned rows):
 //    v_mfma_i32_16x16x64_i8 with bounds-checked staging.
 // Block order is XCD-aware: consecutive tile indices (which share an A row panel)
@@ -232,41 +232,10 @@ struct RingSlot {
   u32x4 b[NB];
 };
 
-template <int NA, int NB>
-__device__ __forceinline__ void ring_load(RingSlot<NA, NB>& r, const uint8_t* const (&a_src)[NA],
-                                          const uint8_t* const (&b_src)[NB], int64_t off) {
-#pragma unroll
-  for (int j = 0; j < NA; ++j) r.a[j] = *reinterpret_cast<const u32x4*>(a_src[j] + off);
-#pragma unroll
-  for (int j = 0; j < NB; ++j) r.b[j] = *reinterpret_cast<const u32x4*>(b_src[j] + off);
-  // Keep ring slots in issue order: a slot's loads must not be scheduled behind later
-  // slots' loads, or waiting for this slot would wait for everything in flight.
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int KIND, int NA, int NB>
-__device__ __forceinline__ void ring_store(const RingSlot<NA, NB>& r, uint8_t* at, uint8_t* bt,
-                                           const int (&a_dst)[NA], const int (&b_dst)[NB],
-                                           uint32_t mc4) {
-#pragma unroll
-  for (int j = 0; j < NA; ++j) *reinterpret_cast<u32x4*>(at + a_dst[j]) = r.a[j];
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
-    u32x4 v = r.b[j];
-    if constexpr (KIND == B_PACKED) {
-      v.x = decode4(v.x, mc4);
-      v.y = decode4(v.y, mc4);
-      v.z = decode4(v.z, mc4);
-      v.w = decode4(v.w, mc4);
-    }
-    *reinterpret_cast<u32x4*>(bt + b_dst[j]) = v;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // 32x32x32 MFMA kernel (aligned shapes): block tile 128 x 128, 4 wavefronts in 2 x 2,
 // wave tile 64 x 64 = 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (two per 64-byte k-step),
-// register ring of S k-steps, LDS ping-pong, one barrier per k-step.
+// register ring of 2 k-steps, LDS ping-pong, one barrier per k-step.
 //
 // The 32x32x32 form issues half as many MFMAs per MAC as 16x16x64 and sustained
 // 4.3-4.5 POP/s in register-resident MFMA chains on MI355X (16x16x64: at most ~3.4).
@@ -302,14 +271,26 @@ __device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j][kh], fa[i][kh], acc[i][j], 0, 0, 0);
 }
 
-template <int KIND, int CDT, int S, bool HAS_RS>
+//
+// The instructions outside the MFMAs bound this kernel at K = 512 (8 k-steps per tile),
+// so it is written to keep them few:
+//  * A, B, ls, rs and C are addressed through buffer descriptors over the block's rows:
+//    rows past M or N read as zeros and their stores are dropped, so there are no
+//    clamps or bounds branches, per-thread offsets are fixed and a k-step only moves a
+//    scalar offset;
+//  * the epilogue stages bf16 results in LDS rows of 264 bytes: the 32 rows of one
+//    8-byte fragment write start 2 banks apart, and a 16-lane row of the 16-byte
+//    copy-out covers 64 banks, so neither side needs a swizzle or a lane swap;
+//  * each thread copies out a fixed 8-column chunk, so the column bound is one compare.
+// ---------------------------------------------------------------------------
+template <int KIND, int CDT, bool HAS_RS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void int8_gemm_m32_kernel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128, BK = 64;
-  constexpr int A_SEGS = BM * BK / 16 / 256;
-  constexpr int B_SEGS = BN * BK / 16 / 256;
-  constexpr int TILE_BYTES = 2 * (BM + BN) * BK;  // 32 KB ping-pong operand tiles
-  __shared__ __attribute__((aligned(16))) uint8_t smem[TILE_BYTES];
+  constexpr int BM = 128, BN = 128, BK = 64, S = 2;
+  constexpr int SEGS = BM * BK / 16 / 256;  // 16-byte pieces per thread per operand (2)
+  constexpr int EPITCH = BN * 2 + 8;        // epilogue staging row, bytes
+  constexpr int SMEM = BM * EPITCH > 2 * (BM + BN) * BK ? BM * EPITCH : 2 * (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   uint8_t* As = smem;
   uint8_t* Bs = smem + 2 * BM * BK;
 
@@ -319,6 +300,8 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
   const int64_t m0 = (b / tiles_n) * BM;
   const int64_t n0 = (b % tiles_n) * BN;
+  const int64_t rows_a = g.M - m0 < BM ? g.M - m0 : BM;
+  const int64_t rows_b = g.N - n0 < BN ? g.N - n0 : BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -326,22 +309,51 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   const int wm = wave & 1, wn = wave >> 1;
   const int arow0 = wm * 64, brow0 = wn * 64;
 
-  const uint8_t* Ab = reinterpret_cast<const uint8_t*>(g.A);
-  const uint8_t* a_src[A_SEGS];
-  const uint8_t* b_src[B_SEGS];
-  int a_dst[A_SEGS], b_dst[B_SEGS];
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      make_buffer(g.A + m0 * g.lda, (rows_a - 1) * g.lda + g.K);
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_buffer(g.B + n0 * g.ldb, (rows_b - 1) * g.ldb + g.K);
+  int a_voff[SEGS], b_voff[SEGS], st_off[SEGS];
 #pragma unroll
-  for (int j = 0; j < A_SEGS; ++j) {
+  for (int j = 0; j < SEGS; ++j) {
     const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
-    a_src[j] = Ab + min(m0 + row, g.M - 1) * g.lda + 16 * seg;
-    a_dst[j] = row * BK + 16 * (seg ^ swz32(row));
+    a_voff[j] = row * static_cast<int>(g.lda) + 16 * seg;
+    b_voff[j] = row * static_cast<int>(g.ldb) + 16 * seg;
+    st_off[j] = row * BK + 16 * (seg ^ swz32(row));
   }
+
+  RingSlot<SEGS, SEGS> ring[S];
+  auto load = [&](RingSlot<SEGS, SEGS>& r, int kt) {
 #pragma unroll
-  for (int j = 0; j < B_SEGS; ++j) {
-    const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
-    b_src[j] = g.B + min(n0 + row, g.N - 1) * g.ldb + 16 * seg;
-    b_dst[j] = row * BK + 16 * (seg ^ swz32(row));
-  }
+    for (int j = 0; j < SEGS; ++j)
+      r.a[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             a_rsrc, a_voff[j], kt * BK, 0));
+#pragma unroll
+    for (int j = 0; j < SEGS; ++j)
+      r.b[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             b_rsrc, b_voff[j], kt * BK, 0));
+  };
+  auto store = [&](RingSlot<SEGS, SEGS>& r, int buf) {
+    // Pin the slot here (see the grad_weight kernel): otherwise the decode of every slot
+    // is computed as soon as its load is issued and the wait covers the whole ring.
+#pragma unroll
+    for (int j = 0; j < SEGS; ++j) asm volatile("" : "+v"(r.a[j]), "+v"(r.b[j]));
+    uint8_t* at = As + buf * BM * BK;
+    uint8_t* bt = Bs + buf * BN * BK;
+#pragma unroll
+    for (int j = 0; j < SEGS; ++j) *reinterpret_cast<u32x4*>(at + st_off[j]) = r.a[j];
+#pragma unroll
+    for (int j = 0; j < SEGS; ++j) {
+      u32x4 v = r.b[j];
+      if constexpr (KIND == B_PACKED) {
+        v.x = decode4(v.x, g.mc4);
+        v.y = decode4(v.y, g.mc4);
+        v.z = decode4(v.z, g.mc4);
+        v.w = decode4(v.w, g.mc4);
+      }
+      *reinterpret_cast<u32x4*>(bt + st_off[j]) = v;
+    }
+  };
 
   v16i acc[2][2];
 #pragma unroll
@@ -349,117 +361,108 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
 
+  // Ring of S = 2 k-steps (registers) over an LDS ping-pong: the loads of step kt + 2 are
+  // issued right after step kt is written to LDS. Pairs of k-steps run without a branch;
+  // an odd last step follows. Loads past the last k-step are never consumed (past the
+  // last row's end they read zeros, elsewhere the next row: always in bounds).
   const int nk = static_cast<int>(g.K / BK);
-  const int last = nk - 1;
-  RingSlot<A_SEGS, B_SEGS> r0, r1, r2, r3;
-  ring_load(r0, a_src, b_src, 0);
-  if constexpr (S > 1) ring_load(r1, a_src, b_src, static_cast<int64_t>(min(1, last)) * BK);
-  if constexpr (S > 2) ring_load(r2, a_src, b_src, static_cast<int64_t>(min(2, last)) * BK);
-  if constexpr (S > 3) ring_load(r3, a_src, b_src, static_cast<int64_t>(min(3, last)) * BK);
-
-  // Full groups of S k-steps run without a branch around the MFMAs (one basic block per
-  // group, so the scheduler can overlap a step's MFMAs with the next step's staging);
-  // a final partial group (nk % S != 0) checks each step. Loads past the last k-step
-  // re-read the last tile and are never consumed.
-#define RK_M32_STEP(R, KT, GUARD)                                                           \
-  {                                                                                         \
-    const int kt_ = (KT);                                                                   \
-    const int buf_ = kt_ & 1;                                                               \
-    ring_store<KIND>(R, As + buf_ * BM * BK, Bs + buf_ * BN * BK, a_dst, b_dst, g.mc4);     \
-    ring_load(R, a_src, b_src, static_cast<int64_t>(min(kt_ + S, last)) * BK);              \
-    __syncthreads();                                                                        \
-    if (!(GUARD) || kt_ < nk)                                                               \
-      mfma32_step(acc, As + buf_ * BM * BK, Bs + buf_ * BN * BK, arow0, brow0, lane);       \
+  load(ring[0], 0);
+  __builtin_amdgcn_sched_barrier(0);
+  load(ring[1], 1);
+  __builtin_amdgcn_sched_barrier(0);
+  const int nk_pairs = nk & ~1;
+  for (int kb = 0; kb < nk_pairs; kb += S) {
+#pragma unroll
+    for (int slot = 0; slot < S; ++slot) {
+      store(ring[slot], slot);
+      load(ring[slot], kb + slot + S);
+      __syncthreads();
+      mfma32_step(acc, As + slot * BM * BK, Bs + slot * BN * BK, arow0, brow0, lane);
+    }
   }
-  const int nk_full = nk - nk % S;
-  for (int kb = 0; kb < nk_full; kb += S) {
-    RK_M32_STEP(r0, kb, false)
-    if constexpr (S > 1) RK_M32_STEP(r1, kb + 1, false)
-    if constexpr (S > 2) RK_M32_STEP(r2, kb + 2, false)
-    if constexpr (S > 3) RK_M32_STEP(r3, kb + 3, false)
+  if (nk & 1) {
+    store(ring[0], 0);
+    __syncthreads();
+    mfma32_step(acc, As, Bs, arow0, brow0, lane);
   }
-  if (nk_full < nk) {
-    RK_M32_STEP(r0, nk_full, true)
-    if constexpr (S > 1) RK_M32_STEP(r1, nk_full + 1, true)
-    if constexpr (S > 2) RK_M32_STEP(r2, nk_full + 2, true)
-    if constexpr (S > 3) RK_M32_STEP(r3, nk_full + 3, true)
-  }
-#undef RK_M32_STEP
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer
 
-  // Epilogue: (acc * ls) * rs -> bf16 into a [128][128] bf16 staging tile (32 KB) whose
-  // 8-byte units are XOR-swizzled by (row & 31) (conflict-free 32-row writes), then
-  // 16-byte coalesced copy-out (a lane re-orders the two 8-byte halves of its chunk
-  // when the row's swizzle flips unit parity). fp32 output widens the bf16 value.
-  constexpr int PITCH = BN * 2;       // bytes per staged row
-  constexpr int UNITS = PITCH / 8;    // 8-byte units per row (32)
+  // Epilogue. acc[i][j][e]: row m = arow0 + 32 i + (lane & 31), columns
+  // n = brow0 + 32 j + 8 q + 4 (lane >> 5) + (e % 4), q = e / 4.
   const int r32 = lane & 31, hh = lane >> 5;
+  const __amdgpu_buffer_rsrc_t ls_rsrc = make_buffer(g.ls + m0, rows_a * 4);
   float lsv[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) lsv[i] = g.ls[min(m0 + arow0 + i * 32 + r32, g.M - 1)];
+  for (int i = 0; i < 2; ++i)
+    lsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           ls_rsrc, (arow0 + 32 * i + r32) * 4, 0, 0));
+  float4 rs4[2][4];
+  if constexpr (HAS_RS) {
+    const __amdgpu_buffer_rsrc_t rs_rsrc = make_buffer(g.rs + n0, rows_b * 4);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int col = brow0 + j * 32 + 8 * q + 4 * hh;  // first of 4 columns
-      float4 rs4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
-      if constexpr (HAS_RS) rs4 = *reinterpret_cast<const float4*>(g.rs + min(n0 + col, g.N - 4));
+      for (int q = 0; q < 4; ++q)
+        rs4[j][q] = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(
+                        rs_rsrc, (brow0 + 32 * j + 8 * q + 4 * hh) * 4, 0, 0));
+  }
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = arow0 + i * 32 + r32;
+  for (int i = 0; i < 2; ++i) {
+    uint8_t* srow = smem + (arow0 + 32 * i + r32) * EPITCH;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
         float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
         float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
         float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
         float v3 = static_cast<float>(acc[i][j][4 * q + 3]) * lsv[i];
         if constexpr (HAS_RS) {
-          v0 = v0 * rs4.x;
-          v1 = v1 * rs4.y;
-          v2 = v2 * rs4.z;
-          v3 = v3 * rs4.w;
+          v0 = v0 * rs4[j][q].x;
+          v1 = v1 * rs4[j][q].y;
+          v2 = v2 * rs4[j][q].z;
+          v3 = v3 * rs4[j][q].w;
         }
-        const int unit = (col >> 2) ^ (row & 31);
-        *reinterpret_cast<uint2*>(smem + row * PITCH + unit * 8) =
+        *reinterpret_cast<uint2*>(srow + (brow0 + 32 * j + 8 * q + 4 * hh) * 2) =
             make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
       }
-    }
   }
   __syncthreads();
-  constexpr int CHUNKS = PITCH / 16;
+  constexpr int ES = CDT == RK_BF16 ? 2 : 4;
+  const int ch = tid & 15;  // 8-column chunk of this thread
+  if (n0 + 8 * ch < g.N) {
+    const __amdgpu_buffer_rsrc_t c_rsrc =
+        make_buffer(static_cast<char*>(g.C) + (m0 * g.ldc + n0) * ES,
+                    ((rows_a - 1) * g.ldc + (g.N - n0)) * ES);
 #pragma unroll
-  for (int c = tid; c < BM * CHUNKS; c += 256) {
-    const int row = c / CHUNKS, ch = c % CHUNKS;
-    const int64_t m = m0 + row;
-    const int64_t n = n0 + ch * 8;
-    if (m < g.M && n < g.N) {
-      const int u0 = (2 * ch) ^ (row & 31);  // staged unit of columns 8 ch .. 8 ch + 3
-      uint4 v = *reinterpret_cast<const uint4*>(smem + row * PITCH + (u0 & ~1) * 8);
-      if (u0 & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+    for (int it = 0; it < BM / 16; ++it) {
+      const int row = (tid >> 4) + 16 * it;
+      const uint8_t* src = smem + row * EPITCH + 16 * ch;
+      const uint2 lo = *reinterpret_cast<const uint2*>(src);
+      const uint2 hi = *reinterpret_cast<const uint2*>(src + 8);
+      const int voff = (row * static_cast<int>(g.ldc) + 8 * ch) * ES;
       if constexpr (CDT == RK_BF16) {
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.C) + m * g.ldc + n) = v;
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_rsrc, voff, 0, 0);
       } else {
-        float* out = static_cast<float*>(g.C) + m * g.ldc + n;
-        *reinterpret_cast<uint4*>(out) = make_uint4(v.x << 16, v.x & 0xffff0000u,
-                                                    v.y << 16, v.y & 0xffff0000u);
-        *reinterpret_cast<uint4*>(out + 4) = make_uint4(v.z << 16, v.z & 0xffff0000u,
-                                                        v.w << 16, v.w & 0xffff0000u);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(v4i, make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16,
+                                               lo.y & 0xffff0000u)),
+            c_rsrc, voff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(v4i, make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16,
+                                               hi.y & 0xffff0000u)),
+            c_rsrc, voff + 16, 0, 0);
       }
     }
   }
-  (void)UNITS;
 }
 
 template <int KIND, int CDT, bool HAS_RS>
-static void launch_m32(const GemmArgs& g, int stages, hipStream_t stream) {
+static void launch_m32(const GemmArgs& g, hipStream_t stream) {
   const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
-  const dim3 grid(static_cast<unsigned>(tiles)), block(256);
-  if (stages == 3) int8_gemm_m32_kernel<KIND, CDT, 3, HAS_RS><<<grid, block, 0, stream>>>(g);
-  else if (stages == 4) int8_gemm_m32_kernel<KIND, CDT, 4, HAS_RS><<<grid, block, 0, stream>>>(g);
-  else int8_gemm_m32_kernel<KIND, CDT, 2, HAS_RS><<<grid, block, 0, stream>>>(g);
-}
-
-static int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v ? atoi(v) : dflt;
+  int8_gemm_m32_kernel<KIND, CDT, HAS_RS><<<dim3(static_cast<unsigned>(tiles)), 256, 0, stream>>>(g);
 }
 
 template <int KIND, int CDT>
@@ -469,13 +472,16 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const int es = CDT == RK_BF16 ? 2 : 4;
   const bool aligned_out = fast && (g.N % 8) == 0 && ((g.ldc * es) % 16) == 0 &&
                            aligned16(g.C) && (g.rs == nullptr || aligned16(g.rs));
-  if (aligned_out) {
-    // Register-ring depth (2..4); every setting gives identical results.
-    static const int st_env = env_int("RK_GEMM_STAGES", 2);
+  // Buffer offsets are 32-bit: a block's furthest A/B load (128 rows, prefetch two
+  // k-steps past K) and C store (128 rows) must stay below 2^31 bytes.
+  const bool fits32 = 128 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
+                      128 * g.ldb + g.K + 256 < (int64_t{1} << 31) &&
+                      128 * g.ldc * es < (int64_t{1} << 31);
+  if (aligned_out && fits32) {
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
     if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
-    if (g.rs) launch_m32<KIND, CDT, true>(g, st_env, stream);
-    else launch_m32<KIND, CDT, false>(g, st_env, stream);
+    if (g.rs) launch_m32<KIND, CDT, true>(g, stream);
+    else launch_m32<KIND, CDT, false>(g, stream);
     return launch_status("int8_gemm");
   }
   const int64_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN);

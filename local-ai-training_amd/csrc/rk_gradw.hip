@@ -53,25 +53,12 @@ constexpr int GW_BM = 32;                  // tokens per pipeline step
 // rows start at banks 0, 16, 32, 48 and the second half adds 8, so the eight 8-bank
 // segments are disjoint.
 constexpr int GW_PITCH = GW_BN * 2 + 64;
-constexpr int kGwBufferWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (32-bit data)
 constexpr int kGwMaxRing = 6;
 
 __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   const bf2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
   return __builtin_bit_cast(uint32_t, v);
-}
-
-// Raw buffer descriptor (stride 0) over [base, base + bytes). The inputs are made
-// wave-uniform explicitly: the 64-bit arithmetic that produces them runs on the vector
-// unit, and a descriptor left in vector registers turns every load into a waterfall loop.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t gw_buffer(const void* base, int64_t bytes) {
-  const uint64_t addr = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32));
-  const int n = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-  void* p = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(p, 0, n, kGwBufferWord3);
 }
 
 // A [BM tokens][128 features] tile of an operand with ES-byte elements is read as
@@ -156,14 +143,14 @@ void grad_weight_partial_kernel(GwArgs a) {
   // loads exactly and waits only for the ring slot it consumes. Per-thread offsets are
   // fixed; the step advances a scalar offset. The host guarantees offsets < 2^31.
   const int64_t rows = m_end - m_begin;
-  const __amdgpu_buffer_rsrc_t g_rsrc = gw_buffer(
+  const __amdgpu_buffer_rsrc_t g_rsrc = make_buffer(
       static_cast<const char*>(a.g) + (m_begin * a.ldg + n0) * GE,
       rows > 0 ? ((rows - 1) * a.ldg + (a.N - n0)) * GE : 0);
-  const __amdgpu_buffer_rsrc_t x_rsrc = gw_buffer(
+  const __amdgpu_buffer_rsrc_t x_rsrc = make_buffer(
       static_cast<const char*>(a.x) + (m_begin * a.ldx + k0) * XE,
       rows > 0 ? ((rows - 1) * a.ldx + (a.K - k0)) * XE : 0);
   const __amdgpu_buffer_rsrc_t s_rsrc =
-      gw_buffer(XK == GW_X_Q8 ? a.s + m_begin : a.s, XK == GW_X_Q8 && rows > 0 ? rows * 4 : 0);
+      make_buffer(XK == GW_X_Q8 ? a.s + m_begin : a.s, XK == GW_X_Q8 && rows > 0 ? rows * 4 : 0);
   int g_voff[GV], g_lds[GV], x_voff[XV], x_lds[XV], s_voff[XV];
 #pragma unroll
   for (int j = 0; j < GV; ++j) {
