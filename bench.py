@@ -59,6 +59,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--no-graph", action="store_true",
                     help="time the eager autograd step instead of its HIP-graph replay")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run each op-step stage and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the HBM traffic summary from two rocprofv3 counter CSVs")
     return ap.parse_args()
 
 
@@ -128,8 +132,25 @@ def op_bench(args, device):
     return graph_s, eager_s, layer, x.detach(), g
 
 
-def kernel_breakdown(layer, x, g, iters: int):
-    """Average device time of each launch of one op step, HIP events on the launch stream."""
+def stage_work(m: int, n: int, k: int, g_elem: int) -> dict:
+    """Algorithmic work per launch of each op-step stage: name -> (kind, amount[, bytes]);
+    kind "bytes", "ops" (int8 MFMA) or "flops" (bf16 MFMA). Bytes count each operand
+    read once and each result written once."""
+    mnk2 = 2.0 * m * n * k
+    return {
+        "quant_rows": ("bytes", m * k * 2 + m * k + m * 4),
+        "fwd_gemm_packed": ("ops", mnk2, m * k + n * k + m * n * 2 + m * 4 + n * 4),
+        "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
+        "unpack_transpose": ("bytes", 2 * n * k),
+        "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
+        "grad_weight_bf16": ("flops", mnk2, m * n * g_elem + m * k + m * 4 + n * k * 2),
+        "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
+    }
+
+
+def op_stages(layer, x, g):
+    """The launches of one op step as separately callable stages (same shapes, buffers and
+    kernels as the autograd step), with each stage's algorithmic work (stage_work)."""
     import torch
 
     from local_ai_training import _native as nat
@@ -158,12 +179,14 @@ def kernel_breakdown(layer, x, g, iters: int):
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
     row_rms = torch.empty(n, dtype=torch.float32, device=dev)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    rms_mean = torch.empty((), dtype=torch.float32, device=dev)
     holder = {}
 
     def update():
         nat.call("rk_ratchet_update_grad", packed.data_ptr(), k, gw.data_ptr(), nat.RK_BF16, k,
                  n, k, MAX_CODE, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
-                 row_rms.data_ptr(), None, flag.data_ptr(), nat.stream_handle(dev))
+                 row_rms.data_ptr(), None, flag.data_ptr(), rms_mean.data_ptr(),
+                 nat.stream_handle(dev))
 
     stages = [
         ("quant_rows", lambda: quantize_rows_into(x, q, s)),
@@ -176,6 +199,15 @@ def kernel_breakdown(layer, x, g, iters: int):
         ("grad_weight_bf16", lambda: grad_weight_bf16(g, q, s, splits, out=gw, work=gw_work)),
         ("ratchet_update_grad", update),
     ]
+    work = stage_work(m, n, k, g.element_size())
+    return stages, work
+
+
+def kernel_breakdown(layer, x, g, iters: int):
+    """Average device time of each launch of one op step, HIP events on the launch stream."""
+    import torch
+
+    stages, work = op_stages(layer, x, g)
     for _, fn in stages:  # warm
         fn()
     torch.cuda.synchronize()
@@ -191,17 +223,6 @@ def kernel_breakdown(layer, x, g, iters: int):
     torch.cuda.synchronize()
     avg_ms = {name: sum(a.elapsed_time(b) for a, b in ev) / len(ev) for name, ev in events.items()}
 
-    mnk2 = 2.0 * m * n * k
-    work = {  # name: (kind, algorithmic amount per launch)
-        "quant_rows": ("bytes", m * k * 2 + m * k + m * 4),
-        "fwd_gemm_packed": ("ops", mnk2, m * k + n * k + m * n * 2 + m * 4 + n * 4),
-        "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
-        "unpack_transpose": ("bytes", 2 * n * k),
-        "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
-        "grad_weight_bf16": ("flops", mnk2, m * n * g.element_size() + m * k + m * 4
-                             + n * k * 2),
-        "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
-    }
     report = {}
     for name, ms in avg_ms.items():
         sec = ms * 1e-3
@@ -213,6 +234,7 @@ def kernel_breakdown(layer, x, g, iters: int):
             entry["hbm_frac"] = round(w[1] / sec / PEAK_HBM_BPS, 4)
         else:
             peak = PEAK_INT8_OPS if w[0] == "ops" else PEAK_BF16_FLOPS
+            entry["kind"] = "int8" if w[0] == "ops" else "bf16"
             entry["alg_ops"] = w[1]
             entry["alg_bytes"] = w[2]
             entry["TOPS"] = round(w[1] / sec / 1e12, 1)
@@ -225,29 +247,160 @@ def kernel_breakdown(layer, x, g, iters: int):
     return report
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic per launch from rocprofv3 counters. `--pmc-probe` runs each op-step stage
+# and a plain 256 MiB device copy a few times; run it once under
+# `rocprofv3 --pmc FETCH_SIZE` and once under `--pmc WRITE_SIZE`, then
+# `--traffic-summary FETCH_CSV WRITE_CSV` scales each stage's per-dispatch KiB by what the
+# same counter reads for the copy (bytes known) and writes the summary that the default
+# run reads for roofline.traffic.
+# ---------------------------------------------------------------------------
+TRAFFIC_FILE = REPO / "profiles" / f"op_step_M{M_TOK}_K{K_IN}_N{N_OUT}_hbm_traffic.md"
+COPY_BYTES = 256 << 20
+# rocprofv3 kernel-name fragments of each stage's launches (summed per launch)
+STAGE_KERNELS = {
+    "quant_rows": ["quant_rows_kernel<1, 0, false"],
+    "fwd_gemm_packed": ["int8_gemm_m32_kernel<1,"],
+    "sr_quant_rows": ["quant_rows_kernel<1, 0, true"],
+    "unpack_transpose": ["unpack_transpose"],
+    "grad_input_gemm": ["int8_gemm_m32_kernel<0,"],
+    "grad_weight_bf16": ["grad_weight_partial_kernel", "grad_weight_reduce_kernel"],
+    "ratchet_update_grad": ["ratchet_update_grad_kernel"],
+}
+PROBE_REPEATS = 5
+
+
+def pmc_probe(device) -> None:
+    import torch
+
+    layer, x, g = synthetic_layer(device)
+    stages, _ = op_stages(layer, x, g)
+    for _, fn in stages:
+        fn()
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(PROBE_REPEATS):
+        for _, fn in stages:
+            fn()
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"pmc probe: {PROBE_REPEATS} x {len(stages)} stages + {COPY_BYTES} B copy")
+
+
+def _per_dispatch_kib(csv_path: str, counter: str) -> list[tuple[str, float]]:
+    import csv
+
+    rows = []
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter:
+                rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    rows.sort()
+    return [(name, kib) for _, name, kib in rows]
+
+
+def _stage_means(rows: list[tuple[str, float]]) -> tuple[dict, float]:
+    """Mean KiB per launch of each stage (its kernels summed), and of the copy."""
+    sums = {name: 0.0 for name in STAGE_KERNELS}
+    copies = [kib for name, kib in rows if "copy" in name.lower() and "rk::" not in name]
+    # the calibration copies (setup copies of small tensors excluded)
+    copy = [kib for kib in copies if kib >= 0.25 * max(copies, default=0.0)]
+    for name, kib in rows:
+        for stage, frags in STAGE_KERNELS.items():
+            if any(f in name for f in frags):
+                sums[stage] += kib
+    warm = 1  # the first launch of each stage precedes the timed repeats
+    return {k: v / (PROBE_REPEATS + warm) for k, v in sums.items()}, sum(copy) / max(len(copy), 1)
+
+
+def traffic_summary(fetch_csv: str, write_csv: str) -> dict:
+    fetch, fcopy = _stage_means(_per_dispatch_kib(fetch_csv, "FETCH_SIZE"))
+    write, wcopy = _stage_means(_per_dispatch_kib(write_csv, "WRITE_SIZE"))
+    f_scale = fcopy * 1024 / COPY_BYTES
+    w_scale = wcopy * 1024 / COPY_BYTES
+    work = stage_work(M_TOK, N_OUT, K_IN, 2)  # the op step's gradient is bfloat16
+    alg = {name: w[2] if len(w) > 2 else w[1] for name, w in work.items()}
+    kernels = {}
+    for stage in STAGE_KERNELS:
+        fb = fetch[stage] * 1024 / f_scale
+        wb = write[stage] * 1024 / w_scale
+        kernels[stage] = {"fetch_bytes": round(fb), "write_bytes": round(wb),
+                          "traffic_bytes": round(fb + wb), "alg_bytes": alg[stage],
+                          "traffic_over_alg": round((fb + wb) / alg[stage], 3)}
+    return {"copy_bytes": COPY_BYTES, "fetch_scale": round(f_scale, 4),
+            "write_scale": round(w_scale, 4), "kernels": kernels}
+
+
+def write_traffic_file(summary: dict, fetch_csv: str, write_csv: str) -> None:
+    lines = [
+        f"# HBM traffic per launch: int8 ratchet linear op step (M={M_TOK}, K={K_IN}, "
+        f"N={N_OUT})",
+        "",
+        "Commands (repository root R on the MI355X box; the second runs the same probe with "
+        "WRITE_SIZE):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc FETCH_SIZE -d $R/gpurun_out/pmc_fetch "
+        "-o p --output-format csv -- python3 $R/bench.py --pmc-probe",
+        "cd /tmp && export TMPDIR=/tmp && rocprofv3 --pmc WRITE_SIZE -d $R/gpurun_out/pmc_write "
+        "-o p --output-format csv -- python3 $R/bench.py --pmc-probe",
+        f"python3 $R/bench.py --traffic-summary {fetch_csv} {write_csv}",
+        "```",
+        "",
+        f"Counters are KiB per dispatch. Calibration: a {COPY_BYTES >> 20} MiB device copy "
+        f"reads FETCH_SIZE x {summary['fetch_scale']} and WRITE_SIZE x "
+        f"{summary['write_scale']} of its true bytes; every figure below is divided by "
+        "that factor.",
+        "",
+        "| stage | HBM read B | HBM write B | traffic B | algorithmic B | traffic / alg |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for stage, e in summary["kernels"].items():
+        lines.append(f"| {stage} | {e['fetch_bytes']} | {e['write_bytes']} | "
+                     f"{e['traffic_bytes']} | {e['alg_bytes']} | {e['traffic_over_alg']} |")
+    lines += ["", "```json", json.dumps(summary), "```", ""]
+    TRAFFIC_FILE.write_text("\n".join(lines))
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    if not TRAFFIC_FILE.is_file():
+        return None
+    text = TRAFFIC_FILE.read_text()
+    start = text.find("```json")
+    if start < 0:
+        return None
+    body = text[start + 7:text.find("```", start + 7)]
+    try:
+        return json.loads(body)["kernels"][kernel]["traffic_bytes"]
+    except (ValueError, KeyError):
+        return None
+
+
 def roofline_entry(kernels: dict) -> dict:
-    """The dominant hand-written kernel (largest average time, BLAS excluded)."""
-    own = {k: v for k, v in kernels.items() if not k.endswith("_blas")}
-    name = max(own, key=lambda k: own[k]["avg_us"])
-    e = own[name]
+    """The dominant hand-written kernel (largest average time) against its roofline: MFMA
+    kernels against their MFMA peak (int8 or bf16) unless their algorithmic bytes bound
+    them first, elementwise kernels against HBM bandwidth. `traffic` is the measured HBM
+    bytes per launch (counter summary), null if not measured."""
+    name = max(kernels, key=lambda k: kernels[k]["avg_us"])
+    e = kernels[name]
     sec = e["avg_us"] * 1e-6
+    traffic = measured_traffic(name)
     if "alg_ops" in e:
+        peak = PEAK_INT8_OPS if e.get("kind") == "int8" else PEAK_BF16_FLOPS
         ai = e["alg_ops"] / e["alg_bytes"]
-        if ai * PEAK_HBM_BPS < PEAK_INT8_OPS:
-            achieved = e["alg_bytes"] / sec / 1e9
-            return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1),
-                    "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
-                    "frac": round(achieved * 1e9 / PEAK_HBM_BPS, 4), "traffic": None,
-                    "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
-        achieved = e["alg_ops"] / sec / 1e12
-        return {"kernel": name, "bound": "mfma", "achieved": round(achieved, 1),
-                "peak": PEAK_INT8_OPS / 1e12, "unit": "TFLOP/s",
-                "frac": round(achieved * 1e12 / PEAK_INT8_OPS, 4), "traffic": None,
-                "alg_ops_per_launch": e["alg_ops"], "avg_us": e["avg_us"]}
+        if ai * PEAK_HBM_BPS >= peak:
+            achieved = e["alg_ops"] / sec / 1e12
+            return {"kernel": name, "bound": "mfma", "achieved": round(achieved, 1),
+                    "peak": peak / 1e12, "unit": "TFLOP/s",
+                    "frac": round(achieved * 1e12 / peak, 4), "traffic": traffic,
+                    "alg_ops_per_launch": e["alg_ops"], "alg_bytes_per_launch": e["alg_bytes"],
+                    "avg_us": e["avg_us"]}
     achieved = e["alg_bytes"] / sec / 1e9
     return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1),
             "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
-            "frac": round(achieved * 1e9 / PEAK_HBM_BPS, 4), "traffic": None,
+            "frac": round(achieved * 1e9 / PEAK_HBM_BPS, 4), "traffic": traffic,
             "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
 
 
@@ -321,6 +474,11 @@ def cpu_baseline(seconds: float) -> dict:
 
 def main() -> int:
     args = parse_args()
+    if args.traffic_summary:
+        summary = traffic_summary(*args.traffic_summary)
+        write_traffic_file(summary, *args.traffic_summary)
+        print(json.dumps(summary), flush=True)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
               "build (single-GPU ratchet-linear path)", file=sys.stderr)
@@ -331,6 +489,9 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     device = torch.device("cuda:0")
+    if args.pmc_probe:
+        pmc_probe(device)
+        return 0
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
     step_s, eager_s, layer, x, g = op_bench(args, device)
     ops = 3 * 2.0 * M_TOK * N_OUT * K_IN

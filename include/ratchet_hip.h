@@ -200,6 +200,9 @@ int rk_ratchet_update(uint8_t* packed, int64_t ldp, const float* z, int64_t ldz,
  *   grad_scale [rows] float32 <- sum_k g * code (pre-update code; trainable scale)
  *   nonfinite int32 flag, set to 1 when a row holds a NaN/Inf; such rows are left
  *            unchanged and do not contribute to counts.
+ *   rms_mean float32 <- mean of row_rms over the rows (the stats' gradient_rms_mean),
+ *            summed in a fixed order by a one-block kernel after the update; needs
+ *            row_rms.
  * Replaces: _capture_weight_gradient  ratchet.py:487-537 (isfinite guard 501, stats
  *           525-537), _normalize 539-556, apply_weight_gradient 558-580, and the
  *           trainable-scale reduction ratchet.py:143-147, 167-169.
@@ -208,7 +211,7 @@ int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* g, int g_dt
                            int64_t ldg, int64_t rows, int64_t K, int max_code, int threshold,
                            float low, float high, float eps, float* rms_ema, float beta1,
                            float beta2, int64_t* counts, float* row_rms, float* grad_scale,
-                           int32_t* nonfinite, void* stream);
+                           int32_t* nonfinite, float* rms_mean, void* stream);
 
 /*
  * Row normalization alone: z = g / (rms + eps) with rms = sqrt(sum_k g^2 / K) in the

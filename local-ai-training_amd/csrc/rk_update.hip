@@ -161,6 +161,21 @@ struct GradUpdateArgs {
   int vec_g, vec_p;
 };
 
+// mean[0] = mean of row_rms[0 .. rows): one block, each thread a strided partial in
+// fixed order, then a fixed LDS tree, so the result is reproducible.
+__global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms, int64_t rows,
+                                                            float* mean) {
+  __shared__ float part[256];
+  float acc = 0.0f;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) acc = acc + row_rms[r];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) mean[0] = part[0] / static_cast<float>(rows);
+}
 // ZONLY = true: write z = g / (rms + eps) instead of updating (the reference's
 // _normalize, ratchet.py:539-556), with the identical reduction order.
 template <int DT, int NC, bool ZONLY>
@@ -361,7 +376,7 @@ extern "C" int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* 
                                       int threshold, float low, float high, float eps,
                                       float* rms_ema, float beta1, float beta2, int64_t* counts,
                                       float* row_rms, float* grad_scale, int32_t* nonfinite,
-                                      void* stream) {
+                                      float* rms_mean, void* stream) {
   clear_error();
   if (int st = check_update_common(packed, ldp, rows, K, max_code, threshold, low, high)) return st;
   if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
@@ -388,10 +403,14 @@ extern "C" int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* 
   a.row_rms = row_rms;
   a.grad_scale = grad_scale;
   a.nonfinite = nonfinite;
+  if (rms_mean && !row_rms) return fail(RK_ERR_ARG, "rms_mean needs row_rms");
   const int V = g_dtype == RK_F32 ? 4 : 8;
   a.vec_g = aligned16(g) && (ldg % V) == 0 && (K % V) == 0;
   a.vec_p = (reinterpret_cast<uintptr_t>(packed) % V) == 0 && (ldp % V) == 0 && (K % V) == 0;
-  return launch_grad_kernel<false>(a, g_dtype, as_stream(stream));
+  if (int e = launch_grad_kernel<false>(a, g_dtype, as_stream(stream))) return e;
+  if (!rms_mean) return RK_OK;
+  row_rms_mean_kernel<<<1, 256, 0, as_stream(stream)>>>(row_rms, rows, rms_mean);
+  return launch_status("row_rms_mean");
 }
 
 extern "C" int rk_normalize_rows(const void* g, int g_dtype, int64_t ldg, int64_t rows, int64_t K,

@@ -178,6 +178,18 @@ class TransformerBlock(nn.Module):
         return inputs
 
 
+def _total(values):
+    """Sum of per-layer statistics: device scalars are stacked and summed in one
+    reduction (not one addition kernel per layer); host numbers are added as numbers."""
+    values = list(values)
+    tensors = [v.reshape(()) for v in values if isinstance(v, Tensor)]
+    host = sum(v for v in values if not isinstance(v, Tensor))
+    if not tensors:
+        return host
+    total = torch.stack(tensors).sum()
+    return total + host if host else total
+
+
 class RatchetGPT(nn.Module):
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -230,11 +242,11 @@ class RatchetGPT(nn.Module):
                    if isinstance(m, DiscreteRatchetLinear)]
         aggregated = RatchetUpdateStats(
             total_weights=sum(u.total_weights for u in updates),
-            positive_moves=sum(u.positive_moves for u in updates),
-            negative_moves=sum(u.negative_moves for u in updates),
-            blocked_positive_moves=sum(u.blocked_positive_moves for u in updates),
-            blocked_negative_moves=sum(u.blocked_negative_moves for u in updates),
-            gradient_rms_mean=(sum(u.gradient_rms_mean for u in updates) / len(updates)
+            positive_moves=_total(u.positive_moves for u in updates),
+            negative_moves=_total(u.negative_moves for u in updates),
+            blocked_positive_moves=_total(u.blocked_positive_moves for u in updates),
+            blocked_negative_moves=_total(u.blocked_negative_moves for u in updates),
+            gradient_rms_mean=(_total(u.gradient_rms_mean for u in updates) / len(updates)
                                if updates else 0.0),
         )
         return aggregated.materialize() if validate else aggregated

@@ -403,7 +403,8 @@ class DiscreteRatchetLinear(nn.Module):
     def _reset_pending_stats(self) -> None:
         self._pending_stats_total_weights = 0
         self._pending_counts: Tensor | None = None
-        self._pending_stats_rms_sum: Tensor | float = 0.0
+        # per launch: mean row rms over all out_features rows (a device scalar)
+        self._pending_rms_means: list[Tensor] = []
         self._nonfinite: Tensor | None = None
 
     @classmethod
@@ -491,14 +492,19 @@ class DiscreteRatchetLinear(nn.Module):
         rows, k = gradient.shape
         ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
         beta = self.rms_ema_beta
+        # the launch also writes the mean of row_rms (the stats' gradient_rms_mean)
+        rms_mean = (torch.empty((), device=self.packed.device, dtype=torch.float32)
+                    if row_rms is not None else None)
         nat.call(
             "rk_ratchet_update_grad", self.packed.data_ptr(), self.packed.stride(0),
             gradient.data_ptr(), nat.dtype_code(gradient.dtype),
             gradient.stride(0) if rows > 1 else k, rows, k, self.max_code,
             self.pressure_threshold, self.bucket_low, self.bucket_high, self.eps,
             nat.ptr(ema), beta, 1.0 - beta, counts.data_ptr(), nat.ptr(row_rms),
-            nat.ptr(grad_scale), nat.ptr(nonfinite), nat.stream_handle(self.packed.device),
+            nat.ptr(grad_scale), nat.ptr(nonfinite), nat.ptr(rms_mean),
+            nat.stream_handle(self.packed.device),
         )
+        self._last_rms_mean = rms_mean
         self._generation += 1
 
     def _fused_update(self, grad_weight: Tensor, *, want_grad_scale: bool) -> Tensor | None:
@@ -511,7 +517,7 @@ class DiscreteRatchetLinear(nn.Module):
         self._launch_update(grad_weight, self._counts(), row_rms, grad_scale,
                             self._nonfinite_flag())
         self._pending_stats_total_weights += self.out_features * self.in_features
-        self._pending_stats_rms_sum = self._pending_stats_rms_sum + row_rms.sum()
+        self._pending_rms_means.append(self._last_rms_mean)
         return grad_scale
 
     @torch.no_grad()
@@ -551,7 +557,7 @@ class DiscreteRatchetLinear(nn.Module):
             negative_moves=counts[1],
             blocked_positive_moves=counts[2],
             blocked_negative_moves=counts[3],
-            gradient_rms_mean=row_rms.mean(),
+            gradient_rms_mean=self._last_rms_mean,
         )
 
     @torch.no_grad()
@@ -615,7 +621,12 @@ class DiscreteRatchetLinear(nn.Module):
                 negative_moves=neg,
                 blocked_positive_moves=bpos,
                 blocked_negative_moves=bneg,
-                gradient_rms_mean=self._pending_stats_rms_sum / max(1, self.out_features),
+                # sum over launches of sum(row_rms) / out_features; each launch covers all
+                # out_features rows, so that is the sum of the launches' mean row rms
+                gradient_rms_mean=(self._pending_rms_means[0]
+                                   if len(self._pending_rms_means) == 1
+                                   else torch.stack(self._pending_rms_means).sum()
+                                   if self._pending_rms_means else 0.0),
             )
             nonfinite = self._nonfinite
             self._reset_pending_stats()

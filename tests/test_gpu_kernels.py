@@ -391,8 +391,33 @@ def _update_grad(packed, g, mc, T, eps=1e-8, ema=None, beta=0.0, want_scale=True
     nat.call("rk_ratchet_update_grad", packed.data_ptr(), packed.stride(0), g.data_ptr(),
              nat.dtype_code(g.dtype), g.stride(0), rows, k, mc, T, 0.5, 1.5, eps, nat.ptr(ema),
              beta, 1.0 - beta, counts.data_ptr(), row_rms.data_ptr(), nat.ptr(gscale),
-             flag.data_ptr(), nat.stream_handle(dev))
+             flag.data_ptr(), None, nat.stream_handle(dev))
     return counts, row_rms, gscale, flag
+
+
+@pytest.mark.parametrize("rows,k", [(6, 8), (37, 1001), (2048, 512), (8192, 512), (1, 64)])
+def test_update_writes_the_mean_row_rms(cuda, rows, k):
+    # rms_mean = mean of row_rms, summed in a fixed order: matches float64 and repeats
+    # bit for bit.
+    packed, _ = synthetic_state(rows, k, 2, seed=rows + k)
+    g = torch.randn(rows, k, generator=gen(rows)).to(cuda) * 1e-2
+    means = []
+    for _ in range(3):
+        pd = torch.from_numpy(packed).to(cuda)
+        counts = torch.zeros(4, dtype=torch.int64, device=cuda)
+        row_rms = torch.empty(rows, device=cuda)
+        mean = torch.empty((), device=cuda)
+        nat.call("rk_ratchet_update_grad", pd.data_ptr(), k, g.data_ptr(), nat.RK_F32, k, rows,
+                 k, 2, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
+                 row_rms.data_ptr(), None, None, mean.data_ptr(), nat.stream_handle(cuda))
+        want = row_rms.double().mean().item()
+        assert abs(mean.item() - want) <= 1e-6 * abs(want)
+        means.append(mean.view(torch.int32).item())
+    assert means[0] == means[1] == means[2]
+    with pytest.raises(nat.NativeError, match="rms_mean needs row_rms"):
+        nat.call("rk_ratchet_update_grad", pd.data_ptr(), k, g.data_ptr(), nat.RK_F32, k, rows,
+                 k, 2, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(), None, None, None,
+                 mean.data_ptr(), nat.stream_handle(cuda))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
