@@ -265,7 +265,7 @@ STAGE_KERNELS = {
     "unpack_transpose": ["unpack_transpose"],
     "grad_input_gemm": ["int8_gemm_m32_kernel<0,"],
     "grad_weight_bf16": ["grad_weight_partial_kernel", "grad_weight_reduce_kernel"],
-    "ratchet_update_grad": ["ratchet_update_grad_kernel"],
+    "ratchet_update_grad": ["ratchet_update_grad_kernel", "row_rms_mean_kernel"],
 }
 PROBE_REPEATS = 5
 
