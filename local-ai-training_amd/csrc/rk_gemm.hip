@@ -459,6 +459,99 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-M kernel (M <= 16 tokens: decode steps): the weight matrix is read once, so the
+// kernel is an HBM stream over B. One block = 16 output rows n, its 4 wavefronts split K;
+// each wavefront issues its 16-byte loads in batches of 8 (all in flight before the
+// first decode), multiplies with v_mfma_i32_16x16x64_i8 (B rows as the first operand:
+// lane l then holds token m = l & 15 and outputs n = 4 (l >> 4) .. +3), and the four
+// int32 partials are added through LDS (exact, so any order gives the same sum) before
+// the same (acc * ls) * rs -> bf16 epilogue. Token rows past M read zeros through the
+// descriptor; k-blocks past a wavefront's range re-read its last block (in bounds) and
+// skip the MFMA.
+// ---------------------------------------------------------------------------
+template <int KIND, int CDT, bool HAS_RS>
+__global__ __launch_bounds__(256) void int8_gemv_kernel(GemmArgs g) {
+  constexpr int NB = 16, KB = 64, W = 4, BATCH = 8;
+  __shared__ v4i red[W][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NB;
+  const int64_t rows_b = g.N - n0 < NB ? g.N - n0 : NB;
+  const __amdgpu_buffer_rsrc_t b_rsrc =
+      make_buffer(g.B + n0 * g.ldb, (rows_b - 1) * g.ldb + g.K);
+  const __amdgpu_buffer_rsrc_t a_rsrc = make_buffer(g.A, (g.M - 1) * g.lda + g.K);
+  const int b_voff = r16 * static_cast<int>(g.ldb) + 16 * g4;
+  const int a_voff = r16 * static_cast<int>(g.lda) + 16 * g4;
+  const int nkb = static_cast<int>(g.K / KB);
+  const int per = (nkb + W - 1) / W;
+  const int kb_begin = wave * per;
+  const int kb_end = kb_begin + per < nkb ? kb_begin + per : nkb;
+
+  v4i acc = v4i{0, 0, 0, 0};
+  for (int kb0 = kb_begin; kb0 < kb_end; kb0 += BATCH) {
+    u32x4 bw[BATCH], aw[BATCH];
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      const int kb = kb0 + j < kb_end ? kb0 + j : kb_end - 1;
+      bw[j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, b_voff, kb * KB, 0));
+      aw[j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, kb * KB, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < BATCH; ++j) {
+      if (kb0 + j < kb_end) {
+        u32x4 v = bw[j];
+        if constexpr (KIND == B_PACKED) {
+          v.x = decode4(v.x, g.mc4);
+          v.y = decode4(v.y, g.mc4);
+          v.z = decode4(v.z, g.mc4);
+          v.w = decode4(v.w, g.mc4);
+        }
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, v),
+                                                    __builtin_bit_cast(v4i, aw[j]), acc, 0, 0, 0);
+      }
+    }
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  v4i sum = red[0][lane];
+#pragma unroll
+  for (int w = 1; w < W; ++w) {
+    const v4i t = red[w][lane];
+    sum = v4i{sum[0] + t[0], sum[1] + t[1], sum[2] + t[2], sum[3] + t[3]};
+  }
+  const int m = r16;
+  const int64_t n = n0 + 4 * g4;
+  if (m >= g.M || n >= g.N) return;
+  const float lsm = g.ls[m];
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = static_cast<float>(sum[r]) * lsm;
+  if constexpr (HAS_RS) {
+    const float4 rs4 = *reinterpret_cast<const float4*>(g.rs + n);
+    v[0] = v[0] * rs4.x;
+    v[1] = v[1] * rs4.y;
+    v[2] = v[2] * rs4.z;
+    v[3] = v[3] * rs4.w;
+  }
+  const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+  if constexpr (CDT == RK_BF16) {
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.C) + m * g.ldc + n) = make_uint2(lo, hi);
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<float*>(g.C) + m * g.ldc + n) =
+        make_uint4(lo << 16, lo & 0xffff0000u, hi << 16, hi & 0xffff0000u);
+  }
+}
+
+template <int KIND, int CDT, bool HAS_RS>
+static void launch_gemv(const GemmArgs& g, hipStream_t stream) {
+  const int64_t blocks = (g.N + 15) / 16;
+  int8_gemv_kernel<KIND, CDT, HAS_RS><<<dim3(static_cast<unsigned>(blocks)), 256, 0, stream>>>(g);
+}
+
 template <int KIND, int CDT, bool HAS_RS>
 static void launch_m32(const GemmArgs& g, hipStream_t stream) {
   const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
@@ -477,6 +570,13 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const bool fits32 = 128 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
                       128 * g.ldb + g.K + 256 < (int64_t{1} << 31) &&
                       128 * g.ldc * es < (int64_t{1} << 31);
+  if (aligned_out && fits32 && g.M <= 16) {
+    // decode-sized M: one pass over B spread over the whole chip
+    if ((g.N + 15) / 16 > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
+    if (g.rs) launch_gemv<KIND, CDT, true>(g, stream);
+    else launch_gemv<KIND, CDT, false>(g, stream);
+    return launch_status("int8_gemv");
+  }
   if (aligned_out && fits32) {
     const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
     if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");

@@ -94,6 +94,42 @@ def _is_int8(layer: nn.Module) -> bool:
     return getattr(layer, "matmul_mode", "fp32") == "int8"
 
 
+class KVCache:
+    """Per-layer keys/values [B, H, max_len, D] for incremental decoding, plus the number of
+    filled positions. ``pos`` is that number as a device tensor, so a decode step (which
+    reads the position and the mask from it) has fixed shapes and can be replayed as a HIP
+    graph; ``length`` is the host copy."""
+
+    def __init__(self, n_layer: int, batch: int, n_head: int, head_size: int, max_len: int,
+                 device: torch.device) -> None:
+        self.n_layer, self.batch, self.n_head = n_layer, batch, n_head
+        self.head_size, self.max_len, self.device = head_size, max_len, device
+        self.keys: list[Tensor | None] = [None] * n_layer
+        self.values: list[Tensor | None] = [None] * n_layer
+        self.length = 0
+        self.pos = torch.zeros(1, dtype=torch.long, device=device)
+        self._arange = torch.arange(max_len, device=device)
+
+    def buffers(self, layer: int, like: Tensor) -> tuple[Tensor, Tensor]:
+        if self.keys[layer] is None or self.keys[layer].dtype != like.dtype:
+            shape = (self.batch, self.n_head, self.max_len, self.head_size)
+            self.keys[layer] = torch.zeros(shape, dtype=like.dtype, device=self.device)
+            self.values[layer] = torch.zeros(shape, dtype=like.dtype, device=self.device)
+        return self.keys[layer], self.values[layer]
+
+    def decode_mask(self, dtype: torch.dtype) -> Tensor:
+        """Additive mask [1, 1, 1, max_len] for a one-token step at position ``pos``:
+        0 for keys 0..pos, -inf after (computed on the device from ``pos``)."""
+        valid = self._arange <= self.pos
+        zero = torch.zeros((), dtype=dtype, device=self.device)
+        ninf = torch.full((), float("-inf"), dtype=dtype, device=self.device)
+        return torch.where(valid, zero, ninf).view(1, 1, 1, self.max_len)
+
+    def advance(self, steps: int) -> None:
+        self.length += steps
+        self.pos.add_(steps)
+
+
 class CausalSelfAttention(nn.Module):
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -104,7 +140,8 @@ class CausalSelfAttention(nn.Module):
         self.dropout = config.dropout
 
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
-                inputs_scale: Tensor | None = None) -> Tensor:
+                inputs_scale: Tensor | None = None, cache: KVCache | None = None,
+                layer: int = 0, decode: bool = False) -> Tensor:
         batch_size, sequence_length, channels = inputs.shape
         if inputs_int8 is not None:
             qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
@@ -117,7 +154,9 @@ class CausalSelfAttention(nn.Module):
 
         q, k, v = heads(query), heads(key), heads(value)
         dropout_p = self.dropout if self.training else 0.0
-        if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
+        if cache is not None:
+            attended = self._cached_attention(q, k, v, cache, layer, decode)
+        elif q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
             # Fused attention kernels only: the math fallback runs 16-bit batched
             # products on transposed views, which this path avoids.
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
@@ -131,6 +170,30 @@ class CausalSelfAttention(nn.Module):
             return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale)
         joined = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, channels)
         return self.projection(joined)
+
+    def _cached_attention(self, q: Tensor, k: Tensor, v: Tensor, cache: KVCache, layer: int,
+                          decode: bool) -> Tensor:
+        """Attention of the new positions against the cache, after appending their keys and
+        values. ``decode``: one token at the device-side position ``cache.pos``, attending
+        over the whole buffer under a mask (fixed shapes); otherwise a prompt of S tokens
+        written at the host-side ``cache.length`` (causal among themselves)."""
+        keys, values = cache.buffers(layer, k)
+        if decode:
+            keys.index_copy_(2, cache.pos, k)
+            values.index_copy_(2, cache.pos, v)
+            return F.scaled_dot_product_attention(q, keys, values,
+                                                  attn_mask=cache.decode_mask(q.dtype))
+        start, length = cache.length, q.shape[2]
+        end = start + length
+        if end > cache.max_len:
+            raise ValueError("KV cache is full")
+        keys[:, :, start:end] = k
+        values[:, :, start:end] = v
+        if start == 0:
+            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        mask = torch.ones(length, end, dtype=torch.bool, device=q.device).tril(diagonal=start)
+        return F.scaled_dot_product_attention(q, keys[:, :, :end], values[:, :, :end],
+                                              attn_mask=mask)
 
 
 class FeedForward(nn.Module):
@@ -163,12 +226,14 @@ class TransformerBlock(nn.Module):
         self.feed_forward_norm = nn.RMSNorm(config.n_embd)
         self.feed_forward = FeedForward(config, max_code=max_code)
 
-    def forward(self, inputs: Tensor) -> Tensor:
+    def forward(self, inputs: Tensor, *, cache: KVCache | None = None, layer: int = 0,
+                decode: bool = False) -> Tensor:
+        kv = dict(cache=cache, layer=layer, decode=decode) if cache is not None else {}
         if _is_int8(self.attention.qkv):
             q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight, 1e-5)
-            inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s)
+            inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s, **kv)
         else:
-            inputs = inputs + self.attention(self.attention_norm(inputs))
+            inputs = inputs + self.attention(self.attention_norm(inputs), **kv)
         if _is_int8(self.feed_forward.expand):
             q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
                                                        1e-5)
@@ -236,6 +301,45 @@ class RatchetGPT(nn.Module):
                 raise ValueError("targets must have the same shape as tokens")
             loss = F.cross_entropy(logits.flatten(0, 1), targets.flatten())
         return logits, loss
+
+    # -- incremental decoding ---------------------------------------------------
+    def new_cache(self, batch: int, max_len: int | None = None) -> KVCache:
+        """An empty KV cache for `batch` sequences of up to `max_len` (<= block_size) tokens."""
+        max_len = max_len or self.config.block_size
+        if max_len > self.config.block_size:
+            raise ValueError("a cache cannot outgrow block_size (positions are absolute)")
+        device = self.position_encoding.device
+        return KVCache(self.config.n_layer, batch, self.config.n_head,
+                       self.config.n_embd // self.config.n_head, max_len, device)
+
+    @torch.no_grad()
+    def prefill(self, tokens: Tensor, cache: KVCache) -> Tensor:
+        """Run `tokens` [B, S] at positions cache.length .. +S, append their keys/values, and
+        return the logits of the last position [B, vocab]."""
+        start, length = cache.length, tokens.shape[1]
+        hidden = self.token_embedding(tokens) + self.position_encoding[start:start + length]
+        for index, block in enumerate(self.blocks):
+            hidden = block(hidden, cache=cache, layer=index)
+        cache.advance(length)
+        return self.lm_head(self.final_norm(hidden[:, -1:]))[:, 0]
+
+    @torch.no_grad()
+    def decode_step(self, tokens: Tensor, cache: KVCache) -> Tensor:
+        """One token per sequence (`tokens` [B, 1]) at the device-side position cache.pos;
+        returns its logits [B, vocab] and advances the cache. Shapes do not depend on the
+        position, so the step can be captured once and replayed (the caller then advances
+        the cache itself)."""
+        logits = self.decode_logits(tokens, cache)
+        cache.advance(1)
+        return logits
+
+    def decode_logits(self, tokens: Tensor, cache: KVCache) -> Tensor:
+        """decode_step without advancing the cache (the capturable part)."""
+        hidden = self.token_embedding(tokens) + self.position_encoding.index_select(
+            0, cache.pos).view(1, 1, -1)
+        for index, block in enumerate(self.blocks):
+            hidden = block(hidden, cache=cache, layer=index, decode=True)
+        return self.lm_head(self.final_norm(hidden))[:, 0]
 
     def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
         updates = [m.ratchet_update(validate=validate) for m in self.modules()

@@ -253,6 +253,40 @@ def test_packed_gemm_bit_exact(cuda, m, n, k, max_code):
     assert np.array_equal(bits16(out), ref)
 
 
+# Decode-sized M (<= 16 tokens) takes the small-M kernel: 1B-model layer shapes (qkv 6144 x
+# 2048, contract 2048 x 5632, lm_head 8192 x 2048), partial 16-row groups, M of 1..16.
+SMALL_M_SHAPES = [(1, 6144, 2048), (16, 2048, 5632), (3, 136, 64), (16, 8, 64), (5, 1032, 1024),
+                  (1, 8192, 2048), (11, 5632, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", SMALL_M_SHAPES)
+def test_small_m_int8_gemm_bit_exact(cuda, m, n, k):
+    g = gen(m * 13 + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
+    b = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    ls = torch.rand(m, generator=g) * 1e-3 + 1e-5
+    rs = torch.rand(n, generator=g) + 0.01
+    out = int8_mm_nt(a.to(cuda), b.to(cuda), ls.to(cuda), rs.to(cuda))
+    ref = ogemm.scaled_int8_mm(a.numpy(), b.numpy().T, ls.numpy(), rs.numpy())
+    assert np.array_equal(bits16(out), ref)
+    out1 = int8_mm_nt(a.to(cuda), b.to(cuda), ls.to(cuda), None, torch.float32)
+    ref1 = ogemm.scaled_int8_mm(a.numpy(), b.numpy().T, ls.numpy(), None)
+    assert np.array_equal(f32bits(out1), (ref1.astype(np.uint32) << 16))
+
+
+@pytest.mark.parametrize("max_code", [2, 3])
+@pytest.mark.parametrize("m,n,k", SMALL_M_SHAPES)
+def test_small_m_packed_gemm_bit_exact(cuda, m, n, k, max_code):
+    packed, scale = synthetic_state(n, k, max_code, seed=m + n + k + max_code)
+    code, _ = oupd.unpack(packed, max_code)
+    q = torch.randint(-127, 128, (m, k), generator=gen(m + k), dtype=torch.int8)
+    ls = torch.rand(m, generator=gen(m + 1)) * 0.05 + 1e-3
+    out = packed_int8_mm(q.to(cuda), torch.from_numpy(packed).to(cuda), max_code,
+                         ls.to(cuda), torch.from_numpy(scale).to(cuda))
+    ref = ogemm.scaled_int8_mm(q.numpy(), code.T, ls.numpy(), scale)
+    assert np.array_equal(bits16(out), ref)
+
+
 def test_forward_gemm_full_op_shape_bit_exact(cuda):
     # BASELINE op: M=16384 tokens, K=512, N=2048, quinary codes, scales U[0.02, 0.1].
     m, n, k, mc = 16384, 2048, 512, 2
