@@ -54,6 +54,9 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--model-steps", type=int, default=10)
     ap.add_argument("--model-warmup", type=int, default=3)
     ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=64)
+    ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 16])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--kernel-iters", type=int, default=20)
@@ -439,7 +442,180 @@ def model_bench(args, device):
         loss = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    return batch * block * args.model_steps / elapsed, elapsed / args.model_steps, float(loss)
+    return batch * block * args.model_steps / elapsed, elapsed / args.model_steps, float(loss.detach())
+
+
+DECODE_LAYERS = dict(vocab=8192, block=1024, n_layer=24, n_head=16, n_embd=2048, ffn=5632)
+DECODE_MAX_CODE = 3
+
+
+def decode_model(device):
+    """The 1B septenary ratchet transformer (24 layers, d 2048, 16 heads, FFN 5632, vocab
+    8192, block 1024) in int8 inference mode."""
+    from local_ai_training.model import ModelConfig, build_seeded_model
+
+    d = DECODE_LAYERS
+    config = ModelConfig(vocab_size=d["vocab"], block_size=d["block"], n_layer=d["n_layer"],
+                         n_head=d["n_head"], n_embd=d["n_embd"], ffn_hidden=d["ffn"],
+                         matmul_mode="int8")
+    return build_seeded_model(config, max_code=DECODE_MAX_CODE, seed=1337).to(device).eval()
+
+
+def decode_weight_bytes(model) -> int:
+    """Bytes every decode step must stream: packed codes + fp32 row scales of every ratchet
+    layer (the GEMVs read each weight once per step)."""
+    from local_ai_training.ratchet import DiscreteRatchetLinear
+
+    return sum(m.packed.numel() + 4 * m.packed.shape[0] for m in model.modules()
+               if isinstance(m, DiscreteRatchetLinear))
+
+
+def gemv_chain(model, batch: int, device, iters: int) -> dict:
+    """Every ratchet GEMV of one decode step as the fused decode path runs it (qkv and
+    expand: RMSNorm+quant prologue; proj and contract: per-token quant prologue with the
+    residual add; lm_head: RMSNorm prologue), in model order over all 24 layers (0.97 GB
+    of packed codes, more than the last-level cache), on seeded float32 activations. HIP
+    events on the launch stream around each launch give the per-kind averages."""
+    import torch
+
+    from local_ai_training import decode as dec
+
+    gen = torch.Generator().manual_seed(3)
+    c, f = model.config.n_embd, model.config.hidden_size
+
+    def rows(width):
+        return (torch.randn(batch, width, generator=gen) * 2.0).to(device)
+
+    hidden, att, ffn_in = rows(c), rows(c), rows(f)
+    qkv = torch.empty(batch, 3 * c, dtype=torch.bfloat16, device=device)
+    ffn = torch.empty(batch, f, dtype=torch.float32, device=device)
+    logits = torch.empty(batch, model.config.vocab_size, dtype=torch.float32, device=device)
+    residual = rows(c)
+    calls = []
+    for block in model.blocks:
+        calls += [
+            ("qkv", block.attention.qkv, qkv, dict(prologue=dec.PRO_RMSNORM,
+             epilogue=dec.EPI_STORE, x=hidden, norm_weight=block.attention_norm.weight,
+             eps=dec.BLOCK_NORM_EPS)),
+            ("projection", block.attention.projection, residual,
+             dict(prologue=dec.PRO_PLAIN, epilogue=dec.EPI_ADD, x=att)),
+            ("expand", block.feed_forward.expand, ffn, dict(prologue=dec.PRO_RMSNORM,
+             epilogue=dec.EPI_GELU, x=hidden, norm_weight=block.feed_forward_norm.weight,
+             eps=dec.BLOCK_NORM_EPS)),
+            ("contract", block.feed_forward.contract, residual,
+             dict(prologue=dec.PRO_PLAIN, epilogue=dec.EPI_ADD, x=ffn_in)),
+        ]
+    calls.append(("lm_head", model.lm_head, logits, dict(prologue=dec.PRO_RMSNORM,
+                  epilogue=dec.EPI_STORE, x=hidden, norm_weight=model.final_norm.weight,
+                  eps=float(torch.finfo(torch.float32).eps))))
+
+    def run(events=None):
+        for i, (_, layer, out, kw) in enumerate(calls):
+            if events is not None:
+                events[i][0].record()
+            dec.decode_gemv(layer, out, **kw)
+            if events is not None:
+                events[i][1].record()
+
+    run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        run()
+    torch.cuda.synchronize()
+    chain_s = (time.perf_counter() - t0) / iters
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in calls]
+    per_kind: dict = {}
+    for _ in range(iters):
+        run(events)
+        torch.cuda.synchronize()
+        for (kind, layer, _, _), (e0, e1) in zip(calls, events):
+            n, k = layer.packed.shape
+            e = per_kind.setdefault(kind, {"N": n, "K": k, "count": 0, "us": 0.0})
+            e["count"] += 1
+            e["us"] += e0.elapsed_time(e1) * 1e3
+
+    def alg_bytes(n, k):
+        # packed codes + row scales, activation rows (f32) in, outputs (bf16 / f32) out
+        return n * k + 4 * n + 4 * batch * k + 4 * batch * n
+
+    kinds = {}
+    for kind, e in per_kind.items():
+        n, k = e["N"], e["K"]
+        us = e["us"] / e["count"]
+        alg = alg_bytes(n, k)
+        kinds[kind] = {"N": n, "K": k, "avg_us": round(us, 2), "alg_bytes": alg,
+                       "GB_s": round(alg / us / 1e3, 1),
+                       "frac": round(alg / us * 1e6 / PEAK_HBM_BPS, 4)}
+    total = sum(alg_bytes(*layer.packed.shape) for _, layer, _, _ in calls)
+    return {"launches": len(calls), "chain_us": round(chain_s * 1e6, 1),
+            "chain_GB_s": round(total / chain_s / 1e9, 1),
+            "chain_frac": round(total / chain_s / PEAK_HBM_BPS, 4), "kinds": kinds}
+
+
+def decode_bench(args, device) -> dict:
+    """KV-cached int8 decode of the 1B model at a 1024-token window: batch 1 and 16, a
+    prompt of 1024 - steps tokens prefilled, then `steps` greedy decode steps replayed as
+    one HIP graph each (argmax feeds the next token on the device, no host sync)."""
+    import numpy as np
+    import torch
+
+    from local_ai_training.decode import fused_decode_supported
+    from local_ai_training.generate import DecodeGraph
+
+    d = DECODE_LAYERS
+    model = decode_model(device)
+    weight_bytes = decode_weight_bytes(model)
+    steps = min(args.decode_steps, d["block"] - 1)
+    prompt_len = d["block"] - steps
+    head = d["n_embd"] // d["n_head"]
+    out = {"config": {"workload": "KV-cached int8 decode, 1B septenary ratchet transformer",
+                      "n_layer": d["n_layer"], "n_embd": d["n_embd"], "n_head": d["n_head"],
+                      "ffn": d["ffn"], "vocab": d["vocab"], "window": d["block"],
+                      "prompt": prompt_len, "steps": steps, "kv_dtype": "bf16",
+                      "codes": "septenary"},
+           "weight_bytes_per_step": weight_bytes}
+    rng = np.random.default_rng(1337)
+    for batch in args.decode_batches:
+        ids = (rng.zipf(1.1, size=(batch, prompt_len)) - 1) % d["vocab"]
+        tokens = torch.from_numpy(ids.astype(np.int64)).to(device)
+        cache = model.new_cache(batch, dtype=torch.bfloat16)
+        logits = model.prefill(tokens, cache)
+        graph = DecodeGraph(model, cache)
+        nxt = logits.argmax(-1, keepdim=True)
+
+        def run(count):
+            nonlocal nxt
+            for _ in range(count):
+                nxt = graph.step(nxt).argmax(-1, keepdim=True)
+
+        run(min(args.warmup, steps))
+        cache.length = prompt_len  # rewind: the timed steps rewrite the same positions
+        cache.pos.fill_(prompt_len)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run(steps)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / steps
+        # keys+values the attention reads per step (positions 0..p, bf16; p averaged over
+        # the timed steps)
+        mean_len = prompt_len + (steps + 1) / 2
+        kv_bytes = int(d["n_layer"] * 2 * batch * d["n_head"] * mean_len * head * 2)
+        chain = gemv_chain(model, batch, device, args.kernel_iters)
+        entry = {"tokens_per_s": round(batch / step_s, 1), "ms_per_step": round(step_s * 1e3, 4),
+                 "path": "fused" if fused_decode_supported(model, cache) else "modules",
+                 "launches_per_step": 6 * d["n_layer"] + 3,
+                 "weight_GB_s": round(weight_bytes / step_s / 1e9, 1),
+                 "step_bytes": weight_bytes + kv_bytes,
+                 "step_frac_hbm": round((weight_bytes + kv_bytes) / step_s / PEAK_HBM_BPS, 4),
+                 "gemv": chain}
+        out[f"batch_{batch}"] = entry
+        log(f"decode B={batch}: {step_s * 1e3:.3f} ms/step -> {batch / step_s:.0f} tok/s; "
+            f"GEMV chain {chain['chain_us']} us ({chain['chain_GB_s']} GB/s)")
+        del graph, cache
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -532,6 +708,9 @@ def main() -> int:
         result["train_config"] = {"model": "ratchet-gpt-25M", "n_layer": 8, "n_embd": 512,
                                   "n_head": 8, "ffn": 2048, "vocab": 8192, "seq_len": 512,
                                   "batch": 32, "matmul_mode": "int8", "int8_backward": True}
+    if not args.no_decode:
+        log(f"decode bench: 1B int8, batches {args.decode_batches}, {args.decode_steps} steps")
+        result["decode"] = decode_bench(args, device)
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of fp32 eager CPU work")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

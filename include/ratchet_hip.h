@@ -298,6 +298,61 @@ int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* 
                      int64_t ldx, int64_t M, int64_t K, void* grad_x, int64_t ldgx,
                      void* stream);
 
+/* ---------------------------------------------------------------------------
+ * KV-cached decode (one token per sequence, M <= 16 rows). The reference has no
+ * incremental path: generate.py:183-201 runs the whole window through the model for
+ * every token and reads the last position. These entry points compute that last
+ * position's step against a key/value cache instead; a transformer layer is six
+ * launches (qkv GEMV, attention partial + combine, proj / expand / contract GEMVs).
+ * ------------------------------------------------------------------------- */
+enum { RK_DEC_PRO_INT8 = 0, RK_DEC_PRO_PLAIN = 1, RK_DEC_PRO_RMSNORM = 2 };
+enum { RK_DEC_EPI_STORE = 0, RK_DEC_EPI_GELU = 1, RK_DEC_EPI_ADD = 2 };
+
+/* y = epilogue(bf16((q @ code^T) * s[m] * row_scale[n])) for M <= 16 token rows,
+ * code = (packed & 15) - max_code, packed [N, K] (ldp).
+ * Prologue, giving the int8 rows q and their scales s:
+ *   RK_DEC_PRO_INT8     q = xq [M, K] (ldxq), s = xs [M] as given;
+ *   RK_DEC_PRO_PLAIN    per-token absmax quantization of the float32 rows x [M, K]
+ *                       (ldx): the arithmetic of rk_quantize_rows (round to nearest);
+ *   RK_DEC_PRO_RMSNORM  x * rsqrt(mean(x^2) + eps) * norm_w, then quantized: the
+ *                       arithmetic of rk_rmsnorm_quantize (same summation order).
+ * Epilogue: RK_DEC_EPI_STORE writes the bf16 value (y_dtype RK_BF16) or it widened
+ * (RK_F32); RK_DEC_EPI_GELU writes tanh-GELU of the widened value (float32, the input
+ * of rk_gelu_quantize in int8_fused.py:58-84); RK_DEC_EPI_ADD adds it to the float32
+ * rows y in place (the residual `hidden + out`). With the same q and s the int32 sums
+ * and outputs equal rk_int8_gemm_packed's. Requires N % 16 == 0, K % 64 == 0,
+ * K <= 6144, 16-byte aligned rows (RK_ERR_UNSUPPORTED otherwise). */
+int rk_decode_gemv(const float* x, int64_t ldx, const int8_t* xq, int64_t ldxq,
+                   const float* xs, int prologue, const float* norm_w, float eps,
+                   const uint8_t* packed, int64_t ldp, int max_code, const float* row_scale,
+                   void* y, int y_dtype, int64_t ldy, int epilogue, int64_t M, int64_t N,
+                   int64_t K, void* stream);
+
+/* Number of position splits rk_decode_attention uses for B sequences of H heads with
+ * a cache of max_len positions (its workspace holds B * H * splits * (D + 4) floats). */
+int64_t rk_decode_attention_splits(int64_t B, int64_t H, int64_t max_len);
+
+/* One decode step of causal attention at position p = *pos (a device int64, so the
+ * step can be captured once and replayed). qkv [B, 3*H*D] (ld_qkv; q | k | v, head h at
+ * h*D) holds the step's projections; k_cache / v_cache are [B, H, max_len, D] with
+ * element strides sb, sh, sl (d contiguous). The step's k and v are written to
+ * position p, then softmax(q . k_j * scale) over j = 0..p weights v_j (float32
+ * arithmetic, positions split across workgroups and merged with the log-sum-exp
+ * rule). out [B, H*D] (ldo) receives the float32 rows, heads concatenated as the
+ * reference's transpose + view (model.py:128-130). Head size 64, 128 or 256. A
+ * position outside [0, max_len) writes nothing to the cache and NaN rows. */
+int rk_decode_attention(const void* qkv, int qkv_dtype, int64_t ld_qkv, void* k_cache,
+                        void* v_cache, int cache_dtype, int64_t sb, int64_t sh, int64_t sl,
+                        const int64_t* pos, int64_t B, int64_t H, int64_t D, int64_t max_len,
+                        float scale, float* work, int64_t work_floats, float* out,
+                        int64_t ldo, void* stream);
+
+/* hidden[b] = table[tokens[b]] + pos_table[*pos] (float32; model.py:237 at one
+ * position). An id outside [0, vocab) or a position outside [0, n_pos) gives a NaN row. */
+int rk_decode_embed(const int64_t* tokens, int64_t B, const float* table, int64_t vocab,
+                    int64_t C, const float* pos_table, int64_t n_pos, const int64_t* pos,
+                    float* hidden, int64_t ldh, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,49 @@
+// Row-quantization arithmetic shared by the training quant kernels and the decode
+// kernels: tanh-GELU and the rounding of x / s to an integer (nearest-even, or floor
+// after adding a uniform for stochastic rounding).
+#pragma once
+
+#include "rk_common.h"
+
+namespace rk {
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), evaluated in the
+  // operation order of int8_fused.py:72-75.
+  const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  const float t = tanhf(inner);
+  return 0.5f * x * (1.0f + t);
+}
+
+// Margin of the reciprocal fast path (2^-12). With r = RN(1/s) and |x/s| <= 127.00002,
+// ya = RN(x * r) differs from x/s by at most |x/s| * 2^-23 < 2^-16, and the correctly
+// rounded quotient Y = RN(x / s) by at most 2^-16 + 2^-18 < 2^-15. For stochastic
+// rounding the sums RN(Y + u) and RN(ya + u) then differ by less than 2^-14 (each add
+// rounds by at most half an ulp of a value below 128). So whenever ya (or ya + u) lies
+// more than the margin away from a rounding boundary (a half-integer for rint, an
+// integer for floor), the fast result equals the one computed from Y; otherwise, and
+// for non-finite inputs, the lane takes the IEEE division x / s (int8_matmul.py:142,
+// div_rn) and rounds that.
+constexpr float kAmbiguity = 0.000244140625f;
+
+template <bool SR>
+__device__ __forceinline__ float round_quotient(float y, float s, float r, float u) {
+  const float ya = y * r;
+  if constexpr (SR) {
+    const float v = ya + u;
+    const float f = floorf(v);
+    const float d = v - f;
+    if (!(fabsf(ya) <= 128.0f) || d < kAmbiguity || d > 1.0f - kAmbiguity) {
+      return floorf(y / s + u);
+    }
+    return f;
+  } else {
+    const float t = __builtin_rintf(ya);
+    if (!(fabsf(ya) <= 128.0f) || fabsf(ya - t) > 0.5f - kAmbiguity) {
+      return __builtin_rintf(y / s);
+    }
+    return t;
+  }
+}
+
+}  // namespace rk

@@ -58,8 +58,20 @@ SIGNATURES: dict[str, list] = {
                             _p, _i64, _p],
     "rk_rmsnorm_backward_parts": [_i64],
     "rk_gelu_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
+    "rk_decode_gemv": [_p, _i64, _p, _i64, _p, _i32, _p, _f32, _p, _i64, _i32, _p, _p, _i32,
+                       _i64, _i32, _i64, _i64, _i64, _p],
+    "rk_decode_attention_splits": [_i64, _i64, _i64],
+    "rk_decode_attention": [_p, _i32, _i64, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _i64,
+                            _i64, _i64, _f32, _p, _i64, _p, _i64, _p],
+    "rk_decode_embed": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p],
     "rk_version": [],
     "rk_last_error": [],
+}
+
+# return types other than int (the status, or an int count)
+RESTYPES = {
+    "rk_last_error": ctypes.c_char_p,
+    "rk_decode_attention_splits": ctypes.c_int64,
 }
 
 _lib: ctypes.CDLL | None = None
@@ -79,7 +91,7 @@ def load_library() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "rk_last_error" else ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     _lib = lib
     return lib
 

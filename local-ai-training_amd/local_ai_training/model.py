@@ -101,33 +101,55 @@ class KVCache:
     graph; ``length`` is the host copy."""
 
     def __init__(self, n_layer: int, batch: int, n_head: int, head_size: int, max_len: int,
-                 device: torch.device) -> None:
+                 device: torch.device, dtype: torch.dtype | None = None) -> None:
         self.n_layer, self.batch, self.n_head = n_layer, batch, n_head
         self.head_size, self.max_len, self.device = head_size, max_len, device
+        self.dtype = dtype
         self.keys: list[Tensor | None] = [None] * n_layer
         self.values: list[Tensor | None] = [None] * n_layer
         self.length = 0
         self.pos = torch.zeros(1, dtype=torch.long, device=device)
         self._arange = torch.arange(max_len, device=device)
+        self._mask: Tensor | None = None
+        self.step_buffers: dict[str, Tensor] = {}  # fixed-shape work buffers of a step
 
     def buffers(self, layer: int, like: Tensor) -> tuple[Tensor, Tensor]:
-        if self.keys[layer] is None or self.keys[layer].dtype != like.dtype:
+        """The layer's key/value buffers, allocated on first use in the cache dtype
+        (``like``'s when none was given) and kept from then on (later steps convert to
+        their dtype, so keys written by a prefill are never dropped)."""
+        if self.keys[layer] is None:
+            dtype = self.dtype or like.dtype
             shape = (self.batch, self.n_head, self.max_len, self.head_size)
-            self.keys[layer] = torch.zeros(shape, dtype=like.dtype, device=self.device)
-            self.values[layer] = torch.zeros(shape, dtype=like.dtype, device=self.device)
+            self.keys[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
+            self.values[layer] = torch.zeros(shape, dtype=dtype, device=self.device)
         return self.keys[layer], self.values[layer]
 
     def decode_mask(self, dtype: torch.dtype) -> Tensor:
         """Additive mask [1, 1, 1, max_len] for a one-token step at position ``pos``:
-        0 for keys 0..pos, -inf after (computed on the device from ``pos``)."""
-        valid = self._arange <= self.pos
-        zero = torch.zeros((), dtype=dtype, device=self.device)
-        ninf = torch.full((), float("-inf"), dtype=dtype, device=self.device)
-        return torch.where(valid, zero, ninf).view(1, 1, 1, self.max_len)
+        0 for keys 0..pos, -inf after (computed on the device from ``pos``). Built once per
+        step (``begin_step``) and shared by the layers."""
+        if self._mask is None or self._mask.dtype != dtype:
+            valid = self._arange <= self.pos
+            zero = torch.zeros((), dtype=dtype, device=self.device)
+            ninf = torch.full((), float("-inf"), dtype=dtype, device=self.device)
+            self._mask = torch.where(valid, zero, ninf).view(1, 1, 1, self.max_len)
+        return self._mask
+
+    def begin_step(self) -> None:
+        self._mask = None
 
     def advance(self, steps: int) -> None:
         self.length += steps
         self.pos.add_(steps)
+
+
+def _attend(q: Tensor, k: Tensor, v: Tensor, **kwargs) -> Tensor:
+    """scaled_dot_product_attention; 16-bit GPU inputs go to the fused kernels only (the
+    math fallback runs 16-bit batched products on transposed views, avoided here)."""
+    if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, **kwargs)
+    return F.scaled_dot_product_attention(q, k, v, **kwargs)
 
 
 class CausalSelfAttention(nn.Module):
@@ -156,15 +178,8 @@ class CausalSelfAttention(nn.Module):
         dropout_p = self.dropout if self.training else 0.0
         if cache is not None:
             attended = self._cached_attention(q, k, v, cache, layer, decode)
-        elif q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
-            # Fused attention kernels only: the math fallback runs 16-bit batched
-            # products on transposed views, which this path avoids.
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                attended = F.scaled_dot_product_attention(q, k, v, dropout_p=dropout_p,
-                                                          is_causal=True)
         else:
-            attended = F.scaled_dot_product_attention(q, k, v, dropout_p=dropout_p,
-                                                      is_causal=True)
+            attended = _attend(q, k, v, dropout_p=dropout_p, is_causal=True)
         if _is_int8(self.projection):
             attn_int8, attn_scale, dummy = FusedTransposeQuantizeFn.apply(attended)
             return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale)
@@ -178,11 +193,14 @@ class CausalSelfAttention(nn.Module):
         over the whole buffer under a mask (fixed shapes); otherwise a prompt of S tokens
         written at the host-side ``cache.length`` (causal among themselves)."""
         keys, values = cache.buffers(layer, k)
+        out_dtype = q.dtype
+        if keys.dtype != q.dtype:
+            q, k, v = q.to(keys.dtype), k.to(keys.dtype), v.to(keys.dtype)
         if decode:
             keys.index_copy_(2, cache.pos, k)
             values.index_copy_(2, cache.pos, v)
-            return F.scaled_dot_product_attention(q, keys, values,
-                                                  attn_mask=cache.decode_mask(q.dtype))
+            out = _attend(q, keys, values, attn_mask=cache.decode_mask(q.dtype))
+            return out.to(out_dtype)
         start, length = cache.length, q.shape[2]
         end = start + length
         if end > cache.max_len:
@@ -190,10 +208,10 @@ class CausalSelfAttention(nn.Module):
         keys[:, :, start:end] = k
         values[:, :, start:end] = v
         if start == 0:
-            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            return _attend(q, k, v, is_causal=True).to(out_dtype)
         mask = torch.ones(length, end, dtype=torch.bool, device=q.device).tril(diagonal=start)
-        return F.scaled_dot_product_attention(q, keys[:, :, :end], values[:, :, :end],
-                                              attn_mask=mask)
+        out = _attend(q, keys[:, :, :end], values[:, :, :end], attn_mask=mask)
+        return out.to(out_dtype)
 
 
 class FeedForward(nn.Module):
@@ -256,6 +274,10 @@ def _total(values):
 
 
 class RatchetGPT(nn.Module):
+    # decode steps use the fused HIP decode kernels where supported (False: the module
+    # forwards, e.g. to compare the two)
+    fused_decode: bool = True
+
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
         self.config = config
@@ -303,14 +325,17 @@ class RatchetGPT(nn.Module):
         return logits, loss
 
     # -- incremental decoding ---------------------------------------------------
-    def new_cache(self, batch: int, max_len: int | None = None) -> KVCache:
-        """An empty KV cache for `batch` sequences of up to `max_len` (<= block_size) tokens."""
+    def new_cache(self, batch: int, max_len: int | None = None,
+                  dtype: torch.dtype | None = None) -> KVCache:
+        """An empty KV cache for `batch` sequences of up to `max_len` (<= block_size) tokens.
+        `dtype` (e.g. bfloat16) stores keys/values and runs the cached attention in that
+        type; by default they keep the activations' dtype."""
         max_len = max_len or self.config.block_size
         if max_len > self.config.block_size:
             raise ValueError("a cache cannot outgrow block_size (positions are absolute)")
         device = self.position_encoding.device
         return KVCache(self.config.n_layer, batch, self.config.n_head,
-                       self.config.n_embd // self.config.n_head, max_len, device)
+                       self.config.n_embd // self.config.n_head, max_len, device, dtype)
 
     @torch.no_grad()
     def prefill(self, tokens: Tensor, cache: KVCache) -> Tensor:
@@ -329,12 +354,20 @@ class RatchetGPT(nn.Module):
         returns its logits [B, vocab] and advances the cache. Shapes do not depend on the
         position, so the step can be captured once and replayed (the caller then advances
         the cache itself)."""
-        logits = self.decode_logits(tokens, cache)
+        logits = self.decode_logits(tokens, cache).clone()
         cache.advance(1)
         return logits
 
     def decode_logits(self, tokens: Tensor, cache: KVCache) -> Tensor:
-        """decode_step without advancing the cache (the capturable part)."""
+        """decode_step without advancing the cache (the capturable part). On a ROCm GPU
+        with int8 ratchet layers of supported shapes the step runs on the fused decode
+        kernels (``decode.fused_decode_logits``; its result buffer is reused by the next
+        step); otherwise through the module forwards."""
+        from .decode import fused_decode_logits, fused_decode_supported
+
+        if self.fused_decode and fused_decode_supported(self, cache):
+            return fused_decode_logits(self, tokens, cache)
+        cache.begin_step()
         hidden = self.token_embedding(tokens) + self.position_encoding.index_select(
             0, cache.pos).view(1, 1, -1)
         for index, block in enumerate(self.blocks):

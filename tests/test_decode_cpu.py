@@ -37,6 +37,26 @@ def test_cached_decode_reproduces_the_full_window_forward():
                                rtol=1e-5, atol=1e-5)
 
 
+def test_bfloat16_cache_stores_bfloat16_and_returns_the_activation_dtype():
+    model = _model()
+    tokens = torch.randint(0, 64, (2, 20), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        full, _ = model(tokens)
+    cache = model.new_cache(2, dtype=torch.bfloat16)
+    logits = model.prefill(tokens[:, :6], cache)
+    assert cache.keys[0].dtype == torch.bfloat16 and logits.dtype == torch.float32
+    for t in range(6, 20):
+        logits = model.decode_step(tokens[:, t:t + 1], cache)
+        scale = float(full[:, t].abs().max())
+        assert float((logits - full[:, t]).abs().max()) <= 3e-2 * scale, t
+    # the stored keys are the bfloat16 rounding of the float32 keys
+    ref = model.new_cache(2)
+    model.prefill(tokens, ref)
+    torch.testing.assert_close(cache.keys[1][:, :, :20].float(),
+                               ref.keys[1][:, :, :20].to(torch.bfloat16).float(),
+                               rtol=1e-2, atol=1e-2)
+
+
 def test_cache_bounds():
     model = _model()
     with pytest.raises(ValueError, match="outgrow block_size"):

@@ -14,6 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from local_ai_training.decode import fused_decode_supported
 from local_ai_training.generate import DecodeGraph, generate
 from local_ai_training.model import ModelConfig, build_seeded_model
 
@@ -24,6 +25,14 @@ def _model(cuda, mode="int8", **kw):
     config = ModelConfig(vocab_size=256, block_size=64, n_layer=2, n_head=4, n_embd=128,
                          matmul_mode=mode, **kw)
     return build_seeded_model(config, max_code=2, seed=11).to(cuda).eval()
+
+
+def _fused_model(cuda):
+    # head size 64: the fused decode kernels' shapes (the model above has head size 32,
+    # which decodes through the module forwards)
+    config = ModelConfig(vocab_size=256, block_size=64, n_layer=2, n_head=4, n_embd=256,
+                         matmul_mode="int8")
+    return build_seeded_model(config, max_code=3, seed=13).to(cuda).eval()
 
 
 def _close(got, want, rel=1e-2):
@@ -56,11 +65,33 @@ def test_prefill_and_decode_match_the_full_window_forward(cuda, mode):
     assert _close(logits2, full[:, 29])
 
 
-def test_decode_graph_replays_equal_eager_steps(cuda):
+def test_bfloat16_cache_decode_tracks_the_full_window_forward(cuda):
+    # keys/values stored and attended in bfloat16 (fused attention kernels): the logits
+    # follow the float32 full-window forward at the bfloat16 rounding of the attention.
+    model = _model(cuda)
+    gen = torch.Generator().manual_seed(8)
+    tokens = torch.randint(0, 256, (4, 48), generator=gen).to(cuda)
+    with torch.no_grad():
+        full, _ = model(tokens)
+    cache = model.new_cache(4, dtype=torch.bfloat16)
+    logits = model.prefill(tokens[:, :16], cache)
+    assert cache.keys[0].dtype == torch.bfloat16 and logits.dtype == full.dtype
+    assert _close(logits, full[:, 15], rel=3e-2)
+    agree = total = 0
+    for t in range(16, 48):
+        logits = model.decode_step(tokens[:, t:t + 1], cache)
+        assert _close(logits, full[:, t], rel=3e-2), t
+        agree += int((logits.argmax(-1) == full[:, t].argmax(-1)).sum())
+        total += 4
+    assert agree >= 0.9 * total
+
+
+@pytest.mark.parametrize("kv_dtype", [None, torch.bfloat16])
+def test_decode_graph_replays_equal_eager_steps(cuda, kv_dtype):
     model = _model(cuda)
     gen = torch.Generator().manual_seed(6)
     tokens = torch.randint(0, 256, (2, 24), generator=gen).to(cuda)
-    eager, graphed = model.new_cache(2), model.new_cache(2)
+    eager, graphed = model.new_cache(2, dtype=kv_dtype), model.new_cache(2, dtype=kv_dtype)
     model.prefill(tokens[:, :4], eager)
     model.prefill(tokens[:, :4], graphed)
     graph = DecodeGraph(model, graphed)
@@ -110,3 +141,67 @@ def test_sliding_window_step_matches_the_reference_recompute(cuda):
     with torch.no_grad():
         logits, _ = model(window)
     assert out[1] == vocabulary[int(logits[0, -1].argmax())]
+
+
+@pytest.mark.parametrize("kv_dtype", [None, torch.bfloat16])
+@pytest.mark.parametrize("batch", [1, 5, 16])
+def test_fused_decode_matches_the_module_path_and_the_window(cuda, kv_dtype, batch):
+    model = _fused_model(cuda)
+    small = _model(cuda)
+    assert not fused_decode_supported(small, small.new_cache(1))  # head size 32
+    assert fused_decode_supported(model, model.new_cache(batch))
+    gen = torch.Generator().manual_seed(20 + batch)
+    tokens = torch.randint(0, 256, (batch, 40), generator=gen).to(cuda)
+    with torch.no_grad():
+        full, _ = model(tokens)
+    fused, plain = model.new_cache(batch, dtype=kv_dtype), model.new_cache(batch, dtype=kv_dtype)
+    model.prefill(tokens[:, :8], fused)
+    model.prefill(tokens[:, :8], plain)
+    agree = total = 0
+    try:
+        for t in range(8, 40):
+            got = model.decode_step(tokens[:, t:t + 1], fused)
+            model.fused_decode = False
+            want = model.decode_step(tokens[:, t:t + 1], plain)
+            model.fused_decode = True
+            # a bfloat16 cache is filled by a prefill with bfloat16 attention (the fused
+            # step's own attention is float32 over bf16-exact keys)
+            rel = 1e-2 if kv_dtype is None else 3e-2
+            assert _close(got, want, rel), ("vs module path", t)
+            assert _close(got, full[:, t], rel), ("vs full window", t)
+            agree += int((got.argmax(-1) == full[:, t].argmax(-1)).sum())
+            total += batch
+    finally:
+        model.fused_decode = True
+    assert agree >= (0.95 if kv_dtype is None else 0.9) * total
+    assert fused.length == plain.length == 40 and int(fused.pos) == 40
+    # layer 0 sees the same hidden rows on both paths: its appended keys/values are equal
+    assert torch.equal(fused.keys[0][:, :, 8:40], plain.keys[0][:, :, 8:40])
+    assert torch.equal(fused.values[0][:, :, 8:40], plain.values[0][:, :, 8:40])
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_fused_decode_graph_replays_equal_eager_steps(cuda, batch):
+    model = _fused_model(cuda)
+    gen = torch.Generator().manual_seed(40 + batch)
+    tokens = torch.randint(0, 256, (batch, 30), generator=gen).to(cuda)
+    eager = model.new_cache(batch, dtype=torch.bfloat16)
+    graphed = model.new_cache(batch, dtype=torch.bfloat16)
+    model.prefill(tokens[:, :6], eager)
+    model.prefill(tokens[:, :6], graphed)
+    graph = DecodeGraph(model, graphed)
+    for t in range(6, 30):
+        want = model.decode_step(tokens[:, t:t + 1], eager)
+        got = graph.step(tokens[:, t:t + 1])
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), t
+    assert torch.equal(graphed.keys[1], eager.keys[1])
+
+
+def test_fused_generate_is_graph_independent(cuda):
+    model = _fused_model(cuda)
+    vocabulary = tuple(chr(0x100 + i) for i in range(256))
+    prompt = "".join(vocabulary[i] for i in (3, 1, 4, 1, 5, 9, 2, 6))
+    a = generate(model, vocabulary, prompt, max_new_tokens=70, temperature=0.0)
+    b = generate(model, vocabulary, prompt, max_new_tokens=70, temperature=0.0, use_graph=True)
+    assert len(a) == 70 and a == b
