@@ -55,6 +55,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--model-warmup", type=int, default=3)
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the decode bench and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=64)
     ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 16])
     ap.add_argument("--no-cpu", action="store_true")
@@ -667,6 +669,9 @@ def main() -> int:
     device = torch.device("cuda:0")
     if args.pmc_probe:
         pmc_probe(device)
+        return 0
+    if args.decode_only:
+        print(json.dumps({"decode": decode_bench(args, device)}), flush=True)
         return 0
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
     step_s, eager_s, layer, x, g = op_bench(args, device)
