@@ -146,7 +146,6 @@ def stage_work(m: int, n: int, k: int, g_elem: int) -> dict:
         "quant_rows": ("bytes", m * k * 2 + m * k + m * 4),
         "fwd_gemm_packed": ("ops", mnk2, m * k + n * k + m * n * 2 + m * 4 + n * 4),
         "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
-        "unpack_transpose": ("bytes", 2 * n * k),
         "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
         "grad_weight_bf16": ("flops", mnk2, m * n * g_elem + m * k + m * 4 + n * k * 2),
         "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
@@ -162,10 +161,9 @@ def op_stages(layer, x, g):
     from local_ai_training.int8_matmul import (
         grad_weight_bf16,
         grad_weight_splits,
-        int8_mm_nt,
         packed_int8_mm,
+        packed_int8_mm_t,
         quantize_rows_into,
-        unpack_transpose,
     )
 
     dev = x.device
@@ -185,7 +183,6 @@ def op_stages(layer, x, g):
     row_rms = torch.empty(n, dtype=torch.float32, device=dev)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
     rms_mean = torch.empty((), dtype=torch.float32, device=dev)
-    holder = {}
 
     def update():
         nat.call("rk_ratchet_update_grad", packed.data_ptr(), k, gw.data_ptr(), nat.RK_BF16, k,
@@ -198,9 +195,8 @@ def op_stages(layer, x, g):
         ("fwd_gemm_packed", lambda: packed_int8_mm(q, packed, MAX_CODE, s, scale, out=out)),
         ("sr_quant_rows", lambda: quantize_rows_into(g, gq, gs, col_scale=scale,
                                                      stochastic=True, seed=12345)),
-        ("unpack_transpose", lambda: holder.__setitem__("ct", unpack_transpose(packed,
-                                                                               MAX_CODE))),
-        ("grad_input_gemm", lambda: int8_mm_nt(gq, holder["ct"], gs, None, out=gin)),
+        ("grad_input_gemm", lambda: packed_int8_mm_t(gq, packed, MAX_CODE, gs, None,
+                                                     out=gin)),
         ("grad_weight_bf16", lambda: grad_weight_bf16(g, q, s, splits, out=gw, work=gw_work)),
         ("ratchet_update_grad", update),
     ]
@@ -267,8 +263,7 @@ STAGE_KERNELS = {
     "quant_rows": ["quant_rows_kernel<1, 0, false"],
     "fwd_gemm_packed": ["int8_gemm_m32_kernel<1,"],
     "sr_quant_rows": ["quant_rows_kernel<1, 0, true"],
-    "unpack_transpose": ["unpack_transpose"],
-    "grad_input_gemm": ["int8_gemm_m32_kernel<0,"],
+    "grad_input_gemm": ["int8_gemm_m32_kernel<2,"],
     "grad_weight_bf16": ["grad_weight_partial_kernel", "grad_weight_reduce_kernel"],
     "ratchet_update_grad": ["ratchet_update_grad_kernel", "row_rms_mean_kernel"],
 }

@@ -97,6 +97,22 @@ int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* packed, int
                         void* stream);
 
 /*
+ * The same GEMM with the packed state as the K x N operand, read in place:
+ *   C[m, n] = bf16( (float(sum_k A[m,k] * code[k, n]) * ls[m]) * rs[n] ),
+ *   code[k, n] = (packed[k, n] & 15) - max_code, packed [K, N] uint8 (row stride ldp).
+ * The int8 grad_input GEMM (grad_int8 [M, N_out] @ code [N_out, K_in]) contracts over the
+ * packed rows; this form stages packed tiles as they lie and transposes them in LDS, so
+ * no decoded/transposed copy of the codes is made.
+ * Replaces: scaled_int8_mm(grad_int8, code, ...)  ratchet.py:133-134 (with the unpack of
+ *           ratchet.py:195-199 and the transposed copy rk_unpack_transpose would make).
+ * Requires K % 64 == 0, N % 8 == 0, 16-byte aligned rows (RK_ERR_UNSUPPORTED otherwise).
+ */
+int rk_int8_gemm_packed_t(const int8_t* A, int64_t lda, const uint8_t* packed, int64_t ldp,
+                          int max_code, const float* ls, const float* rs, void* C,
+                          int c_dtype, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                          void* stream);
+
+/*
  * Decode + transpose the packed state: codeT[k, n] = (packed[n, k] & 15) - max_code.
  *   packed [N, K] (row stride ldp) -> codeT int8 [K, N] (row stride ldt).
  * Feeds the int8 grad_input GEMM (contraction over the output features), replacing

@@ -30,7 +30,9 @@ constexpr int kBN = 128;
 constexpr int kBK = 64;
 constexpr int kLdsRow = kBK + 16;  // bytes
 
-enum { B_INT8 = 0, B_PACKED = 1 };
+// B_PACKED_T: the packed state read as the K x N operand, code[k, n] = packed[k, n]
+// decoded (the grad_input GEMM contracts over the packed rows; aligned kernel only).
+enum { B_INT8 = 0, B_PACKED = 1, B_PACKED_T = 2 };
 
 struct GemmArgs {
   const int8_t* A;
@@ -248,6 +250,17 @@ struct RingSlot {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
 
+// B_PACKED_T tiles are staged as they lie in memory, [64 k rows][128 n bytes] at a
+// 160-byte pitch (eight consecutive rows then cover all 64 banks), and the fragments
+// (16 consecutive k of one column n per lane) come from gfx950's transposing LDS read
+// ds_read_b64_tr_b8: within each 16-lane group, source lane s points at row s >> 1,
+// bytes 8 (s & 1) .. +7, and lane l receives byte column l of the eight rows, in row
+// order (checked on the device).
+constexpr int kBtPitch = 160;
+typedef int v2i_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i_t* lds_v2i_ptr;
+
+template <bool BT>
 __device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at,
                                             const uint8_t* bt, int arow0, int brow0, int lane) {
   const int r32 = lane & 31, h = lane >> 5;
@@ -259,7 +272,18 @@ __device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       fa[i][kh] = *reinterpret_cast<const v4i*>(at + ra * 64 + 16 * ((h + 2 * kh) ^ swz32(ra)));
-      fb[i][kh] = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
+      if constexpr (BT) {
+        const int sl = lane & 15;
+        const int col = brow0 + i * 32 + 16 * ((lane >> 4) & 1) + 8 * (sl & 1);
+        const int r0 = 16 * (h + 2 * kh) + (sl >> 1);
+        const v2i_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i_ptr)(bt + r0 * kBtPitch + col));
+        const v2i_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i_ptr)(bt + (r0 + 8) * kBtPitch + col));
+        fb[i][kh] = v4i{lo.x, lo.y, hi.x, hi.y};
+      } else {
+        fb[i][kh] = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
+      }
     }
   }
 #pragma unroll
@@ -287,9 +311,12 @@ template <int KIND, int CDT, bool HAS_RS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void int8_gemm_m32_kernel(GemmArgs g) {
   constexpr int BM = 128, BN = 128, BK = 64, S = 2;
+  constexpr bool BT = KIND == B_PACKED_T;
   constexpr int SEGS = BM * BK / 16 / 256;  // 16-byte pieces per thread per operand (2)
   constexpr int EPITCH = BN * 2 + 8;        // epilogue staging row, bytes
-  constexpr int SMEM = BM * EPITCH > 2 * (BM + BN) * BK ? BM * EPITCH : 2 * (BM + BN) * BK;
+  constexpr int BSTAGE = BT ? BK * kBtPitch : BN * BK;  // bytes of one B stage
+  constexpr int TILES = 2 * BM * BK + 2 * BSTAGE;
+  constexpr int SMEM = BM * EPITCH > TILES ? BM * EPITCH : TILES;
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   uint8_t* As = smem;
   uint8_t* Bs = smem + 2 * BM * BK;
@@ -311,15 +338,27 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_buffer(g.A + m0 * g.lda, (rows_a - 1) * g.lda + g.K);
+  // B_PACKED_T: the descriptor spans columns n0.. of all K rows (a k-step moves the
+  // scalar offset by 64 rows); columns past N in the last row read zeros, elsewhere the
+  // next columns (in bounds; their outputs are never stored)
   const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_buffer(g.B + n0 * g.ldb, (rows_b - 1) * g.ldb + g.K);
-  int a_voff[SEGS], b_voff[SEGS], st_off[SEGS];
+      BT ? make_buffer(g.B + n0, (g.K - 1) * g.ldb + (g.N - n0))
+         : make_buffer(g.B + n0 * g.ldb, (rows_b - 1) * g.ldb + g.K);
+  const int b_step = BT ? BK * static_cast<int>(g.ldb) : BK;
+  int a_voff[SEGS], b_voff[SEGS], st_off[SEGS], bst_off[SEGS];
 #pragma unroll
   for (int j = 0; j < SEGS; ++j) {
     const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
     a_voff[j] = row * static_cast<int>(g.lda) + 16 * seg;
-    b_voff[j] = row * static_cast<int>(g.ldb) + 16 * seg;
     st_off[j] = row * BK + 16 * (seg ^ swz32(row));
+    if constexpr (BT) {
+      const int krow = c >> 3, nseg = c & 7;  // 64 rows of 128 bytes
+      b_voff[j] = krow * static_cast<int>(g.ldb) + 16 * nseg;
+      bst_off[j] = krow * kBtPitch + 16 * nseg;
+    } else {
+      b_voff[j] = row * static_cast<int>(g.ldb) + 16 * seg;
+      bst_off[j] = st_off[j];
+    }
   }
 
   RingSlot<SEGS, SEGS> ring[S];
@@ -331,7 +370,7 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < SEGS; ++j)
       r.b[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             b_rsrc, b_voff[j], kt * BK, 0));
+                                             b_rsrc, b_voff[j], kt * b_step, 0));
   };
   auto store = [&](RingSlot<SEGS, SEGS>& r, int buf) {
     // Pin the slot here (see the grad_weight kernel): otherwise the decode of every slot
@@ -339,19 +378,19 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < SEGS; ++j) asm volatile("" : "+v"(r.a[j]), "+v"(r.b[j]));
     uint8_t* at = As + buf * BM * BK;
-    uint8_t* bt = Bs + buf * BN * BK;
+    uint8_t* bt = Bs + buf * BSTAGE;
 #pragma unroll
     for (int j = 0; j < SEGS; ++j) *reinterpret_cast<u32x4*>(at + st_off[j]) = r.a[j];
 #pragma unroll
     for (int j = 0; j < SEGS; ++j) {
       u32x4 v = r.b[j];
-      if constexpr (KIND == B_PACKED) {
+      if constexpr (KIND == B_PACKED || KIND == B_PACKED_T) {
         v.x = decode4(v.x, g.mc4);
         v.y = decode4(v.y, g.mc4);
         v.z = decode4(v.z, g.mc4);
         v.w = decode4(v.w, g.mc4);
       }
-      *reinterpret_cast<u32x4*>(bt + st_off[j]) = v;
+      *reinterpret_cast<u32x4*>(bt + bst_off[j]) = v;
     }
   };
 
@@ -377,13 +416,13 @@ void int8_gemm_m32_kernel(GemmArgs g) {
       store(ring[slot], slot);
       load(ring[slot], kb + slot + S);
       __syncthreads();
-      mfma32_step(acc, As + slot * BM * BK, Bs + slot * BN * BK, arow0, brow0, lane);
+      mfma32_step<BT>(acc, As + slot * BM * BK, Bs + slot * BSTAGE, arow0, brow0, lane);
     }
   }
   if (nk & 1) {
     store(ring[0], 0);
     __syncthreads();
-    mfma32_step(acc, As, Bs, arow0, brow0, lane);
+    mfma32_step<BT>(acc, As, Bs, arow0, brow0, lane);
   }
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer
 
@@ -595,6 +634,31 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   return launch_status("int8_gemm");
 }
 
+// C = (A @ code) * ls * rs with code = decode(packed) as the [K, N] operand: the m32
+// kernel only (aligned shapes; RK_ERR_UNSUPPORTED otherwise).
+template <int CDT>
+static int launch_gemm_packed_t(const GemmArgs& g, hipStream_t stream) {
+  const int es = CDT == RK_BF16 ? 2 : 4;
+  const bool aligned = (g.K % 64) == 0 && (g.lda % 16) == 0 && (g.ldb % 16) == 0 &&
+                       aligned16(g.A) && aligned16(g.B) && (g.N % 8) == 0 &&
+                       ((g.ldc * es) % 16) == 0 && aligned16(g.C) &&
+                       (g.rs == nullptr || aligned16(g.rs));
+  if (!aligned)
+    return fail(RK_ERR_UNSUPPORTED,
+                "packed [K, N] GEMM needs K %% 64 == 0, N %% 8 == 0 and 16-byte aligned rows");
+  // 32-bit buffer offsets: A as in the NT form; B's furthest scalar + vector offset is
+  // (K + 2 k-steps) rows of ldb bytes
+  const bool fits32 = 128 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
+                      (g.K + 128) * g.ldb + 128 < (int64_t{1} << 31) &&
+                      128 * g.ldc * es < (int64_t{1} << 31);
+  if (!fits32) return fail(RK_ERR_UNSUPPORTED, "packed [K, N] GEMM operands too large");
+  const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+  if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
+  if (g.rs) launch_m32<B_PACKED_T, CDT, true>(g, stream);
+  else launch_m32<B_PACKED_T, CDT, false>(g, stream);
+  return launch_status("int8_gemm_packed_t");
+}
+
 static int gemm_entry(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, int kind,
                       int max_code, const float* ls, const float* rs, void* C, int c_dtype,
                       int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream) {
@@ -648,4 +712,35 @@ extern "C" int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* 
                                    int64_t K, void* stream) {
   return gemm_entry(A, lda, packed, ldp, B_PACKED, max_code, ls, rs, C, c_dtype, ldc, M, N, K,
                     stream);
+}
+
+extern "C" int rk_int8_gemm_packed_t(const int8_t* A, int64_t lda, const uint8_t* packed,
+                                     int64_t ldp, int max_code, const float* ls,
+                                     const float* rs, void* C, int c_dtype, int64_t ldc,
+                                     int64_t M, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative GEMM extent");
+  if (c_dtype != RK_F32 && c_dtype != RK_BF16) return fail(RK_ERR_ARG, "bad output dtype");
+  if (K > 133144) return fail(RK_ERR_ARG, "K too large for an int32 accumulator");
+  if (max_code < 1 || max_code > 7) return fail(RK_ERR_ARG, "max_code must be in 1..7");
+  if (M == 0 || N == 0) return RK_OK;
+  if (!A || !packed || !ls || !C) return fail(RK_ERR_ARG, "null GEMM operand");
+  if (lda < K || ldp < N || ldc < N) return fail(RK_ERR_ARG, "leading dimension too small");
+  GemmArgs g{};
+  g.A = A;
+  g.lda = lda;
+  g.B = packed;
+  g.ldb = ldp;
+  g.max_code = max_code;
+  g.mc4 = static_cast<uint32_t>(max_code) * 0x01010101u;
+  g.ls = ls;
+  g.rs = rs;
+  g.C = C;
+  g.ldc = ldc;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  hipStream_t s = as_stream(stream);
+  return c_dtype == RK_BF16 ? launch_gemm_packed_t<RK_BF16>(g, s)
+                            : launch_gemm_packed_t<RK_F32>(g, s);
 }

@@ -136,6 +136,32 @@ def packed_int8_mm(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
     return out
 
 
+def packed_t_supported(a: Tensor, packed: Tensor) -> bool:
+    """Whether packed_int8_mm_t can run on these operands (aligned shapes)."""
+    k, n = packed.shape
+    return (k % 64 == 0 and n % 8 == 0 and a.stride(-1) == 1 and packed.stride(-1) == 1
+            and _ld(a) % 16 == 0 and _ld(packed) % 16 == 0 and a.data_ptr() % 16 == 0
+            and packed.data_ptr() % 16 == 0)
+
+
+def packed_int8_mm_t(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
+                     row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16,
+                     out: Tensor | None = None) -> Tensor:
+    """C = bf16((A @ code) * a_scale * row_scale) with code = decode(packed) as the [K, N]
+    operand (A [M, K] int8, packed [K, N]): the grad_input GEMM against the packed state,
+    without an unpacked or transposed copy of the codes."""
+    m, k = a.shape
+    n = packed.shape[1]
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=out_dtype)
+    nat.call(
+        "rk_int8_gemm_packed_t", a.data_ptr(), _ld(a), packed.data_ptr(), _ld(packed),
+        max_code, a_scale.data_ptr(), nat.ptr(row_scale), out.data_ptr(),
+        nat.dtype_code(out.dtype), _ld(out), m, n, k, nat.stream_handle(a.device),
+    )
+    return out
+
+
 def scaled_int8_mm(lhs: Tensor, rhs: Tensor, lhs_scale: Tensor, rhs_scale: Tensor) -> Tensor:
     """Multiply int8 matrices [M,K] @ [K,N] and fuse row/column scales into a BF16 output."""
     if not lhs.is_cuda or not rhs.is_cuda:

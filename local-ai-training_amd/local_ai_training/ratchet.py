@@ -42,6 +42,8 @@ from .int8_matmul import (
     grad_weight_bf16_x,
     int8_mm_nt,
     packed_int8_mm,
+    packed_int8_mm_t,
+    packed_t_supported,
     quantize_rows_into,
     transpose_bf16,
     unpack_transpose,
@@ -264,10 +266,15 @@ class _RatchetMatmul(torch.autograd.Function):
                 gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
             quantize_rows_into(g, grad_q, grad_s, col_scale=scale_d.float().contiguous(),
                                stochastic=True, seed=_sr_seed(), bf16_out=gradient_bf16)
-            code_t = unpack_transpose(packed, layer.max_code)
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
-            grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
+            if packed_t_supported(grad_q, packed):
+                # contraction over the packed rows, read in place (no unpacked copy)
+                grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
+                                              out_dtype)
+            else:
+                code_t = unpack_transpose(packed, layer.max_code)
+                grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
         else:
             gradient_bf16 = flat_gradient.to(torch.bfloat16)
             grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)

@@ -327,6 +327,56 @@ def test_grad_input_gemm_full_op_shape_bit_exact(cuda):
     assert np.array_equal(f32bits(out), (ref.astype(np.uint32) << 16))
 
 
+# The packed state as the [K, N] operand (grad_input contracts over the packed rows): tiles
+# staged as they lie, transposed by ds_read_b64_tr_b8. Shapes: the op shape, partial 128-wide
+# column tiles, small and ragged M, K of one k-step, every max_code.
+PACKED_T_SHAPES = [(16384, 2048, 512), (300, 1024, 144), (1, 64, 16), (129, 192, 1040),
+                   (77, 128, 2064)]
+
+
+@pytest.mark.parametrize("m,k,n", PACKED_T_SHAPES)
+@pytest.mark.parametrize("mc", [1, 3, 7])
+def test_packed_t_gemm_matches_oracle(cuda, m, k, n, mc):
+    from local_ai_training.int8_matmul import packed_int8_mm_t
+
+    packed, scale = synthetic_state(k, n, mc, seed=m + k + n + mc)  # [K, N]
+    code, _ = oupd.unpack(packed, mc)
+    gq = torch.randint(-127, 128, (m, k), generator=gen(m + mc), dtype=torch.int8)
+    gs = torch.rand(m, generator=gen(m + 7)) * 1e-3 + 1e-5
+    out = packed_int8_mm_t(gq.to(cuda), torch.from_numpy(packed).to(cuda), mc, gs.to(cuda),
+                           None, torch.float32)
+    ref = ogemm.scaled_int8_mm(gq.numpy(), code, gs.numpy(), None)
+    assert np.array_equal(f32bits(out), (ref.astype(np.uint32) << 16))
+    if m <= 300:
+        rs = (torch.rand(n, generator=gen(n)) + 0.01)
+        out16 = packed_int8_mm_t(gq.to(cuda), torch.from_numpy(packed).to(cuda), mc,
+                                 gs.to(cuda), rs.to(cuda))
+        ref16 = ogemm.scaled_int8_mm(gq.numpy(), code, gs.numpy(), rs.numpy())
+        assert np.array_equal(bits16(out16), ref16)
+
+
+def test_packed_t_gemm_strided_rows_and_unsupported_shapes(cuda):
+    from local_ai_training.int8_matmul import packed_int8_mm_t, packed_t_supported
+
+    mc = 2
+    packed, _ = synthetic_state(128, 96, mc, seed=5)
+    code, _ = oupd.unpack(packed, mc)
+    wide = torch.zeros(128, 160, dtype=torch.uint8)
+    wide[:, :96] = torch.from_numpy(packed)
+    p_view = wide.to(cuda)[:, :96]                      # ldp 160
+    gq = torch.randint(-127, 128, (40, 144), generator=gen(9), dtype=torch.int8)
+    a_view = gq.to(cuda)[:, :128]                       # lda 144
+    gs = torch.rand(40, generator=gen(10)) * 1e-3 + 1e-5
+    assert packed_t_supported(a_view, p_view)
+    out = packed_int8_mm_t(a_view, p_view, mc, gs.to(cuda), None, torch.float32)
+    ref = ogemm.scaled_int8_mm(gq[:, :128].numpy(), code, gs.numpy(), None)
+    assert np.array_equal(f32bits(out), (ref.astype(np.uint32) << 16))
+    ragged = torch.from_numpy(synthetic_state(100, 96, mc, seed=6)[0]).to(cuda)  # K % 64
+    assert not packed_t_supported(gq.to(cuda)[:, :100], ragged)
+    with pytest.raises(nat.NativeError, match="K % 64"):
+        packed_int8_mm_t(gq.to(cuda)[:, :100].contiguous(), ragged, mc, gs.to(cuda), None)
+
+
 def test_scaled_int8_mm_public_api_strided_and_errors(cuda):
     # tests/test_int8_matmul.py:172-207
     g = gen(5)
