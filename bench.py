@@ -137,18 +137,19 @@ def op_bench(args, device):
     return graph_s, eager_s, layer, x.detach(), g
 
 
-def stage_work(m: int, n: int, k: int, g_elem: int) -> dict:
+def stage_work(m: int, n: int, k: int, g_elem: int, nsplit: int) -> dict:
     """Algorithmic work per launch of each op-step stage: name -> (kind, amount[, bytes]);
     kind "bytes", "ops" (int8 MFMA) or "flops" (bf16 MFMA). Bytes count each operand
-    read once and each result written once."""
+    read once and each result written once. grad_weight's result is its float32 split
+    partials (nsplit per weight), which the update then reads."""
     mnk2 = 2.0 * m * n * k
     return {
         "quant_rows": ("bytes", m * k * 2 + m * k + m * 4),
         "fwd_gemm_packed": ("ops", mnk2, m * k + n * k + m * n * 2 + m * 4 + n * 4),
         "sr_quant_rows": ("bytes", m * n * 2 + m * n + m * 4 + n * 4),
         "grad_input_gemm": ("ops", mnk2, m * n + n * k + m * k * 2 + m * 4),
-        "grad_weight_bf16": ("flops", mnk2, m * n * g_elem + m * k + m * 4 + n * k * 2),
-        "ratchet_update_grad": ("bytes", n * k * (1 + 2 + 1) + n * 4),
+        "grad_weight_partials": ("flops", mnk2, m * n * g_elem + m * k + m * 4 + n * k * 4 * nsplit),
+        "ratchet_update_partials": ("bytes", n * k * (1 + 4 * nsplit + 1) + n * 4),
     }
 
 
@@ -176,7 +177,6 @@ def op_stages(layer, x, g):
     gq = torch.empty(m, n, dtype=torch.int8, device=dev)
     gs = torch.empty(m, dtype=torch.float32, device=dev)
     gin = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
-    gw = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
     splits = grad_weight_splits(m, n, k)
     gw_work = torch.empty(splits, n, k, dtype=torch.float32, device=dev)
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -185,9 +185,9 @@ def op_stages(layer, x, g):
     rms_mean = torch.empty((), dtype=torch.float32, device=dev)
 
     def update():
-        nat.call("rk_ratchet_update_grad", packed.data_ptr(), k, gw.data_ptr(), nat.RK_BF16, k,
+        nat.call("rk_ratchet_update_partials", packed.data_ptr(), k, gw_work.data_ptr(), splits,
                  n, k, MAX_CODE, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
-                 row_rms.data_ptr(), None, flag.data_ptr(), rms_mean.data_ptr(),
+                 row_rms.data_ptr(), None, flag.data_ptr(), rms_mean.data_ptr(), None, k,
                  nat.stream_handle(dev))
 
     stages = [
@@ -197,10 +197,11 @@ def op_stages(layer, x, g):
                                                      stochastic=True, seed=12345)),
         ("grad_input_gemm", lambda: packed_int8_mm_t(gq, packed, MAX_CODE, gs, None,
                                                      out=gin)),
-        ("grad_weight_bf16", lambda: grad_weight_bf16(g, q, s, splits, out=gw, work=gw_work)),
-        ("ratchet_update_grad", update),
+        ("grad_weight_partials", lambda: grad_weight_bf16(g, q, s, splits, work=gw_work,
+                                                          reduce=False)),
+        ("ratchet_update_partials", update),
     ]
-    work = stage_work(m, n, k, g.element_size())
+    work = stage_work(m, n, k, g.element_size(), splits)
     return stages, work
 
 
@@ -264,8 +265,8 @@ STAGE_KERNELS = {
     "fwd_gemm_packed": ["int8_gemm_m32_kernel<1,"],
     "sr_quant_rows": ["quant_rows_kernel<1, 0, true"],
     "grad_input_gemm": ["int8_gemm_m32_kernel<2,"],
-    "grad_weight_bf16": ["grad_weight_partial_kernel", "grad_weight_reduce_kernel"],
-    "ratchet_update_grad": ["ratchet_update_grad_kernel", "row_rms_mean_kernel"],
+    "grad_weight_partials": ["grad_weight_partial_kernel"],
+    "ratchet_update_partials": ["ratchet_update_grad_kernel<2,", "row_rms_mean_kernel"],
 }
 PROBE_REPEATS = 5
 
@@ -319,7 +320,10 @@ def traffic_summary(fetch_csv: str, write_csv: str) -> dict:
     write, wcopy = _stage_means(_per_dispatch_kib(write_csv, "WRITE_SIZE"))
     f_scale = fcopy * 1024 / COPY_BYTES
     w_scale = wcopy * 1024 / COPY_BYTES
-    work = stage_work(M_TOK, N_OUT, K_IN, 2)  # the op step's gradient is bfloat16
+    from local_ai_training.int8_matmul import grad_weight_splits
+
+    # the op step's gradient is bfloat16; the split count is the library's (host-side)
+    work = stage_work(M_TOK, N_OUT, K_IN, 2, grad_weight_splits(M_TOK, N_OUT, K_IN))
     alg = {name: w[2] if len(w) > 2 else w[1] for name, w in work.items()}
     kernels = {}
     for stage in STAGE_KERNELS:

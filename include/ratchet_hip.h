@@ -230,6 +230,27 @@ int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* g, int g_dt
                            int32_t* nonfinite, float* rms_mean, void* stream);
 
 /*
+ * The same fused normalize + update, fed by the grad_weight GEMM's split partials instead
+ * of a materialized gradient: partials float32 [nsplit, rows, K] (as left in the
+ * workspace by rk_grad_weight_bf16 / rk_grad_weight_bf16_x called with out = NULL) are
+ * added in split order and rounded to bf16 exactly as those entry points' reduction does,
+ * and the resulting rows go through rk_ratchet_update_grad's arithmetic with a bf16
+ * gradient. State, counts, row_rms, grad_scale, nonfinite and rms_mean are therefore
+ * bit-identical to reducing first and updating after, while the bf16 gradient never
+ * reaches memory (unless grad_out, bf16 [rows, K] with row stride ld_grad_out, asks
+ * for a copy). K % 8 == 0 and 16-byte aligned partials (RK_ERR_UNSUPPORTED otherwise).
+ * Replaces: the hand-off of each grad_weight tile (ratchet.py:162-165, gradient_sink) to
+ *           the fused update of _capture_weight_gradient (ratchet.py:487-537).
+ */
+int rk_ratchet_update_partials(uint8_t* packed, int64_t ldp, const float* partials,
+                               int nsplit, int64_t rows, int64_t K, int max_code,
+                               int threshold, float low, float high, float eps,
+                               float* rms_ema, float beta1, float beta2, int64_t* counts,
+                               float* row_rms, float* grad_scale, int32_t* nonfinite,
+                               float* rms_mean, uint16_t* grad_out, int64_t ld_grad_out,
+                               void* stream);
+
+/*
  * Row normalization alone: z = g / (rms + eps) with rms = sqrt(sum_k g^2 / K) in the
  * same fixed order as rk_ratchet_update_grad (or sqrt of the per-row EMA, which is
  * updated in place when rms_ema is non-NULL). z float32 [rows, K] (row stride ldz);

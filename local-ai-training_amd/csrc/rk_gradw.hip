@@ -330,10 +330,11 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
   if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
   if (N == 0 || K == 0) return RK_OK;
-  if (!g || !x || (x_kind == GW_X_Q8 && !s) || !workspace || !out)
+  if (!g || !x || (x_kind == GW_X_Q8 && !s) || !workspace)
     return fail(RK_ERR_ARG, "null pointer");
   if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
-  if (ldg < N || ldx < K || ldo < K) return fail(RK_ERR_ARG, "leading dimension too small");
+  if (ldg < N || ldx < K || (out && ldo < K))
+    return fail(RK_ERR_ARG, "leading dimension too small");
   const int ge = g_dtype == RK_F32 ? 4 : 2;
   const int xe = x_kind == GW_X_Q8 ? 1 : (x_kind == GW_X_BF16 ? 2 : 4);
   if ((N % 8) != 0 || (K % 16) != 0 || ((ldg * ge) % 16) != 0 || ((ldx * xe) % 16) != 0 ||
@@ -369,6 +370,7 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16>(a, g_dtype, grid, st);
   else launch_partial_g<GW_X_F32>(a, g_dtype, grid, st);
   if (int e = launch_status("grad_weight_partial")) return e;
+  if (!out) return RK_OK;  // partials only (rk_ratchet_update_partials reduces them)
   const int64_t total4 = N * K / 4;
   const int64_t rblocks = (total4 + 255) / 256;
   grad_weight_reduce_kernel<<<static_cast<unsigned>(rblocks < 4096 ? rblocks : 4096), 256, 0, st>>>(

@@ -139,14 +139,32 @@ __global__ __launch_bounds__(256) void ratchet_update_z_kernel(
 }
 
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t upd_pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const bf2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Fused normalize + update from the raw weight gradient (one wavefront per row).
 // NC > 0: the row's gradient stays in registers between the two passes.
 // ---------------------------------------------------------------------------
+// Gradient source of the fused kernel besides RK_F32 / RK_BF16 tensors: the fp32 split
+// partials of the grad_weight GEMM, part[s][row][k] (split stride part_stride), added in
+// split order and rounded to bf16 exactly as grad_weight_reduce_kernel does, then consumed
+// with the bf16 source's vector width (so every later operation, including the
+// sum-of-squares order, is the one the bf16 gradient would see).
+constexpr int SRC_SPLITS = 2;
+
 struct GradUpdateArgs {
   uint8_t* packed;
   int64_t ldp;
   const void* g;
   int64_t ldg;
+  const float* part;      // SRC_SPLITS: partials and their count / split stride
+  int nsplit;
+  int64_t part_stride;
+  uint16_t* g_out;        // SRC_SPLITS: optional copy of the bf16 gradient consumed
+  int64_t ldgo;
   int64_t rows, K;
   int mc, T;
   float low, high, eps;
@@ -180,7 +198,7 @@ __global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms,
 // _normalize, ratchet.py:539-556), with the identical reduction order.
 template <int DT, int NC, bool ZONLY>
 __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs a) {
-  constexpr int V = Vec<DT>::N;
+  constexpr int V = DT == RK_F32 ? 4 : 8;
   constexpr int SPAN = 64 * V;
   constexpr int NW = V / 4;
   const int lane = threadIdx.x & 63;
@@ -195,11 +213,54 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
     uint8_t* prow = a.packed + row * a.ldp;
 
     auto load_g = [&](int64_t e0, float* v) {
-      if (a.vec_g && e0 + V <= a.K) {
+      if constexpr (DT == SRC_SPLITS) {
+        // K % 8 == 0 (checked on the host): a vector is wholly inside or past the row
+        if (e0 < a.K) {
+          const float* p = a.part + row * a.K + e0;
+          float4 lo = *reinterpret_cast<const float4*>(p);
+          float4 hi = *reinterpret_cast<const float4*>(p + 4);
+#pragma unroll 8
+          for (int s = 1; s < a.nsplit; ++s) {
+            const float4 l2 = *reinterpret_cast<const float4*>(p + s * a.part_stride);
+            const float4 h2 = *reinterpret_cast<const float4*>(p + s * a.part_stride + 4);
+            lo.x = lo.x + l2.x;
+            lo.y = lo.y + l2.y;
+            lo.z = lo.z + l2.z;
+            lo.w = lo.w + l2.w;
+            hi.x = hi.x + h2.x;
+            hi.y = hi.y + h2.y;
+            hi.z = hi.z + h2.z;
+            hi.w = hi.w + h2.w;
+          }
+          const uint32_t w[4] = {upd_pack_bf16x2(lo.x, lo.y), upd_pack_bf16x2(lo.z, lo.w),
+                                 upd_pack_bf16x2(hi.x, hi.y), upd_pack_bf16x2(hi.z, hi.w)};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i) v[i] = 0.0f;
+        }
+      } else if (a.vec_g && e0 + V <= a.K) {
         load_vec16<DT>(grow, e0, v);
       } else {
 #pragma unroll
         for (int i = 0; i < V; ++i) v[i] = e0 + i < a.K ? load_elem<DT>(grow, e0 + i) : 0.0f;
+      }
+    };
+    // SRC_SPLITS with a gradient copy requested: written once, from pass 1
+    auto keep_g = [&](int64_t e0, const float* v) {
+      if constexpr (DT == SRC_SPLITS) {
+        if (a.g_out && e0 < a.K) {
+          uint4 w;
+          w.x = (__float_as_uint(v[0]) >> 16) | (__float_as_uint(v[1]) & 0xffff0000u);
+          w.y = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[3]) & 0xffff0000u);
+          w.z = (__float_as_uint(v[4]) >> 16) | (__float_as_uint(v[5]) & 0xffff0000u);
+          w.w = (__float_as_uint(v[6]) >> 16) | (__float_as_uint(v[7]) & 0xffff0000u);
+          *reinterpret_cast<uint4*>(a.g_out + row * a.ldgo + e0) = w;
+        }
       }
     };
 
@@ -212,6 +273,7 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       for (int c = 0; c < NC; ++c) {
         if (c < nchunks) {
           load_g(c * SPAN + lane0, xr[c]);
+          keep_g(c * SPAN + lane0, xr[c]);
         } else {
 #pragma unroll
           for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
@@ -226,6 +288,7 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       for (int64_t c = 0; c < nchunks; ++c) {
         float v[V];
         load_g(c * SPAN + lane0, v);
+        keep_g(c * SPAN + lane0, v);
 #pragma unroll
         for (int i = 0; i < V; ++i) {
           bad |= !finite_f32(v[i]);
@@ -343,11 +406,16 @@ static int launch_grad_kernel(const GradUpdateArgs& a, int g_dtype, hipStream_t 
     if (nchunks <= 2) ratchet_update_grad_kernel<RK_F32, 2, ZONLY><<<grid, block, 0, s>>>(a);
     else if (nchunks <= 8) ratchet_update_grad_kernel<RK_F32, 8, ZONLY><<<grid, block, 0, s>>>(a);
     else ratchet_update_grad_kernel<RK_F32, 0, ZONLY><<<grid, block, 0, s>>>(a);
-  } else {
+  } else if (g_dtype == RK_BF16) {
     if (nchunks <= 1) ratchet_update_grad_kernel<RK_BF16, 1, ZONLY><<<grid, block, 0, s>>>(a);
     else if (nchunks <= 4) ratchet_update_grad_kernel<RK_BF16, 4, ZONLY><<<grid, block, 0, s>>>(a);
     else if (nchunks <= 12) ratchet_update_grad_kernel<RK_BF16, 12, ZONLY><<<grid, block, 0, s>>>(a);
     else ratchet_update_grad_kernel<RK_BF16, 0, ZONLY><<<grid, block, 0, s>>>(a);
+  } else if constexpr (!ZONLY) {
+    if (nchunks <= 1) ratchet_update_grad_kernel<SRC_SPLITS, 1, false><<<grid, block, 0, s>>>(a);
+    else if (nchunks <= 4) ratchet_update_grad_kernel<SRC_SPLITS, 4, false><<<grid, block, 0, s>>>(a);
+    else if (nchunks <= 12) ratchet_update_grad_kernel<SRC_SPLITS, 12, false><<<grid, block, 0, s>>>(a);
+    else ratchet_update_grad_kernel<SRC_SPLITS, 0, false><<<grid, block, 0, s>>>(a);
   }
   return launch_status(ZONLY ? "normalize_rows" : "ratchet_update_grad");
 }
@@ -408,6 +476,54 @@ extern "C" int rk_ratchet_update_grad(uint8_t* packed, int64_t ldp, const void* 
   a.vec_g = aligned16(g) && (ldg % V) == 0 && (K % V) == 0;
   a.vec_p = (reinterpret_cast<uintptr_t>(packed) % V) == 0 && (ldp % V) == 0 && (K % V) == 0;
   if (int e = launch_grad_kernel<false>(a, g_dtype, as_stream(stream))) return e;
+  if (!rms_mean) return RK_OK;
+  row_rms_mean_kernel<<<1, 256, 0, as_stream(stream)>>>(row_rms, rows, rms_mean);
+  return launch_status("row_rms_mean");
+}
+
+extern "C" int rk_ratchet_update_partials(uint8_t* packed, int64_t ldp, const float* partials,
+                                          int nsplit, int64_t rows, int64_t K, int max_code,
+                                          int threshold, float low, float high, float eps,
+                                          float* rms_ema, float beta1, float beta2,
+                                          int64_t* counts, float* row_rms, float* grad_scale,
+                                          int32_t* nonfinite, float* rms_mean,
+                                          uint16_t* grad_out, int64_t ld_grad_out,
+                                          void* stream) {
+  clear_error();
+  if (int st = check_update_common(packed, ldp, rows, K, max_code, threshold, low, high)) return st;
+  if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
+  if (rows == 0) return RK_OK;
+  if (!partials) return fail(RK_ERR_ARG, "null partials");
+  if (K % 8 != 0 || !aligned16(partials))
+    return fail(RK_ERR_UNSUPPORTED, "partials need K %% 8 == 0 and 16-byte alignment");
+  if (grad_out && (ld_grad_out < K || ld_grad_out % 8 != 0 || !aligned16(grad_out)))
+    return fail(RK_ERR_ARG, "grad_out needs ld >= K, ld %% 8 == 0, 16-byte alignment");
+  if (!(eps > 0.0f)) return fail(RK_ERR_ARG, "eps must be positive");
+  if (rms_mean && !row_rms) return fail(RK_ERR_ARG, "rms_mean needs row_rms");
+  GradUpdateArgs a{};
+  a.packed = packed;
+  a.ldp = ldp;
+  a.part = partials;
+  a.nsplit = nsplit;
+  a.part_stride = rows * K;
+  a.g_out = grad_out;
+  a.ldgo = ld_grad_out;
+  a.rows = rows;
+  a.K = K;
+  a.mc = max_code;
+  a.T = threshold;
+  a.low = low;
+  a.high = high;
+  a.eps = eps;
+  a.rms_ema = rms_ema;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.counts = counts;
+  a.row_rms = row_rms;
+  a.grad_scale = grad_scale;
+  a.nonfinite = nonfinite;
+  a.vec_p = (reinterpret_cast<uintptr_t>(packed) % 8) == 0 && (ldp % 8) == 0;
+  if (int e = launch_grad_kernel<false>(a, SRC_SPLITS, as_stream(stream))) return e;
   if (!rms_mean) return RK_OK;
   row_rms_mean_kernel<<<1, 256, 0, as_stream(stream)>>>(row_rms, rows, rms_mean);
   return launch_status("row_rms_mean");

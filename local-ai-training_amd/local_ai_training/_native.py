@@ -49,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "rk_ratchet_update": [_p, _i64, _p, _i64, _i64, _i64, _i32, _i32, _f32, _f32, _p, _p],
     "rk_ratchet_update_grad": [_p, _i64, _p, _i32, _i64, _i64, _i64, _i32, _i32, _f32, _f32,
                                _f32, _p, _f32, _f32, _p, _p, _p, _p, _p, _p],
+    "rk_ratchet_update_partials": [_p, _i64, _p, _i32, _i64, _i64, _i32, _i32, _f32, _f32,
+                                   _f32, _p, _f32, _f32, _p, _p, _p, _p, _p, _p, _i64, _p],
     "rk_normalize_rows": [_p, _i32, _i64, _i64, _i64, _f32, _p, _f32, _f32, _p, _i64, _p, _p],
     "rk_pressure_leak": [_p, _i64, _i32, _p],
     "rk_validate_state": [_p, _i64, _i32, _p, _i64, _p, _p],

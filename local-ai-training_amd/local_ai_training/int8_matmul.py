@@ -244,13 +244,15 @@ def grad_weight_splits(m: int, n: int, k: int) -> int:
 
 
 def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = None, *,
-                     out: Tensor | None = None, work: Tensor | None = None) -> Tensor:
+                     out: Tensor | None = None, work: Tensor | None = None,
+                     reduce: bool = True) -> Tensor:
     """Gw = bf16(bf16(grad)^T @ bf16(bf16(q) * bf16(s)[:, None])) as [N, K] bf16.
 
     The BF16 weight gradient of ratchet.py:148-163 computed straight from the saved int8
     activations (q [M, K], s [M]) and the upstream gradient grad [M, N] (float32 or
     bfloat16), with no transposed copies. ``work`` (float32 [nsplit, N, K]) and ``out``
-    may be passed preallocated.
+    may be passed preallocated. ``reduce=False`` stops at the split partials and returns
+    ``work`` (for rk_ratchet_update_partials, which reduces them inside the update).
     """
     m, n = grad.shape
     k = q.shape[1]
@@ -261,20 +263,23 @@ def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = No
     splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
     if work is None:
         work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
-    if out is None:
+    if out is None and reduce:
         out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
     nat.call("rk_grad_weight_bf16", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
              q.data_ptr(), _ld(q), s.contiguous().data_ptr(), m, n, k, work.data_ptr(), splits,
-             out.data_ptr(), _ld(out), nat.stream_handle(grad.device))
-    return out
+             nat.ptr(out) if reduce else None, _ld(out) if reduce else k,
+             nat.stream_handle(grad.device))
+    return out if reduce else work
 
 
 def grad_weight_bf16_x(grad: Tensor, x: Tensor, nsplit: int | None = None, *,
-                       out: Tensor | None = None, work: Tensor | None = None) -> Tensor:
+                       out: Tensor | None = None, work: Tensor | None = None,
+                       reduce: bool = True) -> Tensor:
     """Gw = bf16(bf16(grad)^T @ bf16(x)) as [N, K] bf16, for activations x [M, K] given
     directly (float32 or bfloat16): the non-fused BF16 grad_weight of ratchet.py:159-163
     (``grad_out_tile.to(bf16) @ flat_inputs.to(bf16)``), or the fused one on a
-    dequantized copy (dequant_bf16). ``work`` / ``out`` as in grad_weight_bf16."""
+    dequantized copy (dequant_bf16). ``work`` / ``out`` / ``reduce`` as in
+    grad_weight_bf16."""
     m, n = grad.shape
     k = x.shape[1]
     if grad.stride(-1) != 1:
@@ -284,9 +289,10 @@ def grad_weight_bf16_x(grad: Tensor, x: Tensor, nsplit: int | None = None, *,
     splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
     if work is None:
         work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
-    if out is None:
+    if out is None and reduce:
         out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
     nat.call("rk_grad_weight_bf16_x", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
              x.data_ptr(), nat.dtype_code(x.dtype), _ld(x), m, n, k, work.data_ptr(), splits,
-             out.data_ptr(), _ld(out), nat.stream_handle(grad.device))
-    return out
+             nat.ptr(out) if reduce else None, _ld(out) if reduce else k,
+             nat.stream_handle(grad.device))
+    return out if reduce else work

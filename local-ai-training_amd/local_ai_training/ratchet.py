@@ -279,6 +279,7 @@ class _RatchetMatmul(torch.autograd.Function):
             gradient_bf16 = flat_gradient.to(torch.bfloat16)
             grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)
 
+        partials = None  # grad_weight split partials, reduced inside the update
         if mode == "fp32":
             grad_weight = gradient_fp32.t() @ inputs_fp32
         else:
@@ -292,11 +293,13 @@ class _RatchetMatmul(torch.autograd.Function):
                 x_direct = flat_inputs if flat_inputs.dtype in (torch.float32, torch.bfloat16) \
                     else flat_inputs.to(torch.bfloat16)
             if ctx.used_fused_int8 and _grad_weight_supported(g, q):
-                # straight from the saved int8 activations, no transposed copies
-                grad_weight = grad_weight_bf16(g, q, s)
+                # straight from the saved int8 activations, no transposed copies; the
+                # update reduces the split partials itself (the bf16 gradient is never
+                # written)
+                partials = grad_weight_bf16(g, q, s, reduce=False)
             elif x_direct is not None and _grad_weight_supported(g, x_direct):
                 # straight from the saved inputs (bf16 cast while staging)
-                grad_weight = grad_weight_bf16_x(g, x_direct)
+                partials = grad_weight_bf16_x(g, x_direct, reduce=False)
             else:
                 # NT GEMM on transposed bf16 copies (both operands contiguous along tokens)
                 grad_t = transpose_bf16(g)
@@ -305,7 +308,11 @@ class _RatchetMatmul(torch.autograd.Function):
                 else:
                     inputs_t = transpose_bf16(x_direct)
                 grad_weight = grad_t @ inputs_t.t()
-        grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
+        if partials is not None:
+            grad_scale = layer._fused_update(partials, want_grad_scale=needs_scale,
+                                             from_partials=True)
+        else:
+            grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
             grad_scale, None
 
@@ -374,6 +381,10 @@ class DiscreteRatchetLinear(nn.Module):
         self.trainable_scale = trainable_scale
         self.matmul_mode = matmul_mode
         self.fuse_backward_update = fuse_backward_update
+        # keep the bf16 weight gradient each fused update consumed (last_weight_gradient),
+        # e.g. to check it; off by default, since the fused update never writes it
+        self.keep_weight_gradient = False
+        self.last_weight_gradient: Tensor | None = None
         self.int8_backward = int8_backward
         self.tile_size = tile_size
 
@@ -490,39 +501,61 @@ class DiscreteRatchetLinear(nn.Module):
         self._pending_weight_gradient = gradient
 
     def _launch_update(self, gradient: Tensor, counts: Tensor, row_rms: Tensor | None,
-                       grad_scale: Tensor | None, nonfinite: Tensor | None) -> None:
+                       grad_scale: Tensor | None, nonfinite: Tensor | None, *,
+                       from_partials: bool = False) -> None:
+        """One update launch from a weight gradient [N, K], or (``from_partials``) from the
+        grad_weight GEMM's float32 split partials [nsplit, N, K], reduced inside the update
+        with the same arithmetic. With ``keep_weight_gradient`` set, the bf16 gradient the
+        update consumed is kept in ``last_weight_gradient``."""
         nat.require_rocm(gradient, self.packed, what="the ratchet update")
-        if gradient.dtype not in (torch.float32, torch.bfloat16):
-            gradient = gradient.float()
-        if gradient.stride(-1) != 1:
-            gradient = gradient.contiguous()
-        rows, k = gradient.shape
         ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
         beta = self.rms_ema_beta
         # the launch also writes the mean of row_rms (the stats' gradient_rms_mean)
         rms_mean = (torch.empty((), device=self.packed.device, dtype=torch.float32)
                     if row_rms is not None else None)
-        nat.call(
-            "rk_ratchet_update_grad", self.packed.data_ptr(), self.packed.stride(0),
-            gradient.data_ptr(), nat.dtype_code(gradient.dtype),
-            gradient.stride(0) if rows > 1 else k, rows, k, self.max_code,
-            self.pressure_threshold, self.bucket_low, self.bucket_high, self.eps,
-            nat.ptr(ema), beta, 1.0 - beta, counts.data_ptr(), nat.ptr(row_rms),
-            nat.ptr(grad_scale), nat.ptr(nonfinite), nat.ptr(rms_mean),
-            nat.stream_handle(self.packed.device),
-        )
+        stream = nat.stream_handle(self.packed.device)
+        if from_partials:
+            nsplit, rows, k = gradient.shape
+            kept = None
+            if self.keep_weight_gradient:
+                kept = torch.empty((rows, k), device=gradient.device, dtype=torch.bfloat16)
+            nat.call(
+                "rk_ratchet_update_partials", self.packed.data_ptr(), self.packed.stride(0),
+                gradient.data_ptr(), nsplit, rows, k, self.max_code, self.pressure_threshold,
+                self.bucket_low, self.bucket_high, self.eps, nat.ptr(ema), beta, 1.0 - beta,
+                counts.data_ptr(), nat.ptr(row_rms), nat.ptr(grad_scale), nat.ptr(nonfinite),
+                nat.ptr(rms_mean), nat.ptr(kept), k, stream,
+            )
+            self.last_weight_gradient = kept
+        else:
+            if gradient.dtype not in (torch.float32, torch.bfloat16):
+                gradient = gradient.float()
+            if gradient.stride(-1) != 1:
+                gradient = gradient.contiguous()
+            rows, k = gradient.shape
+            nat.call(
+                "rk_ratchet_update_grad", self.packed.data_ptr(), self.packed.stride(0),
+                gradient.data_ptr(), nat.dtype_code(gradient.dtype),
+                gradient.stride(0) if rows > 1 else k, rows, k, self.max_code,
+                self.pressure_threshold, self.bucket_low, self.bucket_high, self.eps,
+                nat.ptr(ema), beta, 1.0 - beta, counts.data_ptr(), nat.ptr(row_rms),
+                nat.ptr(grad_scale), nat.ptr(nonfinite), nat.ptr(rms_mean), stream,
+            )
+            self.last_weight_gradient = gradient if self.keep_weight_gradient else None
         self._last_rms_mean = rms_mean
         self._generation += 1
 
-    def _fused_update(self, grad_weight: Tensor, *, want_grad_scale: bool) -> Tensor | None:
-        """Normalize + update every output row in one launch (fused backward path)."""
-        if grad_weight.shape != (self.out_features, self.in_features):
+    def _fused_update(self, grad_weight: Tensor, *, want_grad_scale: bool,
+                      from_partials: bool = False) -> Tensor | None:
+        """Normalize + update every output row in one launch (fused backward path);
+        ``grad_weight`` is the gradient, or its split partials with ``from_partials``."""
+        if grad_weight.shape[-2:] != (self.out_features, self.in_features):
             raise ValueError("fused gradient shape mismatch")
         row_rms = torch.empty(self.out_features, device=grad_weight.device, dtype=torch.float32)
         grad_scale = (torch.empty(self.out_features, device=grad_weight.device,
                                   dtype=torch.float32) if want_grad_scale else None)
         self._launch_update(grad_weight, self._counts(), row_rms, grad_scale,
-                            self._nonfinite_flag())
+                            self._nonfinite_flag(), from_partials=from_partials)
         self._pending_stats_total_weights += self.out_features * self.in_features
         self._pending_rms_means.append(self._last_rms_mean)
         return grad_scale

@@ -522,6 +522,75 @@ def test_fused_normalize_update_bit_exact(cuda, rows, k, dtype):
     assert int(flag.item()) == 0
 
 
+def _reduce_partials(part):
+    """bf16(sum of the splits in order), the grad_weight reduction (IEEE float adds)."""
+    acc = part[0].clone()
+    for sp in range(1, part.shape[0]):
+        acc = acc + part[sp]
+    return acc.to(torch.bfloat16)
+
+
+# The update fed by grad_weight's split partials (reduction fused into the update): every
+# output equal to reducing to bf16 first and updating after. Shapes: the op shape, one
+# chunk, several register chunks, streaming rows (K > 12 chunks), one split, many splits.
+@pytest.mark.parametrize("rows,k,nsplit", [(2048, 512, 8), (96, 1024, 3), (64, 6144, 2),
+                                           (33, 7168, 5), (8, 8, 1), (130, 2048, 17)])
+def test_update_from_partials_equals_reduce_then_update(cuda, rows, k, nsplit):
+    mc, beta = 3, 0.9
+    packed, _ = synthetic_state(rows, k, mc, seed=rows + k)
+    part = torch.randn(nsplit, rows, k, generator=gen(rows * k)) * 1e-3
+    part[:, 3 % rows, 1] = float("nan") if rows > 3 else 0.0  # a non-finite row is skipped
+    part = part.to(cuda)
+    gw = _reduce_partials(part)
+    outs = []
+    for fused in (False, True):
+        pd = torch.from_numpy(packed).to(cuda)
+        ema = torch.full((rows,), 0.25, device=cuda)
+        counts = torch.zeros(4, dtype=torch.int64, device=cuda)
+        row_rms = torch.empty(rows, device=cuda)
+        gscale = torch.empty(rows, device=cuda)
+        flag = torch.zeros(1, dtype=torch.int32, device=cuda)
+        mean = torch.empty((), device=cuda)
+        kept = torch.zeros(rows, k, dtype=torch.bfloat16, device=cuda)
+        if fused:
+            nat.call("rk_ratchet_update_partials", pd.data_ptr(), k, part.data_ptr(), nsplit,
+                     rows, k, mc, 8, 0.5, 1.5, 1e-8, ema.data_ptr(), beta, 1.0 - beta,
+                     counts.data_ptr(), row_rms.data_ptr(), gscale.data_ptr(),
+                     flag.data_ptr(), mean.data_ptr(), kept.data_ptr(), k,
+                     nat.stream_handle(cuda))
+        else:
+            nat.call("rk_ratchet_update_grad", pd.data_ptr(), k, gw.data_ptr(), nat.RK_BF16,
+                     k, rows, k, mc, 8, 0.5, 1.5, 1e-8, ema.data_ptr(), beta, 1.0 - beta,
+                     counts.data_ptr(), row_rms.data_ptr(), gscale.data_ptr(),
+                     flag.data_ptr(), mean.data_ptr(), nat.stream_handle(cuda))
+            kept = gw
+        torch.cuda.synchronize()
+        outs.append((pd, ema, counts, row_rms, gscale, flag, mean, kept))
+    (pa, ea, ca, ra, ga, fa, ma, ka), (pb, eb, cb, rb, gb, fb, mb, kb) = outs
+    assert torch.equal(pa, pb) and torch.equal(ca, cb) and torch.equal(fa, fb)
+    finite = torch.isfinite(ra)
+    for x, y in ((ea, eb), (ra, rb), (ga, gb)):
+        assert torch.equal(x[finite].view(torch.int32), y[finite].view(torch.int32))
+    assert torch.equal(ma.view(torch.int32), mb.view(torch.int32)) or bool(ma.isnan() & mb.isnan())
+    ok = torch.isfinite(gw.float()).all(dim=1)
+    assert torch.equal(ka[ok].view(torch.int16), kb[ok].view(torch.int16))
+    if rows > 3:
+        assert int(fb.item()) == 1
+
+
+def test_grad_weight_partials_reduce_to_the_entry_point_result(cuda):
+    # grad_weight with out = NULL leaves partials whose in-order sum, rounded to bf16, is
+    # exactly what the entry point's own reduction writes
+    m, n, k = 2048, 384, 512
+    q = torch.randint(-127, 128, (m, k), generator=gen(41), dtype=torch.int8).to(cuda)
+    s = (torch.rand(m, generator=gen(42)) * 0.05 + 1e-3).to(cuda)
+    g = (torch.randn(m, n, generator=gen(43)) * 1e-2).to(torch.bfloat16).to(cuda)
+    part = grad_weight_bf16(g, q, s, reduce=False)
+    assert part.dtype == torch.float32 and part.shape[1:] == (n, k)
+    want = grad_weight_bf16(g, q, s, part.shape[0])
+    assert torch.equal(_reduce_partials(part).view(torch.int16), want.view(torch.int16))
+
+
 def test_fused_update_rms_ema_bit_exact(cuda):
     rows, k, mc, beta = 64, 512, 3, 0.9
     packed, _ = synthetic_state(rows, k, mc, seed=5)

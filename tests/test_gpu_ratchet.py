@@ -307,14 +307,7 @@ def test_float32_gradient_grad_weight_from_the_quant_pass_bf16_copy(cuda):
     torch.manual_seed(5)
     layer = DiscreteRatchetLinear(k, n, max_code=2, matmul_mode="int8", int8_backward=True,
                                   fuse_backward_update=True).to(cuda).train()
-    captured = {}
-    original = layer._launch_update
-
-    def capture(gradient, *rest):
-        captured["gw"] = gradient.detach().clone()
-        return original(gradient, *rest)
-
-    layer._launch_update = capture
+    layer.keep_weight_gradient = True  # the bf16 gradient the fused update consumed
     data = torch.Generator().manual_seed(8)
     x = torch.randn(m, k, generator=data).to(cuda)
     g = (torch.randn(m, n, generator=data) * 1e-2).to(cuda)
@@ -323,7 +316,7 @@ def test_float32_gradient_grad_weight_from_the_quant_pass_bf16_copy(cuda):
     assert out.dtype == torch.float32
     out.backward(g)
     want = grad_weight_bf16(g, q, s)
-    assert torch.equal(captured["gw"].view(torch.int16), want.view(torch.int16))
+    assert torch.equal(layer.last_weight_gradient.view(torch.int16), want.view(torch.int16))
 
 
 def test_unfused_int8_layer_grad_weight_reads_the_saved_inputs(cuda):
@@ -335,23 +328,16 @@ def test_unfused_int8_layer_grad_weight_reads_the_saved_inputs(cuda):
     torch.manual_seed(6)
     layer = DiscreteRatchetLinear(k, n, max_code=2, matmul_mode="int8",
                                   fuse_backward_update=True).to(cuda).train()
-    captured = {}
-    original = layer._launch_update
-
-    def capture(gradient, *rest):
-        captured["gw"] = gradient.detach().clone()
-        return original(gradient, *rest)
-
-    layer._launch_update = capture
+    layer.keep_weight_gradient = True
     data = torch.Generator().manual_seed(9)
     x = torch.randn(m, k, generator=data).to(cuda)
     g = torch.randn(m, n, generator=data).to(cuda) * 1e-2
     out = layer(x.clone().requires_grad_(True))
     out.backward(g)
     want = grad_weight_bf16_x(g.to(torch.bfloat16), x)
-    assert torch.equal(captured["gw"].view(torch.int16), want.view(torch.int16))
+    assert torch.equal(layer.last_weight_gradient.view(torch.int16), want.view(torch.int16))
     ref = g.to(torch.bfloat16).float().t() @ x.to(torch.bfloat16).float()
-    got = captured["gw"].float()
+    got = layer.last_weight_gradient.float()
     assert bool(((got - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
 
 
@@ -368,16 +354,9 @@ def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
                                   fuse_backward_update=True).to(cuda).train()
     packed_ref = layer.packed.cpu().numpy().copy()
     scale = layer.scale.float().cpu().numpy()
-    captured = {}
-    original = layer._launch_update
-
-    def capture(gradient, counts, row_rms, grad_scale, nonfinite):
-        # the weight gradient the update consumes (the one float producer shared with
-        # the oracle); runs on whichever stream the update is enqueued on
-        captured["gw"] = gradient.detach().clone()
-        return original(gradient, counts, row_rms, grad_scale, nonfinite)
-
-    layer._launch_update = capture
+    # the weight gradient the fused update consumes (the one float producer shared with
+    # the oracle), kept by the update itself
+    layer.keep_weight_gradient = True
     data = torch.Generator().manual_seed(99)
     for step in range(100):
         x = torch.randn(m, k, generator=data).to(torch.bfloat16)
@@ -400,7 +379,7 @@ def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
         gin_ref = ogemm.scaled_int8_mm(gq, code, gs, None)
         gin = xd.grad.to(torch.bfloat16).cpu().view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(gin, gin_ref), f"grad_input differs at step {step}"
-        gw = captured["gw"]
+        gw = layer.last_weight_gradient
         assert gw.dtype == torch.bfloat16
         # grad_weight = bf16(g)^T @ bf16(x_hat) in fp32, bf16 output: rel 1e-2 / abs 1e-3.
         xh = (torch.from_numpy(q_ref).to(torch.bfloat16)
