@@ -40,6 +40,7 @@ from .int8_matmul import (
     effective_bf16,
     grad_weight_bf16,
     grad_weight_bf16_x,
+    grad_weight_splits,
     int8_mm_nt,
     packed_int8_mm,
     packed_int8_mm_t,
@@ -248,6 +249,49 @@ class _RatchetMatmul(torch.autograd.Function):
 
         m, n = flat_gradient.shape
         gradient_bf16 = None
+        partials = None  # grad_weight split partials, reduced inside the update
+
+        def split_weight_gradient(g: Tensor) -> Tensor | None:
+            """grad_weight's split partials straight from the saved activations (int8 q, s
+            or the inputs themselves, bf16 cast while staging), or None where the split
+            kernel does not apply. The partials go to the layer's persistent workspace."""
+            if ctx.used_fused_int8:
+                if not _grad_weight_supported(g, q):
+                    return None
+                return grad_weight_bf16(g, q, s, reduce=False,
+                                        work=layer._split_workspace(m, g.device))
+            x_direct = flat_inputs if flat_inputs.dtype in (torch.float32, torch.bfloat16) \
+                else flat_inputs.to(torch.bfloat16)
+            if not _grad_weight_supported(g, x_direct):
+                return None
+            return grad_weight_bf16_x(g, x_direct, reduce=False,
+                                      work=layer._split_workspace(m, g.device))
+
+        # grad_weight (bf16 MFMA) reads only the upstream gradient and the saved
+        # activations: on a side stream it runs concurrently with the SR quant (VALU, Philox)
+        # and the grad_input GEMM; the update joins both (it must follow grad_input, which
+        # reads the pre-update codes). Done while a HIP graph is being captured, where the
+        # fork and join are graph edges; eagerly, a cross-stream wait costs more than the
+        # overlap gains at these kernel sizes (measured).
+        side = None
+        if mode != "fp32" and layer.overlap_weight_gradient and flat_gradient.is_cuda \
+                and torch.cuda.is_current_stream_capturing():
+            g_w = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
+                else flat_gradient.float()
+            if g_w.stride(-1) != 1:
+                g_w = g_w.contiguous()
+            main = torch.cuda.current_stream(g_w.device)
+            side = _side_stream(g_w.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                partials = split_weight_gradient(g_w)
+            if partials is None:
+                main.wait_stream(side)
+                side = None
+            else:
+                for t in (g_w, *ctx.saved_tensors):
+                    t.record_stream(side)
+
         if mode == "fp32":
             gradient_fp32 = flat_gradient.to(torch.float32)
             grad_input = gradient_fp32 @ layer._effective_weight_f32(scale_d)
@@ -259,7 +303,8 @@ class _RatchetMatmul(torch.autograd.Function):
                 g = g.float()
             grad_q = torch.empty((m, n), device=g.device, dtype=torch.int8)
             grad_s = torch.empty((m,), device=g.device, dtype=torch.float32)
-            if g.dtype == torch.float32 and _grad_weight_supported(g, ctx.saved_tensors[0]):
+            if partials is None and g.dtype == torch.float32 \
+                    and _grad_weight_supported(g, ctx.saved_tensors[0]):
                 # The same pass writes bf16(g), the grad_weight GEMM's gradient operand
                 # (grad_out_tile.to(bf16), ratchet.py:162), so that GEMM reads 2-byte
                 # values instead of converting float32 ones.
@@ -279,35 +324,31 @@ class _RatchetMatmul(torch.autograd.Function):
             gradient_bf16 = flat_gradient.to(torch.bfloat16)
             grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)
 
-        partials = None  # grad_weight split partials, reduced inside the update
         if mode == "fp32":
             grad_weight = gradient_fp32.t() @ inputs_fp32
-        else:
+        elif partials is None:
             # BF16 grad_weight [N, K] = bf16(g)^T @ bf16(x) (ratchet.py:159-163).
             g = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
                 else flat_gradient.float()
             if gradient_bf16 is not None:
                 g = gradient_bf16  # the bf16 copy this backward already made
-            x_direct = None
-            if not ctx.used_fused_int8:
-                x_direct = flat_inputs if flat_inputs.dtype in (torch.float32, torch.bfloat16) \
-                    else flat_inputs.to(torch.bfloat16)
-            if ctx.used_fused_int8 and _grad_weight_supported(g, q):
-                # straight from the saved int8 activations, no transposed copies; the
-                # update reduces the split partials itself (the bf16 gradient is never
-                # written)
-                partials = grad_weight_bf16(g, q, s, reduce=False)
-            elif x_direct is not None and _grad_weight_supported(g, x_direct):
-                # straight from the saved inputs (bf16 cast while staging)
-                partials = grad_weight_bf16_x(g, x_direct, reduce=False)
-            else:
+            # the update reduces the split partials itself (the bf16 gradient is never
+            # written)
+            partials = split_weight_gradient(g)
+            if partials is None:
                 # NT GEMM on transposed bf16 copies (both operands contiguous along tokens)
                 grad_t = transpose_bf16(g)
                 if ctx.used_fused_int8:
                     inputs_t = dequant_transpose_bf16(q, s)
                 else:
+                    x_direct = flat_inputs if flat_inputs.dtype in (torch.float32,
+                                                                    torch.bfloat16) \
+                        else flat_inputs.to(torch.bfloat16)
                     inputs_t = transpose_bf16(x_direct)
                 grad_weight = grad_t @ inputs_t.t()
+        if side is not None:
+            torch.cuda.current_stream(partials.device).wait_stream(side)
+            partials.record_stream(torch.cuda.current_stream(partials.device))
         if partials is not None:
             grad_scale = layer._fused_update(partials, want_grad_scale=needs_scale,
                                              from_partials=True)
@@ -317,11 +358,26 @@ class _RatchetMatmul(torch.autograd.Function):
             grad_scale, None
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The per-device stream the fused backward runs grad_weight on (default priority)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _SIDE_STREAMS:
+        _SIDE_STREAMS[index] = torch.cuda.Stream(device=index)
+    return _SIDE_STREAMS[index]
+
+
 # ---------------------------------------------------------------------------
 # Layer
 # ---------------------------------------------------------------------------
 class DiscreteRatchetLinear(nn.Module):
     """Linear layer with integer codes and pressure, but no master weight parameter."""
+
+    # fused backward under HIP-graph capture: grad_weight on a side stream, concurrent with
+    # grad_input (False: one stream, e.g. to compare the two)
+    overlap_weight_gradient: bool = True
 
     def __init__(
         self,
@@ -385,6 +441,7 @@ class DiscreteRatchetLinear(nn.Module):
         # e.g. to check it; off by default, since the fused update never writes it
         self.keep_weight_gradient = False
         self.last_weight_gradient: Tensor | None = None
+        self._gw_workspace: Tensor | None = None
         self.int8_backward = int8_backward
         self.tile_size = tile_size
 
@@ -499,6 +556,18 @@ class DiscreteRatchetLinear(nn.Module):
                 "(missing ratchet_update or unsupported weight sharing)"
             )
         self._pending_weight_gradient = gradient
+
+    def _split_workspace(self, tokens: int, device: torch.device) -> Tensor:
+        """float32 [nsplit, out, in] split-partial workspace of the grad_weight GEMM, kept
+        across steps (reused in stream order: each backward's GEMM follows the previous
+        update that read it)."""
+        nsplit = grad_weight_splits(tokens, self.out_features, self.in_features)
+        shape = (nsplit, self.out_features, self.in_features)
+        work = self._gw_workspace
+        if work is None or work.shape != shape or work.device != device:
+            work = torch.empty(shape, device=device, dtype=torch.float32)
+            self._gw_workspace = work
+        return work
 
     def _launch_update(self, gradient: Tensor, counts: Tensor, row_rms: Tensor | None,
                        grad_scale: Tensor | None, nonfinite: Tensor | None, *,
