@@ -16,6 +16,11 @@ Also reported on the same line:
   roofline       the dominant hand-written kernel against its roofline
   train_tokens_per_s  the 25M ratchet transformer (8 layers, d 512, 8 heads, FFN 2048,
                  vocab 8192, seq 512, batch 32, int8 + int8_backward) full training step
+  update_1b      the fused update of every layer of the 1B model (973 M weights) from its
+                 grad_weight split partials: HBM GB/s against 8 TB/s
+  train_1b       the 1B septenary ratchet transformer (24 layers, d 2048, 16 heads, FFN
+                 5632, vocab 8192, seq 1024, batch 8) training step, tokens/s
+  decode         KV-cached int8 decode of the 1B model at batch 1 and 16, tokens/s
   cpu_baseline   the reference's fp32 eager CPU path for the same op on a bounded
                  token sample, timed on this host's cores
 """
@@ -55,6 +60,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--model-warmup", type=int, default=3)
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-update-1b", action="store_true")
+    ap.add_argument("--no-train-1b", action="store_true")
+    ap.add_argument("--train-1b-steps", type=int, default=3)
+    ap.add_argument("--train-1b-warmup", type=int, default=2)
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the decode bench and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=64)
@@ -408,17 +417,26 @@ def roofline_entry(kernels: dict) -> dict:
             "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
 
 
-def model_bench(args, device):
-    """25M ratchet transformer training steps/s (sustained, syncs only at both ends)."""
+TRAIN_25M = dict(model="ratchet-gpt-25M", vocab=8192, block=512, batch=32, n_layer=8, n_head=8,
+                 n_embd=512, ffn=2048, max_code=MAX_CODE, codes="quinary")
+TRAIN_1B = dict(model="ratchet-gpt-1B", vocab=8192, block=1024, batch=8, n_layer=24, n_head=16,
+                n_embd=2048, ffn=5632, max_code=3, codes="septenary")
+
+
+def train_bench(shape: dict, steps: int, warmup: int, device):
+    """Training steps/s of a ratchet transformer (int8 + int8_backward, fused update every
+    step, AdamW on the float parameters, Zipf(1.1) token ids), sustained: syncs only at
+    both ends of the timed steps."""
     import numpy as np
     import torch
 
     from local_ai_training.model import ModelConfig, build_seeded_model
 
-    vocab, block, batch = 8192, 512, 32
-    config = ModelConfig(vocab_size=vocab, block_size=block, n_layer=8, n_head=8, n_embd=512,
-                         matmul_mode="int8", int8_backward=True)
-    model = build_seeded_model(config, max_code=MAX_CODE, seed=1337).to(device).train()
+    vocab, block, batch = shape["vocab"], shape["block"], shape["batch"]
+    config = ModelConfig(vocab_size=vocab, block_size=block, n_layer=shape["n_layer"],
+                         n_head=shape["n_head"], n_embd=shape["n_embd"],
+                         ffn_hidden=shape["ffn"], matmul_mode="int8", int8_backward=True)
+    model = build_seeded_model(config, max_code=shape["max_code"], seed=1337).to(device).train()
     optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.0)
     rng = np.random.default_rng(1337)
     ids = (rng.zipf(1.1, size=batch * (block + 1)) - 1) % vocab  # Zipf(s=1.1) token ids
@@ -435,15 +453,74 @@ def model_bench(args, device):
         optimizer.step()
         return loss
 
-    for _ in range(args.model_warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.model_steps):
+    for _ in range(steps):
         loss = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    return batch * block * args.model_steps / elapsed, elapsed / args.model_steps, float(loss.detach())
+    del model, optimizer
+    torch.cuda.empty_cache()
+    return batch * block * steps / elapsed, elapsed / steps, float(loss.detach())
+
+
+def model_bench(args, device):
+    """25M ratchet transformer training steps/s."""
+    return train_bench(TRAIN_25M, args.model_steps, args.model_warmup, device)
+
+
+def update_1b_bench(device, iters: int) -> dict:
+    """The fused update of one 1B training step at full scale: every ratchet layer of the 1B
+    septenary model (24 x qkv 6144x2048, proj 2048x2048, expand 5632x2048, contract
+    2048x5632, then lm_head 8192x2048; 973 M weights) updated from its grad_weight split
+    partials (the split counts of 8192 tokens), in model order. The partials (4 B per
+    weight and split) and packed states (1 B read + 1 B write) total more than the
+    last-level cache, so every sweep streams them from HBM."""
+    import torch
+
+    from local_ai_training import _native as nat
+    from local_ai_training.int8_matmul import grad_weight_splits
+
+    tokens, mc = 8192, 3
+    shapes = [(6144, 2048), (2048, 2048), (5632, 2048), (2048, 5632)] * 24 + [(8192, 2048)]
+    gen = torch.Generator().manual_seed(11)
+    layers = []
+    for n, k in shapes:
+        nsplit = grad_weight_splits(tokens, n, k)
+        code = torch.randint(-mc, mc + 1, (n, k), generator=gen, dtype=torch.int8)
+        packed = (((code + mc) & 0x0F) | (7 << 4)).to(torch.uint8).to(device)
+        part = torch.empty(nsplit, n, k, device=device).normal_(0.0, 1e-3)
+        layers.append((packed, part, nsplit, n, k, torch.empty(n, device=device)))
+    counts = torch.zeros(4, dtype=torch.int64, device=device)
+    flag = torch.zeros(1, dtype=torch.int32, device=device)
+    stream = nat.stream_handle(device)
+
+    def sweep():
+        for packed, part, nsplit, n, k, row_rms in layers:
+            nat.call("rk_ratchet_update_partials", packed.data_ptr(), k, part.data_ptr(),
+                     nsplit, n, k, mc, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
+                     row_rms.data_ptr(), None, flag.data_ptr(), None, None, k, stream)
+
+    sweep()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        sweep()
+    e1.record()
+    torch.cuda.synchronize()
+    sweep_s = e0.elapsed_time(e1) * 1e-3 / iters
+    weights = sum(n * k for n, k in shapes)
+    alg = sum(n * k * (2 + 4 * nsp) + 4 * n for _, _, nsp, n, k, _ in layers)
+    del layers
+    torch.cuda.empty_cache()
+    return {"workload": "fused update of every 1B ratchet layer from grad_weight split partials",
+            "weights": weights, "launches": len(shapes), "alg_bytes": alg,
+            "ms": round(sweep_s * 1e3, 3), "GB_s": round(alg / sweep_s / 1e9, 1),
+            "frac_hbm": round(alg / sweep_s / PEAK_HBM_BPS, 4)}
 
 
 DECODE_LAYERS = dict(vocab=8192, block=1024, n_layer=24, n_head=16, n_embd=2048, ffn=5632)
@@ -712,6 +789,19 @@ def main() -> int:
         result["train_config"] = {"model": "ratchet-gpt-25M", "n_layer": 8, "n_embd": 512,
                                   "n_head": 8, "ffn": 2048, "vocab": 8192, "seq_len": 512,
                                   "batch": 32, "matmul_mode": "int8", "int8_backward": True}
+    if not args.no_update_1b:
+        log("update bench: the fused update of every 1B layer from split partials")
+        result["update_1b"] = update_1b_bench(device, 5)
+        log(f"  {result['update_1b']}")
+    if not args.no_train_1b:
+        log(f"1B training bench: warmup={args.train_1b_warmup} steps={args.train_1b_steps}")
+        tok_s, step_1b, loss_1b = train_bench(TRAIN_1B, args.train_1b_steps,
+                                              args.train_1b_warmup, device)
+        log(f"1B model {step_1b * 1e3:.1f} ms/step -> {tok_s:.0f} tok/s (loss {loss_1b:.3f})")
+        result["train_1b"] = {"tokens_per_s": round(tok_s, 1),
+                              "ms_per_step": round(step_1b * 1e3, 2),
+                              "config": {k: TRAIN_1B[k] for k in TRAIN_1B},
+                              "matmul_mode": "int8", "int8_backward": True}
     if not args.no_decode:
         log(f"decode bench: 1B int8, batches {args.decode_batches}, {args.decode_steps} steps")
         result["decode"] = decode_bench(args, device)

@@ -40,6 +40,80 @@ __device__ __forceinline__ uint32_t ratchet_byte(uint32_t byte, float z, int mc,
   return static_cast<uint32_t>((cn + mc) & 15) | (static_cast<uint32_t>((p + 7) & 15) << 4);
 }
 
+// Smallest float t >= 0 with RN(t / d) >= c, for c > 0 and 0 < d < inf (+inf if no finite t
+// qualifies). RN(x / d) is non-decreasing in x, so for every float g:
+//   RN(|g| / d) >= c  <=>  |g| >= t,
+// which turns the update's bucket tests on z = g / d into compares on |g| with no division
+// per weight. The search starts at RN(c * d), within a few ulps of the boundary; `ok` is
+// cleared if it does not settle within 8 steps (the caller then divides per weight).
+__device__ __forceinline__ float bucket_threshold(float c, float d, bool& ok) {
+  constexpr float kMax = 3.40282347e38f;
+  float t = c * d;
+  if (!(t < kMax)) t = kMax;
+  int i = 0;
+  for (; i < 8 && !(t / d >= c); ++i) {
+    if (t == kMax) return INFINITY;
+    t = __uint_as_float(__float_as_uint(t) + 1u);
+  }
+  if (i == 8) ok = false;
+  int j = 0;
+  for (; j < 8; ++j) {
+    const float prev = __uint_as_float(__float_as_uint(t) - 1u);
+    if (!(prev / d >= c)) break;
+    t = prev;
+  }
+  if (j == 8) ok = false;
+  return t;
+}
+
+// Per-launch byte constants of ratchet_word (ratchet.py:248-301 on four packed weights).
+struct SwarConsts {
+  uint32_t ge_pr;    // + x: bit 7 of a byte set iff x >= T + 9 (pressure reset up)
+  uint32_t ge_nr;    // + x: bit 7 set iff x >= 10 - T (clear: pressure reset down)
+  uint32_t ge_cmax;  // + code: bit 7 set iff code byte >= 2 * max_code
+  uint32_t T;
+};
+
+__device__ __forceinline__ SwarConsts swar_consts(int T, int mc) {
+  const int c_pr = T + 9 < 20 ? T + 9 : 20;   // x <= 19: thresholds above never fire
+  const int c_nr = 10 - T > 0 ? 10 - T : 0;
+  SwarConsts k;
+  k.ge_pr = static_cast<uint32_t>(128 - c_pr) * 0x01010101u;
+  k.ge_nr = static_cast<uint32_t>(128 - c_nr) * 0x01010101u;
+  k.ge_cmax = static_cast<uint32_t>(128 - 2 * mc) * 0x01010101u;
+  k.T = static_cast<uint32_t>(T);
+  return k;
+}
+
+// The update of four weights in one packed word, byte i holding weight i, and e holding
+// per byte 2 - sign(z) * mag(z) in [0, 4] (from the bucket compares). With the pressure
+// biased by 9 (x = (p + 7) + 2 - sign * mag = p_new + 9 in [0, 19]) every per-byte step
+// stays inside its byte: the compares add (128 - bound) and read bit 7, the resets
+// subtract / add T only where x >= T + 9 / x <= 9 - T (never both, T >= 1), codes move
+// only inside [0, 2 max_code]. Bit-identical to ratchet_byte on each byte: the pressure
+// nibble wraps the same way and the int8 clamp never binds for |p| <= 10. A byte 0x70
+// (pressure 0) with e = 2 changes nothing and counts nothing, which is how the bytes
+// past the end of a row are filled.
+__device__ __forceinline__ uint32_t ratchet_word(uint32_t w, uint32_t e, const SwarConsts& k,
+                                                 MoveCounts& cnt) {
+  const uint32_t cb = w & 0x0F0F0F0Fu;
+  const uint32_t x = ((w >> 4) & 0x0F0F0F0Fu) + e;
+  const uint32_t pr = ((x + k.ge_pr) >> 7) & 0x01010101u;
+  const uint32_t nr = (((x + k.ge_nr) >> 7) & 0x01010101u) ^ 0x01010101u;
+  const uint32_t cmax = ((cb + k.ge_cmax) >> 7) & 0x01010101u;
+  const uint32_t cpos = ((cb + 0x7F7F7F7Fu) >> 7) & 0x01010101u;
+  const uint32_t pm = pr & (cmax ^ 0x01010101u);
+  const uint32_t nm = nr & cpos;
+  const uint32_t y = x - pr * k.T + nr * k.T;
+  cnt.pos += __builtin_popcount(pm);
+  cnt.neg += __builtin_popcount(nm);
+  cnt.bpos += __builtin_popcount(pr & cmax);
+  cnt.bneg += __builtin_popcount(nr & (cpos ^ 0x01010101u));
+  const uint32_t cn = cb + pm - nm;
+  const uint32_t pn = (y + 0x0E0E0E0Eu) & 0x0F0F0F0Fu;
+  return cn | (pn << 4);
+}
+
 // Block-level count reduction and one 64-bit atomic per counter per block.
 __device__ __forceinline__ void flush_counts(MoveCounts cnt, int64_t* counts) {
   __shared__ int sc[4];
@@ -65,8 +139,8 @@ __device__ __forceinline__ bool finite_f32(float x) {
   return (__float_as_uint(x) & 0x7f800000u) != 0x7f800000u;
 }
 
-// Loads V packed bytes (zeros past K) into one word per 4 bytes.
-template <int V>
+// Loads V packed bytes (FILL past K) into one word per 4 bytes.
+template <int V, uint32_t FILL = 0u>
 __device__ __forceinline__ void load_bytes(const uint8_t* p, int64_t e0, int64_t K, bool vec,
                                            uint32_t* w) {
   if (vec && e0 + V <= K) {
@@ -79,10 +153,12 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, int64_t e0, int64_t
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < V / 4; ++j) w[j] = 0;
+    for (int j = 0; j < V / 4; ++j) w[j] = FILL * 0x01010101u;
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (e0 + i < K) w[i >> 2] |= static_cast<uint32_t>(p[e0 + i]) << (8 * (i & 3));
+      if (e0 + i < K)
+        w[i >> 2] = (w[i >> 2] & ~(0xffu << (8 * (i & 3)))) |
+                    (static_cast<uint32_t>(p[e0 + i]) << (8 * (i & 3)));
   }
 }
 
@@ -264,10 +340,11 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       }
     };
 
-    // Pass 1: sum of squares (fixed order) and the finiteness check.
+    // Pass 1: sum of squares (fixed order). A non-finite gradient element makes the sum
+    // non-finite, so only a row whose sum is not finite (overflow of finite values
+    // included) is searched element by element.
     float xr[NC > 0 ? NC : 1][V];
     float acc = 0.0f;
-    int bad = 0;
     if constexpr (NC > 0) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -279,10 +356,7 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
           for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-          bad |= !finite_f32(xr[c][i]);
-          acc = acc + xr[c][i] * xr[c][i];
-        }
+        for (int i = 0; i < V; ++i) acc = acc + xr[c][i] * xr[c][i];
       }
     } else {
       for (int64_t c = 0; c < nchunks; ++c) {
@@ -290,14 +364,27 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
         load_g(c * SPAN + lane0, v);
         keep_g(c * SPAN + lane0, v);
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-          bad |= !finite_f32(v[i]);
-          acc = acc + v[i] * v[i];
-        }
+        for (int i = 0; i < V; ++i) acc = acc + v[i] * v[i];
       }
     }
     acc = wave_sum_butterfly(acc);
-    bad = wave_or_int(bad);
+    int bad = 0;
+    if (!finite_f32(acc)) {
+      if constexpr (NC > 0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < V; ++i) bad |= !finite_f32(xr[c][i]);
+      } else {
+        for (int64_t c = 0; c < nchunks; ++c) {
+          float v[V];
+          load_g(c * SPAN + lane0, v);
+#pragma unroll
+          for (int i = 0; i < V; ++i) bad |= !finite_f32(v[i]);
+        }
+      }
+      bad = wave_or_int(bad);
+    }
 
     const float ms = acc / static_cast<float>(a.K);
     const float rms_inst = sqrtf(ms);
@@ -340,19 +427,51 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
     const float d = rms + a.eps;
 
     // Pass 2: normalize, update, repack; optional sum_k g * code (pre-update code).
+    // z = g / d is never formed on the fast path: with tl / th the smallest floats whose
+    // quotient by d reaches low / high, |z| >= low <=> |g| >= tl and likewise for high
+    // (division is monotone), and for low > 0 a weight that moves has z != 0, so
+    // sign(z) = sign(g). The per-weight division stays for low == 0 (where an underflowed
+    // z of sign 0 still buckets), d not finite and positive, or an unsettled search.
+    bool fast = a.low > 0.0f && d > 0.0f && d < INFINITY;
+    float tl = 0.0f, th = 0.0f;
+    if (fast) {
+      tl = bucket_threshold(a.low, d, fast);
+      th = bucket_threshold(a.high, d, fast);
+    }
+    const SwarConsts kc = swar_consts(a.T, a.mc);
     float gs = 0.0f;
     auto do_chunk = [&](int64_t e0, const float* v) {
       uint32_t w[NW], out[NW];
-      load_bytes<V>(prow, e0, a.K, a.vec_p, w);
+      load_bytes<V, 0x70u>(prow, e0, a.K, a.vec_p, w);
+      if (a.grad_scale) {
 #pragma unroll
-      for (int j = 0; j < NW; ++j) out[j] = 0;
+        for (int i = 0; i < V; ++i) {
+          const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+          gs = gs + v[i] * static_cast<float>(static_cast<int>(byte & 15u) - a.mc);
+        }
+      }
+      if (fast) {
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
-        if (a.grad_scale) gs = gs + v[i] * static_cast<float>(static_cast<int>(byte & 15u) - a.mc);
-        if (e0 + i < a.K) {
-          const float zz = v[i] / d;
-          out[i >> 2] |= ratchet_byte(byte, zz, a.mc, a.T, a.low, a.high, cnt) << (8 * (i & 3));
+        for (int j = 0; j < NW; ++j) {
+          uint32_t e = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float g = v[4 * j + q];
+            const uint32_t m = (fabsf(g) >= tl ? 1u : 0u) + (fabsf(g) >= th ? 1u : 0u);
+            e |= (__float_as_uint(g) >> 31 ? 2u + m : 2u - m) << (8 * q);
+          }
+          out[j] = ratchet_word(w[j], e, kc, cnt);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NW; ++j) out[j] = 0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          if (e0 + i < a.K) {
+            const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            out[i >> 2] |=
+                ratchet_byte(byte, v[i] / d, a.mc, a.T, a.low, a.high, cnt) << (8 * (i & 3));
+          }
         }
       }
       store_bytes<V>(prow, e0, a.K, a.vec_p, out);

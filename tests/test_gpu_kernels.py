@@ -465,7 +465,8 @@ def test_update_from_normalized_gradient_bit_exact(cuda, rows, k, max_code, thre
     assert counts.cpu().tolist() == ref_counts.tolist()
 
 
-def _update_grad(packed, g, mc, T, eps=1e-8, ema=None, beta=0.0, want_scale=True):
+def _update_grad(packed, g, mc, T, eps=1e-8, ema=None, beta=0.0, want_scale=True, low=0.5,
+                 high=1.5):
     dev = packed.device
     rows, k = g.shape
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -473,7 +474,7 @@ def _update_grad(packed, g, mc, T, eps=1e-8, ema=None, beta=0.0, want_scale=True
     gscale = torch.empty(rows, device=dev) if want_scale else None
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
     nat.call("rk_ratchet_update_grad", packed.data_ptr(), packed.stride(0), g.data_ptr(),
-             nat.dtype_code(g.dtype), g.stride(0), rows, k, mc, T, 0.5, 1.5, eps, nat.ptr(ema),
+             nat.dtype_code(g.dtype), g.stride(0), rows, k, mc, T, low, high, eps, nat.ptr(ema),
              beta, 1.0 - beta, counts.data_ptr(), row_rms.data_ptr(), nat.ptr(gscale),
              flag.data_ptr(), None, nat.stream_handle(dev))
     return counts, row_rms, gscale, flag
@@ -607,6 +608,64 @@ def test_fused_update_rms_ema_bit_exact(cuda):
         packed, ema = ref["packed"], ref["rms_ema"]
         assert np.array_equal(pd.cpu().numpy(), packed)
         assert np.array_equal(f32bits(ema_d), f32bits(ema))
+
+
+def _smallest_reaching(c, d):
+    """Smallest float32 t >= 0 whose float32 quotient t / d is >= c (brute-force walk)."""
+    c, d = np.float32(c), np.float32(d)
+    t = np.float32(c * d)
+    while not np.float32(t / d) >= c:
+        t = np.nextafter(t, np.float32(np.inf))
+    while np.float32(np.nextafter(t, np.float32(0)) / d) >= c:
+        t = np.nextafter(t, np.float32(0))
+    return t
+
+
+# The update buckets |g / d| against low / high; gradients placed on the exact float
+# boundaries of those buckets (the boundary value, one ulp below, one ulp above, both
+# signs) must bucket exactly as the division does. The row divisor d is pinned through
+# the RMS EMA (beta 1: d = sqrt(ema) + eps, whatever the row holds); cases cover
+# d from 1e-15 to 2e10, low == 0, and a subnormal d (eps 1e-39, rows too small to square).
+@pytest.mark.parametrize("low,high,ema_val,eps", [
+    (0.5, 1.5, 0.37, 1e-8), (1e-3, 2.0, 1e-30, 1e-30), (0.7, 0.9, 4e20, 1e-8),
+    (0.5, 1.5, 1.0, 1e-12), (0.0, 1.5, 0.5, 1e-8), (0.25, 3.0, None, 1e-39)])
+def test_fused_update_bucket_boundaries_bit_exact(cuda, low, high, ema_val, eps):
+    rows, k, mc, T = 24, 512, 3, 3
+    packed, _ = synthetic_state(rows, k, mc, seed=77)
+    rng = np.random.default_rng(78)
+    if ema_val is None:
+        d = np.float32(eps)  # every g * g underflows: rms 0
+        scale = d
+    else:
+        d = np.float32(np.sqrt(np.float32(ema_val))) + np.float32(eps)
+        scale = d
+    edges = []
+    for c in (low, high):
+        if c <= 0.0:
+            continue
+        t = _smallest_reaching(c, d)
+        below = np.nextafter(t, np.float32(0))
+        assert np.float32(t / d) >= np.float32(c) > np.float32(below / d)
+        edges += [t, below, np.nextafter(t, np.float32(np.inf))]
+    edges = np.array(edges + [0.0, 1e-45], np.float32)
+    edges = np.concatenate([edges, -edges])
+    g = (rng.standard_normal((rows, k)) * scale).astype(np.float32)
+    for r in range(rows):
+        cols = rng.choice(k, size=4 * edges.size, replace=False)
+        g[r, cols] = np.tile(edges, 4)
+    if ema_val is None:
+        assert not np.any(g * g)
+    pd = torch.from_numpy(packed).to(cuda)
+    ema = None if ema_val is None else np.full(rows, ema_val, np.float32)
+    ema_d = None if ema is None else torch.from_numpy(ema.copy()).to(cuda)
+    beta = 0.0 if ema is None else 1.0
+    counts, _, gscale, flag = _update_grad(pd, torch.from_numpy(g).to(cuda), mc, T, eps=eps,
+                                           ema=ema_d, beta=beta, low=low, high=high)
+    ref = oupd.update_from_gradient(packed, g, mc, T, low, high, eps, 4, rms_ema=ema, beta=beta)
+    assert np.array_equal(pd.cpu().numpy(), ref["packed"])
+    assert counts.cpu().tolist() == ref["counts"].tolist()
+    assert np.array_equal(f32bits(gscale), f32bits(ref["grad_scale"]))
+    assert int(flag.item()) == 0
 
 
 def test_fused_update_nonfinite_rows_unchanged_and_flagged(cuda):
