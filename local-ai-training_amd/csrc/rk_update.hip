@@ -152,11 +152,12 @@ __device__ __forceinline__ void load_bytes(const uint8_t* p, int64_t e0, int64_t
       w[0] = *reinterpret_cast<const uint32_t*>(p + e0);
     }
   } else {
+    const int64_t rem = K - e0;
 #pragma unroll
     for (int j = 0; j < V / 4; ++j) w[j] = FILL * 0x01010101u;
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (e0 + i < K)
+      if (i < rem)
         w[i >> 2] = (w[i >> 2] & ~(0xffu << (8 * (i & 3)))) |
                     (static_cast<uint32_t>(p[e0 + i]) << (8 * (i & 3)));
   }
@@ -172,9 +173,10 @@ __device__ __forceinline__ void store_bytes(uint8_t* p, int64_t e0, int64_t K, b
       *reinterpret_cast<uint32_t*>(p + e0) = w[0];
     }
   } else {
+    const int64_t rem = K - e0;
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (e0 + i < K) p[e0 + i] = static_cast<uint8_t>(w[i >> 2] >> (8 * (i & 3)));
+      if (i < rem) p[e0 + i] = static_cast<uint8_t>(w[i >> 2] >> (8 * (i & 3)));
   }
 }
 
@@ -215,6 +217,10 @@ __global__ __launch_bounds__(256) void ratchet_update_z_kernel(
 }
 
 // ---------------------------------------------------------------------------
+typedef float upd_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t upd_pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   const bf2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
@@ -270,123 +276,291 @@ __global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms,
   }
   if (threadIdx.x == 0) mean[0] = part[0] / static_cast<float>(rows);
 }
+// Element i of a 16-byte gradient vector held as four words (4 fp32, or 8 bf16 in pairs,
+// element 2j in the low half of word j).
+template <int DT>
+__device__ __forceinline__ float vec_elem(const uint32_t* w, int i) {
+  if constexpr (DT == RK_F32) {
+    return __uint_as_float(w[i]);
+  } else {
+    return __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+  }
+}
+
+// Smallest bf16 bit pattern whose value is >= t, for t >= 0 (+inf -> 0x7f80): for a bf16
+// g, |g| >= t <=> bits(|g|) >= bf16_ceil_bits(t).
+__device__ __forceinline__ uint32_t bf16_ceil_bits(float t) {
+  const uint32_t b = __float_as_uint(t);
+  return (b >> 16) + ((b & 0xffffu) != 0u ? 1u : 0u);
+}
+
+// Bucket bytes (2 - sign(g) * mag(g), byte q for element q) of four bf16 gradients held in
+// two words, from 16-bit compares: kl / kh = (0x8000 - threshold bits) in both halves, so
+// bit 15 of a half of |g| + k is set iff |g| >= threshold (|g| <= 0x7fff: no carry between
+// halves). v_perm selectors 8..11 replicate bits 15 / 31 of its second and first source
+// into a byte: 0x0b0a0908 lays out elements 0..3.
+__device__ __forceinline__ uint32_t bucket_bytes_bf16(uint32_t w0, uint32_t w1, uint32_t kl,
+                                                      uint32_t kh) {
+  constexpr uint32_t kSel = 0x0b0a0908u;
+  const uint32_t a0 = w0 & 0x7fff7fffu, a1 = w1 & 0x7fff7fffu;
+  const uint32_t gel = __builtin_amdgcn_perm(a1 + kl, a0 + kl, kSel);
+  const uint32_t geh = __builtin_amdgcn_perm(a1 + kh, a0 + kh, kSel);
+  const uint32_t neg = __builtin_amdgcn_perm(w1, w0, kSel);
+  const uint32_t m = (gel & 0x01010101u) + (geh & 0x01010101u);
+  return 0x02020202u - m + (neg & (m << 1));
+}
+
+// Bucket bytes of four fp32 gradients from float compares against the thresholds.
+__device__ __forceinline__ uint32_t bucket_bytes_f32(const uint32_t* w, float tl, float th) {
+  uint32_t e = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float g = __uint_as_float(w[q]);
+    const uint32_t m = (fabsf(g) >= tl ? 1u : 0u) + (fabsf(g) >= th ? 1u : 0u);
+    e |= ((w[q] >> 31) ? 2u + m : 2u - m) << (8 * q);
+  }
+  return e;
+}
+
 // ZONLY = true: write z = g / (rms + eps) instead of updating (the reference's
 // _normalize, ratchet.py:539-556), with the identical reduction order.
+//
+// A lane holds a row's gradient as 16-byte vectors (four words: 4 fp32 or 8 bf16), chunk c
+// covering elements c * 64 * V + lane * V. NC > 0: the whole row stays in registers between
+// the passes, the packed bytes are fetched with the gradient, and every load of the row is
+// in flight before the first is consumed. NC == 0: rows longer than the register chunks
+// stream twice.
 template <int DT, int NC, bool ZONLY>
 __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs a) {
   constexpr int V = DT == RK_F32 ? 4 : 8;
   constexpr int SPAN = 64 * V;
   constexpr int NW = V / 4;
+  constexpr bool BF16W = DT != RK_F32;  // words hold bf16 pairs
   const int lane = threadIdx.x & 63;
   const int64_t lane0 = static_cast<int64_t>(lane) * V;
-  const int64_t nchunks = (a.K + SPAN - 1) / SPAN;
   MoveCounts cnt;
 
   for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
        row += static_cast<int64_t>(gridDim.x) * 4) {
+    // K opaque per row: the compiler would otherwise hoist every chunk's per-element tail
+    // tests out of the row loop and hold them in registers for the whole kernel
+    int64_t K = a.K;
+    asm volatile("" : "+s"(K));
+    const int64_t nchunks = (K + SPAN - 1) / SPAN;
     const char* grow =
         static_cast<const char*>(a.g) + row * a.ldg * (DT == RK_F32 ? 4 : 2);
     uint8_t* prow = a.packed + row * a.ldp;
+    const float* prt = a.part + row * K;
 
-    auto load_g = [&](int64_t e0, float* v) {
+    // fp32 split sums rounded to bf16, two per word (the grad_weight reduction's rounding)
+    auto pack_sums = [](const float4& lo, const float4& hi, uint32_t* w) {
+      w[0] = upd_pack_bf16x2(lo.x, lo.y);
+      w[1] = upd_pack_bf16x2(lo.z, lo.w);
+      w[2] = upd_pack_bf16x2(hi.x, hi.y);
+      w[3] = upd_pack_bf16x2(hi.z, hi.w);
+    };
+    auto add4 = [](float4& x, const float4& y) {
+      x.x = x.x + y.x;
+      x.y = x.y + y.y;
+      x.z = x.z + y.z;
+      x.w = x.w + y.w;
+    };
+    // One vector of the gradient as words (zeros past K).
+    auto load_words = [&](int64_t e0, uint32_t* w) {
       if constexpr (DT == SRC_SPLITS) {
         // K % 8 == 0 (checked on the host): a vector is wholly inside or past the row
-        if (e0 < a.K) {
-          const float* p = a.part + row * a.K + e0;
-          float4 lo = *reinterpret_cast<const float4*>(p);
-          float4 hi = *reinterpret_cast<const float4*>(p + 4);
+        if (e0 < K) {
+          float4 lo = *reinterpret_cast<const float4*>(prt + e0);
+          float4 hi = *reinterpret_cast<const float4*>(prt + e0 + 4);
 #pragma unroll 8
           for (int s = 1; s < a.nsplit; ++s) {
-            const float4 l2 = *reinterpret_cast<const float4*>(p + s * a.part_stride);
-            const float4 h2 = *reinterpret_cast<const float4*>(p + s * a.part_stride + 4);
-            lo.x = lo.x + l2.x;
-            lo.y = lo.y + l2.y;
-            lo.z = lo.z + l2.z;
-            lo.w = lo.w + l2.w;
-            hi.x = hi.x + h2.x;
-            hi.y = hi.y + h2.y;
-            hi.z = hi.z + h2.z;
-            hi.w = hi.w + h2.w;
+            add4(lo, *reinterpret_cast<const float4*>(prt + s * a.part_stride + e0));
+            add4(hi, *reinterpret_cast<const float4*>(prt + s * a.part_stride + e0 + 4));
           }
-          const uint32_t w[4] = {upd_pack_bf16x2(lo.x, lo.y), upd_pack_bf16x2(lo.z, lo.w),
-                                 upd_pack_bf16x2(hi.x, hi.y), upd_pack_bf16x2(hi.z, hi.w)};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[2 * j] = __uint_as_float(w[j] << 16);
-            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-          }
+          pack_sums(lo, hi, w);
         } else {
 #pragma unroll
-          for (int i = 0; i < V; ++i) v[i] = 0.0f;
+          for (int j = 0; j < 4; ++j) w[j] = 0;
         }
-      } else if (a.vec_g && e0 + V <= a.K) {
-        load_vec16<DT>(grow, e0, v);
+      } else if (a.vec_g && e0 + V <= K) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(grow + e0 * (DT == RK_F32 ? 4 : 2));
+        w[0] = raw.x;
+        w[1] = raw.y;
+        w[2] = raw.z;
+        w[3] = raw.w;
       } else {
 #pragma unroll
-        for (int i = 0; i < V; ++i) v[i] = e0 + i < a.K ? load_elem<DT>(grow, e0 + i) : 0.0f;
+        for (int j = 0; j < 4; ++j) w[j] = 0;
+        const int64_t rem = K - e0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          if (i < rem) {
+            const uint32_t b = __float_as_uint(load_elem<DT>(grow, e0 + i));
+            if constexpr (BF16W) w[i >> 1] |= (i & 1) ? (b & 0xffff0000u) : (b >> 16);
+            else w[i] = b;
+          }
+        }
       }
     };
-    // SRC_SPLITS with a gradient copy requested: written once, from pass 1
-    auto keep_g = [&](int64_t e0, const float* v) {
+    // SRC_SPLITS with a gradient copy requested: the bf16 words, written once, in pass 1
+    auto keep_words = [&](int64_t e0, const uint32_t* w) {
       if constexpr (DT == SRC_SPLITS) {
-        if (a.g_out && e0 < a.K) {
-          uint4 w;
-          w.x = (__float_as_uint(v[0]) >> 16) | (__float_as_uint(v[1]) & 0xffff0000u);
-          w.y = (__float_as_uint(v[2]) >> 16) | (__float_as_uint(v[3]) & 0xffff0000u);
-          w.z = (__float_as_uint(v[4]) >> 16) | (__float_as_uint(v[5]) & 0xffff0000u);
-          w.w = (__float_as_uint(v[6]) >> 16) | (__float_as_uint(v[7]) & 0xffff0000u);
-          *reinterpret_cast<uint4*>(a.g_out + row * a.ldgo + e0) = w;
+        if (a.g_out && e0 < K)
+          *reinterpret_cast<uint4*>(a.g_out + row * a.ldgo + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    };
+    auto sumsq = [&](float acc, const uint32_t* w) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float x = vec_elem<DT>(w, i);
+        acc = acc + x * x;
+      }
+      return acc;
+    };
+
+    // The packed bytes of every register chunk, fetched with the gradient: unconditional
+    // buffer loads (K % V == 0 whenever vec_p, so a vector is wholly inside or past the
+    // row; without vec_p every load reads zero and pass 2 reads the bytes one by one).
+    uint32_t xg[NC > 0 ? NC : 1][4];
+    uint32_t xp[NC > 0 ? NC : 1][NW];
+    auto prefetch_packed = [&]() {
+      if constexpr (!ZONLY && NC > 0) {
+        const __amdgpu_buffer_rsrc_t r = make_buffer(prow, a.vec_p ? static_cast<int>(K) : 0);
+        const uint32_t voff = static_cast<uint32_t>(lane0);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if constexpr (V == 8) {
+            const u32x2_t t = __builtin_bit_cast(
+                u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, c * SPAN, 0));
+            xp[c][0] = t.x;
+            xp[c][NW - 1] = t.y;
+          } else {
+            xp[c][0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, c * SPAN, 0);
+          }
         }
       }
     };
 
-    // Pass 1: sum of squares (fixed order). A non-finite gradient element makes the sum
-    // non-finite, so only a row whose sum is not finite (overflow of finite values
-    // included) is searched element by element.
-    float xr[NC > 0 ? NC : 1][V];
+    // Pass 1: loads, then the sum of squares in fixed order. A non-finite gradient element
+    // makes the sum non-finite, so only a row whose sum is not finite (overflow of finite
+    // values included) is searched element by element.
     float acc = 0.0f;
     if constexpr (NC > 0) {
+      if constexpr (DT == SRC_SPLITS) {
+        // Buffer loads, one descriptor per split of the row: past-K vectors read as zero
+        // (K % 8 == 0, so a vector is wholly inside or past the row). Split 0 of every
+        // chunk is in flight together, then GS splits of every chunk at a time (about 64
+        // registers), added in split order.
+        constexpr int GS = NC >= 8 ? 1 : (NC >= 4 ? 2 : (NC >= 2 ? 4 : 8));
+        const uint32_t voff = static_cast<uint32_t>(lane0) * 4u;
+        auto ld = [&](__amdgpu_buffer_rsrc_t r, int c, int half) {
+          return __builtin_bit_cast(
+              upd_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, c * SPAN * 4 + 16 * half, 0));
+        };
+        upd_f32x4 lo[NC], hi[NC];
+        {
+          const __amdgpu_buffer_rsrc_t r = make_buffer(prt, K * 4);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c < nchunks) {
-          load_g(c * SPAN + lane0, xr[c]);
-          keep_g(c * SPAN + lane0, xr[c]);
-        } else {
+          for (int c = 0; c < NC; ++c) {
+            lo[c] = ld(r, c, 0);
+            hi[c] = ld(r, c, 1);
+          }
+        }
+        prefetch_packed();
+        for (int s = 1; s < a.nsplit; s += GS) {
+          upd_f32x4 l[GS][NC], h[GS][NC];
 #pragma unroll
-          for (int i = 0; i < V; ++i) xr[c][i] = 0.0f;
+          for (int q = 0; q < GS; ++q) {
+            if (s + q < a.nsplit) {
+              const __amdgpu_buffer_rsrc_t r = make_buffer(prt + (s + q) * a.part_stride, K * 4);
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                l[q][c] = ld(r, c, 0);
+                h[q][c] = ld(r, c, 1);
+              }
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < GS; ++q) {
+            if (s + q < a.nsplit) {
+#pragma unroll
+              for (int c = 0; c < NC; ++c) {
+                lo[c] = lo[c] + l[q][c];
+                hi[c] = hi[c] + h[q][c];
+              }
+            }
+          }
         }
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc = acc + xr[c][i] * xr[c][i];
+        for (int c = 0; c < NC; ++c) {
+          xg[c][0] = upd_pack_bf16x2(lo[c].x, lo[c].y);
+          xg[c][1] = upd_pack_bf16x2(lo[c].z, lo[c].w);
+          xg[c][2] = upd_pack_bf16x2(hi[c].x, hi[c].y);
+          xg[c][3] = upd_pack_bf16x2(hi[c].z, hi[c].w);
+        }
+      } else {
+        // unconditional buffer loads (a vector wholly past K, or every vector when the
+        // gradient is not vector-aligned, reads as zero), then the unaligned case element
+        // by element behind one uniform branch
+        constexpr int ES = DT == RK_F32 ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t r = make_buffer(grow, a.vec_g ? static_cast<int>(K) * ES : 0);
+        const uint32_t voff = static_cast<uint32_t>(lane0) * ES;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4_t t = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, c * SPAN * ES, 0));
+          xg[c][0] = t.x;
+          xg[c][1] = t.y;
+          xg[c][2] = t.z;
+          xg[c][3] = t.w;
+        }
+        prefetch_packed();
+        if (!a.vec_g) {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            if (c < nchunks) {
+              load_words(c * SPAN + lane0, xg[c]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) xg[c][j] = 0;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (c < nchunks) keep_words(c * SPAN + lane0, xg[c]);
+        acc = sumsq(acc, xg[c]);
       }
     } else {
       for (int64_t c = 0; c < nchunks; ++c) {
-        float v[V];
-        load_g(c * SPAN + lane0, v);
-        keep_g(c * SPAN + lane0, v);
-#pragma unroll
-        for (int i = 0; i < V; ++i) acc = acc + v[i] * v[i];
+        uint32_t w[4];
+        load_words(c * SPAN + lane0, w);
+        keep_words(c * SPAN + lane0, w);
+        acc = sumsq(acc, w);
       }
     }
     acc = wave_sum_butterfly(acc);
     int bad = 0;
     if (!finite_f32(acc)) {
+      auto scan = [&](const uint32_t* w) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) bad |= !finite_f32(vec_elem<DT>(w, i));
+      };
       if constexpr (NC > 0) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int i = 0; i < V; ++i) bad |= !finite_f32(xr[c][i]);
+        for (int c = 0; c < NC; ++c) scan(xg[c]);
       } else {
         for (int64_t c = 0; c < nchunks; ++c) {
-          float v[V];
-          load_g(c * SPAN + lane0, v);
-#pragma unroll
-          for (int i = 0; i < V; ++i) bad |= !finite_f32(v[i]);
+          uint32_t w[4];
+          load_words(c * SPAN + lane0, w);
+          scan(w);
         }
       }
       bad = wave_or_int(bad);
     }
 
-    const float ms = acc / static_cast<float>(a.K);
+    const float ms = acc / static_cast<float>(K);
     const float rms_inst = sqrtf(ms);
     float rms = rms_inst;
     if (a.rms_ema) {
@@ -402,21 +576,22 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       float* zrow = a.z_out + row * a.ldz;
       for (int64_t c = 0; c < nchunks; ++c) {
         const int64_t e0 = c * SPAN + lane0;
-        if (e0 >= a.K) break;
-        float v[V];
+        if (e0 >= K) break;
+        uint32_t w[4];
         if constexpr (NC > 0) {
 #pragma unroll
           for (int cc = 0; cc < NC; ++cc)
             if (cc == c) {
 #pragma unroll
-              for (int i = 0; i < V; ++i) v[i] = xr[cc][i];
+              for (int j = 0; j < 4; ++j) w[j] = xg[cc][j];
             }
         } else {
-          load_g(e0, v);
+          load_words(e0, w);
         }
+        const int64_t rem = K - e0;
 #pragma unroll
         for (int i = 0; i < V; ++i)
-          if (e0 + i < a.K) zrow[e0 + i] = v[i] / dz;
+          if (i < rem) zrow[e0 + i] = vec_elem<DT>(w, i) / dz;
       }
       continue;
     }
@@ -438,57 +613,68 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       tl = bucket_threshold(a.low, d, fast);
       th = bucket_threshold(a.high, d, fast);
     }
+    const uint32_t kl = (0x8000u - bf16_ceil_bits(tl)) * 0x00010001u;
+    const uint32_t kh = (0x8000u - bf16_ceil_bits(th)) * 0x00010001u;
     const SwarConsts kc = swar_consts(a.T, a.mc);
     float gs = 0.0f;
-    auto do_chunk = [&](int64_t e0, const float* v) {
-      uint32_t w[NW], out[NW];
-      load_bytes<V, 0x70u>(prow, e0, a.K, a.vec_p, w);
+    auto scale_terms = [&](const uint32_t* g, const uint32_t* w) {
       if (a.grad_scale) {
 #pragma unroll
         for (int i = 0; i < V; ++i) {
           const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
-          gs = gs + v[i] * static_cast<float>(static_cast<int>(byte & 15u) - a.mc);
+          gs = gs + vec_elem<DT>(g, i) * static_cast<float>(static_cast<int>(byte & 15u) - a.mc);
         }
       }
-      if (fast) {
-#pragma unroll
-        for (int j = 0; j < NW; ++j) {
-          uint32_t e = 0;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float g = v[4 * j + q];
-            const uint32_t m = (fabsf(g) >= tl ? 1u : 0u) + (fabsf(g) >= th ? 1u : 0u);
-            e |= (__float_as_uint(g) >> 31 ? 2u + m : 2u - m) << (8 * q);
-          }
-          out[j] = ratchet_word(w[j], e, kc, cnt);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < NW; ++j) out[j] = 0;
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          if (e0 + i < a.K) {
-            const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
-            out[i >> 2] |=
-                ratchet_byte(byte, v[i] / d, a.mc, a.T, a.low, a.high, cnt) << (8 * (i & 3));
-          }
-        }
-      }
-      store_bytes<V>(prow, e0, a.K, a.vec_p, out);
     };
-    if constexpr (NC > 0) {
+    auto fast_chunk = [&](int64_t e0, const uint32_t* g, const uint32_t* wp) {
+      uint32_t w[NW];
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int j = 0; j < NW; ++j) w[j] = wp[j];
+      if (NC > 0 && !a.vec_p) load_bytes<V, 0x70u>(prow, e0, K, false, w);
+      scale_terms(g, w);
+      uint32_t out[NW];
+#pragma unroll
+      for (int j = 0; j < NW; ++j) {
+        uint32_t e;
+        if constexpr (BF16W) e = bucket_bytes_bf16(g[2 * j], g[2 * j + 1], kl, kh);
+        else e = bucket_bytes_f32(g, tl, th);
+        out[j] = ratchet_word(w[j], e, kc, cnt);
+      }
+      store_bytes<V>(prow, e0, K, a.vec_p, out);
+    };
+    if (fast && NC > 0) {
+#pragma unroll
+      for (int c = 0; c < (NC > 0 ? NC : 1); ++c) {
         const int64_t e0 = c * SPAN + lane0;
-        if (c < nchunks && e0 < a.K) do_chunk(e0, xr[c]);
+        if (c < nchunks && e0 < K) fast_chunk(e0, xg[c], xp[c]);
       }
     } else {
+      // streaming rows, and the division path (re-read from memory: nothing has been
+      // written yet), one chunk at a time
       for (int64_t c = 0; c < nchunks; ++c) {
         const int64_t e0 = c * SPAN + lane0;
-        if (e0 >= a.K) break;
-        float v[V];
-        load_g(e0, v);
-        do_chunk(e0, v);
+        if (e0 >= K) break;
+        uint32_t g[4], w[NW];
+        load_words(e0, g);
+        load_bytes<V, 0x70u>(prow, e0, K, a.vec_p, w);
+        if (fast) {
+          fast_chunk(e0, g, w);
+        } else {
+          scale_terms(g, w);
+          uint32_t out[NW];
+#pragma unroll
+          for (int j = 0; j < NW; ++j) out[j] = 0;
+          const int64_t rem = K - e0;
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            if (i < rem) {
+              const uint32_t byte = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+              out[i >> 2] |= ratchet_byte(byte, vec_elem<DT>(g, i) / d, a.mc, a.T, a.low,
+                                          a.high, cnt) << (8 * (i & 3));
+            }
+          }
+          store_bytes<V>(prow, e0, K, a.vec_p, out);
+        }
       }
     }
     if (a.grad_scale) {
