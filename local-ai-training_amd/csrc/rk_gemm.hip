@@ -10,7 +10,7 @@
 //
 // Two kernels:
 //  * int8_gemm_m32_kernel, for aligned shapes (K % 64 == 0, 16-byte aligned rows and
-//    scales, N % 8 == 0): v_mfma_i32_32x32x32_i8, 128 x 128 block tiles, buffer
+//    scales, N % 8 == 0): v_mfma_i32_32x32x32_i8, 128 x 128 or 256 x 256 block tiles, buffer
 //    addressing, register ring + LDS ping-pong, LDS-staged coalesced epilogue;
 //  * int8_gemm_nt_kernel, any shape and stride (ragged K, unaligned rows):
 //    v_mfma_i32_16x16x64_i8 with bounds-checked staging.
@@ -250,50 +250,71 @@ struct RingSlot {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int swz32(int row) { return (row >> 2) & 3; }
 
-// B_PACKED_T tiles are staged as they lie in memory, [64 k rows][128 n bytes] at a
-// 160-byte pitch (eight consecutive rows then cover all 64 banks), and the fragments
+// B_PACKED_T tiles are staged as they lie in memory, [64 k rows][BN n bytes] at a
+// BN + 32 byte pitch (eight consecutive rows then cover all 64 banks), and the fragments
 // (16 consecutive k of one column n per lane) come from gfx950's transposing LDS read
 // ds_read_b64_tr_b8: within each 16-lane group, source lane s points at row s >> 1,
 // bytes 8 (s & 1) .. +7, and lane l receives byte column l of the eight rows, in row
 // order (checked on the device).
-constexpr int kBtPitch = 160;
 typedef int v2i_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i_t* lds_v2i_ptr;
 
-template <bool BT>
-__device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at,
+template <bool BT, int MI, int NJ, int BTP>
+__device__ __forceinline__ void mfma32_step(v16i (&acc)[MI][NJ], const uint8_t* at,
                                             const uint8_t* bt, int arow0, int brow0, int lane) {
   const int r32 = lane & 31, h = lane >> 5;
-  v4i fa[2][2], fb[2][2];
+  // one 32-byte k half at a time: MI + NJ fragments live, MI * NJ MFMAs each
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int ra = arow0 + i * 32 + r32;
-    const int rb = brow0 + i * 32 + r32;
+  for (int kh = 0; kh < 2; ++kh) {
+    v4i fa[MI], fb[NJ];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      fa[i][kh] = *reinterpret_cast<const v4i*>(at + ra * 64 + 16 * ((h + 2 * kh) ^ swz32(ra)));
+    for (int i = 0; i < MI; ++i) {
+      const int ra = arow0 + i * 32 + r32;
+      fa[i] = *reinterpret_cast<const v4i*>(at + ra * 64 + 16 * ((h + 2 * kh) ^ swz32(ra)));
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
       if constexpr (BT) {
         const int sl = lane & 15;
-        const int col = brow0 + i * 32 + 16 * ((lane >> 4) & 1) + 8 * (sl & 1);
+        const int col = brow0 + j * 32 + 16 * ((lane >> 4) & 1) + 8 * (sl & 1);
         const int r0 = 16 * (h + 2 * kh) + (sl >> 1);
         const v2i_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (lds_v2i_ptr)(bt + r0 * kBtPitch + col));
+            (lds_v2i_ptr)(bt + r0 * BTP + col));
         const v2i_t hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            (lds_v2i_ptr)(bt + (r0 + 8) * kBtPitch + col));
-        fb[i][kh] = v4i{lo.x, lo.y, hi.x, hi.y};
+            (lds_v2i_ptr)(bt + (r0 + 8) * BTP + col));
+        fb[j] = v4i{lo.x, lo.y, hi.x, hi.y};
       } else {
-        fb[i][kh] = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
+        const int rb = brow0 + j * 32 + r32;
+        fb[j] = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
       }
     }
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
   }
-#pragma unroll
-  for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j][kh], fa[i][kh], acc[i][j], 0, 0, 0);
 }
+
+// Block configurations of the 32x32x32 kernel: BM x BN tile, WM x WN wavefronts, each a
+// (BM / WM) x (BN / WN) wave tile of 32 x 32 MFMA blocks, MINW waves per SIMD.
+//  * 128 x 128, 2 x 2 waves (64 x 64 wave tiles, 64 accumulator registers), two or more
+//    blocks per CU: small grids;
+//  * 256 x 256, 2 x 4 waves (128 x 64 wave tiles, 128 accumulator registers, one block
+//    per CU): twice the MACs per byte fetched from L2 (a 128 x 128 tile needs 1 byte of
+//    A or B per 128 int8 ops, which at MFMA peak is about the whole L2 bandwidth); used
+//    for K >= 1024 when the grid still covers the chip (at K = 512 the single block per CU
+//    leaves the prologue and epilogue exposed and the small tiles are faster).
+template <int BM_, int BN_, int WM_, int WN_, int MINW_, int EROUNDS_>
+struct M32Cfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, MINW = MINW_;
+  static constexpr int EROUNDS = EROUNDS_;  // epilogue staging rounds (LDS holds BM / EROUNDS rows)
+  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int MI = BM / WM / 32, NJ = BN / WN / 32;
+  static constexpr int BTP = BN + 32;  // B_PACKED_T staging pitch: 8 rows cover 64 banks
+};
+using CfgSmall = M32Cfg<128, 128, 2, 2, 2, 1>;
+using CfgBig = M32Cfg<256, 256, 2, 4, 2, 2>;
 
 //
 // The instructions outside the MFMAs bound this kernel at K = 512 (8 k-steps per tile),
@@ -307,16 +328,20 @@ __device__ __forceinline__ void mfma32_step(v16i (&acc)[2][2], const uint8_t* at
 //    copy-out covers 64 banks, so neither side needs a swizzle or a lane swap;
 //  * each thread copies out a fixed 8-column chunk, so the column bound is one compare.
 // ---------------------------------------------------------------------------
-template <int KIND, int CDT, bool HAS_RS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+template <int KIND, int CDT, bool HAS_RS, class CFG>
+__global__ __launch_bounds__(CFG::THREADS) __attribute__((amdgpu_waves_per_eu(CFG::MINW, 8)))
 void int8_gemm_m32_kernel(GemmArgs g) {
-  constexpr int BM = 128, BN = 128, BK = 64, S = 2;
+  constexpr int BM = CFG::BM, BN = CFG::BN, BK = 64, S = 2;
+  constexpr int THREADS = CFG::THREADS, MI = CFG::MI, NJ = CFG::NJ, BTP = CFG::BTP;
   constexpr bool BT = KIND == B_PACKED_T;
-  constexpr int SEGS = BM * BK / 16 / 256;  // 16-byte pieces per thread per operand (2)
-  constexpr int EPITCH = BN * 2 + 8;        // epilogue staging row, bytes
-  constexpr int BSTAGE = BT ? BK * kBtPitch : BN * BK;  // bytes of one B stage
+  constexpr int SEGS = BM * BK / 16 / THREADS;  // 16-byte pieces per thread per operand (2)
+  static_assert(SEGS * 16 * THREADS == BM * BK && BN == BM, "square tiles");
+  constexpr int EPITCH = BN * 2 + 8;  // epilogue staging row, bytes
+  constexpr int EROWS = BM / CFG::EROUNDS;  // rows staged per epilogue round
+  static_assert(CFG::WM % CFG::EROUNDS == 0, "whole wave rows per epilogue round");
+  constexpr int BSTAGE = BT ? BK * BTP : BN * BK;  // bytes of one B stage
   constexpr int TILES = 2 * BM * BK + 2 * BSTAGE;
-  constexpr int SMEM = BM * EPITCH > TILES ? BM * EPITCH : TILES;
+  constexpr int SMEM = EROWS * EPITCH > TILES ? EROWS * EPITCH : TILES;
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   uint8_t* As = smem;
   uint8_t* Bs = smem + 2 * BM * BK;
@@ -332,9 +357,9 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int arow0 = wm * 64, brow0 = wn * 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % CFG::WM, wn = wave / CFG::WM;
+  const int arow0 = wm * (BM / CFG::WM), brow0 = wn * (BN / CFG::WN);
 
   const __amdgpu_buffer_rsrc_t a_rsrc =
       make_buffer(g.A + m0 * g.lda, (rows_a - 1) * g.lda + g.K);
@@ -348,13 +373,13 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   int a_voff[SEGS], b_voff[SEGS], st_off[SEGS], bst_off[SEGS];
 #pragma unroll
   for (int j = 0; j < SEGS; ++j) {
-    const int c = tid + 256 * j, row = c >> 2, seg = c & 3;
+    const int c = tid + THREADS * j, row = c >> 2, seg = c & 3;
     a_voff[j] = row * static_cast<int>(g.lda) + 16 * seg;
     st_off[j] = row * BK + 16 * (seg ^ swz32(row));
     if constexpr (BT) {
-      const int krow = c >> 3, nseg = c & 7;  // 64 rows of 128 bytes
+      const int krow = c / (BN / 16), nseg = c % (BN / 16);  // 64 rows of BN bytes
       b_voff[j] = krow * static_cast<int>(g.ldb) + 16 * nseg;
-      bst_off[j] = krow * kBtPitch + 16 * nseg;
+      bst_off[j] = krow * BTP + 16 * nseg;
     } else {
       b_voff[j] = row * static_cast<int>(g.ldb) + 16 * seg;
       bst_off[j] = st_off[j];
@@ -394,11 +419,11 @@ void int8_gemm_m32_kernel(GemmArgs g) {
     }
   };
 
-  v16i acc[2][2];
+  v16i acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = v16i{};
 
   // Ring of S = 2 k-steps (registers) over an LDS ping-pong: the loads of step kt + 2 are
   // issued right after step kt is written to LDS. Pairs of k-steps run without a branch;
@@ -416,85 +441,92 @@ void int8_gemm_m32_kernel(GemmArgs g) {
       store(ring[slot], slot);
       load(ring[slot], kb + slot + S);
       __syncthreads();
-      mfma32_step<BT>(acc, As + slot * BM * BK, Bs + slot * BSTAGE, arow0, brow0, lane);
+      mfma32_step<BT, MI, NJ, BTP>(acc, As + slot * BM * BK, Bs + slot * BSTAGE, arow0, brow0,
+                                   lane);
     }
   }
   if (nk & 1) {
     store(ring[0], 0);
     __syncthreads();
-    mfma32_step<BT>(acc, As, Bs, arow0, brow0, lane);
+    mfma32_step<BT, MI, NJ, BTP>(acc, As, Bs, arow0, brow0, lane);
   }
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer
 
   // Epilogue. acc[i][j][e]: row m = arow0 + 32 i + (lane & 31), columns
-  // n = brow0 + 32 j + 8 q + 4 (lane >> 5) + (e % 4), q = e / 4.
+  // n = brow0 + 32 j + 8 q + 4 (lane >> 5) + (e % 4), q = e / 4. In round r the waves
+  // whose rows lie in [r EROWS, (r + 1) EROWS) stage them as bf16, then the whole block
+  // copies them out.
   const int r32 = lane & 31, hh = lane >> 5;
   const __amdgpu_buffer_rsrc_t ls_rsrc = make_buffer(g.ls + m0, rows_a * 4);
-  float lsv[2];
+  float lsv[MI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
     lsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                            ls_rsrc, (arow0 + 32 * i + r32) * 4, 0, 0));
-  float4 rs4[2][4];
-  if constexpr (HAS_RS) {
-    const __amdgpu_buffer_rsrc_t rs_rsrc = make_buffer(g.rs + n0, rows_b * 4);
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        rs4[j][q] = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        rs_rsrc, (brow0 + 32 * j + 8 * q + 4 * hh) * 4, 0, 0));
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    uint8_t* srow = smem + (arow0 + 32 * i + r32) * EPITCH;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
-        float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
-        float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
-        float v3 = static_cast<float>(acc[i][j][4 * q + 3]) * lsv[i];
-        if constexpr (HAS_RS) {
-          v0 = v0 * rs4[j][q].x;
-          v1 = v1 * rs4[j][q].y;
-          v2 = v2 * rs4[j][q].z;
-          v3 = v3 * rs4[j][q].w;
-        }
-        *reinterpret_cast<uint2*>(srow + (brow0 + 32 * j + 8 * q + 4 * hh) * 2) =
-            make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
-      }
-  }
-  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rs_rsrc = make_buffer(HAS_RS ? g.rs + n0 : g.ls, HAS_RS ? rows_b * 4 : 0);
   constexpr int ES = CDT == RK_BF16 ? 2 : 4;
-  const int ch = tid & 15;  // 8-column chunk of this thread
-  if (n0 + 8 * ch < g.N) {
-    const __amdgpu_buffer_rsrc_t c_rsrc =
-        make_buffer(static_cast<char*>(g.C) + (m0 * g.ldc + n0) * ES,
-                    ((rows_a - 1) * g.ldc + (g.N - n0)) * ES);
+  constexpr int CHUNKS = BN / 8;             // 8-column chunks per row
+  constexpr int RSTEP = THREADS / CHUNKS;    // rows copied per pass
+  const int ch = tid % CHUNKS;               // 8-column chunk of this thread
+  const __amdgpu_buffer_rsrc_t c_rsrc =
+      make_buffer(static_cast<char*>(g.C) + (m0 * g.ldc + n0) * ES,
+                  ((rows_a - 1) * g.ldc + (g.N - n0)) * ES);
 #pragma unroll
-    for (int it = 0; it < BM / 16; ++it) {
-      const int row = (tid >> 4) + 16 * it;
-      const uint8_t* src = smem + row * EPITCH + 16 * ch;
-      const uint2 lo = *reinterpret_cast<const uint2*>(src);
-      const uint2 hi = *reinterpret_cast<const uint2*>(src + 8);
-      const int voff = (row * static_cast<int>(g.ldc) + 8 * ch) * ES;
-      if constexpr (CDT == RK_BF16) {
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_rsrc, voff, 0, 0);
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(v4i, make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16,
-                                               lo.y & 0xffff0000u)),
-            c_rsrc, voff, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(v4i, make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16,
-                                               hi.y & 0xffff0000u)),
-            c_rsrc, voff + 16, 0, 0);
+  for (int round = 0; round < CFG::EROUNDS; ++round) {
+    if (arow0 / EROWS == round) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        uint8_t* srow = smem + (arow0 - round * EROWS + 32 * i + r32) * EPITCH;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float4 rs4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            if constexpr (HAS_RS)
+              rs4 = __builtin_bit_cast(
+                  float4, __builtin_amdgcn_raw_buffer_load_b128(
+                              rs_rsrc, (brow0 + 32 * j + 8 * q + 4 * hh) * 4, 0, 0));
+            float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
+            float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
+            float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
+            float v3 = static_cast<float>(acc[i][j][4 * q + 3]) * lsv[i];
+            if constexpr (HAS_RS) {
+              v0 = v0 * rs4.x;
+              v1 = v1 * rs4.y;
+              v2 = v2 * rs4.z;
+              v3 = v3 * rs4.w;
+            }
+            *reinterpret_cast<uint2*>(srow + (brow0 + 32 * j + 8 * q + 4 * hh) * 2) =
+                make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+          }
       }
     }
+    __syncthreads();
+    if (n0 + 8 * ch < g.N) {
+#pragma unroll
+      for (int it = 0; it < EROWS / RSTEP; ++it) {
+        const int srow = tid / CHUNKS + RSTEP * it;
+        const int row = round * EROWS + srow;
+        const uint8_t* src = smem + srow * EPITCH + 16 * ch;
+        const uint2 lo = *reinterpret_cast<const uint2*>(src);
+        const uint2 hi = *reinterpret_cast<const uint2*>(src + 8);
+        const int voff = (row * static_cast<int>(g.ldc) + 8 * ch) * ES;
+        if constexpr (CDT == RK_BF16) {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_rsrc, voff, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(v4i, make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16,
+                                                 lo.y & 0xffff0000u)),
+              c_rsrc, voff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(v4i, make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16,
+                                                 hi.y & 0xffff0000u)),
+              c_rsrc, voff + 16, 0, 0);
+        }
+      }
+    }
+    if (round + 1 < CFG::EROUNDS) __syncthreads();
   }
 }
 
@@ -591,10 +623,24 @@ static void launch_gemv(const GemmArgs& g, hipStream_t stream) {
   int8_gemv_kernel<KIND, CDT, HAS_RS><<<dim3(static_cast<unsigned>(blocks)), 256, 0, stream>>>(g);
 }
 
+// 256 x 256 tiles for K >= 1024 when they still give every CU a tile, 128 x 128
+// otherwise.
+static bool use_big_tiles(const GemmArgs& g) {
+  const int64_t big = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+  return g.K >= 1024 && big >= 256;
+}
+
 template <int KIND, int CDT, bool HAS_RS>
 static void launch_m32(const GemmArgs& g, hipStream_t stream) {
-  const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
-  int8_gemm_m32_kernel<KIND, CDT, HAS_RS><<<dim3(static_cast<unsigned>(tiles)), 256, 0, stream>>>(g);
+  if (use_big_tiles(g)) {
+    const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+    int8_gemm_m32_kernel<KIND, CDT, HAS_RS, CfgBig>
+        <<<dim3(static_cast<unsigned>(tiles)), CfgBig::THREADS, 0, stream>>>(g);
+  } else {
+    const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+    int8_gemm_m32_kernel<KIND, CDT, HAS_RS, CfgSmall>
+        <<<dim3(static_cast<unsigned>(tiles)), CfgSmall::THREADS, 0, stream>>>(g);
+  }
 }
 
 template <int KIND, int CDT>
@@ -604,11 +650,11 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const int es = CDT == RK_BF16 ? 2 : 4;
   const bool aligned_out = fast && (g.N % 8) == 0 && ((g.ldc * es) % 16) == 0 &&
                            aligned16(g.C) && (g.rs == nullptr || aligned16(g.rs));
-  // Buffer offsets are 32-bit: a block's furthest A/B load (128 rows, prefetch two
-  // k-steps past K) and C store (128 rows) must stay below 2^31 bytes.
-  const bool fits32 = 128 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
-                      128 * g.ldb + g.K + 256 < (int64_t{1} << 31) &&
-                      128 * g.ldc * es < (int64_t{1} << 31);
+  // Buffer offsets are 32-bit: a block's furthest A/B load (256 rows, prefetch two
+  // k-steps past K) and C store (256 rows) must stay below 2^31 bytes.
+  const bool fits32 = 256 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
+                      256 * g.ldb + g.K + 256 < (int64_t{1} << 31) &&
+                      256 * g.ldc * es < (int64_t{1} << 31);
   if (aligned_out && fits32 && g.M <= 16) {
     // decode-sized M: one pass over B spread over the whole chip
     if ((g.N + 15) / 16 > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
@@ -648,9 +694,9 @@ static int launch_gemm_packed_t(const GemmArgs& g, hipStream_t stream) {
                 "packed [K, N] GEMM needs K %% 64 == 0, N %% 8 == 0 and 16-byte aligned rows");
   // 32-bit buffer offsets: A as in the NT form; B's furthest scalar + vector offset is
   // (K + 2 k-steps) rows of ldb bytes
-  const bool fits32 = 128 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
-                      (g.K + 128) * g.ldb + 128 < (int64_t{1} << 31) &&
-                      128 * g.ldc * es < (int64_t{1} << 31);
+  const bool fits32 = 256 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
+                      (g.K + 128) * g.ldb + 256 < (int64_t{1} << 31) &&
+                      256 * g.ldc * es < (int64_t{1} << 31);
   if (!fits32) return fail(RK_ERR_UNSUPPORTED, "packed [K, N] GEMM operands too large");
   const int64_t tiles = ((g.M + 127) / 128) * ((g.N + 127) / 128);
   if (tiles > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");

@@ -217,12 +217,13 @@ def test_quantize_columns_matches_transposed_rows(cuda):
 # ---------------------------------------------------------------------------
 # int8 GEMM
 # ---------------------------------------------------------------------------
-# Covers the generic kernel (ragged K or N), the ping-pong kernel (K = 64) and the
-# persistent cross-tile kernel (K % 128 == 0, N % 8 == 0): ragged last row/column tiles,
-# several tiles per block, and the fewest k-steps it accepts (K = 128).
+# Covers the generic kernel (ragged K or N) and the 32x32x32 kernel in both block
+# configurations: 128 x 128 tiles (small grids, K < 1024) and 256 x 256 tiles (K >= 1024
+# with at least 256 of them: 4100 x 4136 has ragged last row and column tiles and an odd
+# number of k-steps).
 GEMM_SHAPES = [(67, 35, 53), (48, 40, 53), (1, 64, 1), (128, 128, 64), (130, 200, 129),
                (256, 384, 512), (1000, 1536, 512), (300, 200, 256), (129, 8, 128),
-               (2500, 1032, 1024), (1, 16, 128)]
+               (2500, 1032, 1024), (1, 16, 128), (4100, 4136, 1216)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
@@ -241,7 +242,8 @@ def test_int8_gemm_nt_bit_exact(cuda, m, n, k):
 
 
 @pytest.mark.parametrize("max_code", [1, 2, 3, 7])
-@pytest.mark.parametrize("m,n,k", [(67, 53, 35), (512, 1536, 512), (257, 130, 192)])
+@pytest.mark.parametrize("m,n,k", [(67, 53, 35), (512, 1536, 512), (257, 130, 192),
+                                   (4100, 4104, 1088)])
 def test_packed_gemm_bit_exact(cuda, m, n, k, max_code):
     packed, scale = synthetic_state(n, k, max_code, seed=m + n + k)
     code, _ = oupd.unpack(packed, max_code)
@@ -331,7 +333,7 @@ def test_grad_input_gemm_full_op_shape_bit_exact(cuda):
 # staged as they lie, transposed by ds_read_b64_tr_b8. Shapes: the op shape, partial 128-wide
 # column tiles, small and ragged M, K of one k-step, every max_code.
 PACKED_T_SHAPES = [(16384, 2048, 512), (300, 1024, 144), (1, 64, 16), (129, 192, 1040),
-                   (77, 128, 2064)]
+                   (77, 128, 2064), (4100, 1216, 4112)]
 
 
 @pytest.mark.parametrize("m,k,n", PACKED_T_SHAPES)
