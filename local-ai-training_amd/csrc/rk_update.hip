@@ -335,36 +335,86 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
   constexpr int V = DT == RK_F32 ? 4 : 8;
   constexpr int SPAN = 64 * V;
   constexpr int NW = V / 4;
+  constexpr int NCR = NC > 0 ? NC : 1;
   constexpr bool BF16W = DT != RK_F32;  // words hold bf16 pairs
+  constexpr int ES = DT == RK_F32 ? 4 : 2;
   const int lane = threadIdx.x & 63;
   const int64_t lane0 = static_cast<int64_t>(lane) * V;
   MoveCounts cnt;
 
-  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
-       row += static_cast<int64_t>(gridDim.x) * 4) {
-    // K opaque per row: the compiler would otherwise hoist every chunk's per-element tail
-    // tests out of the row loop and hold them in registers for the whole kernel
-    int64_t K = a.K;
-    asm volatile("" : "+s"(K));
+  // Registers of one row between its loads and its arithmetic.
+  struct Stage {
+    upd_f32x4 lo[NCR], hi[NCR];  // SRC_SPLITS: split 0
+    uint32_t xg[NCR][4];          // other sources: the gradient words
+    uint32_t xp[NCR][NW];         // packed bytes
+  };
+
+  auto add4 = [](float4& x, const float4& y) {
+    x.x = x.x + y.x;
+    x.y = x.y + y.y;
+    x.z = x.z + y.z;
+    x.w = x.w + y.w;
+  };
+
+  // Issues every unconditional load of row `row` into `st`.
+  auto issue = [&](int64_t row, int64_t K, Stage& st) {
+    if constexpr (NC > 0) {
+      const int64_t r = row;
+      if constexpr (DT == SRC_SPLITS) {
+        const __amdgpu_buffer_rsrc_t rs = make_buffer(a.part + r * K, K * 4);
+        const uint32_t voff = static_cast<uint32_t>(lane0) * 4u;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          st.lo[c] = __builtin_bit_cast(
+              upd_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, c * SPAN * 4, 0));
+          st.hi[c] = __builtin_bit_cast(
+              upd_f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, c * SPAN * 4 + 16, 0));
+        }
+      } else {
+        // a vector wholly past K, or every vector when the gradient is not vector-aligned,
+        // reads as zero (the unaligned case is re-read element by element in `body`)
+        const char* grow = static_cast<const char*>(a.g) + r * a.ldg * ES;
+        const __amdgpu_buffer_rsrc_t rg =
+            make_buffer(grow, a.vec_g ? static_cast<int>(K) * ES : 0);
+        const uint32_t voff = static_cast<uint32_t>(lane0) * ES;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const u32x4_t t = __builtin_bit_cast(
+              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, voff, c * SPAN * ES, 0));
+          st.xg[c][0] = t.x;
+          st.xg[c][1] = t.y;
+          st.xg[c][2] = t.z;
+          st.xg[c][3] = t.w;
+        }
+      }
+      if constexpr (!ZONLY) {
+        // K % V == 0 whenever vec_p, so a vector is wholly inside or past the row; without
+        // vec_p every load reads zero and `body` reads the bytes one by one
+        const __amdgpu_buffer_rsrc_t rp =
+            make_buffer(a.packed + r * a.ldp, a.vec_p ? static_cast<int>(K) : 0);
+        const uint32_t voff = static_cast<uint32_t>(lane0);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if constexpr (V == 8) {
+            const u32x2_t t = __builtin_bit_cast(
+                u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rp, voff, c * SPAN, 0));
+            st.xp[c][0] = t.x;
+            st.xp[c][NW - 1] = t.y;
+          } else {
+            st.xp[c][0] = __builtin_amdgcn_raw_buffer_load_b32(rp, voff, c * SPAN, 0);
+          }
+        }
+      }
+    }
+  };
+
+  // Everything after the loads for one row.
+  auto body = [&](int64_t row, int64_t K, Stage& st) {
     const int64_t nchunks = (K + SPAN - 1) / SPAN;
-    const char* grow =
-        static_cast<const char*>(a.g) + row * a.ldg * (DT == RK_F32 ? 4 : 2);
+    const char* grow = static_cast<const char*>(a.g) + row * a.ldg * ES;
     uint8_t* prow = a.packed + row * a.ldp;
     const float* prt = a.part + row * K;
 
-    // fp32 split sums rounded to bf16, two per word (the grad_weight reduction's rounding)
-    auto pack_sums = [](const float4& lo, const float4& hi, uint32_t* w) {
-      w[0] = upd_pack_bf16x2(lo.x, lo.y);
-      w[1] = upd_pack_bf16x2(lo.z, lo.w);
-      w[2] = upd_pack_bf16x2(hi.x, hi.y);
-      w[3] = upd_pack_bf16x2(hi.z, hi.w);
-    };
-    auto add4 = [](float4& x, const float4& y) {
-      x.x = x.x + y.x;
-      x.y = x.y + y.y;
-      x.z = x.z + y.z;
-      x.w = x.w + y.w;
-    };
     // One vector of the gradient as words (zeros past K).
     auto load_words = [&](int64_t e0, uint32_t* w) {
       if constexpr (DT == SRC_SPLITS) {
@@ -377,13 +427,16 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
             add4(lo, *reinterpret_cast<const float4*>(prt + s * a.part_stride + e0));
             add4(hi, *reinterpret_cast<const float4*>(prt + s * a.part_stride + e0 + 4));
           }
-          pack_sums(lo, hi, w);
+          w[0] = upd_pack_bf16x2(lo.x, lo.y);
+          w[1] = upd_pack_bf16x2(lo.z, lo.w);
+          w[2] = upd_pack_bf16x2(hi.x, hi.y);
+          w[3] = upd_pack_bf16x2(hi.z, hi.w);
         } else {
 #pragma unroll
           for (int j = 0; j < 4; ++j) w[j] = 0;
         }
       } else if (a.vec_g && e0 + V <= K) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(grow + e0 * (DT == RK_F32 ? 4 : 2));
+        const uint4 raw = *reinterpret_cast<const uint4*>(grow + e0 * ES);
         w[0] = raw.x;
         w[1] = raw.y;
         w[2] = raw.z;
@@ -418,55 +471,21 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       return acc;
     };
 
-    // The packed bytes of every register chunk, fetched with the gradient: unconditional
-    // buffer loads (K % V == 0 whenever vec_p, so a vector is wholly inside or past the
-    // row; without vec_p every load reads zero and pass 2 reads the bytes one by one).
-    uint32_t xg[NC > 0 ? NC : 1][4];
-    uint32_t xp[NC > 0 ? NC : 1][NW];
-    auto prefetch_packed = [&]() {
-      if constexpr (!ZONLY && NC > 0) {
-        const __amdgpu_buffer_rsrc_t r = make_buffer(prow, a.vec_p ? static_cast<int>(K) : 0);
-        const uint32_t voff = static_cast<uint32_t>(lane0);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          if constexpr (V == 8) {
-            const u32x2_t t = __builtin_bit_cast(
-                u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, voff, c * SPAN, 0));
-            xp[c][0] = t.x;
-            xp[c][NW - 1] = t.y;
-          } else {
-            xp[c][0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, c * SPAN, 0);
-          }
-        }
-      }
-    };
-
-    // Pass 1: loads, then the sum of squares in fixed order. A non-finite gradient element
-    // makes the sum non-finite, so only a row whose sum is not finite (overflow of finite
-    // values included) is searched element by element.
+    // Pass 1: the remaining loads, then the sum of squares in fixed order. A non-finite
+    // gradient element makes the sum non-finite, so only a row whose sum is not finite
+    // (overflow of finite values included) is searched element by element.
+    uint32_t (&xg)[NCR][4] = st.xg;
     float acc = 0.0f;
     if constexpr (NC > 0) {
       if constexpr (DT == SRC_SPLITS) {
-        // Buffer loads, one descriptor per split of the row: past-K vectors read as zero
-        // (K % 8 == 0, so a vector is wholly inside or past the row). Split 0 of every
-        // chunk is in flight together, then GS splits of every chunk at a time (about 64
-        // registers), added in split order.
+        // later splits (buffer loads, one descriptor per split), GS splits of every chunk
+        // in flight at a time, added in split order
         constexpr int GS = NC >= 8 ? 1 : (NC >= 4 ? 2 : (NC >= 2 ? 4 : 8));
         const uint32_t voff = static_cast<uint32_t>(lane0) * 4u;
         auto ld = [&](__amdgpu_buffer_rsrc_t r, int c, int half) {
           return __builtin_bit_cast(
               upd_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, c * SPAN * 4 + 16 * half, 0));
         };
-        upd_f32x4 lo[NC], hi[NC];
-        {
-          const __amdgpu_buffer_rsrc_t r = make_buffer(prt, K * 4);
-#pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            lo[c] = ld(r, c, 0);
-            hi[c] = ld(r, c, 1);
-          }
-        }
-        prefetch_packed();
         for (int s = 1; s < a.nsplit; s += GS) {
           upd_f32x4 l[GS][NC], h[GS][NC];
 #pragma unroll
@@ -485,45 +504,27 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
             if (s + q < a.nsplit) {
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
-                lo[c] = lo[c] + l[q][c];
-                hi[c] = hi[c] + h[q][c];
+                st.lo[c] = st.lo[c] + l[q][c];
+                st.hi[c] = st.hi[c] + h[q][c];
               }
             }
           }
         }
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          xg[c][0] = upd_pack_bf16x2(lo[c].x, lo[c].y);
-          xg[c][1] = upd_pack_bf16x2(lo[c].z, lo[c].w);
-          xg[c][2] = upd_pack_bf16x2(hi[c].x, hi[c].y);
-          xg[c][3] = upd_pack_bf16x2(hi[c].z, hi[c].w);
+          xg[c][0] = upd_pack_bf16x2(st.lo[c].x, st.lo[c].y);
+          xg[c][1] = upd_pack_bf16x2(st.lo[c].z, st.lo[c].w);
+          xg[c][2] = upd_pack_bf16x2(st.hi[c].x, st.hi[c].y);
+          xg[c][3] = upd_pack_bf16x2(st.hi[c].z, st.hi[c].w);
         }
-      } else {
-        // unconditional buffer loads (a vector wholly past K, or every vector when the
-        // gradient is not vector-aligned, reads as zero), then the unaligned case element
-        // by element behind one uniform branch
-        constexpr int ES = DT == RK_F32 ? 4 : 2;
-        const __amdgpu_buffer_rsrc_t r = make_buffer(grow, a.vec_g ? static_cast<int>(K) * ES : 0);
-        const uint32_t voff = static_cast<uint32_t>(lane0) * ES;
+      } else if (!a.vec_g) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          const u32x4_t t = __builtin_bit_cast(
-              u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, c * SPAN * ES, 0));
-          xg[c][0] = t.x;
-          xg[c][1] = t.y;
-          xg[c][2] = t.z;
-          xg[c][3] = t.w;
-        }
-        prefetch_packed();
-        if (!a.vec_g) {
+          if (c < nchunks) {
+            load_words(c * SPAN + lane0, xg[c]);
+          } else {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            if (c < nchunks) {
-              load_words(c * SPAN + lane0, xg[c]);
-            } else {
-#pragma unroll
-              for (int j = 0; j < 4; ++j) xg[c][j] = 0;
-            }
+            for (int j = 0; j < 4; ++j) xg[c][j] = 0;
           }
         }
       }
@@ -593,11 +594,11 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
         for (int i = 0; i < V; ++i)
           if (i < rem) zrow[e0 + i] = vec_elem<DT>(w, i) / dz;
       }
-      continue;
+      return;
     }
     if (bad) {
       if (lane == 0 && a.nonfinite) a.nonfinite[0] = 1;
-      continue;
+      return;
     }
     const float d = rms + a.eps;
 
@@ -644,9 +645,9 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
     };
     if (fast && NC > 0) {
 #pragma unroll
-      for (int c = 0; c < (NC > 0 ? NC : 1); ++c) {
+      for (int c = 0; c < NCR; ++c) {
         const int64_t e0 = c * SPAN + lane0;
-        if (c < nchunks && e0 < K) fast_chunk(e0, xg[c], xp[c]);
+        if (c < nchunks && e0 < K) fast_chunk(e0, xg[c], st.xp[c]);
       }
     } else {
       // streaming rows, and the division path (re-read from memory: nothing has been
@@ -681,6 +682,21 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       gs = wave_sum_butterfly(gs);
       if (lane == 0) a.grad_scale[row] = gs;
     }
+  };
+
+  // K opaque per row: the compiler would otherwise hoist every chunk's per-element tail
+  // tests out of the row loop and hold them in registers for the whole kernel
+  auto opaque_k = [&]() {
+    int64_t K = a.K;
+    asm volatile("" : "+s"(K));
+    return K;
+  };
+  for (int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6); row < a.rows;
+       row += static_cast<int64_t>(gridDim.x) * 4) {
+    const int64_t K = opaque_k();
+    Stage st;
+    issue(row, K, st);
+    body(row, K, st);
   }
   flush_counts(cnt, a.counts);
 }
@@ -702,25 +718,29 @@ static int check_update_common(const uint8_t* packed, int64_t ldp, int64_t rows,
   return RK_OK;
 }
 
+template <int DT, int NC, bool ZONLY>
+static void launch_rows(const GradUpdateArgs& a, hipStream_t s) {
+  ratchet_update_grad_kernel<DT, NC, ZONLY><<<row_grid(a.rows), 256, 0, s>>>(a);
+}
+
 template <bool ZONLY>
 static int launch_grad_kernel(const GradUpdateArgs& a, int g_dtype, hipStream_t s) {
   const int V = g_dtype == RK_F32 ? 4 : 8;
   const int64_t nchunks = (a.K + 64 * V - 1) / (64 * V);
-  const dim3 grid(row_grid(a.rows)), block(256);
   if (g_dtype == RK_F32) {
-    if (nchunks <= 2) ratchet_update_grad_kernel<RK_F32, 2, ZONLY><<<grid, block, 0, s>>>(a);
-    else if (nchunks <= 8) ratchet_update_grad_kernel<RK_F32, 8, ZONLY><<<grid, block, 0, s>>>(a);
-    else ratchet_update_grad_kernel<RK_F32, 0, ZONLY><<<grid, block, 0, s>>>(a);
+    if (nchunks <= 2) launch_rows<RK_F32, 2, ZONLY>(a, s);
+    else if (nchunks <= 8) launch_rows<RK_F32, 8, ZONLY>(a, s);
+    else launch_rows<RK_F32, 0, ZONLY>(a, s);
   } else if (g_dtype == RK_BF16) {
-    if (nchunks <= 1) ratchet_update_grad_kernel<RK_BF16, 1, ZONLY><<<grid, block, 0, s>>>(a);
-    else if (nchunks <= 4) ratchet_update_grad_kernel<RK_BF16, 4, ZONLY><<<grid, block, 0, s>>>(a);
-    else if (nchunks <= 12) ratchet_update_grad_kernel<RK_BF16, 12, ZONLY><<<grid, block, 0, s>>>(a);
-    else ratchet_update_grad_kernel<RK_BF16, 0, ZONLY><<<grid, block, 0, s>>>(a);
+    if (nchunks <= 1) launch_rows<RK_BF16, 1, ZONLY>(a, s);
+    else if (nchunks <= 4) launch_rows<RK_BF16, 4, ZONLY>(a, s);
+    else if (nchunks <= 12) launch_rows<RK_BF16, 12, ZONLY>(a, s);
+    else launch_rows<RK_BF16, 0, ZONLY>(a, s);
   } else if constexpr (!ZONLY) {
-    if (nchunks <= 1) ratchet_update_grad_kernel<SRC_SPLITS, 1, false><<<grid, block, 0, s>>>(a);
-    else if (nchunks <= 4) ratchet_update_grad_kernel<SRC_SPLITS, 4, false><<<grid, block, 0, s>>>(a);
-    else if (nchunks <= 12) ratchet_update_grad_kernel<SRC_SPLITS, 12, false><<<grid, block, 0, s>>>(a);
-    else ratchet_update_grad_kernel<SRC_SPLITS, 0, false><<<grid, block, 0, s>>>(a);
+    if (nchunks <= 1) launch_rows<SRC_SPLITS, 1, false>(a, s);
+    else if (nchunks <= 4) launch_rows<SRC_SPLITS, 4, false>(a, s);
+    else if (nchunks <= 12) launch_rows<SRC_SPLITS, 12, false>(a, s);
+    else launch_rows<SRC_SPLITS, 0, false>(a, s);
   }
   return launch_status(ZONLY ? "normalize_rows" : "ratchet_update_grad");
 }

@@ -507,9 +507,12 @@ def test_update_writes_the_mean_row_rms(cuda, rows, k):
                  mean.data_ptr(), nat.stream_handle(cuda))
 
 
+# 4100 and 9000 rows take the pipelined row loop (several rows per wavefront, the next
+# row's loads in flight during the current row's arithmetic): 9000 leaves wavefronts with
+# two and with three rows, and every wavefront prefetches one row past the end.
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,k", [(6, 8), (37, 1001), (2048, 512), (512, 2048), (64, 5632),
-                                    (16, 12000)])
+                                    (16, 12000), (4100, 512), (9000, 256), (4099, 1000)])
 def test_fused_normalize_update_bit_exact(cuda, rows, k, dtype):
     mc, T = 2, 8
     packed, _ = synthetic_state(rows, k, mc, seed=rows + 3 * k)
@@ -537,7 +540,8 @@ def _reduce_partials(part):
 # output equal to reducing to bf16 first and updating after. Shapes: the op shape, one
 # chunk, several register chunks, streaming rows (K > 12 chunks), one split, many splits.
 @pytest.mark.parametrize("rows,k,nsplit", [(2048, 512, 8), (96, 1024, 3), (64, 6144, 2),
-                                           (33, 7168, 5), (8, 8, 1), (130, 2048, 17)])
+                                           (33, 7168, 5), (8, 8, 1), (130, 2048, 17),
+                                           (4100, 2048, 1), (9000, 512, 3)])
 def test_update_from_partials_equals_reduce_then_update(cuda, rows, k, nsplit):
     mc, beta = 3, 0.9
     packed, _ = synthetic_state(rows, k, mc, seed=rows + k)
