@@ -56,14 +56,20 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--model-steps", type=int, default=10)
-    ap.add_argument("--model-warmup", type=int, default=3)
+    # sustained training throughput: 8 warmup steps, then 30 timed steps with a sync only at
+    # both ends (the reference's scripts/int8_training_throughput.py:89-102 method)
+    ap.add_argument("--model-steps", type=int, default=30)
+    ap.add_argument("--model-warmup", type=int, default=8)
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-update-1b", action="store_true")
     ap.add_argument("--no-train-1b", action="store_true")
-    ap.add_argument("--train-1b-steps", type=int, default=3)
-    ap.add_argument("--train-1b-warmup", type=int, default=2)
+    ap.add_argument("--train-1b-steps", type=int, default=30)
+    ap.add_argument("--train-1b-warmup", type=int, default=8)
+    ap.add_argument("--update-1b-only", action="store_true",
+                    help="run only the 1B fused-update sweep (for profiling)")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="run only the forward GEMM on packed codes at large-K shapes")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the decode bench and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=64)
@@ -191,12 +197,13 @@ def op_stages(layer, x, g):
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
     row_rms = torch.empty(n, dtype=torch.float32, device=dev)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
-    rms_mean = torch.empty((), dtype=torch.float32, device=dev)
 
     def update():
+        # the update kernel alone (the step's separate one-block mean of row_rms is not part
+        # of this stage)
         nat.call("rk_ratchet_update_partials", packed.data_ptr(), k, gw_work.data_ptr(), splits,
                  n, k, MAX_CODE, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
-                 row_rms.data_ptr(), None, flag.data_ptr(), rms_mean.data_ptr(), None, k,
+                 row_rms.data_ptr(), None, flag.data_ptr(), None, None, k,
                  nat.stream_handle(dev))
 
     stages = [
@@ -215,24 +222,40 @@ def op_stages(layer, x, g):
 
 
 def kernel_breakdown(layer, x, g, iters: int):
-    """Average device time of each launch of one op step, HIP events on the launch stream."""
+    """Average device time of each launch of one op step: `iters` back-to-back launches of
+    the stage captured in a HIP graph and replayed between HIP events on the replay stream
+    (no host launch time inside the interval; consecutive graph kernels start back to
+    back, as the kernel trace shows)."""
     import torch
 
     stages, work = op_stages(layer, x, g)
-    for _, fn in stages:  # warm
-        fn()
+    dev = x.device
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _, fn in stages:  # warm, outside the capture
+            fn()
+    torch.cuda.current_stream(dev).wait_stream(side)
     torch.cuda.synchronize()
-    events = {name: [] for name, _ in stages}
-    for _ in range(iters):
-        for name, fn in stages:
+    avg_ms = {}
+    for name, fn in stages:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(iters):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(3):  # the fastest of three replays (graph launch hiccups excluded)
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-            fn()
+            graph.replay()
             e1.record()
-            events[name].append((e0, e1))
-    torch.cuda.synchronize()
-    avg_ms = {name: sum(a.elapsed_time(b) for a, b in ev) / len(ev) for name, ev in events.items()}
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / iters
+            best = ms if best is None else min(best, ms)
+        avg_ms[name] = best
 
     report = {}
     for name, ms in avg_ms.items():
@@ -275,7 +298,7 @@ STAGE_KERNELS = {
     "sr_quant_rows": ["quant_rows_kernel<1, 0, true"],
     "grad_input_gemm": ["int8_gemm_m32_kernel<2,"],
     "grad_weight_partials": ["grad_weight_partial_kernel"],
-    "ratchet_update_partials": ["ratchet_update_grad_kernel<2,", "row_rms_mean_kernel"],
+    "ratchet_update_partials": ["ratchet_update_grad_kernel<2,"],
 }
 PROBE_REPEATS = 5
 
@@ -696,6 +719,50 @@ def decode_bench(args, device) -> dict:
     return out
 
 
+GEMM_SWEEP_SHAPES = [(16384, 512, 2048), (16384, 2048, 2048), (16384, 512, 8192),
+                     (4096, 4096, 4096), (8192, 8192, 8192)]
+
+
+def gemm_sweep(device, iters: int) -> list:
+    """Forward GEMM on packed quinary codes (bf16 out, row and column scales) at the op
+    shape and at larger K, where the 256 x 256 block tiles take over (K >= 1024): device
+    time per launch from HIP events on the launch stream, TOPS and % of the int8 peak."""
+    import torch
+
+    from local_ai_training.int8_matmul import packed_int8_mm
+
+    out_rows = []
+    gen = torch.Generator().manual_seed(5)
+    for m, k, n in GEMM_SWEEP_SHAPES:
+        q = torch.randint(-127, 128, (m, k), generator=gen, dtype=torch.int8).to(device)
+        ls = (torch.rand(m, generator=gen) + 0.5).to(device)
+        code = torch.randint(-MAX_CODE, MAX_CODE + 1, (n, k), generator=gen)
+        packed = (((code + MAX_CODE) & 0x0F) | (7 << 4)).to(torch.uint8).to(device)
+        rs = (torch.rand(n, generator=gen) * 0.08 + 0.02).to(device)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+
+        def run():
+            packed_int8_mm(q, packed, MAX_CODE, ls, rs, out=out)
+
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / iters * 1e3
+        tops = 2.0 * m * n * k / us / 1e6
+        out_rows.append({"M": m, "K": k, "N": n, "avg_us": round(us, 2), "TOPS": round(tops, 1),
+                         "mfma_frac": round(tops * 1e12 / PEAK_INT8_OPS, 4),
+                         "tiles": "256x256" if k >= 1024 else "128x128"})
+        log(f"  gemm {m}x{k}x{n}: {us:.1f} us {tops:.0f} TOPS")
+    return out_rows
+
+
 def cpu_baseline(seconds: float) -> dict:
     import torch
 
@@ -748,6 +815,12 @@ def main() -> int:
         return 0
     if args.decode_only:
         print(json.dumps({"decode": decode_bench(args, device)}), flush=True)
+        return 0
+    if args.update_1b_only:
+        print(json.dumps({"update_1b": update_1b_bench(device, 5)}), flush=True)
+        return 0
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep(device, args.kernel_iters)}), flush=True)
         return 0
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
     step_s, eager_s, layer, x, g = op_bench(args, device)
