@@ -793,6 +793,26 @@ def cpu_baseline(seconds: float) -> dict:
                       f"{per_step * 1e3:.1f} ms/step"}
 
 
+def cpu_baseline_model() -> dict:
+    """The reference's CPU training path at its tiny CPU config (2 layers, d 128, 4 heads,
+    FFN 512, byte vocab 256, seq 64, batch 8, quinary codes; fp32 ratchet linears with the
+    update fused into backward, bf16 autocast, AdamW): 20 steps, tokens/s over steps 3-20,
+    on the host's cores."""
+    import torch
+
+    from oracle.cpu_reference import tiny_training_tokens_per_s
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    r = tiny_training_tokens_per_s()
+    return {"value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"tiny ratchet transformer (2L, d128, 4h, FFN 512, vocab 256, seq 64, "
+                      f"batch 8) fp32 eager + bf16 autocast training, {r['timed_steps']} of "
+                      f"{r['steps']} steps timed, {r['ms_per_step']:.1f} ms/step, loss "
+                      f"{r['first_loss']:.3f} -> {r['last_loss']:.3f}"}
+
+
 def main() -> int:
     args = parse_args()
     if args.traffic_summary:
@@ -881,6 +901,8 @@ def main() -> int:
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_seconds:.0f} s of fp32 eager CPU work")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline_model"] = cpu_baseline_model()
+        log(f"  {result['cpu_baseline_model']}")
     print(json.dumps(result), flush=True)
     return 0
 
