@@ -305,16 +305,17 @@ __device__ __forceinline__ void mfma32_step(v16i (&acc)[MI][NJ], const uint8_t* 
 //    A or B per 128 int8 ops, which at MFMA peak is about the whole L2 bandwidth); used
 //    for K >= 1024 when the grid still covers the chip (at K = 512 the single block per CU
 //    leaves the prologue and epilogue exposed and the small tiles are faster).
-template <int BM_, int BN_, int WM_, int WN_, int MINW_, int EROUNDS_>
+template <int BM_, int BN_, int WM_, int WN_, int MINW_, int EROUNDS_, int RING_>
 struct M32Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, MINW = MINW_;
+  static constexpr int RING = RING_;  // k-steps of global loads held in registers (1 or 2)
   static constexpr int EROUNDS = EROUNDS_;  // epilogue staging rounds (LDS holds BM / EROUNDS rows)
   static constexpr int THREADS = 64 * WM * WN;
   static constexpr int MI = BM / WM / 32, NJ = BN / WN / 32;
   static constexpr int BTP = BN + 32;  // B_PACKED_T staging pitch: 8 rows cover 64 banks
 };
-using CfgSmall = M32Cfg<128, 128, 2, 2, 2, 1>;
-using CfgBig = M32Cfg<256, 256, 2, 4, 2, 2>;
+using CfgSmall = M32Cfg<128, 128, 2, 2, 2, 1, 2>;
+using CfgBig = M32Cfg<256, 256, 2, 4, 2, 2, 1>;
 
 //
 // The instructions outside the MFMAs bound this kernel at K = 512 (8 k-steps per tile),
@@ -331,7 +332,7 @@ using CfgBig = M32Cfg<256, 256, 2, 4, 2, 2>;
 template <int KIND, int CDT, bool HAS_RS, class CFG>
 __global__ __launch_bounds__(CFG::THREADS) __attribute__((amdgpu_waves_per_eu(CFG::MINW, 8)))
 void int8_gemm_m32_kernel(GemmArgs g) {
-  constexpr int BM = CFG::BM, BN = CFG::BN, BK = 64, S = 2;
+  constexpr int BM = CFG::BM, BN = CFG::BN, BK = 64, S = CFG::RING;
   constexpr int THREADS = CFG::THREADS, MI = CFG::MI, NJ = CFG::NJ, BTP = CFG::BTP;
   constexpr bool BT = KIND == B_PACKED_T;
   constexpr int SEGS = BM * BK / 16 / THREADS;  // 16-byte pieces per thread per operand (2)
@@ -430,25 +431,39 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   // an odd last step follows. Loads past the last k-step are never consumed (past the
   // last row's end they read zeros, elsewhere the next row: always in bounds).
   const int nk = static_cast<int>(g.K / BK);
-  load(ring[0], 0);
-  __builtin_amdgcn_sched_barrier(0);
-  load(ring[1], 1);
-  __builtin_amdgcn_sched_barrier(0);
-  const int nk_pairs = nk & ~1;
-  for (int kb = 0; kb < nk_pairs; kb += S) {
+  if constexpr (S == 2) {
+    load(ring[0], 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(ring[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+    const int nk_pairs = nk & ~1;
+    for (int kb = 0; kb < nk_pairs; kb += S) {
 #pragma unroll
-    for (int slot = 0; slot < S; ++slot) {
-      store(ring[slot], slot);
-      load(ring[slot], kb + slot + S);
+      for (int slot = 0; slot < S; ++slot) {
+        store(ring[slot], slot);
+        load(ring[slot], kb + slot + S);
+        __syncthreads();
+        mfma32_step<BT, MI, NJ, BTP>(acc, As + slot * BM * BK, Bs + slot * BSTAGE, arow0,
+                                     brow0, lane);
+      }
+    }
+    if (nk & 1) {
+      store(ring[0], 0);
       __syncthreads();
-      mfma32_step<BT, MI, NJ, BTP>(acc, As + slot * BM * BK, Bs + slot * BSTAGE, arow0, brow0,
+      mfma32_step<BT, MI, NJ, BTP>(acc, As, Bs, arow0, brow0, lane);
+    }
+  } else {
+    // one k-step in registers: the loads of step kt + 1 are issued right after step kt is
+    // written to LDS (the same LDS ping-pong and one barrier per step)
+    load(ring[0], 0);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      store(ring[0], buf);
+      load(ring[0], kt + 1);
+      __syncthreads();
+      mfma32_step<BT, MI, NJ, BTP>(acc, As + buf * BM * BK, Bs + buf * BSTAGE, arow0, brow0,
                                    lane);
     }
-  }
-  if (nk & 1) {
-    store(ring[0], 0);
-    __syncthreads();
-    mfma32_step<BT, MI, NJ, BTP>(acc, As, Bs, arow0, brow0, lane);
   }
   __syncthreads();  // all fragment reads done: the tiles become the staging buffer
 
