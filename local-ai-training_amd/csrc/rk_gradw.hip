@@ -45,14 +45,11 @@ struct GwArgs {
   int nsplit;
 };
 
-constexpr int GW_BN = 128;                 // output rows (n) per block
-constexpr int GW_BK = 128;                 // output columns (k) per block
 constexpr int GW_BM = 32;                  // tokens per pipeline step
-// LDS row pitch: 320 bytes = 80 dwords, so consecutive token rows start 16 banks apart.
-// A transposing read serves 32 lanes per pass (rows r..r+3, two 32-byte column halves):
-// rows start at banks 0, 16, 32, 48 and the second half adds 8, so the eight 8-bank
-// segments are disjoint.
-constexpr int GW_PITCH = GW_BN * 2 + 64;
+// LDS row pitch: FEAT * 2 + 64 bytes (320 or 576, 80 or 144 dwords: 16 banks mod 64), so
+// consecutive token rows start 16 banks apart. A transposing read serves 32 lanes per pass
+// (rows r..r+3, two 32-byte column halves): rows start at banks 0, 16, 32, 48 and the
+// second half adds 8, so the eight 8-bank segments are disjoint.
 constexpr int kGwMaxRing = 6;
 
 __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
@@ -61,14 +58,32 @@ __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// A [BM tokens][128 features] tile of an operand with ES-byte elements is read as
-// 16-byte pieces: 8 * ES pieces per token row, 16 / ES elements each, 256 threads,
-// BM * ES / 32 pieces per thread (piece c = tid + 256 j).
-template <int ES, int BM>
+// Block configurations: FEAT x FEAT output tiles (n x k) over WN x WK wavefronts, each a
+// (FEAT / WN) x (FEAT / WK) wave tile of 32 x 32 MFMA blocks; staged LDS rows of FEAT bf16
+// features plus 64 bytes (the pitch keeps consecutive token rows 16 banks apart).
+//  * 128 x 128, 2 x 2 waves: the op shape and small layers;
+//  * 256 x 256, 2 x 4 waves: large layers. A 128 x 128 bf16 tile fetches 64 bytes of g and
+//    X per token step for 1 MFLOP, about the whole L2 bandwidth at the bf16 MFMA peak; the
+//    large tile halves the bytes per FLOP.
+template <int FEAT_, int WN_, int WK_>
+struct GwCfg {
+  static constexpr int FEAT = FEAT_, WN = WN_, WK = WK_;
+  static constexpr int THREADS = 64 * WN * WK;
+  static constexpr int PITCH = FEAT * 2 + 64;
+  static constexpr int MI = FEAT / WN / 32, NJ = FEAT / WK / 32;
+};
+using GwSmall = GwCfg<128, 2, 2>;
+using GwBig = GwCfg<256, 2, 4>;
+
+// A [BM tokens][FEAT features] tile of an operand with ES-byte elements is read as
+// 16-byte pieces: FEAT * ES / 16 pieces per token row, 16 / ES elements each, spread over
+// the block's THREADS (piece c = tid + THREADS j).
+template <int ES, int BM, int FEAT, int THREADS>
 struct GwPieces {
-  static constexpr int kPerRow = 8 * ES;
+  static constexpr int kPerRow = FEAT * ES / 16;
   static constexpr int kElems = 16 / ES;
-  static constexpr int kPerThread = BM * ES / 32;
+  static constexpr int kPerThread = BM * FEAT * ES / 16 / THREADS;
+  static_assert(kPerThread * THREADS == BM * kPerRow, "whole pieces per thread");
   __device__ static int row(int c) { return c / kPerRow; }
   __device__ static int col(int c) { return (c % kPerRow) * kElems; }
 };
@@ -97,44 +112,49 @@ struct GwSlot {
 
 // Fragment of 8 consecutive tokens for feature column `col0 + lane % 16` (+16 for the
 // upper half of each 32-lane half) from a staged [token][feature] tile.
+template <int PITCH>
 __device__ __forceinline__ v8bf gw_fragment(const uint8_t* tile, int tok0, int col0, int lane) {
   const int grp = lane >> 4, sl = lane & 15;
   const int row = tok0 + 8 * (grp >> 1) + (sl >> 2);
   const int col = col0 + 16 * (grp & 1) + 4 * (sl & 3);
-  const uint8_t* p = tile + row * GW_PITCH + col * 2;
+  const uint8_t* p = tile + row * PITCH + col * 2;
   const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(p));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(p + 4 * GW_PITCH));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(p + 4 * PITCH));
   const v4s both[2] = {lo, hi};
   v8bf f;
   __builtin_memcpy(&f, both, sizeof(f));
   return f;
 }
 
-template <int GDT, int XK, int S, int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8)))
+template <int GDT, int XK, int S, int BM, class CFG>
+__global__ __launch_bounds__(CFG::THREADS) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void grad_weight_partial_kernel(GwArgs a) {
   constexpr int GE = GDT == RK_F32 ? 4 : 2;                          // g element bytes
   constexpr int XE = XK == GW_X_Q8 ? 1 : (XK == GW_X_BF16 ? 2 : 4);  // X element bytes
-  using GP = GwPieces<GE, BM>;
-  using XP = GwPieces<XE, BM>;
+  constexpr int FEAT = CFG::FEAT, THREADS = CFG::THREADS, PITCH = CFG::PITCH;
+  constexpr int MI = CFG::MI, NJ = CFG::NJ;
+  using GP = GwPieces<GE, BM, FEAT, THREADS>;
+  using XP = GwPieces<XE, BM, FEAT, THREADS>;
   constexpr int GV = GP::kPerThread, XV = XP::kPerThread;
-  constexpr int TILE = BM * GW_PITCH;  // one staged operand tile
+  constexpr int TILE = BM * PITCH;  // one staged operand tile
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * TILE];
 
-  const int64_t tiles_k = (a.K + GW_BK - 1) / GW_BK;
-  const int64_t tiles = ((a.N + GW_BN - 1) / GW_BN) * tiles_k;
+  const int64_t tiles_k = (a.K + FEAT - 1) / FEAT;
+  const int64_t tiles = ((a.N + FEAT - 1) / FEAT) * tiles_k;
   int64_t b = blockIdx.x;
   const int64_t nb = gridDim.x;
   if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // one XCD per token range
   const int split = static_cast<int>(b / tiles);
   const int64_t t = b % tiles;
-  const int64_t n0 = (t / tiles_k) * GW_BN, k0 = (t % tiles_k) * GW_BK;
+  const int64_t n0 = (t / tiles_k) * FEAT, k0 = (t % tiles_k) * FEAT;
   const int64_t m_begin = split * a.m_chunk;
   const int64_t m_end = min(a.M, m_begin + a.m_chunk);
   const int steps = m_end > m_begin ? static_cast<int>((m_end - m_begin + BM - 1) / BM) : 0;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave & 1, wk = wave >> 1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % CFG::WN, wk = wave / CFG::WN;
+  const int nw0 = wn * (FEAT / CFG::WN), kw0 = wk * (FEAT / CFG::WK);  // wave tile origin
 
   // Buffer descriptors over this block's token range. num_records ends at the last valid
   // byte (row m_end - 1, column N - 1 / K - 1), so every load past the range - token rows
@@ -154,15 +174,15 @@ void grad_weight_partial_kernel(GwArgs a) {
   int g_voff[GV], g_lds[GV], x_voff[XV], x_lds[XV], s_voff[XV];
 #pragma unroll
   for (int j = 0; j < GV; ++j) {
-    const int c = tid + 256 * j;
+    const int c = tid + THREADS * j;
     g_voff[j] = (GP::row(c) * static_cast<int>(a.ldg) + GP::col(c)) * GE;
-    g_lds[j] = GP::row(c) * GW_PITCH + GP::col(c) * 2;
+    g_lds[j] = GP::row(c) * PITCH + GP::col(c) * 2;
   }
 #pragma unroll
   for (int j = 0; j < XV; ++j) {
-    const int c = tid + 256 * j;
+    const int c = tid + THREADS * j;
     x_voff[j] = (XP::row(c) * static_cast<int>(a.ldx) + XP::col(c)) * XE;
-    x_lds[j] = TILE + XP::row(c) * GW_PITCH + XP::col(c) * 2;
+    x_lds[j] = TILE + XP::row(c) * PITCH + XP::col(c) * 2;
     s_voff[j] = XP::row(c) * 4;
   }
   const int g_step = BM * static_cast<int>(a.ldg) * GE;
@@ -224,11 +244,11 @@ void grad_weight_partial_kernel(GwArgs a) {
     }
   };
 
-  v16f acc[2][2];
+  v16f acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = v16f{};
 
   // Register ring of S steps: the global loads of step st + S are issued right after
   // step st is written to LDS, so S steps of g and X stream in while the MFMAs run. The
@@ -261,15 +281,15 @@ void grad_weight_partial_kernel(GwArgs a) {
         // staging.
 #pragma unroll
         for (int u = 0; u < BM / 16; ++u) {
-          v8bf fa[2], fb[2];
+          v8bf fa[MI], fb[NJ];
 #pragma unroll
-          for (int i = 0; i < 2; ++i) fa[i] = gw_fragment(gt, 16 * u, wn * 64 + 32 * i, lane);
+          for (int i = 0; i < MI; ++i) fa[i] = gw_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
 #pragma unroll
-          for (int j = 0; j < 2; ++j) fb[j] = gw_fragment(xt, 16 * u, wk * 64 + 32 * j, lane);
+          for (int j = 0; j < NJ; ++j) fb[j] = gw_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int i = 0; i < MI; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < NJ; ++j)
               acc[i][j] =
                   __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
@@ -277,18 +297,18 @@ void grad_weight_partial_kernel(GwArgs a) {
     }
   }
 
-  // Partial sums: acc[i][j][e] is C[n][k] with k = k0 + wk*64 + 32 j + lane % 32 and
-  // n = n0 + wn*64 + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4.
+  // Partial sums: acc[i][j][e] is C[n][k] with k = k0 + kw0 + 32 j + lane % 32 and
+  // n = n0 + nw0 + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4.
   float* out = a.part + static_cast<int64_t>(split) * a.N * a.K;
   const int lk = lane & 31, lh = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t k = k0 + wk * 64 + 32 * j + lk;
+    for (int j = 0; j < NJ; ++j) {
+      const int64_t k = k0 + kw0 + 32 * j + lk;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t n = n0 + wn * 64 + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
+        const int64_t n = n0 + nw0 + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
         if (n < a.N && k < a.K) out[n * a.K + k] = acc[i][j][e];
       }
     }
@@ -317,10 +337,18 @@ __global__ __launch_bounds__(256) void grad_weight_reduce_kernel(const float* pa
 
 // Ring depth 2 and 32-token steps: ring depths 4 and 6 and 64-token steps (BM = 64, 80 KB
 // of LDS) measure the same or slower on MI355X at the op and model shapes.
-template <int XK>
+template <int XK, class CFG>
 void launch_partial_g(const GwArgs& a, int g_dtype, dim3 grid, hipStream_t st) {
-  if (g_dtype == RK_F32) grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM><<<grid, 256, 0, st>>>(a);
-  else grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM><<<grid, 256, 0, st>>>(a);
+  if (g_dtype == RK_F32)
+    grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM, CFG><<<grid, CFG::THREADS, 0, st>>>(a);
+  else
+    grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM, CFG><<<grid, CFG::THREADS, 0, st>>>(a);
+}
+
+// The 256 x 256 tile where it still leaves at least 64 output tiles (the op shape's
+// 2048 x 512 gradient keeps 128 x 128 tiles and fewer split partials).
+static bool gw_big_tiles(int64_t N, int64_t K) {
+  return N >= 256 && K >= 256 && ((N + 255) / 256) * ((K + 255) / 256) >= 64;
 }
 
 // Shared validation and launch of both entry points; x_kind is a GW_X_* form.
@@ -342,7 +370,9 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
       (reinterpret_cast<uintptr_t>(out) % 8) != 0)
     return fail(RK_ERR_UNSUPPORTED,
                 "grad_weight needs N %% 8 == 0, K %% 16 == 0 and 16-byte aligned rows");
-  const int64_t tiles = ((N + GW_BN - 1) / GW_BN) * ((K + GW_BK - 1) / GW_BK);
+  const bool big = gw_big_tiles(N, K);
+  const int64_t feat = big ? GwBig::FEAT : GwSmall::FEAT;
+  const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
   const int64_t chunk = ((M + nsplit - 1) / nsplit + GW_BM - 1) / GW_BM * GW_BM;
   // Buffer offsets are 32-bit: the furthest load of a block (ring padding and prefetch
   // included) must stay below 2^31 bytes from the block's first row.
@@ -366,9 +396,15 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
   hipStream_t st = as_stream(stream);
   const dim3 grid(static_cast<unsigned>(blocks));
-  if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8>(a, g_dtype, grid, st);
-  else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16>(a, g_dtype, grid, st);
-  else launch_partial_g<GW_X_F32>(a, g_dtype, grid, st);
+  if (big) {
+    if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwBig>(a, g_dtype, grid, st);
+    else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16, GwBig>(a, g_dtype, grid, st);
+    else launch_partial_g<GW_X_F32, GwBig>(a, g_dtype, grid, st);
+  } else {
+    if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwSmall>(a, g_dtype, grid, st);
+    else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16, GwSmall>(a, g_dtype, grid, st);
+    else launch_partial_g<GW_X_F32, GwSmall>(a, g_dtype, grid, st);
+  }
   if (int e = launch_status("grad_weight_partial")) return e;
   if (!out) return RK_OK;  // partials only (rk_ratchet_update_partials reduces them)
   const int64_t total4 = N * K / 4;
@@ -384,8 +420,14 @@ using namespace rk;
 
 extern "C" int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 1;
-  const int64_t tiles = ((N + GW_BN - 1) / GW_BN) * ((K + GW_BK - 1) / GW_BK);
-  int64_t splits = (512 + tiles - 1) / tiles;       // about two blocks per CU
+  const bool big = gw_big_tiles(N, K);
+  const int64_t feat = big ? GwBig::FEAT : GwSmall::FEAT;
+  const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
+  // small tiles: about two 4-wave blocks per CU. Large tiles: one split while the tiles
+  // alone occupy half the CUs (each further split adds 4 B per weight of partials that
+  // the update reads back, which costs more than the idle CUs: measured at the 1B
+  // shapes), else about one 8-wave block per CU.
+  int64_t splits = big ? (tiles >= 128 ? 1 : (256 + tiles - 1) / tiles) : (512 + tiles - 1) / tiles;
   const int64_t max_by_m = (M + 511) / 512;         // at least 512 tokens per split
   if (splits > max_by_m) splits = max_by_m;
   if (splits > 64) splits = 64;

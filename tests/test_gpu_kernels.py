@@ -725,9 +725,11 @@ def _xhat(q: np.ndarray, s: np.ndarray) -> np.ndarray:
     return round_to_bf16(q.astype(np.float32) * round_to_bf16(s.astype(np.float32))[:, None])
 
 
+# (1000, 2056, 2048) and (4096, 2048, 2064) take the 256 x 256 output tiles (ragged last
+# row / column tile, ragged token range, two or more splits); the others 128 x 128.
 @pytest.mark.parametrize("gdtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("m,n,k", [(4096, 256, 128), (1000, 136, 48), (16384, 2048, 512),
-                                   (31, 8, 16)])
+                                   (31, 8, 16), (1000, 2056, 2048), (4096, 2048, 2064)])
 def test_grad_weight_bit_exact_when_every_sum_is_exact(cuda, m, n, k, gdtype):
     # g = small integers * 2^-4, q integers, s = 2^-7: every product and every partial sum
     # is exactly representable in fp32, so the result is order-free and must equal the
@@ -764,7 +766,8 @@ def test_grad_weight_op_shape_within_tolerance_and_deterministic(cuda, gdtype):
     assert bool(((one.float() - ref).abs() <= 1e-3 + 1e-2 * ref.abs()).all())
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 256, 128), (1000, 136, 48), (31, 8, 16)])
+@pytest.mark.parametrize("m,n,k", [(4096, 256, 128), (1000, 136, 48), (31, 8, 16),
+                                   (1000, 2056, 2048)])
 @pytest.mark.parametrize("xdtype", [torch.float32, torch.bfloat16])
 def test_grad_weight_x_bit_exact_when_every_sum_is_exact(cuda, m, n, k, xdtype):
     # Activations given directly: x = integers * 2^-6 (exact in bf16), g = integers / 16,
