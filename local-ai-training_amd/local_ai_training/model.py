@@ -152,6 +152,14 @@ def _attend(q: Tensor, k: Tensor, v: Tensor, **kwargs) -> Tensor:
     return F.scaled_dot_product_attention(q, k, v, **kwargs)
 
 
+def _autocast_bf16(t: Tensor) -> torch.dtype | None:
+    """torch.bfloat16 when `t`'s device runs under bf16 autocast, else None."""
+    dev = t.device.type
+    if torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16:
+        return torch.bfloat16
+    return None
+
+
 class CausalSelfAttention(nn.Module):
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -166,7 +174,11 @@ class CausalSelfAttention(nn.Module):
                 layer: int = 0, decode: bool = False) -> Tensor:
         batch_size, sequence_length, channels = inputs.shape
         if inputs_int8 is not None:
-            qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
+            # Under bf16 autocast the attention casts q, k, v to bf16 (and their gradients
+            # back): take the GEMM's bf16 result directly instead (the same values; no cast
+            # kernels, half the bytes for the gradient concatenation)
+            qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale,
+                           out_dtype=_autocast_bf16(inputs))
         else:
             qkv = self.qkv(inputs)
         query, key, value = qkv.chunk(3, dim=-1)

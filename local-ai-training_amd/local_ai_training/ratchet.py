@@ -154,13 +154,15 @@ def _grad_weight_supported(g: Tensor, x: Tensor) -> bool:
 class _RatchetMatmul(torch.autograd.Function):
     """Ratchet matmul whose backward feeds the effective-weight gradient to the update.
 
-    Inputs: (inputs, inputs_int8, inputs_scale, packed, scale, layer). The packed state
-    is read in place (never unpacked); ``layer`` carries the mode switches and owns the
-    update (``ratchet.py:18-182``).
+    Inputs: (inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype). The packed
+    state is read in place (never unpacked); ``layer`` carries the mode switches and owns the
+    update (``ratchet.py:18-182``). ``out_dtype`` (int8 mode, None = the input dtype) lets a
+    caller that casts the output anyway take the GEMM's bf16 result directly: the values are
+    the same either way (the float32 output is the bf16 result widened).
     """
 
     @staticmethod
-    def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer):
+    def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype=None):
         input_shape = inputs.shape
         flat_inputs = inputs.flatten(0, -2)
         mode = layer.matmul_mode
@@ -169,7 +171,9 @@ class _RatchetMatmul(torch.autograd.Function):
         ctx.input_dtype = inputs.dtype
         ctx.generation = layer._generation
         out_features = packed.shape[0]
-        out_dtype = inputs.dtype if inputs.dtype in (torch.float32, torch.bfloat16) else None
+        requested = out_dtype if mode not in ("fp32", "bf16") else None
+        out_dtype = requested or (inputs.dtype if inputs.dtype in (torch.float32, torch.bfloat16)
+                                  else None)
 
         if mode == "int8" and inputs_int8 is not None and inputs_scale is not None:
             nat.require_rocm(inputs_int8, packed, what="int8 ratchet matmul")
@@ -202,7 +206,9 @@ class _RatchetMatmul(torch.autograd.Function):
                 output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
                                         out_dtype or torch.bfloat16)
         output = output.reshape(*input_shape[:-1], out_features)
-        return output if output.dtype == inputs.dtype else output.to(inputs.dtype)
+        if requested is not None or output.dtype == inputs.dtype:
+            return output
+        return output.to(inputs.dtype)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor):
@@ -245,7 +251,7 @@ class _RatchetMatmul(torch.autograd.Function):
             if needs_scale:
                 grad_scale = (grad_weight_fp32 * layer.code.float()).sum(dim=1)
             return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-                grad_scale, None
+                grad_scale, None, None
 
         m, n = flat_gradient.shape
         gradient_bf16 = None
@@ -355,7 +361,7 @@ class _RatchetMatmul(torch.autograd.Function):
         else:
             grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-            grad_scale, None
+            grad_scale, None, None
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -534,10 +540,13 @@ class DiscreteRatchetLinear(nn.Module):
 
     # -- forward --------------------------------------------------------------
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
-                inputs_scale: Tensor | None = None) -> Tensor:
+                inputs_scale: Tensor | None = None,
+                out_dtype: torch.dtype | None = None) -> Tensor:
+        """``out_dtype`` (int8 mode only): the output dtype in place of the input's, for a
+        caller that would cast the result anyway (same values)."""
         if self.matmul_mode != "fp32" or self.fuse_backward_update:
             return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
-                                        self.scale, self)
+                                        self.scale, self, out_dtype)
         effective = self.effective_weight().to(dtype=inputs.dtype)
         if self.training and torch.is_grad_enabled():
             if self.trainable_scale:
