@@ -395,3 +395,35 @@ def test_hundred_step_integer_state_parity_with_shared_grad_weight(cuda):
                 m_stats.blocked_negative_moves] == ref["counts"].tolist()
     c, p = oupd.unpack(packed_ref, mc)
     assert np.abs(p).max() <= 7 and np.abs(c).max() <= mc
+
+
+def test_int8_out_dtype_override_gives_the_same_values_and_update(cuda):
+    # out_dtype=bf16 hands over the GEMM's bf16 result; the default float32 output is that
+    # result widened. Forward values, grad_input and the updated state are identical when
+    # the gradient is the same (bf16-exact) values in either dtype.
+    m, k, n, mc = 512, 256, 384, 2
+    layers = []
+    for _ in range(2):
+        torch.manual_seed(11)
+        layers.append(DiscreteRatchetLinear(k, n, max_code=mc, matmul_mode="int8",
+                                            int8_backward=True,
+                                            fuse_backward_update=True).to(cuda).train())
+    torch.manual_seed(12)
+    x = torch.randn(m, k, device=cuda)
+    g = (torch.randn(m, n, device=cuda) * 1e-2).to(torch.bfloat16)
+    q, s = quantize_rows(x)
+    start = layers[0].packed.clone()
+    outs, grads = [], []
+    for layer, dt in zip(layers, (None, torch.bfloat16)):
+        xi = x.clone().requires_grad_(True)
+        out = layer(xi, inputs_int8=q, inputs_scale=s, out_dtype=dt)
+        torch.manual_seed(13)  # the SR seed is drawn from the host RNG in backward
+        out.backward(g.float() if dt is None else g)
+        layer.ratchet_update(validate=True)
+        outs.append(out)
+        grads.append(xi.grad)
+    assert outs[0].dtype == torch.float32 and outs[1].dtype == torch.bfloat16
+    assert torch.equal(outs[1].float(), outs[0])
+    assert torch.equal(grads[0], grads[1])
+    assert torch.equal(layers[0].packed, layers[1].packed)
+    assert not torch.equal(layers[0].packed, start)  # the update did move pressure
