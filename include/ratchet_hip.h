@@ -28,7 +28,7 @@ enum {
   RK_OK = 0,
   RK_ERR_ARG = 1,         /* invalid shape, stride, dtype, null pointer, alignment  */
   RK_ERR_LAUNCH = 2,      /* the HIP runtime reported an error at launch           */
-  RK_ERR_UNSUPPORTED = 3  /* a valid request this build does not implement         */
+  RK_ERR_UNSUPPORTED = 3  /* a valid request the library does not implement         */
 };
 
 enum { RK_F32 = 0, RK_BF16 = 1 };

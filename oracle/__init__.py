@@ -6,7 +6,7 @@ path (LoomNode/local-ai-training, ``src/local_ai_training/ratchet.py`` and
 bit-for-bit on identical inputs.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import anything from here, and only as the checker or as the
+``bench.py`` may import anything from here, and only to check results or as the
 timed CPU baseline. The product package (``local-ai-training_amd/``) never
 imports, links or executes this code and has no CPU fallback.
 
@@ -22,8 +22,8 @@ Pinning (what fixes each function independently of this restatement):
 * ``update``     — the reference's known-answer tests (``tests/test_ratchet.py``
                    17-22, 54-78, 183-193, 224-233) and its golden 60-step vector
                    (196-208, seed 1234).
-* ``update.row_sumsq`` — the reduction order is this build's own (documented in
-                   the function); it is pinned exactly on inputs whose partial
+* ``update.row_sumsq`` — the reduction order is the HIP kernel's fixed one
+                   (documented in the function); it is pinned exactly on inputs whose partial
                    sums are all representable (order-free) and by tolerance
                    against float64 elsewhere.
 """

@@ -15,7 +15,7 @@ Update (``ratchet.py:248-301``), all integer given the normalized gradient z:
     counts = (sum PM, sum NM, sum PR & !PM, sum NR & !NM)
 
 Normalization (``ratchet.py:539-556``): z = g / (sqrt(mean_k g^2) + eps), or with the
-opt-in per-row EMA of the mean square. The mean square here uses this build's fixed
+opt-in per-row EMA of the mean square. The mean square here uses the HIP kernel's fixed
 reduction order (``lane_order_sum``) so that the HIP kernel is reproducible bit for bit;
 the reference's own order (a BLAS/ATen reduction) is not reproducible by any other
 implementation.
