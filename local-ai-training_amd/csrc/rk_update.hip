@@ -359,9 +359,8 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
   // Issues every unconditional load of row `row` into `st`.
   auto issue = [&](int64_t row, int64_t K, Stage& st) {
     if constexpr (NC > 0) {
-      const int64_t r = row;
       if constexpr (DT == SRC_SPLITS) {
-        const __amdgpu_buffer_rsrc_t rs = make_buffer(a.part + r * K, K * 4);
+        const __amdgpu_buffer_rsrc_t rs = make_buffer(a.part + row * K, K * 4);
         const uint32_t voff = static_cast<uint32_t>(lane0) * 4u;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -373,7 +372,7 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
       } else {
         // a vector wholly past K, or every vector when the gradient is not vector-aligned,
         // reads as zero (the unaligned case is re-read element by element in `body`)
-        const char* grow = static_cast<const char*>(a.g) + r * a.ldg * ES;
+        const char* grow = static_cast<const char*>(a.g) + row * a.ldg * ES;
         const __amdgpu_buffer_rsrc_t rg =
             make_buffer(grow, a.vec_g ? static_cast<int>(K) * ES : 0);
         const uint32_t voff = static_cast<uint32_t>(lane0) * ES;
@@ -391,7 +390,7 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
         // K % V == 0 whenever vec_p, so a vector is wholly inside or past the row; without
         // vec_p every load reads zero and `body` reads the bytes one by one
         const __amdgpu_buffer_rsrc_t rp =
-            make_buffer(a.packed + r * a.ldp, a.vec_p ? static_cast<int>(K) : 0);
+            make_buffer(a.packed + row * a.ldp, a.vec_p ? static_cast<int>(K) : 0);
         const uint32_t voff = static_cast<uint32_t>(lane0);
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
