@@ -73,16 +73,27 @@ def fused_transpose_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
     return out, scale
 
 
+def _no_grad_outputs(ctx, int8_out: Tensor, scale_out: Tensor) -> None:
+    """The int8 values and their scales carry no gradient (only the dummy output's gradient
+    flows back): mark them so, and do not have autograd build zero gradients for outputs
+    nothing used (one fill kernel each per backward otherwise)."""
+    ctx.mark_non_differentiable(int8_out, scale_out)
+    ctx.set_materialize_grads(False)
+
+
 class FusedRMSNormQuantizeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, weight: Tensor, eps: float = 1e-5):
         int8_out, scale_out = fused_rmsnorm_quantize(x, weight, eps)
         ctx.save_for_backward(x, weight)
         ctx.eps = eps
+        _no_grad_outputs(ctx, int8_out, scale_out)
         return int8_out, scale_out, torch.empty_like(x)
 
     @staticmethod
     def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        if grad_dummy is None:
+            return None, None, None
         x, weight = ctx.saved_tensors
         from .int8_backward import rmsnorm_backward
 
@@ -95,10 +106,13 @@ class FusedGELUQuantizeFn(torch.autograd.Function):
     def forward(ctx, x: Tensor):
         int8_out, scale_out = fused_gelu_quantize(x)
         ctx.save_for_backward(x)
+        _no_grad_outputs(ctx, int8_out, scale_out)
         return int8_out, scale_out, torch.empty_like(x)
 
     @staticmethod
     def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        if grad_dummy is None:
+            return None
         (x,) = ctx.saved_tensors
         from .int8_backward import gelu_backward
 
@@ -113,9 +127,12 @@ class FusedTransposeQuantizeFn(torch.autograd.Function):
         ctx.shape = attended.shape
         dummy = torch.empty((batch_size, seq_len, n_head * head_dim), device=attended.device,
                             dtype=attended.dtype)
+        _no_grad_outputs(ctx, int8_out, scale_out)
         return int8_out, scale_out, dummy
 
     @staticmethod
     def backward(ctx, grad_int8, grad_scale, grad_dummy):
+        if grad_dummy is None:
+            return None
         batch_size, n_head, seq_len, head_dim = ctx.shape
         return grad_dummy.view(batch_size, seq_len, n_head, head_dim).transpose(1, 2)
