@@ -97,6 +97,22 @@ int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* packed, int
                         void* stream);
 
 /*
+ * rk_int8_gemm_packed with a float32 output and a residual added in the epilogue:
+ * C[m, n] = R[m, n] + float(bf16_RNE((acc * ls[m]) * rs[n])), the same float32 add as
+ * adding R to rk_int8_gemm_packed's float32 output afterwards. R (row stride ldr) may be
+ * C itself. 32x32x32-kernel shapes only (M > 16, K % 64 == 0, N % 8 == 0, 16-byte aligned
+ * rows); RK_ERR_UNSUPPORTED otherwise.
+ * Replaces: the residual adds around the attention projection and the feed-forward
+ *           contraction, model.py:181-195 (inputs = inputs + self.attention(...),
+ *           inputs = inputs + self.feed_forward(...)), whose last linears run through
+ *           _RatchetMatmul (ratchet.py:22-67).
+ */
+int rk_int8_gemm_packed_residual(const int8_t* A, int64_t lda, const uint8_t* packed,
+                                 int64_t ldp, int max_code, const float* ls, const float* rs,
+                                 const float* R, int64_t ldr, float* C, int64_t ldc, int64_t M,
+                                 int64_t N, int64_t K, void* stream);
+
+/*
  * The same GEMM with the packed state as the K x N operand, read in place:
  *   C[m, n] = bf16( (float(sum_k A[m,k] * code[k, n]) * ls[m]) * rs[n] ),
  *   code[k, n] = (packed[k, n] & 15) - max_code, packed [K, N] uint8 (row stride ldp).

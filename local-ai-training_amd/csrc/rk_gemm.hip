@@ -46,6 +46,8 @@ struct GemmArgs {
   void* C;
   int64_t ldc;
   int64_t M, N, K;
+  const float* R;  // optional residual added to a float32 output (32x32x32 kernel only)
+  int64_t ldr;
 };
 
 // Loads the 16-byte segment (row, k0 .. k0+15) of an operand; zeros outside
@@ -486,6 +488,13 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t c_rsrc =
       make_buffer(static_cast<char*>(g.C) + (m0 * g.ldc + n0) * ES,
                   ((rows_a - 1) * g.ldc + (g.N - n0)) * ES);
+  // float32 output with a residual: C = R + (the bf16 result widened), the same float32
+  // add as adding the two tensors afterwards (R may be C itself: each thread reads its
+  // residual before it stores over it)
+  const bool has_r = CDT == RK_F32 && g.R != nullptr;
+  const __amdgpu_buffer_rsrc_t r_rsrc =
+      make_buffer(has_r ? g.R + m0 * g.ldr + n0 : g.ls,
+                  has_r ? ((rows_a - 1) * g.ldr + (g.N - n0)) * 4 : 0);
 #pragma unroll
   for (int round = 0; round < CFG::EROUNDS; ++round) {
     if (arow0 / EROWS == round) {
@@ -530,14 +539,26 @@ void int8_gemm_m32_kernel(GemmArgs g) {
           __builtin_amdgcn_raw_buffer_store_b128(
               __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_rsrc, voff, 0, 0);
         } else {
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(v4i, make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16,
-                                                 lo.y & 0xffff0000u)),
-              c_rsrc, voff, 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(v4i, make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16,
-                                                 hi.y & 0xffff0000u)),
-              c_rsrc, voff + 16, 0, 0);
+          uint4 w0 = make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16, lo.y & 0xffff0000u);
+          uint4 w1 = make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16, hi.y & 0xffff0000u);
+          if (has_r) {
+            const int roff = (row * static_cast<int>(g.ldr) + 8 * ch) * 4;
+            const float4 r0 = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(r_rsrc, roff, 0, 0));
+            const float4 r1 = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(r_rsrc, roff + 16, 0, 0));
+            w0.x = __float_as_uint(r0.x + __uint_as_float(w0.x));
+            w0.y = __float_as_uint(r0.y + __uint_as_float(w0.y));
+            w0.z = __float_as_uint(r0.z + __uint_as_float(w0.z));
+            w0.w = __float_as_uint(r0.w + __uint_as_float(w0.w));
+            w1.x = __float_as_uint(r1.x + __uint_as_float(w1.x));
+            w1.y = __float_as_uint(r1.y + __uint_as_float(w1.y));
+            w1.z = __float_as_uint(r1.z + __uint_as_float(w1.z));
+            w1.w = __float_as_uint(r1.w + __uint_as_float(w1.w));
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w0), c_rsrc, voff, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w1), c_rsrc, voff + 16,
+                                                 0, 0);
         }
       }
     }
@@ -670,6 +691,18 @@ static int launch_gemm(const GemmArgs& g, hipStream_t stream) {
   const bool fits32 = 256 * g.lda + g.K + 256 < (int64_t{1} << 31) &&
                       256 * g.ldb + g.K + 256 < (int64_t{1} << 31) &&
                       256 * g.ldc * es < (int64_t{1} << 31);
+  if (g.R) {
+    // the residual epilogue exists in the 32x32x32 kernel only
+    const bool r_ok = CDT == RK_F32 && aligned_out && fits32 && g.M > 16 && aligned16(g.R) &&
+                      (g.ldr % 4) == 0 && g.ldr >= g.N && 256 * g.ldr * 4 < (int64_t{1} << 31);
+    if (!r_ok)
+      return fail(RK_ERR_UNSUPPORTED,
+                  "residual GEMM needs float32 output, M > 16, K %% 64 == 0, N %% 8 == 0 and "
+                  "16-byte aligned rows");
+    if (g.rs) launch_m32<KIND, CDT, true>(g, stream);
+    else launch_m32<KIND, CDT, false>(g, stream);
+    return launch_status("int8_gemm_residual");
+  }
   if (aligned_out && fits32 && g.M <= 16) {
     // decode-sized M: one pass over B spread over the whole chip
     if ((g.N + 15) / 16 > 0x7fffffff) return fail(RK_ERR_ARG, "GEMM grid too large");
@@ -722,7 +755,8 @@ static int launch_gemm_packed_t(const GemmArgs& g, hipStream_t stream) {
 
 static int gemm_entry(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ldb, int kind,
                       int max_code, const float* ls, const float* rs, void* C, int c_dtype,
-                      int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream) {
+                      int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream,
+                      const float* R = nullptr, int64_t ldr = 0) {
   clear_error();
   if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative GEMM extent");
   if (c_dtype != RK_F32 && c_dtype != RK_BF16) return fail(RK_ERR_ARG, "bad output dtype");
@@ -747,6 +781,8 @@ static int gemm_entry(const int8_t* A, int64_t lda, const uint8_t* B, int64_t ld
   g.M = M;
   g.N = N;
   g.K = K;
+  g.R = R;
+  g.ldr = ldr;
   hipStream_t s = as_stream(stream);
   if (kind == B_PACKED) {
     return c_dtype == RK_BF16 ? launch_gemm<B_PACKED, RK_BF16>(g, s)
@@ -773,6 +809,19 @@ extern "C" int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* 
                                    int64_t K, void* stream) {
   return gemm_entry(A, lda, packed, ldp, B_PACKED, max_code, ls, rs, C, c_dtype, ldc, M, N, K,
                     stream);
+}
+
+extern "C" int rk_int8_gemm_packed_residual(const int8_t* A, int64_t lda,
+                                            const uint8_t* packed, int64_t ldp, int max_code,
+                                            const float* ls, const float* rs, const float* R,
+                                            int64_t ldr, float* C, int64_t ldc, int64_t M,
+                                            int64_t N, int64_t K, void* stream) {
+  if (!R) {
+    clear_error();
+    return fail(RK_ERR_ARG, "null residual");
+  }
+  return gemm_entry(A, lda, packed, ldp, B_PACKED, max_code, ls, rs, C, RK_F32, ldc, M, N, K,
+                    stream, R, ldr);
 }
 
 extern "C" int rk_int8_gemm_packed_t(const int8_t* A, int64_t lda, const uint8_t* packed,

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, list] = {
                             _p],
     "rk_int8_gemm_packed_t": [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i64, _i64, _i64,
                               _i64, _p],
+    "rk_int8_gemm_packed_residual": [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _p, _i64,
+                                     _i64, _i64, _i64, _p],
     "rk_unpack_transpose": [_p, _i64, _i32, _p, _i64, _i64, _i64, _p],
     "rk_unpack": [_p, _i64, _i32, _p, _p, _p],
     "rk_effective_bf16": [_p, _i64, _i32, _p, _p, _i64, _i64, _i64, _p],

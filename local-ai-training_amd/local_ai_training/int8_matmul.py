@@ -136,6 +136,38 @@ def packed_int8_mm(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
     return out
 
 
+def residual_supported(a: Tensor, packed: Tensor, residual: Tensor) -> bool:
+    """Whether packed_int8_mm_residual can run on these operands: the 32x32x32 kernel's
+    shapes (more than 16 rows, K % 64 == 0, N % 8 == 0, 16-byte aligned rows) and a float32
+    residual [M, N] with unit column stride."""
+    m, k = a.shape
+    n = packed.shape[0]
+    return (m > 16 and k % 64 == 0 and n % 8 == 0 and residual.dtype == torch.float32
+            and residual.shape == (m, n) and residual.stride(-1) == 1
+            and a.stride(-1) == 1 and packed.stride(-1) == 1 and _ld(a) % 16 == 0
+            and _ld(packed) % 16 == 0 and _ld(residual) % 4 == 0
+            and a.data_ptr() % 16 == 0 and packed.data_ptr() % 16 == 0
+            and residual.data_ptr() % 16 == 0)
+
+
+def packed_int8_mm_residual(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
+                            row_scale: Tensor | None, residual: Tensor,
+                            out: Tensor | None = None) -> Tensor:
+    """C = residual + float32(bf16((A @ code^T) * a_scale * row_scale)) in one launch: the
+    forward GEMM's float32 output with the residual add fused into its epilogue (the same
+    float32 add as adding afterwards)."""
+    m, k = a.shape
+    n = packed.shape[0]
+    if out is None:
+        out = torch.empty((m, n), device=a.device, dtype=torch.float32)
+    nat.call(
+        "rk_int8_gemm_packed_residual", a.data_ptr(), _ld(a), packed.data_ptr(), _ld(packed),
+        max_code, a_scale.data_ptr(), nat.ptr(row_scale), residual.data_ptr(), _ld(residual),
+        out.data_ptr(), _ld(out), m, n, k, nat.stream_handle(a.device),
+    )
+    return out
+
+
 def packed_t_supported(a: Tensor, packed: Tensor) -> bool:
     """Whether packed_int8_mm_t can run on these operands (aligned shapes)."""
     k, n = packed.shape

@@ -171,7 +171,10 @@ class CausalSelfAttention(nn.Module):
 
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None, cache: KVCache | None = None,
-                layer: int = 0, decode: bool = False) -> Tensor:
+                layer: int = 0, decode: bool = False,
+                residual: Tensor | None = None) -> Tensor:
+        """``residual``: return residual + attention output (int8 projection: added in the
+        GEMM epilogue)."""
         batch_size, sequence_length, channels = inputs.shape
         if inputs_int8 is not None:
             # Under bf16 autocast the attention casts q, k, v to bf16 (and their gradients
@@ -194,9 +197,11 @@ class CausalSelfAttention(nn.Module):
             attended = _attend(q, k, v, dropout_p=dropout_p, is_causal=True)
         if _is_int8(self.projection):
             attn_int8, attn_scale, dummy = FusedTransposeQuantizeFn.apply(attended)
-            return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale)
+            return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale,
+                                   residual=residual)
         joined = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, channels)
-        return self.projection(joined)
+        out = self.projection(joined)
+        return out if residual is None else residual + out
 
     def _cached_attention(self, q: Tensor, k: Tensor, v: Tensor, cache: KVCache, layer: int,
                           decode: bool) -> Tensor:
@@ -235,20 +240,32 @@ class FeedForward(nn.Module):
         self.dropout = config.dropout
 
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
-                inputs_scale: Tensor | None = None) -> Tensor:
+                inputs_scale: Tensor | None = None,
+                residual: Tensor | None = None) -> Tensor:
+        """``residual``: return residual + feed-forward output (int8 contraction without
+        active dropout: added in the GEMM epilogue)."""
         if inputs_int8 is not None:
             expanded = self.expand(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
         else:
             expanded = self.expand(inputs)
+        no_dropout = self.dropout == 0.0 or not self.training
         if _is_int8(self.contract):
             gelu_int8, gelu_scale, dummy = FusedGELUQuantizeFn.apply(expanded)
+            if no_dropout:
+                return self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale,
+                                     residual=residual)
             contracted = self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale)
         else:
             contracted = self.contract(F.gelu(expanded))
-        return F.dropout(contracted, p=self.dropout, training=self.training)
+        out = F.dropout(contracted, p=self.dropout, training=self.training)
+        return out if residual is None else residual + out
 
 
 class TransformerBlock(nn.Module):
+    # int8 blocks hand the residual stream to the attention projection and the feed-forward
+    # contraction, whose GEMMs add it in their epilogue (the same float32 add)
+    fuse_residual: bool = True
+
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
         self.attention_norm = nn.RMSNorm(config.n_embd)
@@ -261,13 +278,20 @@ class TransformerBlock(nn.Module):
         kv = dict(cache=cache, layer=layer, decode=decode) if cache is not None else {}
         if _is_int8(self.attention.qkv):
             q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight, 1e-5)
-            inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s, **kv)
+            if self.fuse_residual:
+                inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, residual=inputs,
+                                        **kv)
+            else:
+                inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s, **kv)
         else:
             inputs = inputs + self.attention(self.attention_norm(inputs), **kv)
         if _is_int8(self.feed_forward.expand):
             q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
                                                        1e-5)
-            inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
+            if self.fuse_residual:
+                inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s, residual=inputs)
+            else:
+                inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
         else:
             inputs = inputs + self.feed_forward(self.feed_forward_norm(inputs))
         return inputs

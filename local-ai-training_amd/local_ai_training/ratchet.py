@@ -43,9 +43,11 @@ from .int8_matmul import (
     grad_weight_splits,
     int8_mm_nt,
     packed_int8_mm,
+    packed_int8_mm_residual,
     packed_int8_mm_t,
     packed_t_supported,
     quantize_rows_into,
+    residual_supported,
     transpose_bf16,
     unpack_transpose,
 )
@@ -151,6 +153,29 @@ def _grad_weight_supported(g: Tensor, x: Tensor) -> bool:
 # ---------------------------------------------------------------------------
 # Autograd function
 # ---------------------------------------------------------------------------
+def _split_residual_grad(ctx, grad_output: Tensor) -> tuple[Tensor, Tensor | None]:
+    """For output = residual + y: y's gradient and the residual's, each cast to its operand's
+    dtype as autograd casts the gradients of an add of mixed dtypes (a bf16 y gets the
+    bf16-rounded gradient)."""
+    if ctx.residual_dtype is None:
+        return grad_output, None
+    grad_residual = grad_output.to(ctx.residual_dtype) if ctx.needs_input_grad[7] else None
+    return grad_output.to(ctx.y_dtype), grad_residual
+
+
+def _fusable_residual(residual: Tensor | None, q: Tensor, packed: Tensor,
+                      out_dtype: torch.dtype | None) -> Tensor | None:
+    """The residual as a float32 [M, N] view when the forward GEMM can add it in its
+    epilogue, else None. The kernel's float32 output is the bf16-rounded product widened,
+    so residual + product matches the separate add for a bfloat16 or float32 product."""
+    if residual is None or out_dtype not in (torch.float32, torch.bfloat16):
+        return None
+    if residual.dtype != torch.float32:
+        return None
+    flat = residual.reshape(-1, residual.shape[-1])
+    return flat if residual_supported(q, packed, flat) else None
+
+
 class _RatchetMatmul(torch.autograd.Function):
     """Ratchet matmul whose backward feeds the effective-weight gradient to the update.
 
@@ -162,7 +187,8 @@ class _RatchetMatmul(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype=None):
+    def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype=None,
+                residual=None):
         input_shape = inputs.shape
         flat_inputs = inputs.flatten(0, -2)
         mode = layer.matmul_mode
@@ -183,8 +209,7 @@ class _RatchetMatmul(torch.autograd.Function):
                 q = q.contiguous()
             ctx.save_for_backward(q, s, scale)
             ctx.used_fused_int8 = True
-            output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
-                                    out_dtype or torch.bfloat16)
+            output = None
         else:
             ctx.save_for_backward(flat_inputs, scale)
             ctx.used_fused_int8 = False
@@ -203,12 +228,22 @@ class _RatchetMatmul(torch.autograd.Function):
                 if x.dtype not in (torch.float32, torch.bfloat16):
                     x = x.float()
                 quantize_rows_into(x, q, s)
-                output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
-                                        out_dtype or torch.bfloat16)
+                output = None
+        # the dtype of the product itself (residual + product is the function's output)
+        ctx.y_dtype = requested or inputs.dtype
+        ctx.residual_dtype = residual.dtype if residual is not None else None
+        if output is None:
+            flat_res = _fusable_residual(residual, q, packed, out_dtype)
+            if flat_res is not None:
+                output = packed_int8_mm_residual(q, packed, layer.max_code, s,
+                                                 scale.detach().float(), flat_res)
+                return output.reshape(*input_shape[:-1], out_features)
+            output = packed_int8_mm(q, packed, layer.max_code, s, scale.detach().float(),
+                                    out_dtype or torch.bfloat16)
         output = output.reshape(*input_shape[:-1], out_features)
-        if requested is not None or output.dtype == inputs.dtype:
-            return output
-        return output.to(inputs.dtype)
+        if requested is None and output.dtype != inputs.dtype:
+            output = output.to(inputs.dtype)
+        return output if residual is None else residual + output
 
     @staticmethod
     def backward(ctx, grad_output: Tensor):
@@ -229,6 +264,7 @@ class _RatchetMatmul(torch.autograd.Function):
             flat_inputs, scale = ctx.saved_tensors
             inputs_bf16 = None  # bf16(inputs), made only where a path needs the copy
             inputs_fp32 = flat_inputs.to(torch.float32) if mode == "fp32" else None
+        grad_output, grad_residual = _split_residual_grad(ctx, grad_output)
         flat_gradient = grad_output.flatten(0, -2)
         scale_d = scale.detach()
         needs_scale = ctx.needs_input_grad[4]
@@ -251,7 +287,7 @@ class _RatchetMatmul(torch.autograd.Function):
             if needs_scale:
                 grad_scale = (grad_weight_fp32 * layer.code.float()).sum(dim=1)
             return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-                grad_scale, None, None
+                grad_scale, None, None, grad_residual
 
         m, n = flat_gradient.shape
         gradient_bf16 = None
@@ -361,7 +397,7 @@ class _RatchetMatmul(torch.autograd.Function):
         else:
             grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-            grad_scale, None, None
+            grad_scale, None, None, grad_residual
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -541,12 +577,15 @@ class DiscreteRatchetLinear(nn.Module):
     # -- forward --------------------------------------------------------------
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None,
-                out_dtype: torch.dtype | None = None) -> Tensor:
+                out_dtype: torch.dtype | None = None,
+                residual: Tensor | None = None) -> Tensor:
         """``out_dtype`` (int8 mode only): the output dtype in place of the input's, for a
-        caller that would cast the result anyway (same values)."""
+        caller that would cast the result anyway (same values). ``residual``: return
+        ``residual + output`` (added in the GEMM's epilogue where the shapes allow, the same
+        float32 add)."""
         if self.matmul_mode != "fp32" or self.fuse_backward_update:
             return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
-                                        self.scale, self, out_dtype)
+                                        self.scale, self, out_dtype, residual)
         effective = self.effective_weight().to(dtype=inputs.dtype)
         if self.training and torch.is_grad_enabled():
             if self.trainable_scale:
@@ -554,7 +593,8 @@ class DiscreteRatchetLinear(nn.Module):
             else:
                 effective = effective.detach().requires_grad_(True)
             self._effective_weight = effective
-        return F.linear(inputs, effective)
+        output = F.linear(inputs, effective)
+        return output if residual is None else residual + output
 
     # -- gradient capture and the fused update --------------------------------
     def _capture_weight_gradient(self, gradient: Tensor) -> None:

@@ -255,6 +255,25 @@ def test_packed_gemm_bit_exact(cuda, m, n, k, max_code):
     assert np.array_equal(bits16(out), ref)
 
 
+# The forward GEMM with the residual added in its epilogue: the float32 output of the
+# plain GEMM plus R, bit for bit, in both block configurations, with R aliasing the output.
+@pytest.mark.parametrize("m,n,k", [(300, 200, 192), (4100, 4104, 1088)])
+def test_packed_gemm_residual_equals_gemm_then_add(cuda, m, n, k):
+    from local_ai_training.int8_matmul import packed_int8_mm_residual
+
+    packed, scale = synthetic_state(n, k, 2, seed=m + k)
+    q = torch.randint(-127, 128, (m, k), generator=gen(m), dtype=torch.int8).to(cuda)
+    ls = (torch.rand(m, generator=gen(m + 1)) * 0.05 + 1e-3).to(cuda)
+    pd, rs = torch.from_numpy(packed).to(cuda), torch.from_numpy(scale).to(cuda)
+    r = torch.randn(m, n, generator=gen(m + 2)).to(cuda)
+    want = r + packed_int8_mm(q, pd, 2, ls, rs, torch.float32)
+    got = packed_int8_mm_residual(q, pd, 2, ls, rs, r)
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+    inplace = r.clone()
+    packed_int8_mm_residual(q, pd, 2, ls, rs, inplace, out=inplace)
+    assert torch.equal(inplace.view(torch.int32), want.view(torch.int32))
+
+
 # Decode-sized M (<= 16 tokens) takes the small-M kernel: 1B-model layer shapes (qkv 6144 x
 # 2048, contract 2048 x 5632, lm_head 8192 x 2048), partial 16-row groups, M of 1..16.
 SMALL_M_SHAPES = [(1, 6144, 2048), (16, 2048, 5632), (3, 136, 64), (16, 8, 64), (5, 1032, 1024),

@@ -120,3 +120,56 @@ def test_fused_transpose_quantize_is_exact(cuda, dtype):
     xt = x.to(cuda).transpose(2, 3).contiguous().transpose(2, 3)
     q2, s2 = fused_transpose_quantize(xt)
     assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(s2.cpu(), s.cpu())
+
+
+def _int8_steps(cuda, fuse: bool, steps: int = 3):
+    from local_ai_training.model import TransformerBlock
+
+    TransformerBlock.fuse_residual = fuse
+    try:
+        torch.manual_seed(0)
+        config = ModelConfig(vocab_size=64, block_size=64, n_layer=2, n_head=4, n_embd=128,
+                             matmul_mode="int8", int8_backward=True)
+        model = build_seeded_model(config, max_code=2, seed=1337).to(cuda).train()
+        optimizer = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.0)
+        gen = torch.Generator().manual_seed(3)
+        batch = torch.randint(0, 64, (8, 65), generator=gen).to(cuda)
+        losses = []
+        for _ in range(steps):
+            optimizer.zero_grad(set_to_none=True)
+            with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                _, loss = model(batch[:, :64], batch[:, 1:])
+            loss.backward()
+            model.ratchet_update(validate=True)
+            optimizer.step()
+            losses.append(loss.detach())
+        states = [m.packed.clone() for m in model.modules() if isinstance(m, DiscreteRatchetLinear)]
+        params = [p.detach().clone() for p in model.parameters()]
+        return losses, states, params
+    finally:
+        TransformerBlock.fuse_residual = True
+
+
+def test_residual_fused_into_the_gemm_epilogue_changes_nothing(cuda):
+    # The residual stream added by the projection / contraction GEMMs' epilogue instead of a
+    # separate add: identical losses, ratchet states and float parameters over three steps.
+    from local_ai_training import ratchet
+
+    calls = []
+    fused_mm = ratchet.packed_int8_mm_residual
+
+    def counting(*args, **kwargs):
+        calls.append(1)
+        return fused_mm(*args, **kwargs)
+
+    ratchet.packed_int8_mm_residual = counting
+    try:
+        la, sa, pa = _int8_steps(cuda, fuse=True)
+    finally:
+        ratchet.packed_int8_mm_residual = fused_mm
+    assert len(calls) == 3 * 2 * 2  # steps x layers x (projection, contraction)
+    lb, sb, pb = _int8_steps(cuda, fuse=False)
+    assert torch.equal(la[0], lb[0])  # forward
+    assert all(torch.equal(x, y) for x, y in zip(la, lb))
+    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
+    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
