@@ -343,8 +343,10 @@ static int launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
   // (registers and LDS), so grids of up to 512 workgroups run in one round.
   const bool small_k = a.K <= 2048;
   if (a.M <= 1) {
+    // one token row; long rows split K over 8 wavefronts (twice the code loads in flight
+    // per CU: 14.7 -> 12.5 us for N 2048 x K 5632), short ones over 4 (8 were slower)
     if (small_k) decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
-    else decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 24, 24><<<grid, 256, 0, stream>>>(a);
+    else decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
   } else if (a.M <= 4) {
     if (small_k) decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
     else decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 24, 24><<<grid, 256, 0, stream>>>(a);
