@@ -159,7 +159,10 @@ def _split_residual_grad(ctx, grad_output: Tensor) -> tuple[Tensor, Tensor | Non
     bf16-rounded gradient)."""
     if ctx.residual_dtype is None:
         return grad_output, None
-    grad_residual = grad_output.to(ctx.residual_dtype) if ctx.needs_input_grad[7] else None
+    grad_residual = None
+    if ctx.needs_input_grad[7]:
+        # a residual broadcast against the output gets the gradient summed to its shape
+        grad_residual = grad_output.sum_to_size(ctx.residual_shape).to(ctx.residual_dtype)
     return grad_output.to(ctx.y_dtype), grad_residual
 
 
@@ -232,6 +235,7 @@ class _RatchetMatmul(torch.autograd.Function):
         # the dtype of the product itself (residual + product is the function's output)
         ctx.y_dtype = requested or inputs.dtype
         ctx.residual_dtype = residual.dtype if residual is not None else None
+        ctx.residual_shape = residual.shape if residual is not None else None
         if output is None:
             flat_res = _fusable_residual(residual, q, packed, out_dtype)
             if flat_res is not None:

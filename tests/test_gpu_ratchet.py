@@ -427,3 +427,34 @@ def test_int8_out_dtype_override_gives_the_same_values_and_update(cuda):
     assert torch.equal(grads[0], grads[1])
     assert torch.equal(layers[0].packed, layers[1].packed)
     assert not torch.equal(layers[0].packed, start)  # the update did move pressure
+
+
+def test_int8_residual_argument_matches_adding_afterwards(cuda):
+    # residual= on an int8 layer: a full-shape float32 residual goes through the GEMM's
+    # epilogue, a broadcast [n] one through the separate add. Values, the residual's gradient
+    # (summed to its shape), grad_input and the updated state equal those of adding after.
+    m, k, n, mc = 512, 256, 384, 2
+    torch.manual_seed(12)
+    x = torch.randn(m, k, device=cuda)
+    g = torch.randn(m, n, device=cuda) * 1e-2
+    q, s = quantize_rows(x)
+    for shape in ((m, n), (n,)):
+        r0 = torch.randn(*shape, device=cuda)
+        results = []
+        for fused in (True, False):
+            torch.manual_seed(11)
+            layer = DiscreteRatchetLinear(k, n, max_code=mc, matmul_mode="int8",
+                                          int8_backward=True,
+                                          fuse_backward_update=True).to(cuda).train()
+            xi = x.clone().requires_grad_(True)
+            r = r0.clone().requires_grad_(True)
+            if fused:
+                out = layer(xi, inputs_int8=q, inputs_scale=s, residual=r)
+            else:
+                out = r + layer(xi, inputs_int8=q, inputs_scale=s)
+            torch.manual_seed(13)  # the SR seed is drawn from the host RNG in backward
+            out.backward(g)
+            layer.ratchet_update(validate=True)
+            results.append((out.detach(), xi.grad, r.grad, layer.packed.clone()))
+        for a, b in zip(*results):
+            assert a.shape == b.shape and torch.equal(a, b), shape
