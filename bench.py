@@ -106,15 +106,13 @@ def synthetic_layer(device):
 def op_bench(args, device):
     import torch
 
-    from local_ai_training.int8_matmul import quantize_rows_into
+    from local_ai_training.int8_matmul import CapturedSeeds, quantize_rows
 
     layer, x, g = synthetic_layer(device)
     x.requires_grad_(True)
-    q = torch.empty(M_TOK, K_IN, dtype=torch.int8, device=device)
-    s = torch.empty(M_TOK, dtype=torch.float32, device=device)
 
     def step():
-        quantize_rows_into(x.detach(), q, s)
+        q, s = quantize_rows(x.detach())
         out = layer(x, inputs_int8=q, inputs_scale=s)
         out.backward(g)
         x.grad = None
@@ -135,8 +133,10 @@ def op_bench(args, device):
         return eager_s, eager_s, layer, x.detach(), g
     # The whole step (quant, forward, backward, fused update) captured once into a HIP
     # graph and replayed: every replay launches the same kernels on the same buffers, so
-    # the host-side autograd and launch overhead of the eager step disappears. The SR
-    # seed drawn on the host at capture time is part of the graph (same work per step).
+    # the host-side autograd and launch overhead of the eager step disappears. The SR seed
+    # is read from a device slot that the host fills before each replay with a fresh draw
+    # from the CPU generator (the eager step's draw), inside the timed step.
+    seeds = CapturedSeeds(device)
     side = torch.cuda.Stream(device=device)
     side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
@@ -144,11 +144,16 @@ def op_bench(args, device):
             step()
     torch.cuda.current_stream(device).wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with seeds.recording(), torch.cuda.graph(graph):
         step()
-    for _ in range(args.warmup):
+
+    def replay():
+        seeds.refill()
         graph.replay()
-    graph_s = timed(graph.replay, args.steps)
+
+    for _ in range(args.warmup):
+        replay()
+    graph_s = timed(replay, args.steps)
     return graph_s, eager_s, layer, x.detach(), g
 
 
@@ -174,24 +179,16 @@ def op_stages(layer, x, g):
     import torch
 
     from local_ai_training import _native as nat
-    from local_ai_training.int8_matmul import (
-        grad_weight_bf16,
-        grad_weight_splits,
-        packed_int8_mm,
-        packed_int8_mm_t,
-        quantize_rows_into,
-    )
+    from local_ai_training.int8_matmul import grad_weight_splits
+    from local_ai_training.ops import ratchet
 
+    ops = ratchet()
     dev = x.device
     m, k = x.shape
     n = layer.out_features
     packed, scale = layer.packed, layer.scale.float().contiguous()
-    q = torch.empty(m, k, dtype=torch.int8, device=dev)
-    s = torch.empty(m, dtype=torch.float32, device=dev)
-    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-    gq = torch.empty(m, n, dtype=torch.int8, device=dev)
-    gs = torch.empty(m, dtype=torch.float32, device=dev)
-    gin = torch.empty(m, k, dtype=torch.bfloat16, device=dev)
+    q, s = ops.quantize_rows(x)
+    gq, gs = ops.quantize_rows(g, scale, True, 12345)
     splits = grad_weight_splits(m, n, k)
     gw_work = torch.empty(splits, n, k, dtype=torch.float32, device=dev)
     counts = torch.zeros(4, dtype=torch.int64, device=dev)
@@ -200,21 +197,21 @@ def op_stages(layer, x, g):
 
     def update():
         # the update kernel alone (the step's separate one-block mean of row_rms is not part
-        # of this stage)
+        # of this stage), through the C ABI with its fixed buffers
         nat.call("rk_ratchet_update_partials", packed.data_ptr(), k, gw_work.data_ptr(), splits,
                  n, k, MAX_CODE, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
                  row_rms.data_ptr(), None, flag.data_ptr(), None, None, k,
                  nat.stream_handle(dev))
 
+    # each stage is the operator the autograd step calls, with the step's arguments
     stages = [
-        ("quant_rows", lambda: quantize_rows_into(x, q, s)),
-        ("fwd_gemm_packed", lambda: packed_int8_mm(q, packed, MAX_CODE, s, scale, out=out)),
-        ("sr_quant_rows", lambda: quantize_rows_into(g, gq, gs, col_scale=scale,
-                                                     stochastic=True, seed=12345)),
-        ("grad_input_gemm", lambda: packed_int8_mm_t(gq, packed, MAX_CODE, gs, None,
-                                                     out=gin)),
-        ("grad_weight_partials", lambda: grad_weight_bf16(g, q, s, splits, work=gw_work,
-                                                          reduce=False)),
+        ("quant_rows", lambda: ops.quantize_rows(x)),
+        ("fwd_gemm_packed", lambda: ops.packed_mm(q, packed, MAX_CODE, s, scale,
+                                                  torch.bfloat16)),
+        ("sr_quant_rows", lambda: ops.quantize_rows(g, scale, True, 12345)),
+        ("grad_input_gemm", lambda: ops.packed_mm_t(gq, packed, MAX_CODE, gs, None,
+                                                    torch.bfloat16)),
+        ("grad_weight_partials", lambda: ops.grad_weight_partials(g, q, s, gw_work)),
         ("ratchet_update_partials", update),
     ]
     work = stage_work(m, n, k, g.element_size(), splits)
@@ -739,10 +736,9 @@ def gemm_sweep(device, iters: int) -> list:
         code = torch.randint(-MAX_CODE, MAX_CODE + 1, (n, k), generator=gen)
         packed = (((code + MAX_CODE) & 0x0F) | (7 << 4)).to(torch.uint8).to(device)
         rs = (torch.rand(n, generator=gen) * 0.08 + 0.02).to(device)
-        out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
 
         def run():
-            packed_int8_mm(q, packed, MAX_CODE, ls, rs, out=out)
+            packed_int8_mm(q, packed, MAX_CODE, ls, rs)
 
         for _ in range(3):
             run()

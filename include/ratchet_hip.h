@@ -62,6 +62,20 @@ int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t s
                      uint16_t* x_bf16, int64_t ld_xb, void* stream);
 
 /*
+ * rk_quantize_rows with stochastic = 1 and the seed read from device memory when the
+ * kernel runs: seed points to one int64 on the device (the same value rk_quantize_rows
+ * would take as `seed`). A HIP graph that captures this call draws whatever seed the
+ * caller stored there before each replay, so replays of a captured training step take
+ * fresh random bits while the host still draws one seed per call.
+ * Replaces: quantize_rows_colscaled(..., stochastic=True)  int8_matmul.py:262-277 with its
+ *           per-call seed draw int8_matmul.py:200.
+ */
+int rk_quantize_rows_devseed(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                             int64_t sxk, const float* col_scale, const int64_t* seed,
+                             int64_t row_offset, int8_t* q, int64_t ldq, float* scale,
+                             uint16_t* x_bf16, int64_t ld_xb, void* stream);
+
+/*
  * Random words of the stochastic rounding: out[i] = first output word of
  * Philox4x32-10 for counter ((counter0 + i) mod 2^32, 0, 0, 0) and key
  * (seed & 0xffffffff, seed >> 32), exactly the words rk_quantize_rows(stochastic=1)
@@ -100,7 +114,8 @@ int rk_int8_gemm_packed(const int8_t* A, int64_t lda, const uint8_t* packed, int
  * rk_int8_gemm_packed with a float32 output and a residual added in the epilogue:
  * C[m, n] = R[m, n] + float(bf16_RNE((acc * ls[m]) * rs[n])), the same float32 add as
  * adding R to rk_int8_gemm_packed's float32 output afterwards. R (row stride ldr) may be
- * C itself. 32x32x32-kernel shapes only (M > 16, K % 64 == 0, N % 8 == 0, 16-byte aligned
+ * C itself (R == C and ldr == ldc); any other overlap of R and C is rejected with
+ * RK_ERR_ARG. 32x32x32-kernel shapes only (M > 16, K % 64 == 0, N % 8 == 0, 16-byte aligned
  * rows); RK_ERR_UNSUPPORTED otherwise.
  * Replaces: the residual adds around the attention projection and the feed-forward
  *           contraction, model.py:181-195 (inputs = inputs + self.attention(...),

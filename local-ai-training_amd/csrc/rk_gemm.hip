@@ -816,9 +816,18 @@ extern "C" int rk_int8_gemm_packed_residual(const int8_t* A, int64_t lda,
                                             const float* ls, const float* rs, const float* R,
                                             int64_t ldr, float* C, int64_t ldc, int64_t M,
                                             int64_t N, int64_t K, void* stream) {
-  if (!R) {
-    clear_error();
-    return fail(RK_ERR_ARG, "null residual");
+  clear_error();
+  if (!R) return fail(RK_ERR_ARG, "null residual");
+  if (M > 0 && N > 0 && C) {
+    // Each thread reads the residual element it then overwrites, so R may be C itself
+    // (same rows, same stride); any other overlap lets one block overwrite rows another
+    // block still has to read.
+    const char* rb = reinterpret_cast<const char*>(R);
+    const char* cb = reinterpret_cast<const char*>(C);
+    const bool overlap = rb < cb + ((M - 1) * ldc + N) * int64_t{4} &&
+                         cb < rb + ((M - 1) * ldr + N) * int64_t{4};
+    if (overlap && !(R == C && ldr == ldc))
+      return fail(RK_ERR_ARG, "residual overlaps the output without being the output itself");
   }
   return gemm_entry(A, lda, packed, ldp, B_PACKED, max_code, ls, rs, C, RK_F32, ldc, M, N, K,
                     stream, R, ldr);

@@ -28,6 +28,7 @@ struct QuantArgs {
   const float* w;             // rmsnorm weight
   float eps;
   uint32_t key0, key1;        // Philox key (SR only)
+  const int64_t* seed_dev;    // SR only: when set, the key is read here at kernel time
   int64_t row_offset;         // SR counter row offset
   int8_t* q;
   int64_t ldq;
@@ -167,7 +168,15 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
   const bool vec_store = (a.ldq % V) == 0 && ((reinterpret_cast<uintptr_t>(a.q) % V) == 0);
   uint16_t* xbrow = (SRC == SRC_PLAIN && a.xb) ? a.xb + row * a.ldxb : nullptr;
   PhiloxKey key{};
-  if constexpr (SR) key = philox_key(a.key0, a.key1);
+  if constexpr (SR) {
+    uint32_t k0 = a.key0, k1 = a.key1;
+    if (a.seed_dev) {
+      const uint64_t seed = static_cast<uint64_t>(*a.seed_dev);
+      k0 = static_cast<uint32_t>(seed & 0xffffffffu);
+      k1 = static_cast<uint32_t>(seed >> 32);
+    }
+    key = philox_key(k0, k1);
+  }
   const uint32_t ctr_row =
       static_cast<uint32_t>(a.row_offset + row) * static_cast<uint32_t>(a.K);
 
@@ -309,10 +318,11 @@ static int check_common(const void* x, int dt, int64_t M, int64_t K, const int8_
 
 using namespace rk;
 
-extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
-                                int64_t sxk, const float* col_scale, int stochastic,
-                                uint64_t seed, int64_t row_offset, int8_t* q, int64_t ldq,
-                                float* scale, uint16_t* x_bf16, int64_t ld_xb, void* stream) {
+static int quantize_rows_entry(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                               int64_t sxk, const float* col_scale, int stochastic,
+                               uint64_t seed, const int64_t* seed_dev, int64_t row_offset,
+                               int8_t* q, int64_t ldq, float* scale, uint16_t* x_bf16,
+                               int64_t ld_xb, void* stream) {
   clear_error();
   if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
   if (x_bf16 && ld_xb < K) return fail(RK_ERR_ARG, "ld_xb < K");
@@ -326,6 +336,7 @@ extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K
   a.col_scale = col_scale;
   a.key0 = static_cast<uint32_t>(seed & 0xffffffffu);
   a.key1 = static_cast<uint32_t>(seed >> 32);
+  a.seed_dev = seed_dev;
   a.row_offset = row_offset;
   a.q = q;
   a.ldq = ldq;
@@ -335,6 +346,27 @@ extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K
   a.vec_ok = (rows_vec_ok(x, x_dtype, K, sxm, sxk) && (!col_scale || aligned16(col_scale))) ? 1 : 0;
   if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(x_dtype, a, as_stream(stream));
   return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
+}
+
+extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                                int64_t sxk, const float* col_scale, int stochastic,
+                                uint64_t seed, int64_t row_offset, int8_t* q, int64_t ldq,
+                                float* scale, uint16_t* x_bf16, int64_t ld_xb, void* stream) {
+  return quantize_rows_entry(x, x_dtype, M, K, sxm, sxk, col_scale, stochastic, seed, nullptr,
+                             row_offset, q, ldq, scale, x_bf16, ld_xb, stream);
+}
+
+extern "C" int rk_quantize_rows_devseed(const void* x, int x_dtype, int64_t M, int64_t K,
+                                        int64_t sxm, int64_t sxk, const float* col_scale,
+                                        const int64_t* seed, int64_t row_offset, int8_t* q,
+                                        int64_t ldq, float* scale, uint16_t* x_bf16,
+                                        int64_t ld_xb, void* stream) {
+  if (!seed) {
+    clear_error();
+    return fail(RK_ERR_ARG, "null device seed");
+  }
+  return quantize_rows_entry(x, x_dtype, M, K, sxm, sxk, col_scale, 1, 0, seed, row_offset, q,
+                             ldq, scale, x_bf16, ld_xb, stream);
 }
 
 extern "C" int rk_rmsnorm_quantize(const void* x, int x_dtype, int64_t ldx, const float* w,

@@ -1,5 +1,8 @@
 """ctypes binding of libratchet_hip.so (the C ABI declared in include/ratchet_hip.h).
 
+The training path reaches the library through the ``torch.ops.ratchet`` operators
+(``ops.py``); this binding serves the KV-cached decode step, whose kernels write into
+fixed buffers that a captured HIP graph replays, and callers that want the raw C ABI.
 The shared library is the only compute path of this package: if it is missing or
 fails to load, every GPU entry point raises. Tensors are passed as raw device
 pointers plus element strides; the stream is the caller's current torch stream.
@@ -29,6 +32,8 @@ _p = ctypes.c_void_p
 SIGNATURES: dict[str, list] = {
     "rk_quantize_rows": [_p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _u64, _i64, _p, _i64, _p,
                          _p, _i64, _p],
+    "rk_quantize_rows_devseed": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p,
+                                 _p, _i64, _p],
     "rk_philox_word0": [_u64, ctypes.c_uint32, _i64, _p, _p],
     "rk_int8_gemm_nt": [_p, _i64, _p, _i64, _p, _p, _p, _i32, _i64, _i64, _i64, _i64, _p],
     "rk_int8_gemm_packed": [_p, _i64, _p, _i64, _i32, _p, _p, _p, _i32, _i64, _i64, _i64, _i64,
@@ -136,10 +141,3 @@ def dtype_code(dtype: torch.dtype) -> int:
     if dtype == torch.bfloat16:
         return RK_BF16
     raise TypeError(f"unsupported dtype {dtype}; expected float32 or bfloat16")
-
-
-def require_rocm(*tensors: torch.Tensor, what: str) -> None:
-    """The int8 ratchet path runs only on a ROCm GPU (torch device type 'cuda')."""
-    for t in tensors:
-        if t is not None and not t.is_cuda:
-            raise RuntimeError(f"{what} requires CUDA (a ROCm GPU); the int8 path is GPU-only")

@@ -14,7 +14,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _native as nat
+from .ops import ratchet as _ops
 
 _SQRT_2_OVER_PI = 0.7978845608028654
 _MAX_NORM_K = 4096
@@ -56,14 +56,7 @@ def rmsnorm_backward(grad_y: Tensor, x: Tensor, w: Tensor, eps: float = 1e-5
     if k > _MAX_NORM_K:
         grad_x, grad_w = _rmsnorm_backward_torch(gy, x_flat, wf, eps)
     else:
-        grad_x = torch.empty((m, k), device=x.device, dtype=x_flat.dtype)
-        grad_w = torch.empty((k,), device=x.device, dtype=torch.float32)
-        parts = int(nat.load_library().rk_rmsnorm_backward_parts(m))
-        work = torch.empty((max(parts, 1), k), device=x.device, dtype=torch.float32)
-        nat.call("rk_rmsnorm_backward", gy.data_ptr(), nat.dtype_code(gy.dtype), gy.stride(0),
-                 x_flat.data_ptr(), nat.dtype_code(x_flat.dtype), x_flat.stride(0),
-                 wf.data_ptr(), float(eps), m, k, grad_x.data_ptr(), grad_x.stride(0),
-                 grad_w.data_ptr(), work.data_ptr(), work.numel(), nat.stream_handle(x.device))
+        grad_x, grad_w = _ops().rmsnorm_backward(gy, x_flat, wf, float(eps))
     return grad_x.to(x.dtype).reshape(x.shape), grad_w.to(w.dtype)
 
 
@@ -74,9 +67,5 @@ def gelu_backward(grad_y: Tensor, x: Tensor) -> Tensor:
     gy = _rows(_float_or_bf16(grad_y))
     if gy.shape != x_flat.shape:
         raise ValueError(f"grad_y {tuple(grad_y.shape)} does not match x {tuple(x.shape)}")
-    m, k = x_flat.shape
-    grad_x = torch.empty((m, k), device=x.device, dtype=x_flat.dtype)
-    nat.call("rk_gelu_backward", gy.data_ptr(), nat.dtype_code(gy.dtype), gy.stride(0),
-             x_flat.data_ptr(), nat.dtype_code(x_flat.dtype), x_flat.stride(0), m, k,
-             grad_x.data_ptr(), grad_x.stride(0), nat.stream_handle(x.device))
+    grad_x = _ops().gelu_backward(gy, x_flat)
     return grad_x.to(x.dtype).reshape(x.shape)

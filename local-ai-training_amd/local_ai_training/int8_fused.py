@@ -12,48 +12,28 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import _native as nat
+from .ops import ratchet as _ops
 
 
 def _rowwise(x: Tensor) -> Tensor:
     flat = x.flatten(0, -2)
-    if flat.stride(-1) != 1:
-        flat = flat.contiguous()
     if flat.dtype not in (torch.float32, torch.bfloat16):
         flat = flat.float()
     return flat
 
 
-def _ld(t: Tensor) -> int:
-    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
-
-
 def fused_rmsnorm_quantize(x: Tensor, weight: Tensor, eps: float = 1e-5) -> tuple[Tensor, Tensor]:
     if not x.is_cuda:
         raise RuntimeError("CUDA required (a ROCm GPU)")
-    original_shape = x.shape
-    flat = _rowwise(x)
-    m, k = flat.shape
-    out = torch.empty((m, k), device=x.device, dtype=torch.int8)
-    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
-    w = weight.detach().float().contiguous()
-    nat.call("rk_rmsnorm_quantize", flat.data_ptr(), nat.dtype_code(flat.dtype), _ld(flat),
-             w.data_ptr(), float(eps), out.data_ptr(), k, scale.data_ptr(), m, k,
-             nat.stream_handle(x.device))
-    return out.reshape(original_shape), scale.reshape(original_shape[:-1])
+    q, scale = _ops().rmsnorm_quantize(_rowwise(x), weight.detach().float(), float(eps))
+    return q.reshape(x.shape), scale.reshape(x.shape[:-1])
 
 
 def fused_gelu_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
     if not x.is_cuda:
         raise RuntimeError("CUDA required (a ROCm GPU)")
-    original_shape = x.shape
-    flat = _rowwise(x)
-    m, k = flat.shape
-    out = torch.empty((m, k), device=x.device, dtype=torch.int8)
-    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
-    nat.call("rk_gelu_quantize", flat.data_ptr(), nat.dtype_code(flat.dtype), _ld(flat),
-             out.data_ptr(), k, scale.data_ptr(), m, k, nat.stream_handle(x.device))
-    return out.reshape(original_shape), scale.reshape(original_shape[:-1])
+    q, scale = _ops().gelu_quantize(_rowwise(x))
+    return q.reshape(x.shape), scale.reshape(x.shape[:-1])
 
 
 def fused_transpose_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
@@ -62,15 +42,7 @@ def fused_transpose_quantize(x: Tensor) -> tuple[Tensor, Tensor]:
         raise RuntimeError("CUDA required (a ROCm GPU)")
     if x.dtype not in (torch.float32, torch.bfloat16):
         x = x.float()
-    batch_size, n_head, seq_len, head_dim = x.shape
-    m, channels = batch_size * seq_len, n_head * head_dim
-    out = torch.empty((m, channels), device=x.device, dtype=torch.int8)
-    scale = torch.empty((m,), device=x.device, dtype=torch.float32)
-    sb, sh, ss, sd = x.stride()
-    nat.call("rk_transpose_quantize", x.data_ptr(), nat.dtype_code(x.dtype), batch_size, n_head,
-             seq_len, head_dim, sb, sh, ss, sd, out.data_ptr(), channels, scale.data_ptr(),
-             nat.stream_handle(x.device))
-    return out, scale
+    return _ops().transpose_quantize(x)
 
 
 def _no_grad_outputs(ctx, int8_out: Tensor, scale_out: Tensor) -> None:

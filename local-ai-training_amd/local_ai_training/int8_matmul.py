@@ -1,28 +1,31 @@
-"""int8 GEMM and per-token quantizers on gfx950, backed by libratchet_hip.so.
+"""int8 GEMM and per-token quantizers on gfx950, dispatched through ``torch.ops.ratchet``.
 
 Drop-in for the reference module ``int8_matmul.py``: the public functions keep their
 names, argument meaning, return dtypes and exception types
-(``int8_matmul.py:251-343``). Compute runs only in the HIP library; CPU tensors are
+(``int8_matmul.py:251-343``). Each call runs one ``torch.ops.ratchet`` operator
+(``ops.py``), which calls one entry point of the gfx950 kernel library; CPU tensors are
 rejected with RuntimeError exactly where the reference rejects them.
 
-The ratchet layer uses the lower-level entry points below (``packed_int8_mm``,
-``int8_mm_nt``, ``quantize_rows_into``) which skip the host-synchronizing scale
-checks of the public ``scaled_int8_mm`` (``int8_matmul.py:305-309``).
+The ratchet layer uses the lower-level functions below (``packed_int8_mm``,
+``int8_mm_nt``, ``quantize_rows_sr``) which skip the host-synchronizing scale checks of the
+public ``scaled_int8_mm`` (``int8_matmul.py:305-309``).
+
+Stochastic-rounding seeds: the reference draws one seed per stochastic call from the CPU
+generator (``int8_matmul.py:200``), and so does every eager call here. Inside a HIP graph
+capture a seed drawn on the host would be frozen into the graph, so a capture must run under
+``CapturedSeeds.recording()``: each stochastic call then reads its seed from a device slot,
+and ``CapturedSeeds.refill()`` draws the slots' seeds from the CPU generator, in call order,
+before every replay.
 """
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import Tensor
 
-from . import _native as nat
-
-_TINY = torch.finfo(torch.float32).tiny
-
-
-def _ld(t: Tensor) -> int:
-    """Row stride of a 2-D operand with unit column stride."""
-    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+from .ops import ratchet as _ops
 
 
 def _sr_seed() -> int:
@@ -31,18 +34,89 @@ def _sr_seed() -> int:
     return int(torch.randint(0, 2**31 - 1, (1,)).item())
 
 
-def quantize_rows_into(values: Tensor, out: Tensor, scale: Tensor, *,
-                       col_scale: Tensor | None = None, stochastic: bool = False,
-                       seed: int = 0, row_offset: int = 0,
-                       bf16_out: Tensor | None = None) -> None:
-    """Row-quantize a 2-D float32/bfloat16 tensor (any strides) into preallocated outputs."""
-    m, k = values.shape
-    nat.call(
-        "rk_quantize_rows", values.data_ptr(), nat.dtype_code(values.dtype), m, k,
-        values.stride(0), values.stride(1), nat.ptr(col_scale), int(stochastic), seed,
-        row_offset, out.data_ptr(), _ld(out), scale.data_ptr(), nat.ptr(bf16_out),
-        _ld(bf16_out) if bf16_out is not None else 0, nat.stream_handle(values.device),
-    )
+class CapturedSeeds:
+    """Device-resident stochastic-rounding seeds for HIP-graph capture.
+
+    While ``recording()`` is active, every stochastic quantization that is being captured
+    takes the next int64 slot of ``slots`` (in call order) and its kernel reads the seed
+    from there when it runs. ``refill()`` draws one seed per used slot from the CPU
+    generator in slot order, exactly the draws an eager step makes in the same order, and
+    stores them; call it before each replay.
+    """
+
+    def __init__(self, device: torch.device | str, capacity: int = 512) -> None:
+        self.slots = torch.zeros(capacity, dtype=torch.int64, device=device)
+        self.used = 0
+        self.last_drawn: list[int] = []
+        # two pinned staging buffers, so a refill never waits for the replay before it and
+        # never overwrites staging memory whose copy is still queued
+        self._staging = [torch.empty(capacity, dtype=torch.int64, pin_memory=True)
+                         for _ in range(2)]
+        self._copied: list[torch.cuda.Event | None] = [None, None]
+        self._turn = 0
+
+    def take(self) -> Tensor:
+        if self.used >= self.slots.numel():
+            raise RuntimeError("CapturedSeeds: more stochastic calls than slots")
+        slot = self.slots[self.used:self.used + 1]
+        self.used += 1
+        return slot
+
+    @contextlib.contextmanager
+    def recording(self):
+        global _ACTIVE_SEEDS
+        previous, _ACTIVE_SEEDS = _ACTIVE_SEEDS, self
+        self.used = 0
+        try:
+            yield self
+        finally:
+            _ACTIVE_SEEDS = previous
+
+    def refill(self) -> list[int]:
+        """Draw this replay's seeds (host RNG, reference order) and queue their copy into
+        the device slots on the current stream, ahead of the replay that reads them."""
+        drawn = [_sr_seed() for _ in range(self.used)]
+        if drawn:
+            turn = self._turn
+            if self._copied[turn] is not None:
+                self._copied[turn].synchronize()
+            staging = self._staging[turn]
+            staging[:self.used] = torch.tensor(drawn, dtype=torch.int64)
+            self.slots[:self.used].copy_(staging[:self.used], non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+            self._copied[turn] = event
+            self._turn = 1 - turn
+        self.last_drawn = drawn
+        return drawn
+
+
+_ACTIVE_SEEDS: CapturedSeeds | None = None
+
+
+def sr_seed_args(device: torch.device) -> tuple[int, Tensor | None]:
+    """(seed, device slot) for one stochastic call: a host draw in eager mode, a slot of the
+    active CapturedSeeds under graph capture. Capturing without one raises, since the graph
+    would replay the capture-time seed forever."""
+    if device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        if _ACTIVE_SEEDS is None:
+            raise RuntimeError(
+                "stochastic rounding inside a HIP graph capture needs a seed source: "
+                "capture under CapturedSeeds.recording() and call refill() before replays"
+            )
+        return 0, _ACTIVE_SEEDS.take()
+    return _sr_seed(), None
+
+
+def quantize_rows_sr(values: Tensor, col_scale: Tensor | None = None, *,
+                     bf16_out: Tensor | None = None, row_offset: int = 0
+                     ) -> tuple[Tensor, Tensor, int | Tensor]:
+    """Stochastically rounded row quantization of values * col_scale (one Philox draw per
+    element); returns (q, scale, seed) where seed is the host seed drawn for this call or,
+    under graph capture, the device slot it reads. ``bf16_out`` receives bf16(values)."""
+    seed, slot = sr_seed_args(values.device)
+    q, s = _ops().quantize_rows(values, col_scale, True, seed, slot, row_offset, bf16_out)
+    return q, s, (slot if slot is not None else seed)
 
 
 def _quantize_rows_fused(values: Tensor, col_scale: Tensor | None = None, *,
@@ -51,17 +125,12 @@ def _quantize_rows_fused(values: Tensor, col_scale: Tensor | None = None, *,
     (``int8_matmul.py:225-239``), with Philox stochastic rounding when requested."""
     if values.ndim != 2:
         raise ValueError("row quantization requires a 2D tensor")
-    nat.require_rocm(values, what="row quantization")
     if values.dtype not in (torch.float32, torch.bfloat16):
         values = values.float()
-    m, k = values.shape
-    out = torch.empty((m, k), device=values.device, dtype=torch.int8)
-    scale = torch.empty((m,), device=values.device, dtype=torch.float32)
-    seed = _sr_seed() if stochastic else 0
-    if m and k:
-        quantize_rows_into(values, out, scale, col_scale=col_scale, stochastic=stochastic,
-                           seed=seed)
-    return out, scale
+    if stochastic:
+        q, s, _ = quantize_rows_sr(values, col_scale)
+        return q, s
+    return _ops().quantize_rows(values, col_scale)
 
 
 def _quantize_columns_fused(values: Tensor) -> tuple[Tensor, Tensor]:
@@ -102,38 +171,19 @@ def quantize_columns(values: Tensor) -> tuple[Tensor, Tensor]:
 
 
 def int8_mm_nt(a: Tensor, b_nk: Tensor, a_scale: Tensor, b_scale: Tensor | None,
-               out_dtype: torch.dtype = torch.bfloat16, out: Tensor | None = None) -> Tensor:
+               out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
     """C = bf16((A @ B^T) * a_scale[:, None] * b_scale[None, :]); A [M,K], B [N,K] int8.
 
     ``out_dtype`` float32 stores the bf16-rounded value widened (a fused `.float()`).
     No host synchronization.
     """
-    m, k = a.shape
-    n = b_nk.shape[0]
-    if out is None:
-        out = torch.empty((m, n), device=a.device, dtype=out_dtype)
-    nat.call(
-        "rk_int8_gemm_nt", a.data_ptr(), _ld(a), b_nk.data_ptr(), _ld(b_nk), a_scale.data_ptr(),
-        nat.ptr(b_scale), out.data_ptr(), nat.dtype_code(out.dtype), _ld(out), m, n, k,
-        nat.stream_handle(a.device),
-    )
-    return out
+    return _ops().int8_mm_nt(a, b_nk, a_scale, b_scale, out_dtype)
 
 
 def packed_int8_mm(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
-                   row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16,
-                   out: Tensor | None = None) -> Tensor:
+                   row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
     """C = bf16((A @ code^T) * a_scale * row_scale) with code decoded from packed [N, K]."""
-    m, k = a.shape
-    n = packed.shape[0]
-    if out is None:
-        out = torch.empty((m, n), device=a.device, dtype=out_dtype)
-    nat.call(
-        "rk_int8_gemm_packed", a.data_ptr(), _ld(a), packed.data_ptr(), _ld(packed), max_code,
-        a_scale.data_ptr(), nat.ptr(row_scale), out.data_ptr(), nat.dtype_code(out.dtype),
-        _ld(out), m, n, k, nat.stream_handle(a.device),
-    )
-    return out
+    return _ops().packed_mm(a, packed, max_code, a_scale, row_scale, out_dtype)
 
 
 def residual_supported(a: Tensor, packed: Tensor, residual: Tensor) -> bool:
@@ -155,16 +205,13 @@ def packed_int8_mm_residual(a: Tensor, packed: Tensor, max_code: int, a_scale: T
                             out: Tensor | None = None) -> Tensor:
     """C = residual + float32(bf16((A @ code^T) * a_scale * row_scale)) in one launch: the
     forward GEMM's float32 output with the residual add fused into its epilogue (the same
-    float32 add as adding afterwards)."""
-    m, k = a.shape
-    n = packed.shape[0]
+    float32 add as adding afterwards). ``out`` may be ``residual`` itself (accumulate in
+    place); the library rejects any other overlap of the two."""
     if out is None:
-        out = torch.empty((m, n), device=a.device, dtype=torch.float32)
-    nat.call(
-        "rk_int8_gemm_packed_residual", a.data_ptr(), _ld(a), packed.data_ptr(), _ld(packed),
-        max_code, a_scale.data_ptr(), nat.ptr(row_scale), residual.data_ptr(), _ld(residual),
-        out.data_ptr(), _ld(out), m, n, k, nat.stream_handle(a.device),
-    )
+        return _ops().packed_mm_residual(a, packed, max_code, a_scale, row_scale, residual)
+    if out is not residual:
+        out.copy_(residual)
+    _ops().packed_mm_accumulate(a, packed, max_code, a_scale, row_scale, out)
     return out
 
 
@@ -177,21 +224,12 @@ def packed_t_supported(a: Tensor, packed: Tensor) -> bool:
 
 
 def packed_int8_mm_t(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
-                     row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16,
-                     out: Tensor | None = None) -> Tensor:
+                     row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16
+                     ) -> Tensor:
     """C = bf16((A @ code) * a_scale * row_scale) with code = decode(packed) as the [K, N]
     operand (A [M, K] int8, packed [K, N]): the grad_input GEMM against the packed state,
     without an unpacked or transposed copy of the codes."""
-    m, k = a.shape
-    n = packed.shape[1]
-    if out is None:
-        out = torch.empty((m, n), device=a.device, dtype=out_dtype)
-    nat.call(
-        "rk_int8_gemm_packed_t", a.data_ptr(), _ld(a), packed.data_ptr(), _ld(packed),
-        max_code, a_scale.data_ptr(), nat.ptr(row_scale), out.data_ptr(),
-        nat.dtype_code(out.dtype), _ld(out), m, n, k, nat.stream_handle(a.device),
-    )
-    return out
+    return _ops().packed_mm_t(a, packed, max_code, a_scale, row_scale, out_dtype)
 
 
 def scaled_int8_mm(lhs: Tensor, rhs: Tensor, lhs_scale: Tensor, rhs_scale: Tensor) -> Tensor:
@@ -215,116 +253,80 @@ def scaled_int8_mm(lhs: Tensor, rhs: Tensor, lhs_scale: Tensor, rhs_scale: Tenso
             raise TypeError(f"{name} scale must be FP32 on the operand device")
         if not torch.isfinite(scale).all() or torch.any(scale <= 0):
             raise ValueError(f"{name} scale must be finite and positive")
-    a = lhs if lhs.stride(1) == 1 or k <= 1 else lhs.contiguous()
-    b_nk = rhs.t()
-    if b_nk.stride(1) != 1 and k > 1:
-        b_nk = b_nk.contiguous()
-    return int8_mm_nt(a, b_nk, lhs_scale.contiguous(), rhs_scale.contiguous())
+    # B as its [N, K] transposed view: a strided [K, N] operand needs no copy when its
+    # columns are contiguous; the operator copies otherwise
+    return int8_mm_nt(lhs, rhs.t(), lhs_scale.contiguous(), rhs_scale.contiguous())
+
+
+def _ld(t: Tensor) -> int:
+    """Row stride of a 2-D operand with unit column stride."""
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
 
 
 def unpack_transpose(packed: Tensor, max_code: int) -> Tensor:
     """codeT[k, n] = code[n, k] as a contiguous int8 [K, N] tensor."""
-    n, k = packed.shape
-    out = torch.empty((k, n), device=packed.device, dtype=torch.int8)
-    nat.call("rk_unpack_transpose", packed.data_ptr(), _ld(packed), max_code, out.data_ptr(),
-             _ld(out), n, k, nat.stream_handle(packed.device))
-    return out
+    return _ops().unpack_transpose(packed, max_code)
 
 
 def effective_bf16(packed: Tensor, max_code: int, scale: Tensor) -> Tensor:
     """bf16(code) * bf16(scale)[:, None] rounded to bf16, as ratchet.py:140 computes it."""
-    n, k = packed.shape
-    out = torch.empty((n, k), device=packed.device, dtype=torch.bfloat16)
-    nat.call("rk_effective_bf16", packed.data_ptr(), _ld(packed), max_code,
-             scale.float().contiguous().data_ptr(), out.data_ptr(), _ld(out), n, k,
-             nat.stream_handle(packed.device))
-    return out
+    return _ops().effective_bf16(packed, max_code, scale.float())
 
 
 def dequant_bf16(q: Tensor, s: Tensor) -> Tensor:
     """bf16(q) * bf16(s)[:, None] rounded to bf16, as ratchet.py:73-75 computes it."""
-    m, k = q.shape
-    out = torch.empty((m, k), device=q.device, dtype=torch.bfloat16)
-    nat.call("rk_dequant_bf16", q.data_ptr(), _ld(q), s.data_ptr(), out.data_ptr(), _ld(out),
-             m, k, nat.stream_handle(q.device))
-    return out
+    return _ops().dequant_bf16(q, s)
 
 
 def transpose_bf16(x: Tensor) -> Tensor:
-    """bf16 transposed copy of a 2-D float32/bfloat16 tensor (unit column stride)."""
-    if x.stride(-1) != 1:
-        x = x.contiguous()
-    m, n = x.shape
-    out = torch.empty((n, m), device=x.device, dtype=torch.bfloat16)
-    nat.call("rk_transpose_bf16", x.data_ptr(), nat.dtype_code(x.dtype), _ld(x), out.data_ptr(),
-             _ld(out), m, n, nat.stream_handle(x.device))
-    return out
+    """bf16 transposed copy of a 2-D float32/bfloat16 tensor."""
+    return _ops().transpose_bf16(x)
 
 
 def dequant_transpose_bf16(q: Tensor, s: Tensor) -> Tensor:
     """(bf16(q) * bf16(s)[:, None])^T as a contiguous bf16 [K, M] tensor."""
-    m, k = q.shape
-    out = torch.empty((k, m), device=q.device, dtype=torch.bfloat16)
-    nat.call("rk_dequant_transpose_bf16", q.data_ptr(), _ld(q), s.data_ptr(), out.data_ptr(),
-             _ld(out), m, k, nat.stream_handle(q.device))
-    return out
+    return _ops().dequant_transpose_bf16(q, s)
 
 
 def grad_weight_splits(m: int, n: int, k: int) -> int:
-    """Token-range split count rk_grad_weight_bf16 uses by default."""
-    return int(nat.load_library().rk_grad_weight_splits(m, n, k))
+    """Token-range split count the grad_weight kernels use by default."""
+    return int(_ops().grad_weight_splits(m, n, k))
 
 
 def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = None, *,
-                     out: Tensor | None = None, work: Tensor | None = None,
-                     reduce: bool = True) -> Tensor:
+                     work: Tensor | None = None, reduce: bool = True) -> Tensor:
     """Gw = bf16(bf16(grad)^T @ bf16(bf16(q) * bf16(s)[:, None])) as [N, K] bf16.
 
     The BF16 weight gradient of ratchet.py:148-163 computed straight from the saved int8
     activations (q [M, K], s [M]) and the upstream gradient grad [M, N] (float32 or
-    bfloat16), with no transposed copies. ``work`` (float32 [nsplit, N, K]) and ``out``
-    may be passed preallocated. ``reduce=False`` stops at the split partials and returns
-    ``work`` (for rk_ratchet_update_partials, which reduces them inside the update).
+    bfloat16), with no transposed copies. ``reduce=False`` stops at the float32 split
+    partials [nsplit, N, K], written to ``work`` (allocated when not given) and returned, for
+    the update that reduces them itself.
     """
-    m, n = grad.shape
-    k = q.shape[1]
-    if grad.stride(-1) != 1:
-        grad = grad.contiguous()
-    if q.stride(-1) != 1:
-        q = q.contiguous()
-    splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
-    if work is None:
-        work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
-    if out is None and reduce:
-        out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
-    nat.call("rk_grad_weight_bf16", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
-             q.data_ptr(), _ld(q), s.contiguous().data_ptr(), m, n, k, work.data_ptr(), splits,
-             nat.ptr(out) if reduce else None, _ld(out) if reduce else k,
-             nat.stream_handle(grad.device))
-    return out if reduce else work
+    if reduce:
+        return _ops().grad_weight(grad, q, s, nsplit or 0)
+    work = _partials_workspace(grad, q.shape[1], nsplit, work)
+    _ops().grad_weight_partials(grad, q, s, work)
+    return work
 
 
 def grad_weight_bf16_x(grad: Tensor, x: Tensor, nsplit: int | None = None, *,
-                       out: Tensor | None = None, work: Tensor | None = None,
-                       reduce: bool = True) -> Tensor:
+                       work: Tensor | None = None, reduce: bool = True) -> Tensor:
     """Gw = bf16(bf16(grad)^T @ bf16(x)) as [N, K] bf16, for activations x [M, K] given
     directly (float32 or bfloat16): the non-fused BF16 grad_weight of ratchet.py:159-163
     (``grad_out_tile.to(bf16) @ flat_inputs.to(bf16)``), or the fused one on a
-    dequantized copy (dequant_bf16). ``work`` / ``out`` / ``reduce`` as in
-    grad_weight_bf16."""
+    dequantized copy (dequant_bf16). ``work`` / ``reduce`` as in grad_weight_bf16."""
+    if reduce:
+        return _ops().grad_weight_x(grad, x, nsplit or 0)
+    work = _partials_workspace(grad, x.shape[1], nsplit, work)
+    _ops().grad_weight_partials_x(grad, x, work)
+    return work
+
+
+def _partials_workspace(grad: Tensor, k: int, nsplit: int | None,
+                        work: Tensor | None) -> Tensor:
+    if work is not None:
+        return work
     m, n = grad.shape
-    k = x.shape[1]
-    if grad.stride(-1) != 1:
-        grad = grad.contiguous()
-    if x.stride(-1) != 1:
-        x = x.contiguous()
-    splits = nsplit or (work.shape[0] if work is not None else grad_weight_splits(m, n, k))
-    if work is None:
-        work = torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)
-    if out is None and reduce:
-        out = torch.empty((n, k), device=grad.device, dtype=torch.bfloat16)
-    nat.call("rk_grad_weight_bf16_x", grad.data_ptr(), nat.dtype_code(grad.dtype), _ld(grad),
-             x.data_ptr(), nat.dtype_code(x.dtype), _ld(x), m, n, k, work.data_ptr(), splits,
-             nat.ptr(out) if reduce else None, _ld(out) if reduce else k,
-             nat.stream_handle(grad.device))
-    return out if reduce else work
+    splits = nsplit or grad_weight_splits(m, n, k)
+    return torch.empty((splits, n, k), device=grad.device, dtype=torch.float32)

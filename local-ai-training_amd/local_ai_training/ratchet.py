@@ -32,9 +32,7 @@ import torch
 from torch import Tensor, nn
 from torch.nn import functional as F
 
-from . import _native as nat
 from .int8_matmul import (
-    _sr_seed,
     dequant_bf16,
     dequant_transpose_bf16,
     effective_bf16,
@@ -46,11 +44,19 @@ from .int8_matmul import (
     packed_int8_mm_residual,
     packed_int8_mm_t,
     packed_t_supported,
-    quantize_rows_into,
+    quantize_rows_sr,
     residual_supported,
     transpose_bf16,
     unpack_transpose,
 )
+from .ops import ratchet as _ops
+
+
+def _require_gpu(*tensors: Tensor | None, what: str) -> None:
+    """The int8 ratchet path runs only on a ROCm GPU (torch device type 'cuda')."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{what} requires CUDA (a ROCm GPU); the int8 path is GPU-only")
 
 
 # ---------------------------------------------------------------------------
@@ -71,12 +77,7 @@ def pack_code_pressure(code: Tensor, pressure: Tensor, max_code: int) -> Tensor:
 def unpack_code_pressure(packed: Tensor, max_code: int) -> tuple[Tensor, Tensor]:
     """(code, pressure) int8 tensors from the packed bytes (``ratchet.py:195-199``)."""
     if packed.is_cuda:
-        flat = packed.contiguous()
-        code = torch.empty(flat.shape, dtype=torch.int8, device=flat.device)
-        pressure = torch.empty_like(code)
-        nat.call("rk_unpack", flat.data_ptr(), flat.numel(), max_code, code.data_ptr(),
-                 pressure.data_ptr(), nat.stream_handle(flat.device))
-        return code, pressure
+        return _ops().unpack(packed, max_code)
     value = packed.to(torch.int16)
     return ((value & 0x0F) - max_code).to(torch.int8), ((value >> 4) - 7).to(torch.int8)
 
@@ -167,13 +168,17 @@ def _split_residual_grad(ctx, grad_output: Tensor) -> tuple[Tensor, Tensor | Non
 
 
 def _fusable_residual(residual: Tensor | None, q: Tensor, packed: Tensor,
-                      out_dtype: torch.dtype | None) -> Tensor | None:
+                      out_dtype: torch.dtype | None,
+                      out_shape: tuple[int, ...]) -> Tensor | None:
     """The residual as a float32 [M, N] view when the forward GEMM can add it in its
     epilogue, else None. The kernel's float32 output is the bf16-rounded product widened,
-    so residual + product matches the separate add for a bfloat16 or float32 product."""
+    so residual + product matches the separate add for a bfloat16 or float32 product. Only
+    a residual of exactly the output's shape is fused: any other shape (one that would
+    broadcast, or an [M, N] residual beside a [B, T, N] output) takes the separate add,
+    which broadcasts or raises as the unfused expression does."""
     if residual is None or out_dtype not in (torch.float32, torch.bfloat16):
         return None
-    if residual.dtype != torch.float32:
+    if residual.dtype != torch.float32 or tuple(residual.shape) != tuple(out_shape):
         return None
     flat = residual.reshape(-1, residual.shape[-1])
     return flat if residual_supported(q, packed, flat) else None
@@ -205,7 +210,7 @@ class _RatchetMatmul(torch.autograd.Function):
                                   else None)
 
         if mode == "int8" and inputs_int8 is not None and inputs_scale is not None:
-            nat.require_rocm(inputs_int8, packed, what="int8 ratchet matmul")
+            _require_gpu(inputs_int8, packed, what="int8 ratchet matmul")
             q = inputs_int8.flatten(0, -2)
             s = inputs_scale.flatten(0, -1).float()
             if q.stride(-1) != 1:
@@ -223,21 +228,19 @@ class _RatchetMatmul(torch.autograd.Function):
                 effective = effective_bf16(packed, layer.max_code, scale.detach())
                 output = flat_inputs.to(torch.bfloat16) @ effective.t().contiguous()
             else:
-                nat.require_rocm(flat_inputs, packed, what="int8 ratchet matmul")
-                m, k = flat_inputs.shape
-                q = torch.empty((m, k), device=flat_inputs.device, dtype=torch.int8)
-                s = torch.empty((m,), device=flat_inputs.device, dtype=torch.float32)
+                _require_gpu(flat_inputs, packed, what="int8 ratchet matmul")
                 x = flat_inputs
                 if x.dtype not in (torch.float32, torch.bfloat16):
                     x = x.float()
-                quantize_rows_into(x, q, s)
+                q, s = _ops().quantize_rows(x)
                 output = None
         # the dtype of the product itself (residual + product is the function's output)
         ctx.y_dtype = requested or inputs.dtype
         ctx.residual_dtype = residual.dtype if residual is not None else None
         ctx.residual_shape = residual.shape if residual is not None else None
         if output is None:
-            flat_res = _fusable_residual(residual, q, packed, out_dtype)
+            flat_res = _fusable_residual(residual, q, packed, out_dtype,
+                                         (*input_shape[:-1], out_features))
             if flat_res is not None:
                 output = packed_int8_mm_residual(q, packed, layer.max_code, s,
                                                  scale.detach().float(), flat_res)
@@ -347,16 +350,15 @@ class _RatchetMatmul(torch.autograd.Function):
             g = flat_gradient
             if g.dtype not in (torch.float32, torch.bfloat16):
                 g = g.float()
-            grad_q = torch.empty((m, n), device=g.device, dtype=torch.int8)
-            grad_s = torch.empty((m,), device=g.device, dtype=torch.float32)
             if partials is None and g.dtype == torch.float32 \
                     and _grad_weight_supported(g, ctx.saved_tensors[0]):
                 # The same pass writes bf16(g), the grad_weight GEMM's gradient operand
                 # (grad_out_tile.to(bf16), ratchet.py:162), so that GEMM reads 2-byte
                 # values instead of converting float32 ones.
                 gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
-            quantize_rows_into(g, grad_q, grad_s, col_scale=scale_d.float().contiguous(),
-                               stochastic=True, seed=_sr_seed(), bf16_out=gradient_bf16)
+            # one seed per call from the CPU generator (a device slot under graph capture)
+            grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr(
+                g, scale_d.float().contiguous(), bf16_out=gradient_bf16)
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
             if packed_t_supported(grad_q, packed):
@@ -488,6 +490,9 @@ class DiscreteRatchetLinear(nn.Module):
         self.keep_weight_gradient = False
         self.last_weight_gradient: Tensor | None = None
         self._gw_workspace: Tensor | None = None
+        # the stochastic-rounding seed of the last int8 backward (the host draw, or the
+        # device slot it reads under graph capture)
+        self.last_sr_seed: int | Tensor | None = None
         self.int8_backward = int8_backward
         self.tile_size = tile_size
 
@@ -629,40 +634,25 @@ class DiscreteRatchetLinear(nn.Module):
         grad_weight GEMM's float32 split partials [nsplit, N, K], reduced inside the update
         with the same arithmetic. With ``keep_weight_gradient`` set, the bf16 gradient the
         update consumed is kept in ``last_weight_gradient``."""
-        nat.require_rocm(gradient, self.packed, what="the ratchet update")
+        _require_gpu(gradient, self.packed, what="the ratchet update")
         ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
         beta = self.rms_ema_beta
         # the launch also writes the mean of row_rms (the stats' gradient_rms_mean)
         rms_mean = (torch.empty((), device=self.packed.device, dtype=torch.float32)
                     if row_rms is not None else None)
-        stream = nat.stream_handle(self.packed.device)
+        rule = (self.max_code, self.pressure_threshold, self.bucket_low, self.bucket_high,
+                self.eps, ema, beta, counts, row_rms, grad_scale, nonfinite, rms_mean)
         if from_partials:
-            nsplit, rows, k = gradient.shape
             kept = None
             if self.keep_weight_gradient:
-                kept = torch.empty((rows, k), device=gradient.device, dtype=torch.bfloat16)
-            nat.call(
-                "rk_ratchet_update_partials", self.packed.data_ptr(), self.packed.stride(0),
-                gradient.data_ptr(), nsplit, rows, k, self.max_code, self.pressure_threshold,
-                self.bucket_low, self.bucket_high, self.eps, nat.ptr(ema), beta, 1.0 - beta,
-                counts.data_ptr(), nat.ptr(row_rms), nat.ptr(grad_scale), nat.ptr(nonfinite),
-                nat.ptr(rms_mean), nat.ptr(kept), k, stream,
-            )
+                kept = torch.empty(gradient.shape[1:], device=gradient.device,
+                                   dtype=torch.bfloat16)
+            _ops().update_from_partials(self.packed, gradient, *rule, kept)
             self.last_weight_gradient = kept
         else:
             if gradient.dtype not in (torch.float32, torch.bfloat16):
                 gradient = gradient.float()
-            if gradient.stride(-1) != 1:
-                gradient = gradient.contiguous()
-            rows, k = gradient.shape
-            nat.call(
-                "rk_ratchet_update_grad", self.packed.data_ptr(), self.packed.stride(0),
-                gradient.data_ptr(), nat.dtype_code(gradient.dtype),
-                gradient.stride(0) if rows > 1 else k, rows, k, self.max_code,
-                self.pressure_threshold, self.bucket_low, self.bucket_high, self.eps,
-                nat.ptr(ema), beta, 1.0 - beta, counts.data_ptr(), nat.ptr(row_rms),
-                nat.ptr(grad_scale), nat.ptr(nonfinite), nat.ptr(rms_mean), stream,
-            )
+            _ops().update_from_grad(self.packed, gradient, *rule)
             self.last_weight_gradient = gradient if self.keep_weight_gradient else None
         self._last_rms_mean = rms_mean
         self._generation += 1
@@ -685,18 +675,9 @@ class DiscreteRatchetLinear(nn.Module):
     @torch.no_grad()
     def _normalize(self, gradient: Tensor, row_start: int, row_end: int) -> Tensor:
         """z = g / (row rms + eps) (or the per-row EMA rms), ``ratchet.py:539-556``."""
-        nat.require_rocm(gradient, what="ratchet normalization")
-        g = gradient if gradient.dtype in (torch.float32, torch.bfloat16) else gradient.float()
-        g = g.contiguous()
-        rows, k = g.shape
-        z = torch.empty((rows, k), device=g.device, dtype=torch.float32)
-        ema = None
-        if self.rms_ema_beta > 0.0:
-            ema = self.rms_ema[row_start:row_end]
-        nat.call("rk_normalize_rows", g.data_ptr(), nat.dtype_code(g.dtype), k, rows, k,
-                 self.eps, nat.ptr(ema), self.rms_ema_beta, 1.0 - self.rms_ema_beta,
-                 z.data_ptr(), k, None, nat.stream_handle(g.device))
-        return z
+        _require_gpu(gradient, what="ratchet normalization")
+        ema = self.rms_ema[row_start:row_end] if self.rms_ema_beta > 0.0 else None
+        return _ops().normalize_rows(gradient, self.eps, ema, self.rms_ema_beta)
 
     @torch.no_grad()
     def apply_weight_gradient(self, gradient: Tensor, *,
@@ -731,13 +712,10 @@ class DiscreteRatchetLinear(nn.Module):
                 f"got {tuple(normalized.shape)}"
             )
         z = normalized.to(device=self.packed.device, dtype=torch.float32).contiguous()
-        nat.require_rocm(z, self.packed, what="the ratchet update")
+        _require_gpu(z, self.packed, what="the ratchet update")
         counts = torch.zeros(4, dtype=torch.int64, device=self.packed.device)
-        rows, k = z.shape
-        nat.call("rk_ratchet_update", self.packed.data_ptr(), self.packed.stride(0),
-                 z.data_ptr(), k, rows, k, self.max_code, self.pressure_threshold,
-                 self.bucket_low, self.bucket_high, counts.data_ptr(),
-                 nat.stream_handle(z.device))
+        _ops().update_from_z(self.packed, z, self.max_code, self.pressure_threshold,
+                             self.bucket_low, self.bucket_high, counts)
         self._generation += 1
         if validate:
             self._validate_state()
@@ -757,9 +735,8 @@ class DiscreteRatchetLinear(nn.Module):
         self._update_count += 1
         if self._update_count % self.pressure_leak_period != 0:
             return
-        nat.require_rocm(self.packed, what="the pressure leak")
-        nat.call("rk_pressure_leak", self.packed.data_ptr(), self.packed.numel(), self.max_code,
-                 nat.stream_handle(self.packed.device))
+        _require_gpu(self.packed, what="the pressure leak")
+        _ops().pressure_leak(self.packed, self.max_code)
 
     def check_finite_gradients(self) -> None:
         """Raise FloatingPointError if a fused update saw a NaN/Inf gradient (host sync)."""
@@ -817,12 +794,8 @@ class DiscreteRatchetLinear(nn.Module):
         self._effective_weight = None
 
     def _validate_state(self) -> None:
-        nat.require_rocm(self.packed, what="ratchet state validation")
-        flags = torch.zeros(3, dtype=torch.int32, device=self.packed.device)
-        scale = self.scale.detach().float().contiguous()
-        nat.call("rk_validate_state", self.packed.data_ptr(), self.packed.numel(),
-                 self.max_code, scale.data_ptr(), scale.numel(), flags.data_ptr(),
-                 nat.stream_handle(self.packed.device))
+        _require_gpu(self.packed, what="ratchet state validation")
+        flags = _ops().validate_state(self.packed, self.max_code, self.scale.detach())
         bad_code, bad_pressure, bad_scale = flags.tolist()
         if bad_code:
             raise RuntimeError("ratchet code escaped its allowed range")

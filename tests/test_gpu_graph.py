@@ -1,10 +1,12 @@
 """HIP-graph replay of the int8 ratchet-linear training step.
 
 The whole step (per-token quant, int8 forward, SR-quantized int8 grad_input, BF16
-grad_weight, fused update) is captured once and replayed. Every replay must equal an
-eager step of an identical layer on the same inputs: forward output, grad_input, packed
-state and move counts, bit for bit, with eager work and synchronizations between the
-replays.
+grad_weight, fused update) is captured once and replayed. The SR seed of each replay is
+read from a device slot that the host fills before the replay with the draw an eager step
+would make (CapturedSeeds), so replays take fresh random bits. Every replay must equal an
+eager step of an identical layer on the same inputs with the same host RNG state: forward
+output, grad_input, packed state and move counts, bit for bit, with eager work and
+synchronizations between the replays.
 """
 
 from __future__ import annotations
@@ -12,8 +14,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from local_ai_training import ratchet as ratchet_mod
-from local_ai_training.int8_matmul import quantize_rows_into
+from local_ai_training.int8_matmul import CapturedSeeds, quantize_rows, quantize_rows_colscaled
 from local_ai_training.ratchet import DiscreteRatchetLinear
 
 pytestmark = pytest.mark.gpu
@@ -25,55 +26,99 @@ def _layer(k: int, n: int, device) -> DiscreteRatchetLinear:
                                  fuse_backward_update=True).to(device).train()
 
 
-def test_graph_replays_match_eager_steps(cuda, monkeypatch):
-    # The SR seed is drawn on the host once per backward; inside a graph it is the value
-    # drawn at capture time, so both paths use one fixed seed here.
-    monkeypatch.setattr(ratchet_mod, "_sr_seed", lambda: 424242)
-    m, k, n = 1024, 512, 768
-    eager, graphed = _layer(k, n, cuda), _layer(k, n, cuda)
-    assert torch.equal(eager.packed, graphed.packed)
+def _setup(cuda, m=1024, k=512, n=768):
     gen = torch.Generator().manual_seed(3)
     x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(cuda)
     g = (torch.randn(m, n, generator=gen) * 1e-2).to(torch.bfloat16).to(cuda)
 
-    def make_inputs():
-        xi = x.clone().requires_grad_(True)
-        return xi, torch.empty(m, k, dtype=torch.int8, device=cuda), \
-            torch.empty(m, dtype=torch.float32, device=cuda)
-
-    xe, qe, se = make_inputs()
-    xg, qg, sg = make_inputs()
-    held = {}
-
-    def step(layer, xi, qi, si):
+    def step(layer, xi):
         xi.grad = None
-        quantize_rows_into(xi.detach(), qi, si)
+        qi, si = quantize_rows(xi.detach())
         out = layer(xi, inputs_int8=qi, inputs_scale=si)
         out.backward(g)
-        stats = layer.ratchet_update(validate=False)
-        return out, stats
+        return out, layer.ratchet_update(validate=False)
 
-    side = torch.cuda.Stream(device=cuda)
-    side.wait_stream(torch.cuda.current_stream(cuda))
+    return x, step
+
+
+def _capture(layer, xg, step, seeds, device):
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
         for _ in range(2):
-            step(graphed, xg, qg, sg)
-    torch.cuda.current_stream(cuda).wait_stream(side)
+            step(layer, xg)
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with seeds.recording(), torch.cuda.graph(graph):
+        held = step(layer, xg)
+    return graph, held
+
+
+def test_graph_replays_match_eager_steps_with_fresh_seeds(cuda):
+    m, k, n = 1024, 512, 768
+    x, step = _setup(cuda, m, k, n)
+    eager, graphed = _layer(k, n, cuda), _layer(k, n, cuda)
+    xe, xg = x.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    torch.manual_seed(11)
+    seeds = CapturedSeeds(cuda)
+    graph, (out_g, stats_g) = _capture(graphed, xg, step, seeds, cuda)
+    torch.manual_seed(11)
     for _ in range(2):
-        step(eager, xe, qe, se)
+        step(eager, xe)
     torch.cuda.synchronize()
     assert torch.equal(eager.packed, graphed.packed)
+    assert seeds.used == 1  # one stochastic rounding per step: the layer's grad_input
 
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        held["out"], held["stats"] = step(graphed, xg, qg, sg)
+    drawn = []
     for replay in range(3):
+        torch.manual_seed(100 + replay)
+        drawn += seeds.refill()
         graph.replay()
-        out_e, stats_e = step(eager, xe, qe, se)
+        torch.manual_seed(100 + replay)
+        out_e, stats_e = step(eager, xe)
         torch.cuda.synchronize()
-        assert torch.equal(held["out"].view(torch.int16), out_e.view(torch.int16)), replay
+        assert eager.last_sr_seed == drawn[-1], replay
+        assert torch.equal(out_g.view(torch.int16), out_e.view(torch.int16)), replay
         assert torch.equal(xg.grad.view(torch.int16), xe.grad.view(torch.int16)), replay
         assert torch.equal(graphed.packed, eager.packed), replay
-        got = [int(held["stats"].positive_moves), int(held["stats"].negative_moves)]
+        got = [int(stats_g.positive_moves), int(stats_g.negative_moves)]
         want = [int(stats_e.positive_moves), int(stats_e.negative_moves)]
         assert got == want, replay
+    assert len(set(drawn)) == 3
+
+
+def test_replays_with_different_seeds_round_differently(cuda):
+    # Same state, same inputs, two replays: the SR bits follow the slot's seed (equal seeds
+    # give equal grad_input, different seeds a different one).
+    m, k, n = 512, 256, 384
+    x, step = _setup(cuda, m, k, n)
+    layer = _layer(k, n, cuda)
+    xg = x.clone().requires_grad_(True)
+    seeds = CapturedSeeds(cuda)
+    graph, _ = _capture(layer, xg, step, seeds, cuda)
+    start = layer.packed.clone()
+
+    def replay_with(seed_state: int) -> torch.Tensor:
+        layer.packed.copy_(start)
+        torch.manual_seed(seed_state)
+        seeds.refill()
+        graph.replay()
+        torch.cuda.synchronize()
+        return xg.grad.clone()
+
+    a, b, c = replay_with(1), replay_with(2), replay_with(1)
+    assert torch.equal(a.view(torch.int16), c.view(torch.int16))
+    assert not torch.equal(a, b)
+
+
+def test_stochastic_rounding_in_a_capture_needs_a_seed_source(cuda):
+    # A host seed drawn at capture time would be replayed forever: the call raises before
+    # it launches anything (the capture then ends empty).
+    g = torch.randn(64, 128, device=cuda)
+    col = torch.ones(128, device=cuda)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="seed source"):
+        with torch.cuda.graph(graph):
+            quantize_rows_colscaled(g, col, stochastic=True)
+    torch.cuda.synchronize()

@@ -14,6 +14,7 @@ import torch
 
 from helpers import synthetic_state
 from local_ai_training import _native as nat
+from local_ai_training.ops import ratchet as ops
 from local_ai_training.int8_matmul import (
     dequant_bf16,
     dequant_transpose_bf16,
@@ -25,7 +26,6 @@ from local_ai_training.int8_matmul import (
     quantize_columns,
     quantize_rows,
     quantize_rows_colscaled,
-    quantize_rows_into,
     scaled_int8_mm,
     transpose_bf16,
     unpack_transpose,
@@ -93,9 +93,7 @@ def test_stochastic_rounding_bit_exact_given_seed(cuda, shape, dtype):
     col = torch.rand(shape[1], generator=gen(32)) * 0.08 + 0.02
     gd = g.to(cuda)
     for seed in (0, 1, 123456789, 2**31 - 2):
-        q = torch.empty(shape, dtype=torch.int8, device=cuda)
-        s = torch.empty(shape[0], dtype=torch.float32, device=cuda)
-        quantize_rows_into(gd, q, s, col_scale=col.to(cuda), stochastic=True, seed=seed)
+        q, s = ops().quantize_rows(gd, col.to(cuda), True, seed)
         q_ref, s_ref = oquant.quantize_rows_sr(g.float().numpy(), col.numpy(), seed)
         assert np.array_equal(q.cpu().numpy(), q_ref), f"seed {seed}"
         assert np.array_equal(f32bits(s), f32bits(s_ref))
@@ -157,9 +155,7 @@ def test_quantize_rows_near_half_integer_quotients(cuda, rows, cols):
 def test_stochastic_rounding_near_integer_sums(cuda, rows, cols):
     seed = 4242
     x = near_boundary_rows(rows, cols, 5, seed)
-    q = torch.empty(rows, cols, dtype=torch.int8, device=cuda)
-    s = torch.empty(rows, dtype=torch.float32, device=cuda)
-    quantize_rows_into(torch.from_numpy(x).to(cuda), q, s, stochastic=True, seed=seed)
+    q, s = ops().quantize_rows(torch.from_numpy(x).to(cuda), None, True, seed)
     q_ref, s_ref = oquant.quantize_rows_sr(x, None, seed)
     assert np.array_equal(f32bits(s), f32bits(s_ref))
     assert np.array_equal(q.cpu().numpy(), q_ref)
@@ -184,11 +180,8 @@ def test_sr_quant_full_op_shape_sampled_rows_and_bf16_side_output(cuda):
     g = (torch.randn(m, n, generator=gen(51)) * 1e-2).to(torch.bfloat16)
     col = torch.rand(n, generator=gen(52)) * 0.08 + 0.02
     gd = g.to(cuda)
-    q = torch.empty(m, n, dtype=torch.int8, device=cuda)
-    s = torch.empty(m, dtype=torch.float32, device=cuda)
     side = torch.empty(m, n, dtype=torch.bfloat16, device=cuda)
-    quantize_rows_into(gd, q, s, col_scale=col.to(cuda), stochastic=True, seed=987654,
-                       bf16_out=side)
+    q, s = ops().quantize_rows(gd, col.to(cuda), True, 987654, x_bf16=side)
     assert torch.equal(side, gd)
     qc, sc = q.cpu().numpy(), s.cpu().numpy()
     rows = np.random.default_rng(0).choice(m, 256, replace=False)
@@ -200,10 +193,8 @@ def test_sr_quant_full_op_shape_sampled_rows_and_bf16_side_output(cuda):
 
 def test_f32_gradient_side_output_is_rne_bf16(cuda):
     g = torch.randn(64, 512, generator=gen(53))
-    q = torch.empty(64, 512, dtype=torch.int8, device=cuda)
-    s = torch.empty(64, dtype=torch.float32, device=cuda)
     side = torch.empty(64, 512, dtype=torch.bfloat16, device=cuda)
-    quantize_rows_into(g.to(cuda), q, s, stochastic=True, seed=3, bf16_out=side)
+    ops().quantize_rows(g.to(cuda), None, True, 3, x_bf16=side)
     assert np.array_equal(bits16(side), f32_to_bf16_bits(g.numpy()))
 
 
@@ -272,6 +263,24 @@ def test_packed_gemm_residual_equals_gemm_then_add(cuda, m, n, k):
     inplace = r.clone()
     packed_int8_mm_residual(q, pd, 2, ls, rs, inplace, out=inplace)
     assert torch.equal(inplace.view(torch.int32), want.view(torch.int32))
+
+
+def test_residual_gemm_rejects_partial_overlap_of_residual_and_output(cuda):
+    # R == C (same rows, same stride) is the in-place form; an R shifted by one row inside
+    # C's storage would let one block overwrite rows another block still reads.
+    m, n, k = 64, 128, 128
+    packed, scale = synthetic_state(n, k, 2, seed=7)
+    q = torch.randint(-127, 128, (m, k), generator=gen(7), dtype=torch.int8).to(cuda)
+    ls = torch.full((m,), 1e-3, device=cuda)
+    pd, rs = torch.from_numpy(packed).to(cuda), torch.from_numpy(scale).to(cuda)
+    buf = torch.zeros(m + 1, n, device=cuda)
+    args = (q.data_ptr(), k, pd.data_ptr(), k, 2, ls.data_ptr(), rs.data_ptr())
+    with pytest.raises(nat.NativeError, match="overlaps"):
+        nat.call("rk_int8_gemm_packed_residual", *args, buf[1:].data_ptr(), n,
+                 buf[:m].data_ptr(), n, m, n, k, nat.stream_handle(cuda))
+    with pytest.raises(nat.NativeError, match="overlaps"):  # same start, other stride
+        nat.call("rk_int8_gemm_packed_residual", *args, buf.data_ptr(), n // 2,
+                 buf.data_ptr(), n, m, n, k, nat.stream_handle(cuda))
 
 
 # Decode-sized M (<= 16 tokens) takes the small-M kernel: 1B-model layer shapes (qkv 6144 x
@@ -394,7 +403,7 @@ def test_packed_t_gemm_strided_rows_and_unsupported_shapes(cuda):
     assert np.array_equal(f32bits(out), (ref.astype(np.uint32) << 16))
     ragged = torch.from_numpy(synthetic_state(100, 96, mc, seed=6)[0]).to(cuda)  # K % 64
     assert not packed_t_supported(gq.to(cuda)[:, :100], ragged)
-    with pytest.raises(nat.NativeError, match="K % 64"):
+    with pytest.raises(RuntimeError, match="K % 64"):
         packed_int8_mm_t(gq.to(cuda)[:, :100].contiguous(), ragged, mc, gs.to(cuda), None)
 
 
@@ -828,5 +837,5 @@ def test_grad_weight_rejects_unaligned_shapes(cuda):
     g = torch.randn(64, 12, device=cuda)
     q = torch.zeros(64, 16, dtype=torch.int8, device=cuda)
     s = torch.ones(64, device=cuda)
-    with pytest.raises(nat.NativeError, match="N % 8 == 0"):
+    with pytest.raises(RuntimeError, match="N % 8 == 0"):
         grad_weight_bf16(g, q, s)

@@ -1,10 +1,9 @@
-"""Host-side behaviour that needs no GPU: drop-in errors, construction, configs."""
+"""Host-side behaviour that needs no GPU: drop-in errors, construction, model configs."""
 
 import pytest
 import torch
 from torch import nn
 
-from local_ai_training.config import ExperimentConfig
 from local_ai_training.int8_matmul import (
     quantize_columns,
     quantize_rows,
@@ -127,22 +126,3 @@ def test_model_config_validation():
         RatchetGPT(tiny_config(), max_code=2)(torch.zeros((1, 9), dtype=torch.long))
     assert ModelConfig(vocab_size=8, n_embd=2048, n_head=16, ffn_hidden=5632).hidden_size == 5632
     assert ModelConfig(vocab_size=8, n_embd=64, n_head=4).hidden_size == 256
-
-
-def test_experiment_config_toml_round_trip(tmp_path):
-    path = tmp_path / "c.toml"
-    path.write_text(
-        "[model]\nn_embd = 512\nn_layer = 8\nn_head = 8\nblock_size = 512\n"
-        "[ratchet]\ncompile_update = true\n"
-        "[training]\nbatch_size = 32\nsteps = 10\nmatmul_mode = \"int8\"\nint8_backward = true\n"
-    )
-    cfg = ExperimentConfig.from_toml(path)
-    assert cfg.matmul_mode == "int8" and cfg.int8_backward and cfg.compile_update
-    mc = cfg.model_config(vocab_size=8192)
-    assert mc.n_embd == 512 and mc.matmul_mode == "int8" and mc.int8_backward
-    (tmp_path / "bad.toml").write_text("[training]\nbogus = 1\n")
-    with pytest.raises(ValueError, match="unknown keys"):
-        ExperimentConfig.from_toml(tmp_path / "bad.toml")
-    (tmp_path / "bad2.toml").write_text("[training]\nsteps = 1\ntarget_tokens = 5\n")
-    with pytest.raises(ValueError, match="mutually exclusive"):
-        ExperimentConfig.from_toml(tmp_path / "bad2.toml")
