@@ -443,36 +443,43 @@ TRAIN_1B = dict(model="ratchet-gpt-1B", vocab=8192, block=1024, batch=8, n_layer
                 n_embd=2048, ffn=5632, max_code=3, codes="septenary")
 
 
-def train_bench(shape: dict, steps: int, warmup: int, device):
-    """Training steps/s of a ratchet transformer (int8 + int8_backward, fused update every
-    step, AdamW on the float parameters, Zipf(1.1) token ids), sustained: syncs only at
-    both ends of the timed steps."""
+def train_bench(shape: dict, steps: int, warmup: int, device, graph: bool):
+    """Training tokens/s of a ratchet transformer (int8 + int8_backward, fused update every
+    step, AdamW on the float parameters, Zipf(1.1) token ids), sustained: syncs only at both
+    ends of the timed steps. ``graph``: the step is captured once as a HIP graph and
+    replayed (training.CapturedTrainingStep: SR seeds drawn on the host per replay, in the
+    eager order; capturable AdamW); otherwise the eager step (training.training_step)."""
     import numpy as np
     import torch
 
     from local_ai_training.model import ModelConfig, build_seeded_model
+    from local_ai_training.training import CapturedTrainingStep, training_step
 
     vocab, block, batch = shape["vocab"], shape["block"], shape["batch"]
     config = ModelConfig(vocab_size=vocab, block_size=block, n_layer=shape["n_layer"],
                          n_head=shape["n_head"], n_embd=shape["n_embd"],
                          ffn_hidden=shape["ffn"], matmul_mode="int8", int8_backward=True)
     model = build_seeded_model(config, max_code=shape["max_code"], seed=1337).to(device).train()
-    optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.0)
+    # capturable (device-side step count) in both modes: the same AdamW arithmetic, so the
+    # eager and graph runs of the same steps end at the same loss
+    optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.0,
+                                  capturable=True)
     rng = np.random.default_rng(1337)
     ids = (rng.zipf(1.1, size=batch * (block + 1)) - 1) % vocab  # Zipf(s=1.1) token ids
     tokens = torch.from_numpy(ids.astype(np.uint16).astype(np.int64)).view(batch, block + 1)
     tokens = tokens.to(device)
     inputs, targets = tokens[:, :block], tokens[:, 1:]
-
-    def step():
-        optimizer.zero_grad(set_to_none=True)
-        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-            _, loss = model(inputs, targets)
-        loss.backward()
-        model.ratchet_update(validate=False)
-        optimizer.step()
-        return loss
-
+    # the SR seeds come from the CPU generator (one draw per int8-backward layer and step):
+    # seed it, so the run (and its loss) does not depend on what ran before
+    torch.manual_seed(1337)
+    if graph:
+        # the capture's own warm-up steps count toward `warmup`
+        step = CapturedTrainingStep(model, optimizer, inputs, targets, warmup_steps=2)
+        warmup = max(warmup - 2, 0)
+    else:
+        def step():
+            return training_step(model, optimizer, inputs, targets, check_finite=False,
+                                 autocast_cache=False)[0]
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -481,14 +488,15 @@ def train_bench(shape: dict, steps: int, warmup: int, device):
         loss = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    del model, optimizer
+    final_loss = float(loss.detach())
+    del model, optimizer, step
     torch.cuda.empty_cache()
-    return batch * block * steps / elapsed, elapsed / steps, float(loss.detach())
+    return batch * block * steps / elapsed, elapsed / steps, final_loss
 
 
-def model_bench(args, device):
-    """25M ratchet transformer training steps/s."""
-    return train_bench(TRAIN_25M, args.model_steps, args.model_warmup, device)
+def model_bench(args, device, graph: bool):
+    """25M ratchet transformer training tokens/s."""
+    return train_bench(TRAIN_25M, args.model_steps, args.model_warmup, device, graph)
 
 
 def update_1b_bench(device, iters: int) -> dict:
@@ -871,13 +879,21 @@ def main() -> int:
     }
     if not args.no_model:
         log(f"model bench: 25M int8, warmup={args.model_warmup} steps={args.model_steps}")
-        tok_s, step_m, loss = model_bench(args, device)
-        log(f"model {step_m * 1e3:.2f} ms/step -> {tok_s:.0f} tok/s (loss {loss:.3f})")
+        tok_s, step_m, loss = model_bench(args, device, graph=True)
+        log(f"model (HIP graph) {step_m * 1e3:.2f} ms/step -> {tok_s:.0f} tok/s "
+            f"(loss {loss:.4f})")
+        tok_e, step_e, loss_e = model_bench(args, device, graph=False)
+        log(f"model (eager) {step_e * 1e3:.2f} ms/step -> {tok_e:.0f} tok/s (loss {loss_e:.4f})")
         result["train_tokens_per_s"] = round(tok_s, 1)
         result["train_ms_per_step"] = round(step_m * 1e3, 3)
+        result["train_step_mode"] = "hip_graph"
+        result["train_eager"] = {"tokens_per_s": round(tok_e, 1),
+                                 "ms_per_step": round(step_e * 1e3, 3)}
+        result["train_loss"] = {"hip_graph": round(loss, 5), "eager": round(loss_e, 5)}
         result["train_config"] = {"model": "ratchet-gpt-25M", "n_layer": 8, "n_embd": 512,
                                   "n_head": 8, "ffn": 2048, "vocab": 8192, "seq_len": 512,
-                                  "batch": 32, "matmul_mode": "int8", "int8_backward": True}
+                                  "batch": 32, "matmul_mode": "int8", "int8_backward": True,
+                                  "steps": args.model_steps, "warmup": args.model_warmup}
     if not args.no_update_1b:
         log("update bench: the fused update of every 1B layer from split partials")
         result["update_1b"] = update_1b_bench(device, 5)
@@ -885,10 +901,17 @@ def main() -> int:
     if not args.no_train_1b:
         log(f"1B training bench: warmup={args.train_1b_warmup} steps={args.train_1b_steps}")
         tok_s, step_1b, loss_1b = train_bench(TRAIN_1B, args.train_1b_steps,
-                                              args.train_1b_warmup, device)
-        log(f"1B model {step_1b * 1e3:.1f} ms/step -> {tok_s:.0f} tok/s (loss {loss_1b:.3f})")
+                                              args.train_1b_warmup, device, graph=True)
+        log(f"1B model (HIP graph) {step_1b * 1e3:.1f} ms/step -> {tok_s:.0f} tok/s "
+            f"(loss {loss_1b:.3f})")
+        tok_e, step_e, loss_e = train_bench(TRAIN_1B, args.train_1b_steps,
+                                            args.train_1b_warmup, device, graph=False)
+        log(f"1B model (eager) {step_e * 1e3:.1f} ms/step -> {tok_e:.0f} tok/s")
         result["train_1b"] = {"tokens_per_s": round(tok_s, 1),
-                              "ms_per_step": round(step_1b * 1e3, 2),
+                              "ms_per_step": round(step_1b * 1e3, 2), "step_mode": "hip_graph",
+                              "eager": {"tokens_per_s": round(tok_e, 1),
+                                        "ms_per_step": round(step_e * 1e3, 2)},
+                              "loss": {"hip_graph": round(loss_1b, 4), "eager": round(loss_e, 4)},
                               "config": {k: TRAIN_1B[k] for k in TRAIN_1B},
                               "matmul_mode": "int8", "int8_backward": True}
     if not args.no_decode:

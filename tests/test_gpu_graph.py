@@ -111,6 +111,46 @@ def test_replays_with_different_seeds_round_differently(cuda):
     assert not torch.equal(a, b)
 
 
+def test_captured_training_step_equals_eager_steps(cuda):
+    # The model's whole training step (autocast forward, backward with the fused updates,
+    # ratchet_update, capturable AdamW) replayed as a graph: losses, every ratchet state and
+    # every float parameter equal an eager run of the same steps with the same host RNG.
+    from local_ai_training.model import ModelConfig, build_seeded_model
+    from local_ai_training.training import CapturedTrainingStep, training_step
+
+    config = ModelConfig(vocab_size=256, block_size=64, n_layer=2, n_head=4, n_embd=128,
+                         matmul_mode="int8", int8_backward=True)
+    gen = torch.Generator().manual_seed(4)
+    batches = [torch.randint(0, 256, (8, 65), generator=gen).to(cuda) for _ in range(6)]
+    runs = []
+    for graphed in (False, True):
+        model = build_seeded_model(config, max_code=2, seed=21).to(cuda).train()
+        optimizer = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.0,
+                                      capturable=True)
+        torch.manual_seed(8)
+        losses = []
+        if graphed:
+            step = CapturedTrainingStep(model, optimizer, batches[0][:, :-1],
+                                        batches[0][:, 1:], warmup_steps=2)
+            losses += [None, None]  # the two warm-up steps ran batch 0 eagerly
+            for batch in batches[2:]:
+                losses.append(float(step(batch[:, :-1], batch[:, 1:])))
+        else:
+            for index, batch in enumerate(batches):
+                data = batches[0] if index < 2 else batch
+                loss, _ = training_step(model, optimizer, data[:, :-1], data[:, 1:],
+                                        autocast_cache=False)
+                losses.append(float(loss))
+            losses[:2] = [None, None]
+        torch.cuda.synchronize()
+        states = [m.packed.clone() for m in model.modules() if isinstance(m, DiscreteRatchetLinear)]
+        runs.append((losses, states, [p.detach().clone() for p in model.parameters()]))
+    (le, se, pe), (lg, sg, pg) = runs
+    assert le == lg
+    assert all(torch.equal(a, b) for a, b in zip(se, sg))
+    assert all(torch.equal(a, b) for a, b in zip(pe, pg))
+
+
 def test_stochastic_rounding_in_a_capture_needs_a_seed_source(cuda):
     # A host seed drawn at capture time would be replayed forever: the call raises before
     # it launches anything (the capture then ends empty).
