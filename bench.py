@@ -83,6 +83,15 @@ def parse_args() -> argparse.Namespace:
                     help="run each op-step stage and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the HBM traffic summary from two rocprofv3 counter CSVs")
+    ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
+                    help="per-stage SQ/GRBM counter averages of --pmc-probe runs (rocprofv3 "
+                         "counter_collection CSVs), with MFMA and VALU busy fractions")
+    ap.add_argument("--train-only", choices=["25m", "1b"],
+                    help="run only the graph-replayed training step of one model, --steps "
+                         "timed steps after --warmup (for kernel traces)")
+    ap.add_argument("--step-summary", nargs=2, metavar=("KERNEL_TRACE_CSV", "STEPS"),
+                    help="bucket a rocprofv3 kernel trace of --train-only into kernel classes "
+                         "per training step")
     return ap.parse_args()
 
 
@@ -437,6 +446,147 @@ def roofline_entry(kernels: dict) -> dict:
             "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
 
 
+# ---------------------------------------------------------------------------
+# Per-stage SQ/GRBM counters of the op step (`--pmc-probe` under rocprofv3 --pmc, one run
+# per counter group), averaged per launch. Derived figures use AMD's own definitions of
+# the derived metrics rocprofv3 lists for gfx950:
+#   MfmaUtil        = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE * SIMDs)
+#   VALUBusy        = SQ_ACTIVE_INST_VALU / (CUs * GRBM_GUI_ACTIVE)
+#   LDSBankConflict = SQ_LDS_BANK_CONFLICT / (CUs * GRBM_GUI_ACTIVE)
+#   wait fraction   = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (both in wave quad-cycles)
+# GRBM_GUI_ACTIVE is taken per XCD (the CSV sums its 8 XCD instances; the metric takes the
+# maximum, which for one kernel on the whole chip is the sum / 8).
+# ---------------------------------------------------------------------------
+MI355X_CUS, MI355X_SIMDS, MI355X_XCDS = 256, 1024, 8
+
+
+def _counter_rows(csv_paths: list[str]) -> dict:
+    """{dispatch id: {"name": kernel, counter: value, ...}} over every CSV."""
+    import csv
+
+    out: dict = {}
+    for i, path in enumerate(csv_paths):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                key = (i, int(r["Dispatch_Id"]))
+                d = out.setdefault(key, {"name": r["Kernel_Name"]})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def counter_summary(csv_paths: list[str]) -> str:
+    rows = _counter_rows(csv_paths)
+    per_stage: dict = {s: {} for s in STAGE_KERNELS}
+    for d in rows.values():
+        for stage, frags in STAGE_KERNELS.items():
+            if any(f in d["name"] for f in frags):
+                for c, v in d.items():
+                    if c != "name":
+                        per_stage[stage].setdefault(c, []).append(v)
+    lines = ["| stage | counter | mean per launch | launches |", "|---|---|---:|---:|"]
+    derived = {}
+    for stage, cs in per_stage.items():
+        mean = {c: sum(v) / len(v) for c, v in cs.items()}
+        for c in sorted(mean):
+            lines.append(f"| {stage} | {c} | {mean[c]:.4g} | {len(cs[c])} |")
+        grbm = mean.get("GRBM_GUI_ACTIVE")
+        d = {}
+        if grbm:
+            cyc = grbm / MI355X_XCDS
+            d["gpu_cycles"] = round(cyc)
+            d["us_at_2.4GHz"] = round(cyc / 2.4e3, 2)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in mean:
+                d["MfmaUtil"] = round(mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * MI355X_SIMDS), 4)
+            if "SQ_ACTIVE_INST_VALU" in mean:
+                d["VALUBusy"] = round(mean["SQ_ACTIVE_INST_VALU"] / (cyc * MI355X_CUS), 4)
+            if "SQ_LDS_BANK_CONFLICT" in mean:
+                d["LDSBankConflict"] = round(mean["SQ_LDS_BANK_CONFLICT"] / (cyc * MI355X_CUS), 4)
+        if mean.get("SQ_WAVE_CYCLES"):
+            if "SQ_WAIT_INST_ANY" in mean:
+                d["wait_inst_frac"] = round(mean["SQ_WAIT_INST_ANY"] / mean["SQ_WAVE_CYCLES"], 4)
+            if "SQ_WAIT_ANY" in mean:
+                d["wait_any_frac"] = round(mean["SQ_WAIT_ANY"] / mean["SQ_WAVE_CYCLES"], 4)
+        if mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8"):
+            d["mfma_i8_ops"] = mean["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
+        if mean.get("SQ_INSTS_VALU_MFMA_MOPS_BF16"):
+            d["mfma_bf16_flops"] = mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512
+        if mean.get("SQ_WAVES"):
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
+                      "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR"):
+                if c in mean:
+                    d[c.replace("SQ_INSTS_", "") + "_per_wave"] = round(mean[c] / mean["SQ_WAVES"], 1)
+        derived[stage] = d
+    lines += ["", "Derived (per launch):", "", "```json", json.dumps(derived, indent=1), "```"]
+    return "\n".join(lines)
+
+
+# ---------------------------------------------------------------------------
+# Per-step kernel classes of a training step (the reference buckets its step the same way
+# in scripts/int8_step_profile.py:26-38), from a rocprofv3 --kernel-trace CSV of
+# `--train-only`: the timed steps are the last STEPS repeats of the replayed kernel
+# sequence.
+# ---------------------------------------------------------------------------
+STEP_CLASSES = [
+    ("int8 GEMM forward (W8A8, packed codes)", r"int8_gemm_(m32|nt)_kernel<[01],|int8_gemv"),
+    ("int8 GEMM grad_input (packed codes, in place)", r"int8_gemm_m32_kernel<2,"),
+    ("SR gradient quant (Philox)", r"quant_rows_kernel<\d+, \d+, true"),
+    ("activation quant prologues (RMSNorm/GELU/transpose)", r"quant_rows_kernel<\d+, \d+, false"),
+    ("bf16 grad_weight (MFMA)", r"grad_weight_(partial|reduce)_kernel"),
+    ("fused ratchet update", r"ratchet_update|row_rms_mean"),
+    ("prologue backward (RMSNorm/GELU)", r"rmsnorm_bwd|rmsnorm_gw_reduce|gelu_bwd"),
+    ("attention (SDPA)", r"attn|fmha|flash"),
+    ("bf16 GEMM (hipBLASLt, lm_head grad_input)", r"Cijk_|gemm"),
+    ("effective bf16 weights", r"effective_bf16"),
+    ("optimizer (AdamW)", r"multi_tensor|adam"),
+    ("loss / reductions", r"reduce|softmax|nll|cross_entropy"),
+    ("elementwise / cast / copy", r"elementwise|copy|cast|fill|vectorized|index|embedding"),
+]
+
+
+def step_summary(trace_csv: str, steps: int) -> str:
+    import csv
+    import re
+
+    recs = []
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            recs.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    recs.sort()
+    names = [n for _, _, n in recs]
+    # the replayed step's kernels: the shortest period p whose last `steps` windows launch
+    # the same kernels (as multisets: kernels of two streams may start in either order)
+    from collections import Counter
+
+    period = None
+    for p in range(1, len(names) // steps + 1):
+        tail = names[len(names) - p * steps:]
+        first = Counter(tail[:p])
+        if all(Counter(tail[i * p:(i + 1) * p]) == first for i in range(1, steps)):
+            period = p
+            break
+    if period is None:
+        raise SystemExit("no repeated step sequence in the trace")
+    timed = recs[len(recs) - period * steps:]
+    wall_ns = timed[-1][1] - timed[0][0]
+    classes: dict = {}
+    for s, e, n in timed:
+        label = next((lab for lab, pat in STEP_CLASSES if re.search(pat, n, re.I)),
+                     "other: " + n[:60])
+        c = classes.setdefault(label, [0.0, 0])
+        c[0] += (e - s) / 1e3
+        c[1] += 1
+    busy = sum(v[0] for v in classes.values())
+    lines = [f"kernels per step: {period}; wall per step (first start to last end over "
+             f"{steps} steps): {wall_ns / 1e3 / steps:.1f} us; kernel time per step: "
+             f"{busy / steps:.1f} us ({busy * 1e3 / wall_ns * 100:.1f}% of wall)", "",
+             "| kernel class | us / step | % of kernel time | launches / step |",
+             "|---|---:|---:|---:|"]
+    for label, (us, cnt) in sorted(classes.items(), key=lambda kv: -kv[1][0]):
+        lines.append(f"| {label} | {us / steps:.1f} | {us / busy * 100:.1f} | "
+                     f"{cnt // steps} |")
+    return "\n".join(lines)
+
+
 TRAIN_25M = dict(model="ratchet-gpt-25M", vocab=8192, block=512, batch=32, n_layer=8, n_head=8,
                  n_embd=512, ffn=2048, max_code=MAX_CODE, codes="quinary")
 TRAIN_1B = dict(model="ratchet-gpt-1B", vocab=8192, block=1024, batch=8, n_layer=24, n_head=16,
@@ -767,6 +917,25 @@ def gemm_sweep(device, iters: int) -> list:
     return out_rows
 
 
+def host_info() -> dict:
+    """The host CPU's model string (first "model name" of /proc/cpuinfo) and the torch
+    version the CPU baseline ran on."""
+    import platform
+
+    import torch
+
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "torch": torch.__version__}
+
+
 def cpu_baseline(seconds: float) -> dict:
     import torch
 
@@ -774,7 +943,7 @@ def cpu_baseline(seconds: float) -> dict:
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    m_sample = 2048
+    m_sample = M_TOK
     gen = torch.Generator().manual_seed(7)
     code = torch.randint(-MAX_CODE, MAX_CODE + 1, (N_OUT, K_IN), generator=gen)
     packed = (((code + MAX_CODE) & 0x0F) | (7 << 4)).to(torch.uint8)
@@ -791,7 +960,7 @@ def cpu_baseline(seconds: float) -> dict:
     per_step = (time.perf_counter() - t0) / iters
     ops = 3 * 2.0 * m_sample * N_OUT * K_IN
     return {"value": round(ops / per_step / 1e12, 4), "unit": "TOPS", "cores": threads,
-            "kind": "port",
+            "kind": "port", **host_info(),
             "sample": f"fp32 eager torch ratchet linear fwd+bwd+tiled update, M={m_sample} of "
                       f"{M_TOK} tokens, K={K_IN}, N={N_OUT}, {iters} steps, "
                       f"{per_step * 1e3:.1f} ms/step"}
@@ -810,7 +979,7 @@ def cpu_baseline_model() -> dict:
     torch.set_num_threads(threads)
     r = tiny_training_tokens_per_s()
     return {"value": round(r["tokens_per_s"], 1), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
+            "kind": "port", **host_info(),
             "sample": f"tiny ratchet transformer (2L, d128, 4h, FFN 512, vocab 256, seq 64, "
                       f"batch 8) fp32 eager + bf16 autocast training, {r['timed_steps']} of "
                       f"{r['steps']} steps timed, {r['ms_per_step']:.1f} ms/step, loss "
@@ -823,6 +992,12 @@ def main() -> int:
         summary = traffic_summary(*args.traffic_summary)
         write_traffic_file(summary, *args.traffic_summary)
         print(json.dumps(summary), flush=True)
+        return 0
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary), flush=True)
+        return 0
+    if args.step_summary:
+        print(step_summary(args.step_summary[0], int(args.step_summary[1])), flush=True)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
@@ -845,6 +1020,15 @@ def main() -> int:
         return 0
     if args.gemm_sweep:
         print(json.dumps({"gemm_sweep": gemm_sweep(device, args.kernel_iters)}), flush=True)
+        return 0
+    if args.train_only:
+        shape = TRAIN_25M if args.train_only == "25m" else TRAIN_1B
+        log(f"training only: {shape['model']}, warmup={args.warmup} steps={args.steps}")
+        tok_s, step_s, loss = train_bench(shape, args.steps, args.warmup, device,
+                                          graph=not args.no_graph)
+        print(json.dumps({"model": shape["model"], "tokens_per_s": round(tok_s, 1),
+                          "ms_per_step": round(step_s * 1e3, 3), "loss": round(loss, 5),
+                          "steps": args.steps, "graph": not args.no_graph}), flush=True)
         return 0
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
     step_s, eager_s, layer, x, g = op_bench(args, device)

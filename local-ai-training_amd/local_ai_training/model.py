@@ -145,9 +145,13 @@ class KVCache:
 
 def _attend(q: Tensor, k: Tensor, v: Tensor, **kwargs) -> Tensor:
     """scaled_dot_product_attention; 16-bit GPU inputs go to the fused kernels only (the
-    math fallback runs 16-bit batched products on transposed views, avoided here)."""
+    math fallback runs 16-bit batched products on transposed views, avoided here). The
+    memory-efficient kernel comes first: on MI355X its causal forward + backward takes
+    260 us against the flash kernel's 348 us at B 32, H 8, S 512, D 64, and 550 against
+    885 us at B 8, H 16, S 1024, D 128, with the same forward output."""
     if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION],
+                         set_priority=True):
             return F.scaled_dot_product_attention(q, k, v, **kwargs)
     return F.scaled_dot_product_attention(q, k, v, **kwargs)
 

@@ -55,8 +55,11 @@ def _gemv(layer, out, prologue, epilogue, x=None, xq=None, xs=None, w=None, eps=
                        norm_weight=w, eps=eps)
 
 
+# (1, 5632, 2048) and (1, 6144, 32): one token row over rows longer than 2048, the
+# 8-wavefront split of K (the batch-1 contraction of the 1B model)
 SHAPES = [(1, 2048, 6144), (1, 64, 16), (3, 2048, 5632), (4, 5632, 2048), (5, 320, 48),
-          (16, 2048, 2048), (16, 5632, 2048), (11, 6144, 32), (1, 2048, 8192)]
+          (16, 2048, 2048), (16, 5632, 2048), (11, 6144, 32), (1, 2048, 8192),
+          (1, 5632, 2048), (1, 6144, 32)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
@@ -90,7 +93,8 @@ def test_int8_prologue_and_residual_add_match_the_packed_gemm(cuda, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 2048, 6144), (4, 2048, 2048), (16, 2048, 5632),
-                                   (7, 512, 128), (2, 5632, 64)])
+                                   (7, 512, 128), (2, 5632, 64), (1, 5632, 64),
+                                   (1, 6144, 128)])
 def test_rmsnorm_prologue_equals_rmsnorm_quantize_then_gemm(cuda, m, k, n):
     gen = torch.Generator().manual_seed(m + k + 5 * n)
     x = (torch.randn(m, k, generator=gen) * 2.0).to(cuda)
@@ -106,7 +110,8 @@ def test_rmsnorm_prologue_equals_rmsnorm_quantize_then_gemm(cuda, m, k, n):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 2048, 5632), (16, 2048, 5632), (3, 640, 96)])
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 5632), (16, 2048, 5632), (3, 640, 96),
+                                   (1, 5632, 128), (1, 6144, 64)])
 def test_gelu_epilogue_feeds_the_same_quantization_as_gelu_quantize(cuda, m, k, n):
     # expand GEMV with the GELU epilogue, then a plain quant of its float32 rows, must give
     # the q, s that rk_gelu_quantize computes from the GEMM's widened output
