@@ -16,6 +16,8 @@
 //    v_mfma_i32_16x16x64_i8 with bounds-checked staging.
 // Block order is XCD-aware: consecutive tile indices (which share an A row panel)
 // are kept on one XCD's L2.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "rk_common.h"
@@ -567,6 +569,317 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Persistent LDS-ring kernel (aligned shapes, 256 x 256 tiles): the wide token GEMMs
+// (N >= 4096: the lm_head, the 1B qkv / expand).
+//
+// Each of the 8 wavefronts (2 x 4) owns a 128 x 64 wave tile (4 x 2 blocks of
+// v_mfma_i32_32x32x32_i8, accumulators in 128 registers). Operands reach LDS through
+// gfx950's buffer_load_dwordx4 ... lds (16 bytes per lane straight into LDS, no
+// registers, no VALU): one 32 KB stage per 64-byte k-step (A [256][64] + B [256][64], or
+// for the packed [K, N] operand B [64][256]), S stages in a ring. The block is persistent:
+// it walks its tiles in order and the ring runs across tile boundaries, so the loads of the
+// next tile's first S - 1 k-steps are in flight during the current tile's last k-steps and
+// its epilogue. The LDS-DMA destination is fixed by the lane (lane l writes bytes
+// 16 l .. 16 l + 15 of the instruction's 1 KB), so the bank swizzles are applied to the
+// source instead: lane l fetches the segment that belongs at its slot.
+//  * [256][64] stages: slot (row, t) holds segment t ^ ((row >> 2) & 3) (the 32-row MFMA
+//    fragment reads of the register-ring kernel above, conflict-free);
+//  * the packed [64][256] stage: slot (row, t) of a 256-byte row holds segment
+//    t ^ 2 (row & 7): the transposing fragment reads (8 rows x 2 adjacent segments per 32
+//    lanes) then touch 16 distinct 16-byte bank groups.
+// The row scales (and column scales) of each tile go to a double-buffered LDS area by the
+// same DMA, ahead of the tile's first k-step, so the epilogue reads them with no vector
+// memory wait. The epilogue stages the bf16 results in LDS, 64 rows per round, so every
+// store writes 16 bytes of 32-lane-contiguous 512-byte rows (stores straight from the MFMA
+// layout scatter 8 bytes over 32 rows per instruction and cost 18 of 45 us at
+// 16384 x 2048 x 512). Out-of-range columns are stored to an offset past the output
+// descriptor (dropped by the hardware) instead of behind a branch. Tiles are walked in
+// groups of 8 row tiles (n-major inside a group), so the 32 tiles an XCD runs at once
+// share 8 A panels and 4 B panels in its L2 (8192^3: 626 -> 534 us against row-major).
+//
+// Synchronization per k-step: each wavefront waits (vmcnt) for its own DMA loads of the
+// stage, then one s_barrier (no fence: LDS-DMA completion is what vmcnt tracks) makes every
+// wavefront's part visible; the stage refilled after the barrier is the one every
+// wavefront finished reading before it arrived. The DMA loads are inline assembly, which
+// the compiler does not track: its own vmcnt waits (the residual loads) only become
+// stricter, never too weak, with loads it cannot see in flight.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef unsigned int u32x2_v __attribute__((ext_vector_type(2)));
+
+constexpr int kPipeBM = 256, kPipeBN = 256, kPipeBK = 64, kPipeStages = 3;
+// epilogue staging: 64 rows of 256 bf16 at a 520-byte pitch (rows 2 banks apart)
+constexpr int kEPitch = 520, kERows = 64;
+constexpr int kPipeStage = (kPipeBM + kPipeBN) * kPipeBK;  // 32 KB
+constexpr int kPipeScales = 2 * 2 * 1024;                  // ls + rs, two tiles
+
+__host__ __device__ constexpr int vmcnt_imm(int n) {
+  // s_waitcnt immediate that waits for vmcnt <= n only (expcnt 7, lgkmcnt 15)
+  return 0x0F70 | (n & 15) | ((n >> 4) << 14);
+}
+
+// One LDS-DMA load: 16 bytes per lane at buffer offset voff + soff into LDS bytes
+// lds + 16 lane .. + 15. M0 holds the LDS address (wave-uniform).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t lds, int voff, int soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
+struct PipeSched {
+  int tiles, tiles_m, tiles_n, tiles_per_xcd;
+};
+
+template <int KIND, int CDT, bool HAS_RS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void int8_gemm_pipe_kernel(GemmArgs g, PipeSched p) {
+  constexpr int BM = kPipeBM, BN = kPipeBN, BK = kPipeBK, S = kPipeStages;
+  constexpr int NW = 8, THR = 64 * NW, CH = 16 / NW, WNT = BN / (NW / 2);
+  constexpr int MI = 4, NJ = WNT / 32, ASZ = BM * BK, STAGE = kPipeStage;
+  constexpr bool BT = KIND == B_PACKED_T;
+  constexpr bool PACKED = KIND != B_INT8;
+  constexpr int ES = CDT == RK_BF16 ? 2 : 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S * STAGE + kPipeScales + kERows * kEPitch];
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_ptr)smem));
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int arow0 = (wave & 1) * 128, brow0 = (wave >> 1) * WNT;
+  const int r32 = lane & 31, h = lane >> 5;
+
+  // Tiles: row-major over (m tile, n tile), consecutive indices share an A row panel. The
+  // blocks of one XCD (block b runs on XCD b % 8) take one contiguous range of tiles, so
+  // the A panels and B of that range stay in the XCD's L2.
+  const int xcd = blockIdx.x & 7, lb = blockIdx.x >> 3, bpx = gridDim.x >> 3;
+  const int t_begin = xcd * p.tiles_per_xcd;
+  const int t_span = min(p.tiles, t_begin + p.tiles_per_xcd) - t_begin;
+  const int n_my = t_span > lb ? (t_span - lb + bpx - 1) / bpx : 0;
+  const int nk = static_cast<int>(g.K / BK);
+  const int total = n_my * nk;
+
+  // Per-lane DMA source offsets (fixed for the kernel). Wave w fills 1 KB chunks 2w and
+  // 2w + 1 of each operand's stage.
+  const int lda = static_cast<int>(g.lda), ldb = static_cast<int>(g.ldb);
+  const int sg = (lane & 3) ^ ((lane >> 4) & 3);  // [256][64] stage: 16 rows of 4 slots
+  int a_v[CH], b_v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int chunk = CH * wave + c;
+    a_v[c] = (16 * chunk + (lane >> 2)) * lda + 16 * sg;
+    if constexpr (BT) {
+      const int r0 = 4 * chunk + (lane >> 4);
+      b_v[c] = r0 * ldb + 16 * ((lane & 15) ^ (2 * (r0 & 7)));
+    } else {
+      b_v[c] = (16 * chunk + (lane >> 2)) * ldb + 16 * sg;
+    }
+  }
+  const int b_kstep = BT ? BK * ldb : BK;  // B offset per k-step
+
+  // Tile order: groups of GM row tiles, n-major inside a group, so the 32 tiles an XCD
+  // runs at once span GM row panels of A and 32 / GM column panels of B.
+  constexpr int GM = 8;
+  auto tile_origin = [&](int ordinal, int64_t& m0, int64_t& n0) {
+    const int tile = t_begin + lb + ordinal * bpx;
+    const int group = GM * p.tiles_n;
+    const int gidx = tile / group, first_m = gidx * GM;
+    const int gm = p.tiles_m - first_m < GM ? p.tiles_m - first_m : GM;
+    const int r = tile - gidx * group;
+    m0 = static_cast<int64_t>(first_m + r % gm) * BM;
+    n0 = static_cast<int64_t>(r / gm) * BN;
+  };
+
+  // Producer state: the current tile's descriptors, recomputed when the tile changes.
+  int pt = 0, pk = 0, pstage = 0;
+  __amdgpu_buffer_rsrc_t ar = make_buffer(g.A, 0), br = make_buffer(g.B, 0);
+  int64_t pm0 = 0, pn0 = 0, prows = 0, pcols = 0;
+  auto set_tile = [&]() {
+    tile_origin(pt, pm0, pn0);
+    prows = g.M - pm0 < BM ? g.M - pm0 : BM;
+    pcols = g.N - pn0 < BN ? g.N - pn0 : BN;
+    ar = make_buffer(g.A + pm0 * g.lda, (prows - 1) * g.lda + g.K);
+    br = BT ? make_buffer(g.B + pn0, (g.K - 1) * g.ldb + (g.N - pn0))
+            : make_buffer(g.B + pn0 * g.ldb, (pcols - 1) * g.ldb + g.K);
+  };
+  if (total > 0) set_tile();
+  auto issue = [&]() {
+    if (pk == 0 && wave < 2) {
+      const uint32_t dst = lds0 + S * STAGE + (pt & 1) * 2048 + wave * 1024;
+      if (wave == 0) {
+        dma16(make_buffer(g.ls + pm0, prows * 4), dst, 16 * lane, 0);
+      } else if (HAS_RS) {
+        dma16(make_buffer(g.rs + pn0, pcols * 4), dst, 16 * lane, 0);
+      }
+    }
+    const uint32_t st = lds0 + pstage * STAGE + 1024 * CH * wave;
+    const int ak = pk * BK, bk = pk * b_kstep;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) dma16(ar, st + 1024 * c, a_v[c] + ak, 0);
+#pragma unroll
+    for (int c = 0; c < CH; ++c) dma16(br, st + ASZ + 1024 * c, b_v[c] + bk, 0);
+    if (++pstage == S) pstage = 0;
+    if (++pk == nk) {
+      pk = 0;
+      ++pt;
+      if (pt < n_my) set_tile();
+    }
+  };
+
+  v16i acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = v16i{};
+
+  for (int s = 0; s < S - 1 && s < total; ++s) issue();
+  int ct = 0, ck = 0, cstage = 0;  // consumer: tile ordinal, k-step, stage
+  for (int step = 0; step < total; ++step) {
+    // this step's loads landed: at most the loads of the (up to S - 2) later steps in
+    // flight (2 CH per step; the scale loads and stores issued after them only make the
+    // wait stricter)
+    const int ahead = total - 1 - step;
+    if (ahead >= S - 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH * (S - 2)));
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    asm volatile("s_barrier" ::: "memory");
+    if (step + S - 1 < total) issue();
+
+    const uint8_t* at = smem + cstage * STAGE;
+    if (++cstage == S) cstage = 0;
+    const uint8_t* bt = at + ASZ;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      v4i fa[MI], fb[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int ra = arow0 + i * 32 + r32;
+        fa[i] = *reinterpret_cast<const v4i*>(at + ra * 64 + 16 * ((h + 2 * kh) ^ swz32(ra)));
+      }
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        v4i v;
+        if constexpr (BT) {
+          // 16 consecutive k rows of output column `col` per lane (transposing read)
+          const int sl = lane & 15;
+          const int col = brow0 + j * 32 + 16 * ((lane >> 4) & 1) + 8 * (sl & 1);
+          const int r0 = 16 * (h + 2 * kh) + (sl >> 1);  // r0 & 7 == (r0 + 8) & 7
+          const int phys = 16 * ((col >> 4) ^ (2 * (r0 & 7))) + (col & 15);
+          const v2i_t lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_ptr)(bt + r0 * 256 + phys));
+          const v2i_t hi =
+              __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_ptr)(bt + (r0 + 8) * 256 + phys));
+          v = v4i{lo.x, lo.y, hi.x, hi.y};
+        } else {
+          const int rb = brow0 + j * 32 + r32;
+          v = *reinterpret_cast<const v4i*>(bt + rb * 64 + 16 * ((h + 2 * kh) ^ swz32(rb)));
+        }
+        if constexpr (PACKED) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = static_cast<int>(decode4(static_cast<uint32_t>(v[e]), g.mc4));
+        }
+        fb[j] = v;
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[j], fa[i], acc[i][j], 0, 0, 0);
+    }
+    if (++ck < nk) continue;
+
+    // Epilogue of tile ct: C = bf16((acc * ls) * rs), rows m = arow0 + 32 i + lane % 32,
+    // columns n = brow0 + 32 j + 8 q + 4 (lane / 32) + e % 4 (e = 4 q .. 4 q + 3).
+    ck = 0;
+    int64_t m0, n0;
+    tile_origin(ct, m0, n0);
+    const int64_t rows_a = g.M - m0 < BM ? g.M - m0 : BM;
+    const uint8_t* sc = smem + S * STAGE + (ct & 1) * 2048;
+    ++ct;
+    const __amdgpu_buffer_rsrc_t c_r =
+        make_buffer(static_cast<char*>(g.C) + (m0 * g.ldc + n0) * ES,
+                    ((rows_a - 1) * g.ldc + (g.N - n0)) * ES);
+    const bool has_r = CDT == RK_F32 && g.R != nullptr;
+    const __amdgpu_buffer_rsrc_t r_r =
+        make_buffer(has_r ? g.R + m0 * g.ldr + n0 : g.ls,
+                    has_r ? ((rows_a - 1) * g.ldr + (g.N - n0)) * 4 : 0);
+    float lsv[MI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      lsv[i] = *reinterpret_cast<const float*>(sc + (arow0 + 32 * i + r32) * 4);
+    {
+      uint8_t* stg = smem + S * STAGE + kPipeScales;
+      const int wm = wave & 1;
+#pragma unroll
+      for (int round = 0; round < 4; ++round) {
+        if (wm == (round >> 1)) {
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii) {
+            const int i = 2 * (round & 1) + ii;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int nl = brow0 + 32 * j + 8 * q + 4 * h;
+                float4 rs4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+                if constexpr (HAS_RS) rs4 = *reinterpret_cast<const float4*>(sc + 1024 + nl * 4);
+                float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
+                float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
+                float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
+                float v3 = static_cast<float>(acc[i][j][4 * q + 3]) * lsv[i];
+                if constexpr (HAS_RS) {
+                  v0 = v0 * rs4.x; v1 = v1 * rs4.y; v2 = v2 * rs4.z; v3 = v3 * rs4.w;
+                }
+                *reinterpret_cast<uint2*>(stg + (32 * ii + r32) * kEPitch + nl * 2) =
+                    make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+                acc[i][j][4 * q] = 0; acc[i][j][4 * q + 1] = 0; acc[i][j][4 * q + 2] = 0; acc[i][j][4 * q + 3] = 0;
+              }
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+        for (int it = 0; it < 2048 / THR; ++it) {
+          const int c = tid + THR * it, row = c >> 5, seg = c & 31;
+          const uint8_t* src = stg + row * kEPitch + 16 * seg;
+          const uint2 lo = *reinterpret_cast<const uint2*>(src);
+          const uint2 hi = *reinterpret_cast<const uint2*>(src + 8);
+          const int ml = 64 * round + row;
+          const bool in = n0 + 8 * seg < g.N;
+          if constexpr (CDT == RK_BF16) {
+            const int off = in ? static_cast<int>((ml * g.ldc + 8 * seg) * 2) : 0x7ffffff0;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_r, off, 0, 0);
+          } else {
+            const int off = in ? static_cast<int>((ml * g.ldc + 8 * seg) * 4) : 0x7ffffff0;
+            uint4 w0 = make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16, lo.y & 0xffff0000u);
+            uint4 w1 = make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16, hi.y & 0xffff0000u);
+            if (has_r) {
+              // C = R + widened bf16, the float add of adding the tensors afterwards (R may
+              // be C itself: each thread reads the residual it then overwrites)
+              const int roff = in ? static_cast<int>((ml * g.ldr + 8 * seg) * 4) : 0x7ffffff0;
+              const float4 r0 = __builtin_bit_cast(
+                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, roff, 0, 0));
+              const float4 r1 = __builtin_bit_cast(
+                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, roff + 16, 0, 0));
+              w0.x = __float_as_uint(r0.x + __uint_as_float(w0.x));
+              w0.y = __float_as_uint(r0.y + __uint_as_float(w0.y));
+              w0.z = __float_as_uint(r0.z + __uint_as_float(w0.z));
+              w0.w = __float_as_uint(r0.w + __uint_as_float(w0.w));
+              w1.x = __float_as_uint(r1.x + __uint_as_float(w1.x));
+              w1.y = __float_as_uint(r1.y + __uint_as_float(w1.y));
+              w1.z = __float_as_uint(r1.z + __uint_as_float(w1.z));
+              w1.w = __float_as_uint(r1.w + __uint_as_float(w1.w));
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w0), c_r, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w1), c_r, off + 16, 0, 0);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging reads done
+        asm volatile("s_barrier" ::: "memory");
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Small-M kernel (M <= 16 tokens: decode steps): the weight matrix is read once, so the
 // kernel is an HBM stream over B. One block = 16 output rows n, its 4 wavefronts split K;
 // each wavefront issues its 16-byte loads in batches of 8 (all in flight before the
@@ -666,8 +979,58 @@ static bool use_big_tiles(const GemmArgs& g) {
   return g.K >= 1024 && big >= 256;
 }
 
+// Kernel choice for aligned token-sized GEMMs: RATCHET_GEMM_KERNEL=ring forces the
+// register-ring kernel, =pipe the persistent LDS-ring kernel (where its shape conditions
+// hold); unset or anything else picks by shape.
+static int gemm_kernel_override() {
+  static const int mode = [] {
+    const char* e = getenv("RATCHET_GEMM_KERNEL");
+    if (!e) return 0;
+    if (strcmp(e, "ring") == 0) return 1;
+    if (strcmp(e, "pipe") == 0) return 2;
+    return 0;
+  }();
+  return mode;
+}
+
+// The persistent kernel needs K % 64 == 0 and at least 4 k-steps (the scale buffers of two
+// tiles are reused every other tile, refilled S - 1 = 2 steps ahead), and output offsets
+// well inside 32 bits (stores of columns past N go to an offset past the descriptor).
+static bool pipe_supported(const GemmArgs& g, int es) {
+  return g.K >= 256 && g.M > 16 && 256 * g.ldc * es <= (int64_t{1} << 30) &&
+         (g.R == nullptr || 256 * g.ldr * 4 <= (int64_t{1} << 30));
+}
+
+// By shape (MI355X, ring / pipe, us): wide outputs favour the persistent kernel (16384 x
+// 8192 x 512 float32: 218.7 / 183.6; 8192 x 8192 x 2048: 207.0 / 191.2; 8192 x 6144 x 2048:
+// 131.9 / 128.3), narrow ones the register ring (16384 x 2048 x 512: 34.2 / 36.9;
+// grad_input 16384 x 512 x 2048: 25.6 / 37.4).
+static bool use_pipe(const GemmArgs& g, int es) {
+  if (!pipe_supported(g, es)) return false;
+  const int mode = gemm_kernel_override();
+  if (mode != 0) return mode == 2;
+  const int64_t tiles = ((g.M + kPipeBM - 1) / kPipeBM) * ((g.N + kPipeBN - 1) / kPipeBN);
+  return g.N >= 4096 && tiles >= 256;
+}
+
+template <int KIND, int CDT, bool HAS_RS>
+static void launch_pipe(const GemmArgs& g, hipStream_t stream) {
+  PipeSched p{};
+  p.tiles_n = static_cast<int>((g.N + kPipeBN - 1) / kPipeBN);
+  p.tiles_m = static_cast<int>((g.M + kPipeBM - 1) / kPipeBM);
+  p.tiles = p.tiles_m * p.tiles_n;
+  p.tiles_per_xcd = (p.tiles + 7) / 8;
+  // one 512-thread block per CU (256 CUs), 8 per XCD at least; never more blocks than tiles
+  const int per_xcd = p.tiles_per_xcd < 32 ? p.tiles_per_xcd : 32;
+  int8_gemm_pipe_kernel<KIND, CDT, HAS_RS><<<dim3(8 * per_xcd), 512, 0, stream>>>(g, p);
+}
+
 template <int KIND, int CDT, bool HAS_RS>
 static void launch_m32(const GemmArgs& g, hipStream_t stream) {
+  if (use_pipe(g, CDT == RK_BF16 ? 2 : 4)) {
+    launch_pipe<KIND, CDT, HAS_RS>(g, stream);
+    return;
+  }
   if (use_big_tiles(g)) {
     const int64_t tiles = ((g.M + 255) / 256) * ((g.N + 255) / 256);
     int8_gemm_m32_kernel<KIND, CDT, HAS_RS, CfgBig>
