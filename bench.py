@@ -68,6 +68,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--train-1b-warmup", type=int, default=8)
     ap.add_argument("--update-1b-only", action="store_true",
                     help="run only the 1B fused-update sweep (for profiling)")
+    ap.add_argument("--hbm-probe", action="store_true",
+                    help="run only the HBM streaming probe (practical read / copy bandwidth)")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the forward GEMM on packed codes at large-K shapes")
     ap.add_argument("--decode-only", action="store_true",
@@ -649,6 +651,52 @@ def model_bench(args, device, graph: bool):
     return train_bench(TRAIN_25M, args.model_steps, args.model_warmup, device, graph)
 
 
+def hbm_probe(device, gib: float = 1.0) -> dict:
+    """Practical HBM bandwidth of a plain streaming kernel (rk_hbm_stream): read-only and
+    copy over `gib` GiB, swept over loads in flight per thread and grid size; the best of
+    each and the full sweep. Copy counts read + write bytes."""
+    import torch
+
+    from local_ai_training import _native as nat
+
+    nbytes = int(gib * (1 << 30))
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=device).random_()
+    dst = torch.empty(nbytes // 4, dtype=torch.int32, device=device)
+    stream = nat.stream_handle(device)
+    sweep = []
+    for copy in (0, 1):
+        for unroll in (2, 4, 8):
+            for blocks in (1024, 2048, 4096, 8192):
+                def run():
+                    nat.call("rk_hbm_stream", src.data_ptr(), dst.data_ptr(), nbytes, copy,
+                             unroll, blocks, stream)
+                run()
+                torch.cuda.synchronize()
+                best = None
+                for _ in range(3):
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(5):
+                        run()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    ms = e0.elapsed_time(e1) / 5
+                    best = ms if best is None else min(best, ms)
+                moved = nbytes * (2 if copy else 1)
+                sweep.append({"mode": "copy" if copy else "read", "unroll": unroll,
+                              "blocks": blocks, "us": round(best * 1e3, 1),
+                              "TB_s": round(moved / (best * 1e-3) / 1e12, 3)})
+    del src, dst
+    torch.cuda.empty_cache()
+    out = {"bytes": nbytes, "sweep": sweep}
+    for mode in ("read", "copy"):
+        top = max((e for e in sweep if e["mode"] == mode), key=lambda e: e["TB_s"])
+        out[mode] = {"TB_s": top["TB_s"], "frac_hbm": round(top["TB_s"] * 1e12 / PEAK_HBM_BPS, 4),
+                     "unroll": top["unroll"], "blocks": top["blocks"]}
+    return out
+
+
 def update_1b_bench(device, iters: int) -> dict:
     """The fused update of one 1B training step at full scale: every ratchet layer of the 1B
     septenary model (24 x qkv 6144x2048, proj 2048x2048, expand 5632x2048, contract
@@ -1014,6 +1062,9 @@ def main() -> int:
         return 0
     if args.decode_only:
         print(json.dumps({"decode": decode_bench(args, device)}), flush=True)
+        return 0
+    if args.hbm_probe:
+        print(json.dumps({"hbm_probe": hbm_probe(device)}), flush=True)
         return 0
     if args.update_1b_only:
         print(json.dumps({"update_1b": update_1b_bench(device, 5)}), flush=True)

@@ -421,6 +421,14 @@ int rk_decode_embed(const int64_t* tokens, int64_t B, const float* table, int64_
                     int64_t C, const float* pos_table, int64_t n_pos, const int64_t* pos,
                     float* hidden, int64_t ldh, void* stream);
 
+/* HBM streaming probe (measurement only; no counterpart in the reference): reads `bytes`
+ * (a multiple of 16) from src in 16-byte vectors, `unroll` (1, 2, 4, 8) loads in flight
+ * per thread, `blocks` blocks of 256 threads in a grid-stride loop; copy != 0 writes them
+ * to dst, else nothing is written (dst must still hold blocks * 1 KB). The achieved rate is
+ * the device's practical read / copy bandwidth for the bandwidth-bound kernels. */
+int rk_hbm_stream(const void* src, void* dst, int64_t bytes, int copy, int unroll, int blocks,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif
