@@ -6,7 +6,8 @@
  *   - Plain pointers to device memory, element strides (not bytes), int64 sizes.
  *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream).
  *     Work is enqueued on that stream; nothing synchronizes with the host.
- *   - The library never allocates and never frees: the caller owns every buffer.
+ *   - The library never allocates and never frees: the caller owns every buffer (the one
+ *     exception is the file-scope scratch array of rk_grad_weight_bf16_noalloc).
  *   - Return value: RK_OK (0) or an RK_ERR_* code; the message of the last failure
  *     on the calling thread is available from rk_last_error(). Nothing throws
  *     across the ABI.
@@ -219,6 +220,19 @@ int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, const int8_t* q
 int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x, int x_dtype,
                           int64_t ldx, int64_t M, int64_t N, int64_t K, float* workspace,
                           int nsplit, uint16_t* out, int64_t ldo, void* stream);
+
+/*
+ * rk_grad_weight_bf16 without a workspace (no counterpart in the reference): for callers
+ * that cannot allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). The nsplit float32 split partials live in a file-scope device array of
+ * 16 Mi floats (64 MB) per GPU, held until the process ends; nsplit * N * K beyond that
+ * returns RK_ERR_ARG. out is required. Same kernels and split order as rk_grad_weight_bf16,
+ * so the same nsplit gives the same bits. Calls that overlap on one GPU share the array
+ * and race. Allocates nothing (no hipMalloc / hipFree, no allocating library call).
+ */
+int rk_grad_weight_bf16_noalloc(const void* g, int g_dtype, int64_t ldg, const int8_t* q,
+                                int64_t ldq, const float* s, int64_t M, int64_t N, int64_t K,
+                                int nsplit, uint16_t* out, int64_t ldo, void* stream);
 
 /* Default token-range split count of rk_grad_weight_bf16 for an [M] x [N, K] problem. */
 int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K);

@@ -20,6 +20,8 @@
 // The token (contraction) axis is split into `nsplit` ranges; each block writes fp32
 // partial sums of one 128 x 128 output tile for one range, and a second kernel adds the
 // ranges in a fixed order and rounds to bf16, so results are reproducible run to run.
+#include <mutex>
+
 #include "rk_common.h"
 
 namespace rk {
@@ -414,6 +416,49 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   return launch_status("grad_weight_reduce");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free form (rk_grad_weight_bf16_noalloc): the split partials live in one
+// file-scope device array per GPU instead of a caller workspace, for callers that may not
+// allocate (code under graph capture, serving loops). Host code never uses the array's name
+// as an address: its device address is looked up once per device with hipGetSymbolAddress
+// (that device current) and cached. Every call on a GPU shares the array, so calls that
+// overlap on one GPU (two streams, two threads) race; each call overwrites every partial it
+// reads, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchFloats = int64_t{16} << 20;  // 64 MB of float32 partials
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+static float* scratch_address(hipStream_t stream, int& status) {
+  static std::mutex mu;
+  static float* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    status = fail(RK_ERR_ARG, "cannot resolve the stream's device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev]) return addr[dev];
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) {
+    status = fail(RK_ERR_LAUNCH, "hipGetDevice failed");
+    return nullptr;
+  }
+  if (cur != dev && hipSetDevice(dev) != hipSuccess) {
+    status = fail(RK_ERR_LAUNCH, "hipSetDevice(%d) failed", dev);
+    return nullptr;
+  }
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess || p == nullptr) {
+    status = fail(RK_ERR_LAUNCH, "scratch address: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  addr[dev] = static_cast<float*>(p);
+  return addr[dev];
+}
+
 }  // namespace rk
 
 using namespace rk;
@@ -451,4 +496,26 @@ extern "C" int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, co
   if (x_dtype != RK_F32 && x_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported x dtype");
   return grad_weight_launch(g, g_dtype, ldg, x, x_dtype == RK_F32 ? GW_X_F32 : GW_X_BF16, ldx,
                             nullptr, M, N, K, workspace, nsplit, out, ldo, stream);
+}
+
+extern "C" int rk_grad_weight_bf16_noalloc(const void* g, int g_dtype, int64_t ldg,
+                                           const int8_t* q, int64_t ldq, const float* s,
+                                           int64_t M, int64_t N, int64_t K, int nsplit,
+                                           uint16_t* out, int64_t ldo, void* stream) {
+  clear_error();
+  if (N < 0 || K < 0 || nsplit < 1 || nsplit > 64)
+    return fail(RK_ERR_ARG, "nsplit must be in 1..64 and sizes non-negative");
+  if (N == 0 || K == 0) return RK_OK;
+  if (!out) return fail(RK_ERR_ARG, "null output (the partials are not returned)");
+  if (static_cast<int64_t>(nsplit) * N * K > kScratchFloats)
+    return fail(RK_ERR_ARG,
+                "nsplit * N * K = %lld float32 partials exceed the %lld-float scratch "
+                "(use rk_grad_weight_bf16 with a workspace, or fewer splits)",
+                static_cast<long long>(static_cast<int64_t>(nsplit) * N * K),
+                static_cast<long long>(kScratchFloats));
+  int status = RK_OK;
+  float* partials = scratch_address(as_stream(stream), status);
+  if (!partials) return status;
+  return grad_weight_launch(g, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, partials, nsplit,
+                            out, ldo, stream);
 }

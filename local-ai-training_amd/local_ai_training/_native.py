@@ -50,6 +50,8 @@ SIGNATURES: dict[str, list] = {
     "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_grad_weight_bf16": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i32, _p,
                             _i64, _p],
+    "rk_grad_weight_bf16_noalloc": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _i32,
+                                    _p, _i64, _p],
     "rk_grad_weight_bf16_x": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _p,
                               _i64, _p],
     "rk_grad_weight_splits": [_i64, _i64, _i64],
