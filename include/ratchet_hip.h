@@ -32,7 +32,7 @@ enum {
   RK_ERR_UNSUPPORTED = 3  /* a valid request the library does not implement         */
 };
 
-enum { RK_F32 = 0, RK_BF16 = 1 };
+enum { RK_F32 = 0, RK_BF16 = 1, RK_I8 = 2 /* int8 activations with a per-row scale */ };
 
 /* Library version (major*10000 + minor*100 + patch). */
 int rk_version(void);
@@ -233,6 +233,32 @@ int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x
 int rk_grad_weight_bf16_noalloc(const void* g, int g_dtype, int64_t ldg, const int8_t* q,
                                 int64_t ldq, const float* s, int64_t M, int64_t N, int64_t K,
                                 int nsplit, uint16_t* out, int64_t ldo, void* stream);
+
+/*
+ * grad_weight with the fused update in its last blocks: the partial sums of
+ * rk_grad_weight_bf16 (x_dtype RK_I8: int8 x with per-row scale s, as rk_grad_weight_bf16;
+ * RK_F32 / RK_BF16: as rk_grad_weight_bf16_x) go to workspace [nsplit, N, K]; each block
+ * then counts its arrival for its row block, and the block that completes a row block runs
+ * the update of rk_ratchet_update_partials on those rows (same arithmetic, same results:
+ * packed, counts, row_rms, rms_ema, nonfinite, grad_out), so no separate update launch
+ * follows. counters: int32 [rk_grad_weight_update_counters(N, K)], zero before the first
+ * call; every call leaves them zero again (a call that fails part-way does not: zero them
+ * before the next). rms_mean (needs row_rms) is written by the block that completes the
+ * layer. Requires K % 8 == 0 plus rk_grad_weight_bf16's conditions. No trainable-scale
+ * gradient (use rk_grad_weight_bf16 + rk_ratchet_update_partials for that).
+ * Replaces: the grad_weight tile loop and its gradient_sink ratchet.py:148-169, with
+ *           _capture_weight_gradient 487-537 run on each finished row block.
+ */
+int rk_grad_weight_update(const void* g, int g_dtype, int64_t ldg, const void* x, int x_dtype,
+                          int64_t ldx, const float* s, int64_t M, int64_t N, int64_t K,
+                          float* workspace, int nsplit, int32_t* counters, uint8_t* packed,
+                          int64_t ldp, int max_code, int threshold, float low, float high,
+                          float eps, float* rms_ema, float beta1, float beta2, int64_t* counts,
+                          float* row_rms, int32_t* nonfinite, float* rms_mean,
+                          uint16_t* grad_out, int64_t ld_grad_out, void* stream);
+
+/* Length of the counters array rk_grad_weight_update needs for an [N, K] gradient. */
+int64_t rk_grad_weight_update_counters(int64_t N, int64_t K);
 
 /* Default token-range split count of rk_grad_weight_bf16 for an [M] x [N, K] problem. */
 int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K);

@@ -23,6 +23,7 @@
 #include <mutex>
 
 #include "rk_common.h"
+#include "rk_update_row.h"
 
 namespace rk {
 
@@ -45,6 +46,13 @@ struct GwArgs {
   int64_t M, N, K;
   int64_t m_chunk;  // tokens per split, a multiple of GW_BM
   int nsplit;
+  // fused update (rk_grad_weight_update): the update's arguments over these partials, the
+  // arrival counters (one per FEAT-row block, then one for the layer) and the arrivals that
+  // complete a row block (its column tiles times the splits)
+  GradUpdateArgs u;
+  int32_t* counters;
+  int arrivals;
+  float* rms_mean;
 };
 
 constexpr int GW_BM = 32;                  // tokens per pipeline step
@@ -128,7 +136,32 @@ __device__ __forceinline__ v8bf gw_fragment(const uint8_t* tile, int tok0, int c
   return f;
 }
 
-template <int GDT, int XK, int S, int BM, class CFG>
+// mean[0] = mean of row_rms[0 .. rows) by threads 0..255 of the block: each a strided
+// partial sum in row order, then a fixed LDS tree (the order of row_rms_mean_kernel).
+__device__ __forceinline__ void block_row_rms_mean(const float* row_rms, int64_t rows,
+                                                   float* mean) {
+  __shared__ float part[256];
+  const int t = threadIdx.x;
+  if (t < 256) {
+    float acc = 0.0f;
+    for (int64_t r = t; r < rows; r += 256) acc = acc + row_rms[r];
+    part[t] = acc;
+  }
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if (t < w) part[t] = part[t] + part[t + w];
+    __syncthreads();
+  }
+  if (t == 0) mean[0] = part[0] / static_cast<float>(rows);
+}
+
+// UNC < 0: partial sums only. UNC >= 0 (rk_grad_weight_update): after writing its partial
+// tile, each block publishes it (device-scope release: the XCDs' L2s are not coherent) and
+// counts its arrival for its row block; the block that completes a row block acquires and
+// runs the fused update (update_row with the split-partial source, UNC chunks in registers)
+// on those rows, then resets the row block's counter for the next launch. The block that
+// completes the last row block writes the mean row rms the same way.
+template <int GDT, int XK, int S, int BM, class CFG, int UNC = -1>
 __global__ __launch_bounds__(CFG::THREADS) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void grad_weight_partial_kernel(GwArgs a) {
   constexpr int GE = GDT == RK_F32 ? 4 : 2;                          // g element bytes
@@ -314,6 +347,34 @@ void grad_weight_partial_kernel(GwArgs a) {
         if (n < a.N && k < a.K) out[n * a.K + k] = acc[i][j][e];
       }
     }
+
+  if constexpr (UNC >= 0) {
+    __shared__ int finisher;
+    const int64_t rblock = n0 / FEAT;
+    const int64_t rblocks = (a.N + FEAT - 1) / FEAT;
+    __threadfence();  // this thread's partial stores, device-wide, before the arrival
+    __syncthreads();
+    if (tid == 0) finisher = atomicAdd(a.counters + rblock, 1) == a.arrivals - 1;
+    __syncthreads();
+    if (!finisher) return;
+    __threadfence();  // acquire: every split's partials of these rows
+    MoveCounts cnt;
+    const int64_t row_end = n0 + FEAT < a.N ? n0 + FEAT : a.N;
+    for (int64_t row = n0 + wave; row < row_end; row += THREADS / 64)
+      update_row<SRC_SPLITS, UNC, false>(a.u, row, a.K, cnt);
+    flush_counts(cnt, a.u.counts);
+    if (tid == 0) a.counters[rblock] = 0;  // every arrival of this launch is in
+    if (a.rms_mean) {
+      __threadfence();  // this block's row_rms stores, before the layer arrival
+      __syncthreads();
+      if (tid == 0) finisher = atomicAdd(a.counters + rblocks, 1) == rblocks - 1;
+      __syncthreads();
+      if (!finisher) return;
+      __threadfence();
+      block_row_rms_mean(a.u.row_rms, a.N, a.rms_mean);
+      if (tid == 0) a.counters[rblocks] = 0;
+    }
+  }
 }
 
 // Gw[n, k] = bf16(sum over splits of part[s][n][k]), splits added in order 0, 1, ...
@@ -339,12 +400,20 @@ __global__ __launch_bounds__(256) void grad_weight_reduce_kernel(const float* pa
 
 // Ring depth 2 and 32-token steps: ring depths 4 and 6 and 64-token steps (BM = 64, 80 KB
 // of LDS) measure the same or slower on MI355X at the op and model shapes.
-template <int XK, class CFG>
+template <int XK, class CFG, int UNC = -1>
 void launch_partial_g(const GwArgs& a, int g_dtype, dim3 grid, hipStream_t st) {
   if (g_dtype == RK_F32)
-    grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM, CFG><<<grid, CFG::THREADS, 0, st>>>(a);
+    grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM, CFG, UNC><<<grid, CFG::THREADS, 0, st>>>(a);
   else
-    grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM, CFG><<<grid, CFG::THREADS, 0, st>>>(a);
+    grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM, CFG, UNC><<<grid, CFG::THREADS, 0, st>>>(a);
+}
+
+// The fused form: the update's row chunks in registers for rows of up to 512 columns (one
+// 512-element chunk), streamed twice otherwise (the partials re-read from cache).
+template <int XK, class CFG>
+void launch_partial_upd(const GwArgs& a, int g_dtype, dim3 grid, hipStream_t st) {
+  if (a.K <= 512) launch_partial_g<XK, CFG, 1>(a, g_dtype, grid, st);
+  else launch_partial_g<XK, CFG, 0>(a, g_dtype, grid, st);
 }
 
 // The 256 x 256 tile where it still leaves at least 64 output tiles (the op shape's
@@ -356,7 +425,9 @@ static bool gw_big_tiles(int64_t N, int64_t K) {
 // Shared validation and launch of both entry points; x_kind is a GW_X_* form.
 int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, int x_kind,
                        int64_t ldx, const float* s, int64_t M, int64_t N, int64_t K,
-                       float* workspace, int nsplit, uint16_t* out, int64_t ldo, void* stream) {
+                       float* workspace, int nsplit, uint16_t* out, int64_t ldo, void* stream,
+                       const GradUpdateArgs* upd = nullptr, int32_t* counters = nullptr,
+                       float* rms_mean = nullptr) {
   if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
   if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
   if (N == 0 || K == 0) return RK_OK;
@@ -398,6 +469,28 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
   hipStream_t st = as_stream(stream);
   const dim3 grid(static_cast<unsigned>(blocks));
+  if (upd) {
+    // the fused update: the caller's update arguments over these partials
+    a.u = *upd;
+    a.u.part = workspace;
+    a.u.nsplit = nsplit;
+    a.u.part_stride = N * K;
+    a.u.rows = N;
+    a.u.K = K;
+    a.counters = counters;
+    a.arrivals = static_cast<int>(((K + feat - 1) / feat) * nsplit);
+    a.rms_mean = rms_mean;
+    if (big) {
+      if (x_kind == GW_X_Q8) launch_partial_upd<GW_X_Q8, GwBig>(a, g_dtype, grid, st);
+      else if (x_kind == GW_X_BF16) launch_partial_upd<GW_X_BF16, GwBig>(a, g_dtype, grid, st);
+      else launch_partial_upd<GW_X_F32, GwBig>(a, g_dtype, grid, st);
+    } else {
+      if (x_kind == GW_X_Q8) launch_partial_upd<GW_X_Q8, GwSmall>(a, g_dtype, grid, st);
+      else if (x_kind == GW_X_BF16) launch_partial_upd<GW_X_BF16, GwSmall>(a, g_dtype, grid, st);
+      else launch_partial_upd<GW_X_F32, GwSmall>(a, g_dtype, grid, st);
+    }
+    return launch_status("grad_weight_update");
+  }
   if (big) {
     if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwBig>(a, g_dtype, grid, st);
     else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16, GwBig>(a, g_dtype, grid, st);
@@ -518,4 +611,57 @@ extern "C" int rk_grad_weight_bf16_noalloc(const void* g, int g_dtype, int64_t l
   if (!partials) return status;
   return grad_weight_launch(g, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, partials, nsplit,
                             out, ldo, stream);
+}
+
+extern "C" int rk_grad_weight_update(const void* g, int g_dtype, int64_t ldg, const void* x,
+                                     int x_dtype, int64_t ldx, const float* s, int64_t M,
+                                     int64_t N, int64_t K, float* workspace, int nsplit,
+                                     int32_t* counters, uint8_t* packed, int64_t ldp,
+                                     int max_code, int threshold, float low, float high,
+                                     float eps, float* rms_ema, float beta1, float beta2,
+                                     int64_t* counts, float* row_rms, int32_t* nonfinite,
+                                     float* rms_mean, uint16_t* grad_out, int64_t ld_grad_out,
+                                     void* stream) {
+  clear_error();
+  if (x_dtype != RK_F32 && x_dtype != RK_BF16 && x_dtype != RK_I8)
+    return fail(RK_ERR_ARG, "unsupported activation dtype");
+  if (N <= 0 || K <= 0 || M < 0) return fail(RK_ERR_ARG, "invalid shape");
+  if (!packed || !counters) return fail(RK_ERR_ARG, "null packed state or counters");
+  if (ldp < K) return fail(RK_ERR_ARG, "ldp < K");
+  if (max_code < 1 || max_code > 7) return fail(RK_ERR_ARG, "max_code must be in 1..7");
+  if (threshold < 1 || threshold > 127)
+    return fail(RK_ERR_ARG, "pressure_threshold must be in [1, 127]");
+  if (!(low >= 0.0f && low < high))
+    return fail(RK_ERR_ARG, "bucket thresholds must satisfy 0 <= low < high");
+  if (!(eps > 0.0f)) return fail(RK_ERR_ARG, "eps must be positive");
+  if (K % 8 != 0) return fail(RK_ERR_UNSUPPORTED, "the fused update needs K %% 8 == 0");
+  if (rms_mean && !row_rms) return fail(RK_ERR_ARG, "rms_mean needs row_rms");
+  if (grad_out && (ld_grad_out < K || ld_grad_out % 8 != 0 || !aligned16(grad_out)))
+    return fail(RK_ERR_ARG, "grad_out needs ld >= K, ld %% 8 == 0, 16-byte alignment");
+  GradUpdateArgs u{};
+  u.packed = packed;
+  u.ldp = ldp;
+  u.g_out = grad_out;
+  u.ldgo = ld_grad_out;
+  u.mc = max_code;
+  u.T = threshold;
+  u.low = low;
+  u.high = high;
+  u.eps = eps;
+  u.rms_ema = rms_ema;
+  u.beta1 = beta1;
+  u.beta2 = beta2;
+  u.counts = counts;
+  u.row_rms = row_rms;
+  u.nonfinite = nonfinite;
+  u.vec_p = (reinterpret_cast<uintptr_t>(packed) % 8) == 0 && (ldp % 8) == 0;
+  const int kind = x_dtype == RK_I8 ? GW_X_Q8 : (x_dtype == RK_BF16 ? GW_X_BF16 : GW_X_F32);
+  return grad_weight_launch(g, g_dtype, ldg, x, kind, ldx, s, M, N, K, workspace, nsplit,
+                            nullptr, 0, stream, &u, counters, rms_mean);
+}
+
+extern "C" int64_t rk_grad_weight_update_counters(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 1;
+  const int64_t feat = gw_big_tiles(N, K) ? GwBig::FEAT : GwSmall::FEAT;
+  return (N + feat - 1) / feat + 1;
 }

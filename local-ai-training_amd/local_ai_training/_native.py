@@ -21,6 +21,7 @@ LIB_PATH = Path(os.environ.get("RATCHET_HIP_LIB", Path(__file__).with_name(LIB_N
 
 RK_F32 = 0
 RK_BF16 = 1
+RK_I8 = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -50,6 +51,10 @@ SIGNATURES: dict[str, list] = {
     "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_grad_weight_bf16": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _i32, _p,
                             _i64, _p],
+    "rk_grad_weight_update": [_p, _i32, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _p, _i32,
+                              _p, _p, _i64, _i32, _i32, _f32, _f32, _f32, _p, _f32, _f32, _p,
+                              _p, _p, _p, _p, _i64, _p],
+    "rk_grad_weight_update_counters": [_i64, _i64],
     "rk_grad_weight_bf16_noalloc": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _i64, _i32,
                                     _p, _i64, _p],
     "rk_grad_weight_bf16_x": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _i64, _p, _i32, _p,
@@ -86,6 +91,7 @@ SIGNATURES: dict[str, list] = {
 RESTYPES = {
     "rk_last_error": ctypes.c_char_p,
     "rk_decode_attention_splits": ctypes.c_int64,
+    "rk_grad_weight_update_counters": ctypes.c_int64,
 }
 
 _lib: ctypes.CDLL | None = None
