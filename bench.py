@@ -529,8 +529,8 @@ def counter_summary(csv_paths: list[str]) -> str:
 # sequence.
 # ---------------------------------------------------------------------------
 STEP_CLASSES = [
-    ("int8 GEMM forward (W8A8, packed codes)", r"int8_gemm_(m32|nt)_kernel<[01],|int8_gemv"),
-    ("int8 GEMM grad_input (packed codes, in place)", r"int8_gemm_m32_kernel<2,"),
+    ("int8 GEMM forward (W8A8, packed codes)", r"int8_gemm_(m32|nt|pipe)_kernel<[01],|int8_gemv"),
+    ("int8 GEMM grad_input (packed codes, in place)", r"int8_gemm_(m32|pipe)_kernel<2,"),
     ("SR gradient quant (Philox)", r"quant_rows_kernel<\d+, \d+, true"),
     ("activation quant prologues (RMSNorm/GELU/transpose)", r"quant_rows_kernel<\d+, \d+, false"),
     ("bf16 grad_weight (MFMA)", r"grad_weight_(partial|reduce)_kernel"),
