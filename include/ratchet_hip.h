@@ -32,7 +32,13 @@ enum {
   RK_ERR_UNSUPPORTED = 3  /* a valid request the library does not implement         */
 };
 
-enum { RK_F32 = 0, RK_BF16 = 1, RK_I8 = 2 /* int8 activations with a per-row scale */ };
+enum {
+  RK_F32 = 0,
+  RK_BF16 = 1,
+  RK_I8 = 2,          /* int8 activations with a per-row scale                          */
+  RK_F32_AS_BF16 = 3  /* float32 storage whose values are taken as bfloat16(x) (round to
+                         nearest even, as x.to(torch.bfloat16)): rk_quantize_rows[_devseed] */
+};
 
 /* Library version (major*10000 + minor*100 + patch). */
 int rk_version(void);
@@ -47,6 +53,9 @@ const char* rk_last_error(void);
  *   col_scale[K] float32 or NULL
  *   q        [M, K] int8, row stride ldq (unit column stride)
  *   scale    [M]    float32
+ *   x_dtype  RK_F32, RK_BF16, or RK_F32_AS_BF16 (float32 x quantized as bf16(x): the
+ *            gradient a bf16 output receives from a float32 residual stream, without a
+ *            separate cast)
  *   x_bf16   NULL, or [M, K] bf16 (row stride ld_xb) receiving bf16(x) (unscaled):
  *            the cast that the BF16 grad_weight GEMM consumes, produced in the
  *            same pass.
@@ -405,6 +414,22 @@ int rk_rmsnorm_backward_parts(int64_t M);
 int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x, int x_dtype,
                      int64_t ldx, int64_t M, int64_t K, void* grad_x, int64_t ldgx,
                      void* stream);
+
+/* Token-embedding weight gradient: out[v, :] = sum of grad[t, :] over the T tokens with
+ * ids[t] == v (float32 [V, D], every row written; ids outside [0, V) contribute nothing).
+ * grad [T, D] float32 / bfloat16 with row stride ldg; ids int64 (ids_int64 = 1) or int32.
+ * The sum order is fixed: tokens in chunks of 64 positions, token order within a chunk,
+ * chunk order across chunks; no memset, no device-wide sort (legal under HIP-graph
+ * capture). work holds rk_embedding_backward_workspace(T, D) bytes, 16-byte aligned;
+ * nothing needs clearing between calls.
+ * D % 4 != 0 or D > 4096: RK_ERR_UNSUPPORTED.
+ * Replaces: the backward of the model's token lookup, model.py:237 (an nn.Embedding,
+ *           model.py:219, whose torch backward sorts the ids on the device).
+ */
+int64_t rk_embedding_backward_workspace(int64_t T, int64_t D);
+int rk_embedding_backward(const void* grad, int grad_dtype, int64_t ldg, const void* ids,
+                          int ids_int64, int64_t T, int64_t V, int64_t D, float* out,
+                          int64_t ldo, void* work, int64_t work_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * KV-cached decode (one token per sequence, M <= 16 rows). The reference has no

@@ -22,6 +22,7 @@
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <optional>
 
 #include "ratchet_hip.h"
@@ -98,10 +99,12 @@ void packed_matrix(const Tensor& t) {
 std::tuple<Tensor, Tensor> quantize_rows(const Tensor& x, const OptTensor& col_scale,
                                          bool stochastic, int64_t seed,
                                          const OptTensor& seed_slot, int64_t row_offset,
-                                         const OptTensor& x_bf16) {
+                                         const OptTensor& x_bf16, bool round_bf16) {
   require_gpu(x, "row quantization");
   TORCH_CHECK(x.dim() == 2, "row quantization requires a 2D tensor");
-  const int code = dtype_code(x, "row quantization input");
+  int code = dtype_code(x, "row quantization input");
+  // round_bf16: a float32 input is quantized as x.to(bfloat16) (no effect on bf16 inputs)
+  if (round_bf16 && code == RK_F32) code = RK_F32_AS_BF16;
   const c10::DeviceGuard guard(x.device());
   const int64_t m = x.size(0), k = x.size(1);
   Tensor q = at::empty({m, k}, x.options().dtype(at::kChar));
@@ -684,12 +687,43 @@ Tensor gelu_backward(const Tensor& gy_in, const Tensor& x_in) {
   return grad_x;
 }
 
+Tensor embedding_backward(const Tensor& grad_in, const Tensor& ids_in, int64_t num_weights) {
+  require_gpu(grad_in, "embedding backward");
+  same_device(grad_in, ids_in, "embedding backward");
+  TORCH_CHECK(ids_in.scalar_type() == at::kLong || ids_in.scalar_type() == at::kInt,
+              "embedding backward: ids must be int64 or int32, got ", ids_in.scalar_type());
+  TORCH_CHECK(num_weights >= 0, "embedding backward: num_weights must be non-negative");
+  const int64_t d = grad_in.size(-1);
+  const Tensor ids = ids_in.reshape({-1}).contiguous();
+  Tensor grad = grad_in.reshape({-1, d});
+  TORCH_CHECK(grad.size(0) == ids.size(0), "embedding backward: grad has ", grad.size(0),
+              " rows for ", ids.size(0), " ids");
+  if (grad.scalar_type() != at::kFloat && grad.scalar_type() != at::kBFloat16)
+    grad = grad.to(at::kFloat);
+  if (grad.stride(-1) != 1 || (grad.size(0) > 1 && grad.stride(0) % 4 != 0) ||
+      reinterpret_cast<uintptr_t>(grad.data_ptr()) % (4 * grad.element_size()) != 0)
+    grad = grad.contiguous();
+  const int64_t t = grad.size(0);
+  const c10::DeviceGuard guard(grad.device());
+  Tensor out = at::empty({num_weights, d}, grad.options().dtype(at::kFloat));
+  const int64_t bytes = rk_embedding_backward_workspace(t, d);
+  Tensor work = at::empty({std::max<int64_t>(bytes, 16)}, grad.options().dtype(at::kByte));
+  check_status(rk_embedding_backward(grad.data_ptr(), dtype_code(grad, "grad"),
+                                     t > 1 ? grad.stride(0) : d, ids.data_ptr(),
+                                     ids.scalar_type() == at::kLong ? 1 : 0, t, num_weights, d,
+                                     static_cast<float*>(out.data_ptr()), d, work.data_ptr(),
+                                     work.numel(), stream_of(grad)),
+               "rk_embedding_backward");
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(ratchet, m) {
   m.def(
       "quantize_rows(Tensor x, Tensor? col_scale=None, bool stochastic=False, int seed=0, "
-      "Tensor? seed_slot=None, int row_offset=0, Tensor(a!)? x_bf16=None) -> (Tensor, Tensor)");
+      "Tensor? seed_slot=None, int row_offset=0, Tensor(a!)? x_bf16=None, "
+      "bool round_bf16=False) -> (Tensor, Tensor)");
   m.def(
       "int8_mm_nt(Tensor a, Tensor b, Tensor a_scale, Tensor? b_scale, ScalarType out_dtype) "
       "-> Tensor");
@@ -737,6 +771,7 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("transpose_quantize(Tensor x) -> (Tensor, Tensor)");
   m.def("rmsnorm_backward(Tensor grad_y, Tensor x, Tensor w, float eps) -> (Tensor, Tensor)");
   m.def("gelu_backward(Tensor grad_y, Tensor x) -> Tensor");
+  m.def("embedding_backward(Tensor grad, Tensor ids, int num_weights) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
@@ -767,4 +802,5 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("transpose_quantize", &transpose_quantize);
   m.impl("rmsnorm_backward", &rmsnorm_backward);
   m.impl("gelu_backward", &gelu_backward);
+  m.impl("embedding_backward", &embedding_backward);
 }

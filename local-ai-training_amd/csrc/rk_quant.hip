@@ -36,6 +36,7 @@ struct QuantArgs {
   uint16_t* xb;               // plain only: bf16 side output, may be null
   int64_t ldxb;
   int vec_ok;                 // 16-byte vector loads are legal for every chunk
+  int round_bf16;             // plain float32 source: each value is taken as bf16(x) first
 };
 
 constexpr int kMaxChunks = 8;
@@ -69,10 +70,13 @@ __device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t row, int6
 }
 
 // Row transform applied to a raw value at column e (row_factor = rsqrt for rmsnorm).
-template <int SRC>
+template <int DT, int SRC>
 __device__ __forceinline__ float transform(const QuantArgs& a, float x, int64_t e,
                                            float row_factor) {
   if constexpr (SRC == SRC_PLAIN) {
+    if constexpr (DT == RK_F32) {
+      if (a.round_bf16) x = round_bf16(x);
+    }
     return a.col_scale ? x * a.col_scale[e] : x;
   } else if constexpr (SRC == SRC_RMSNORM) {
     return x * row_factor * a.w[e];
@@ -138,6 +142,12 @@ __device__ __forceinline__ void transform_chunk(const QuantArgs& a, int64_t e0, 
                                                 float row_factor) {
   constexpr int V = Vec<DT>::N;
   if constexpr (VEC && SRC == SRC_PLAIN) {
+    if constexpr (DT == RK_F32) {
+      if (a.round_bf16) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = round_bf16(v[i]);
+      }
+    }
     if (a.col_scale) {
 #pragma unroll
       for (int j = 0; j < V / 4; ++j) {
@@ -151,7 +161,7 @@ __device__ __forceinline__ void transform_chunk(const QuantArgs& a, int64_t e0, 
   } else {
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      v[i] = (VEC || e0 + i < a.K) ? transform<SRC>(a, v[i], e0 + i, row_factor) : 0.0f;
+      v[i] = (VEC || e0 + i < a.K) ? transform<DT, SRC>(a, v[i], e0 + i, row_factor) : 0.0f;
   }
 }
 
@@ -324,10 +334,13 @@ static int quantize_rows_entry(const void* x, int x_dtype, int64_t M, int64_t K,
                                int8_t* q, int64_t ldq, float* scale, uint16_t* x_bf16,
                                int64_t ld_xb, void* stream) {
   clear_error();
+  const int round_bf16 = x_dtype == RK_F32_AS_BF16 ? 1 : 0;
+  if (round_bf16) x_dtype = RK_F32;
   if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
   if (x_bf16 && ld_xb < K) return fail(RK_ERR_ARG, "ld_xb < K");
   if (M == 0) return RK_OK;
   QuantArgs a{};
+  a.round_bf16 = round_bf16;
   a.x = x;
   a.M = M;
   a.K = K;

@@ -22,6 +22,7 @@ LIB_PATH = Path(os.environ.get("RATCHET_HIP_LIB", Path(__file__).with_name(LIB_N
 RK_F32 = 0
 RK_BF16 = 1
 RK_I8 = 2
+RK_F32_AS_BF16 = 3
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
@@ -83,6 +84,9 @@ SIGNATURES: dict[str, list] = {
                             _i64, _i64, _f32, _p, _i64, _p, _i64, _p],
     "rk_decode_embed": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p],
     "rk_hbm_stream": [_p, _p, _i64, _i32, _i32, _i32, _p],
+    "rk_embedding_backward_workspace": [_i64, _i64],
+    "rk_embedding_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64,
+                              _p],
     "rk_version": [],
     "rk_last_error": [],
 }
@@ -92,6 +96,7 @@ RESTYPES = {
     "rk_last_error": ctypes.c_char_p,
     "rk_decode_attention_splits": ctypes.c_int64,
     "rk_grad_weight_update_counters": ctypes.c_int64,
+    "rk_embedding_backward_workspace": ctypes.c_int64,
 }
 
 _lib: ctypes.CDLL | None = None

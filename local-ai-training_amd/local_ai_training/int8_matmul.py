@@ -109,13 +109,16 @@ def sr_seed_args(device: torch.device) -> tuple[int, Tensor | None]:
 
 
 def quantize_rows_sr(values: Tensor, col_scale: Tensor | None = None, *,
-                     bf16_out: Tensor | None = None, row_offset: int = 0
-                     ) -> tuple[Tensor, Tensor, int | Tensor]:
+                     bf16_out: Tensor | None = None, row_offset: int = 0,
+                     round_bf16: bool = False) -> tuple[Tensor, Tensor, int | Tensor]:
     """Stochastically rounded row quantization of values * col_scale (one Philox draw per
     element); returns (q, scale, seed) where seed is the host seed drawn for this call or,
-    under graph capture, the device slot it reads. ``bf16_out`` receives bf16(values)."""
+    under graph capture, the device slot it reads. ``bf16_out`` receives bf16(values).
+    ``round_bf16``: float32 values are quantized as values.to(bfloat16), the same result as
+    casting first."""
     seed, slot = sr_seed_args(values.device)
-    q, s = _ops().quantize_rows(values, col_scale, True, seed, slot, row_offset, bf16_out)
+    q, s = _ops().quantize_rows(values, col_scale, True, seed, slot, row_offset, bf16_out,
+                                round_bf16)
     return q, s, (slot if slot is not None else seed)
 
 

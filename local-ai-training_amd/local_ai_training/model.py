@@ -143,17 +143,57 @@ class KVCache:
         self.pos.add_(steps)
 
 
+_FAST_ATTENTION = [SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]
+_DETERMINISTIC_ATTENTION = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+
+
 def _attend(q: Tensor, k: Tensor, v: Tensor, **kwargs) -> Tensor:
     """scaled_dot_product_attention; 16-bit GPU inputs go to the fused kernels only (the
     math fallback runs 16-bit batched products on transposed views, avoided here). The
     memory-efficient kernel comes first: on MI355X its causal forward + backward takes
     260 us against the flash kernel's 348 us at B 32, H 8, S 512, D 64, and 550 against
-    885 us at B 8, H 16, S 1024, D 128, with the same forward output."""
+    885 us at B 8, H 16, S 1024, D 128, with the same forward output. Its backward at head
+    size 128 accumulates dq in an order that varies from run to run (measured: dk, dv and
+    the output repeat bit for bit, dq does not; the flash kernel repeats at both shapes), so
+    under torch.use_deterministic_algorithms(True) the flash kernel comes first."""
     if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
-        with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION],
-                         set_priority=True):
+        order = (_DETERMINISTIC_ATTENTION if torch.are_deterministic_algorithms_enabled()
+                 else _FAST_ATTENTION)
+        with sdpa_kernel(order, set_priority=True):
             return F.scaled_dot_product_attention(q, k, v, **kwargs)
     return F.scaled_dot_product_attention(q, k, v, **kwargs)
+
+
+class _TokenLookup(torch.autograd.Function):
+    """``embedding(tokens, weight)`` whose weight gradient comes from the HIP kernels
+    (``rk_embedding_backward``): a fixed-order float32 sum per vocabulary row, made of plain
+    kernel launches. torch's own backward sorts the ids on the device and clears the sort's
+    state with a memset, which a captured training step would record as a memset node."""
+
+    @staticmethod
+    def forward(ctx, tokens: Tensor, weight: Tensor) -> Tensor:
+        ctx.save_for_backward(tokens)
+        ctx.num_weights = weight.shape[0]
+        ctx.weight_dtype = weight.dtype
+        return F.embedding(tokens, weight)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        (tokens,) = ctx.saved_tensors
+        from .ops import ratchet as _ops
+
+        grad = _ops().embedding_backward(grad_output, tokens, ctx.num_weights)
+        return None, grad.to(ctx.weight_dtype)
+
+
+def _hip_lookup_supported(embedding: nn.Module, tokens: Tensor) -> bool:
+    if type(embedding) is not nn.Embedding:
+        return False
+    w = embedding.weight
+    return (w.is_cuda and tokens.is_cuda and w.dtype in (torch.float32, torch.bfloat16)
+            and embedding.padding_idx is None and embedding.max_norm is None
+            and not embedding.sparse and not embedding.scale_grad_by_freq
+            and w.shape[1] % 4 == 0 and w.shape[1] <= 4096 and w.shape[0] < 2**31 - 1)
 
 
 def _autocast_bf16(t: Tensor) -> torch.dtype | None:
@@ -236,6 +276,13 @@ class CausalSelfAttention(nn.Module):
 
 
 class FeedForward(nn.Module):
+    # Under bf16 autocast an int8 expansion hands its bf16 GEMM result to the GELU prologue
+    # (the float32 result is that value widened): the expansion's output, the contraction's
+    # grad_input, the GELU backward and the expansion's gradient then move 2-byte values.
+    # The contraction keeps the input's dtype for its own output and gradient, as with a
+    # float32 expansion.
+    bf16_expand: bool = True
+
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
         hidden = config.hidden_size
@@ -248,17 +295,23 @@ class FeedForward(nn.Module):
                 residual: Tensor | None = None) -> Tensor:
         """``residual``: return residual + feed-forward output (int8 contraction without
         active dropout: added in the GEMM epilogue)."""
+        int8_contract = _is_int8(self.contract)
+        bf16_out = _autocast_bf16(inputs) if int8_contract and self.bf16_expand else None
+        kw = {"out_dtype": bf16_out} if bf16_out is not None else {}
         if inputs_int8 is not None:
-            expanded = self.expand(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale)
+            expanded = self.expand(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale,
+                                   **kw)
         else:
-            expanded = self.expand(inputs)
+            expanded = self.expand(inputs, **kw)
         no_dropout = self.dropout == 0.0 or not self.training
-        if _is_int8(self.contract):
+        if int8_contract:
             gelu_int8, gelu_scale, dummy = FusedGELUQuantizeFn.apply(expanded)
+            kw = {"out_dtype": inputs.dtype} if expanded.dtype != inputs.dtype else {}
             if no_dropout:
                 return self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale,
-                                     residual=residual)
-            contracted = self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale)
+                                     residual=residual, **kw)
+            contracted = self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale,
+                                       **kw)
         else:
             contracted = self.contract(F.gelu(expanded))
         out = F.dropout(contracted, p=self.dropout, training=self.training)
@@ -317,6 +370,8 @@ class RatchetGPT(nn.Module):
     # decode steps use the fused HIP decode kernels where supported (False: the module
     # forwards, e.g. to compare the two)
     fused_decode: bool = True
+    # the token embedding's weight gradient from the HIP kernels (False: torch's backward)
+    hip_embedding_backward: bool = True
 
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -348,7 +403,11 @@ class RatchetGPT(nn.Module):
         sequence_length = tokens.shape[1]
         if sequence_length > self.config.block_size:
             raise ValueError("token sequence exceeds configured block_size")
-        hidden = self.token_embedding(tokens) + self.position_encoding[:sequence_length]
+        if self.hip_embedding_backward and _hip_lookup_supported(self.token_embedding, tokens):
+            looked_up = _TokenLookup.apply(tokens, self.token_embedding.weight)
+        else:
+            looked_up = self.token_embedding(tokens)
+        hidden = looked_up + self.position_encoding[:sequence_length]
         for block in self.blocks:
             if self.config.gradient_checkpointing and self.training:
                 import torch.utils.checkpoint

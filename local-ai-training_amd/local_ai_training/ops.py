@@ -54,7 +54,7 @@ def _register_fakes() -> None:
 
     @fake("ratchet::quantize_rows")
     def _quantize_rows(x, col_scale=None, stochastic=False, seed=0, seed_slot=None,
-                       row_offset=0, x_bf16=None):
+                       row_offset=0, x_bf16=None, round_bf16=False):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::int8_mm_nt")
@@ -148,6 +148,10 @@ def _register_fakes() -> None:
     def _gelu_backward(grad_y, x):
         return x.new_empty((x.shape[0], x.shape[1]), dtype=float_dtype(x))
 
+    @fake("ratchet::embedding_backward")
+    def _embedding_backward(grad, ids, num_weights):
+        return grad.new_empty((num_weights, grad.shape[-1]), dtype=torch.float32)
+
 
 # every operator the library defines (the opcheck tests walk this list)
 OPERATORS = (
@@ -157,5 +161,5 @@ OPERATORS = (
     "grad_weight_x", "grad_weight_partials", "grad_weight_partials_x", "update_from_z",
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
-    "rmsnorm_backward", "gelu_backward",
+    "rmsnorm_backward", "gelu_backward", "embedding_backward",
 )

@@ -154,17 +154,22 @@ def _grad_weight_supported(g: Tensor, x: Tensor) -> bool:
 # ---------------------------------------------------------------------------
 # Autograd function
 # ---------------------------------------------------------------------------
-def _split_residual_grad(ctx, grad_output: Tensor) -> tuple[Tensor, Tensor | None]:
+def _split_residual_grad(ctx, grad_output: Tensor, defer_bf16: bool = False
+                         ) -> tuple[Tensor, Tensor | None, bool]:
     """For output = residual + y: y's gradient and the residual's, each cast to its operand's
     dtype as autograd casts the gradients of an add of mixed dtypes (a bf16 y gets the
-    bf16-rounded gradient)."""
+    bf16-rounded gradient). ``defer_bf16``: a float32 gradient due for that bf16 rounding is
+    returned as it is, with True as the third result, for consumers that round it themselves
+    (the SR quant's bf16 source mode and the grad_weight GEMM's bf16 staging)."""
     if ctx.residual_dtype is None:
-        return grad_output, None
+        return grad_output, None, False
     grad_residual = None
     if ctx.needs_input_grad[7]:
         # a residual broadcast against the output gets the gradient summed to its shape
         grad_residual = grad_output.sum_to_size(ctx.residual_shape).to(ctx.residual_dtype)
-    return grad_output.to(ctx.y_dtype), grad_residual
+    if defer_bf16 and ctx.y_dtype == torch.bfloat16 and grad_output.dtype == torch.float32:
+        return grad_output, grad_residual, True
+    return grad_output.to(ctx.y_dtype), grad_residual, False
 
 
 def _fusable_residual(residual: Tensor | None, q: Tensor, packed: Tensor,
@@ -271,7 +276,18 @@ class _RatchetMatmul(torch.autograd.Function):
             flat_inputs, scale = ctx.saved_tensors
             inputs_bf16 = None  # bf16(inputs), made only where a path needs the copy
             inputs_fp32 = flat_inputs.to(torch.float32) if mode == "fp32" else None
-        grad_output, grad_residual = _split_residual_grad(ctx, grad_output)
+        # grad_weight on a side stream next to the SR quant and grad_input (below)
+        overlap = (mode != "fp32" and layer.overlap_weight_gradient and grad_output.is_cuda
+                   and torch.cuda.is_current_stream_capturing())
+        # Without the side stream, the int8-backward path consumes the gradient only through
+        # the SR quant, which takes float32 values as bf16 itself and writes the bf16 copy
+        # grad_weight reads: a gradient due for bf16 rounding skips the separate cast. (With
+        # it, grad_weight would read the float32 values, which measured slower than the
+        # cast.)
+        sr_path = (layer.fuse_backward_update and mode == "int8" and layer.int8_backward
+                   and ctx.used_fused_int8)
+        grad_output, grad_residual, round_bf16 = _split_residual_grad(
+            ctx, grad_output, defer_bf16=sr_path and not overlap)
         flat_gradient = grad_output.flatten(0, -2)
         scale_d = scale.detach()
         needs_scale = ctx.needs_input_grad[4]
@@ -323,8 +339,7 @@ class _RatchetMatmul(torch.autograd.Function):
         # fork and join are graph edges; eagerly, a cross-stream wait costs more than the
         # overlap gains at these kernel sizes (measured).
         side = None
-        if mode != "fp32" and layer.overlap_weight_gradient and flat_gradient.is_cuda \
-                and torch.cuda.is_current_stream_capturing():
+        if overlap:
             g_w = flat_gradient if flat_gradient.dtype in (torch.float32, torch.bfloat16) \
                 else flat_gradient.float()
             if g_w.stride(-1) != 1:
@@ -358,7 +373,7 @@ class _RatchetMatmul(torch.autograd.Function):
                 gradient_bf16 = torch.empty((m, n), device=g.device, dtype=torch.bfloat16)
             # one seed per call from the CPU generator (a device slot under graph capture)
             grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr(
-                g, scale_d.float().contiguous(), bf16_out=gradient_bf16)
+                g, scale_d.float().contiguous(), bf16_out=gradient_bf16, round_bf16=round_bf16)
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
             if packed_t_supported(grad_q, packed):

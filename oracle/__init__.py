@@ -22,6 +22,9 @@ Pinning (what fixes each function independently of this restatement):
 * ``update``     — the reference's known-answer tests (``tests/test_ratchet.py``
                    17-22, 54-78, 183-193, 224-233) and its golden 60-step vector
                    (196-208, seed 1234).
+* ``embedding``  — torch's own CPU embedding backward, bit-exact on integer-valued
+                   gradients (every order gives the same sums); the fixed summation order
+                   of the HIP kernels is restated in the function.
 * ``update.row_sumsq`` — the reduction order is the HIP kernel's fixed one
                    (documented in the function); it is pinned exactly on inputs whose partial
                    sums are all representable (order-free) and by tolerance

@@ -198,6 +198,49 @@ def test_f32_gradient_side_output_is_rne_bf16(cuda):
     assert np.array_equal(bits16(side), f32_to_bf16_bits(g.numpy()))
 
 
+@pytest.mark.parametrize("shape,strided", [((16384, 512), False), ((67, 35), False),
+                                            ((33, 2048), True), ((9, 6144), False),
+                                            ((5, 5632), True)])
+def test_sr_quant_of_float32_as_bf16_equals_cast_then_quant(cuda, shape, strided):
+    # round_bf16 (C ABI: RK_F32_AS_BF16) quantizes float32 values as their bf16 rounding:
+    # the same codes, scales and bf16 side output as quantizing x.to(bfloat16), for the
+    # vector and element paths, register-resident and streamed rows, the host seed and the
+    # device seed; and the oracle on those bf16 values agrees on sampled rows.
+    m, k = shape
+    x = torch.randn(m, k, generator=gen(m + k)) * 1e-2
+    x[0, 0] = 1.0 + 2.0 ** -9  # a tie that rounds to even
+    col = torch.rand(k, generator=gen(7)) * 0.08 + 0.02
+    xd = x.to(cuda)
+    if strided:
+        xd = torch.empty(m, k + 3, device=cuda)[:, :k]
+        xd.copy_(x.to(cuda))
+    cd = col.to(cuda)
+    xb = xd.to(torch.bfloat16)
+    side_a = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
+    side_b = torch.empty(m, k, dtype=torch.bfloat16, device=cuda)
+    qa, sa = ops().quantize_rows(xd, cd, True, 4242, x_bf16=side_a, round_bf16=True)
+    qb, sb = ops().quantize_rows(xb, cd, True, 4242, x_bf16=side_b)
+    assert torch.equal(qa, qb) and torch.equal(sa, sb) and torch.equal(side_a, side_b)
+    slot = torch.tensor([4242], dtype=torch.int64, device=cuda)
+    qd, sd = ops().quantize_rows(xd, cd, True, 0, slot, round_bf16=True)
+    assert torch.equal(qd, qb) and torch.equal(sd, sb)
+    qn, sn = ops().quantize_rows(xd, None, False, 0, round_bf16=True)
+    qn_ref, sn_ref = ops().quantize_rows(xb)
+    assert torch.equal(qn, qn_ref) and torch.equal(sn, sn_ref)
+    qc, sc = qa.cpu().numpy(), sa.cpu().numpy()
+    for r0 in (0, m // 2, m - 1):
+        q_ref, s_ref = oquant.quantize_rows_sr(xb[r0:r0 + 1].float().cpu().numpy(),
+                                               col.numpy(), 4242, row_start=r0)
+        assert np.array_equal(qc[r0:r0 + 1], q_ref) and sc[r0] == s_ref[0]
+    q_abi = torch.empty(m, k, dtype=torch.int8, device=cuda)
+    s_abi = torch.empty(m, device=cuda)
+    nat.call("rk_quantize_rows", xd.data_ptr(), nat.RK_F32_AS_BF16, m, k, xd.stride(0), 1,
+             cd.data_ptr(), 1, 4242, 0, q_abi.data_ptr(), k, s_abi.data_ptr(), None, 0,
+             nat.stream_handle(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(q_abi, qb) and torch.equal(s_abi, sb)
+
+
 def test_quantize_columns_matches_transposed_rows(cuda):
     x = torch.randn(384, 200, generator=gen(13)) * 2.0
     q, s = quantize_columns(x.to(cuda))

@@ -122,10 +122,11 @@ def test_fused_transpose_quantize_is_exact(cuda, dtype):
     assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(s2.cpu(), s.cpu())
 
 
-def _int8_steps(cuda, fuse: bool, steps: int = 3):
-    from local_ai_training.model import TransformerBlock
+def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True):
+    from local_ai_training.model import FeedForward, TransformerBlock
 
     TransformerBlock.fuse_residual = fuse
+    FeedForward.bf16_expand = bf16_expand
     try:
         torch.manual_seed(0)
         config = ModelConfig(vocab_size=64, block_size=64, n_layer=2, n_head=4, n_embd=128,
@@ -148,6 +149,7 @@ def _int8_steps(cuda, fuse: bool, steps: int = 3):
         return losses, states, params
     finally:
         TransformerBlock.fuse_residual = True
+        FeedForward.bf16_expand = True
 
 
 def test_residual_fused_into_the_gemm_epilogue_changes_nothing(cuda):
@@ -170,6 +172,34 @@ def test_residual_fused_into_the_gemm_epilogue_changes_nothing(cuda):
     assert len(calls) == 3 * 2 * 2  # steps x layers x (projection, contraction)
     lb, sb, pb = _int8_steps(cuda, fuse=False)
     assert torch.equal(la[0], lb[0])  # forward
+    assert all(torch.equal(x, y) for x, y in zip(la, lb))
+    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
+    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_bf16_expansion_hand_off_changes_nothing(cuda, fuse):
+    # Under bf16 autocast the expansion hands its bf16 GEMM result to the GELU prologue
+    # instead of the float32 widening of it: the GELU quant, the contraction's bf16
+    # grad_input, the GELU backward's bf16-rounded gradient and the expansion's SR quant and
+    # grad_weight see the same values, so losses, ratchet states and float parameters are
+    # identical over three steps (with the residual added in the epilogue and separately).
+    from local_ai_training import int8_backward
+
+    seen = []
+    gelu_bwd = int8_backward.gelu_backward
+
+    def recording(grad_y, x):
+        seen.append((grad_y.dtype, x.dtype))
+        return gelu_bwd(grad_y, x)
+
+    int8_backward.gelu_backward = recording
+    try:
+        la, sa, pa = _int8_steps(cuda, fuse=fuse, bf16_expand=True)
+    finally:
+        int8_backward.gelu_backward = gelu_bwd
+    assert seen and all(d == (torch.bfloat16, torch.bfloat16) for d in seen)
+    lb, sb, pb = _int8_steps(cuda, fuse=fuse, bf16_expand=False)
     assert all(torch.equal(x, y) for x, y in zip(la, lb))
     assert all(torch.equal(x, y) for x, y in zip(sa, sb))
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))

@@ -75,11 +75,15 @@ class StepRecorder:
                                                             res_rows)
             return result
 
-        def sr(values, col_scale=None, *, bf16_out=None, row_offset=0):
-            q, s, seed = orig_sr(values, col_scale, bf16_out=bf16_out, row_offset=row_offset)
+        def sr(values, col_scale=None, *, bf16_out=None, row_offset=0, round_bf16=False):
+            q, s, seed = orig_sr(values, col_scale, bf16_out=bf16_out, row_offset=row_offset,
+                                 round_bf16=round_bf16)
             r = self.rows(values.shape[0], values.device)
             self._sr_by_q[q.data_ptr()] = len(self.sr)
-            self.sr.append([None, values[r].clone(), seed, q[r], s[r]])
+            # the values as quantized: a float32 gradient taken as bf16 is the bf16 gradient
+            # the reference's projection receives from its mixed-dtype residual add
+            consumed = values[r].to(torch.bfloat16) if round_bf16 else values[r].clone()
+            self.sr.append([None, consumed, seed, q[r], s[r]])
             return q, s, seed
 
         def mm_t(a, packed, max_code, a_scale, row_scale, out_dtype=torch.bfloat16):
@@ -266,6 +270,45 @@ def test_25m_training_steps_are_reproducible(cuda):
         results.append((losses, states, [p.detach().clone() for p in model.parameters()]))
         print(f"run losses {losses}", flush=True)
         del model, optimizer
+    (l0, s0, p0), (l1, s1, p1) = results
+    assert l0 == l1
+    assert all(torch.equal(a, b) for a, b in zip(s0, s1))
+    assert all(torch.equal(a, b) for a, b in zip(p0, p1))
+
+
+def test_1b_training_steps_are_reproducible_in_deterministic_mode(cuda):
+    # The 1B step (24 layers, d 2048, 16 heads, FFN 5632, seq 1024, batch 8, septenary
+    # codes) run twice from the same seeds, two steps each: identical losses, ratchet states
+    # and float parameters. Deterministic mode selects the flash attention backward (the
+    # memory-efficient one's dq accumulation order varies at head size 128); every ratchet
+    # kernel sums in a fixed order either way.
+    shape = dict(vocab=8192, block=1024, n_layer=24, n_head=16, n_embd=2048, ffn=5632,
+                 max_code=3)
+    tokens = zipf_tokens(8, 1024, 8192, 1337, cuda)
+    results = []
+    torch.use_deterministic_algorithms(True, warn_only=True)
+    try:
+        for _ in range(2):
+            model = make_model(cuda, seed=1337, random_pressure=True, **shape)
+            optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.0)
+            torch.manual_seed(5)
+            losses = []
+            for _ in range(2):
+                optimizer.zero_grad(set_to_none=True)
+                with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                    _, loss = model(tokens[:, :-1], tokens[:, 1:])
+                loss.backward()
+                model.ratchet_update(validate=False)
+                optimizer.step()
+                losses.append(float(loss))
+            states = [layer.packed.clone() for layer in model.modules()
+                      if isinstance(layer, DiscreteRatchetLinear)]
+            results.append((losses, states, [p.detach().clone() for p in model.parameters()]))
+            print(f"run losses {losses}", flush=True)
+            del model, optimizer
+            torch.cuda.empty_cache()
+    finally:
+        torch.use_deterministic_algorithms(False)
     (l0, s0, p0), (l1, s1, p1) = results
     assert l0 == l1
     assert all(torch.equal(a, b) for a, b in zip(s0, s1))

@@ -91,6 +91,9 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
     gx, gwn = R.rmsnorm_backward(x, x, meta(k), 1e-5)
     assert gx.shape == (m, k) and gx.dtype == torch.bfloat16 and gwn.dtype == torch.float32
     assert R.gelu_backward(meta(m, k), meta(m, k)).dtype == torch.float32
+    emb = R.embedding_backward(meta(2, m // 2, k, dtype=torch.bfloat16),
+                               meta(2, m // 2, dtype=torch.int64), 50)
+    assert emb.shape == (50, k) and emb.dtype == torch.float32
 
 
 def test_split_count_query_runs_on_the_host(R):
