@@ -104,25 +104,32 @@ __device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, uint32_t c
                                                   const float* y, float s, float r,
                                                   int8_t* qrow, bool vec_store) {
   constexpr int V = Vec<DT>::N;
-  int8_t qv[V];
+  float t[V], u[V];
+  bool exact = false;
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    float u = 0.0f;
+    u[i] = 0.0f;
     if constexpr (SR) {
       // counter = (row_offset + m) * K + k, wrapped to 32 bits like the int32 offsets
       // of int8_matmul.py:143
-      u = uniform_from_word(philox_word0(ctr_row + static_cast<uint32_t>(e0 + i), key));
+      u[i] = uniform_from_word(philox_word0(ctr_row + static_cast<uint32_t>(e0 + i), key));
     }
-    float t = round_quotient<SR>(y[i], s, r, u);
-    t = fminf(fmaxf(t, -127.0f), 127.0f);
-    qv[i] = static_cast<int8_t>(static_cast<int>(t));
+    t[i] = round_fast<SR>(y[i], r, u[i], exact);
   }
+  if (exact) {
+    // a value of this lane's chunk lies within the margin of a rounding boundary (or is
+    // not finite): round the chunk through round_quotient, which divides where needed
+#pragma unroll
+    for (int i = 0; i < V; ++i) t[i] = round_quotient<SR>(y[i], s, r, u[i]);
+  }
+  int qi[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) qi[i] = static_cast<int>(fminf(fmaxf(t[i], -127.0f), 127.0f));
   if (vec_store && (ALL || e0 + V <= a.K)) {
     uint32_t w[V / 4];
 #pragma unroll
     for (int j = 0; j < V / 4; ++j)
-      w[j] = (uint32_t)(uint8_t)qv[4 * j] | ((uint32_t)(uint8_t)qv[4 * j + 1] << 8) |
-             ((uint32_t)(uint8_t)qv[4 * j + 2] << 16) | ((uint32_t)(uint8_t)qv[4 * j + 3] << 24);
+      w[j] = pack_bytes4(qi[4 * j], qi[4 * j + 1], qi[4 * j + 2], qi[4 * j + 3]);
     if constexpr (V == 8) {
       *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(w[0], w[1]);
     } else {
@@ -131,7 +138,7 @@ __device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, uint32_t c
   } else {
 #pragma unroll
     for (int i = 0; i < V; ++i)
-      if (e0 + i < a.K) qrow[e0 + i] = qv[i];
+      if (e0 + i < a.K) qrow[e0 + i] = static_cast<int8_t>(qi[i]);
   }
 }
 

@@ -26,6 +26,37 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // div_rn) and rounds that.
 constexpr float kAmbiguity = 0.000244140625f;
 
+// The fast path of round_quotient alone: the rounded value from ya = y * r, with `exact`
+// set (never cleared) where that value may differ from the one computed from y / s (the
+// same test as round_quotient's). Callers round a group of values this way and redo the
+// group with round_quotient only when some value set the flag, so the common case runs
+// without a branch per value.
+template <bool SR>
+__device__ __forceinline__ float round_fast(float y, float r, float u, bool& exact) {
+  const float ya = y * r;
+  if constexpr (SR) {
+    const float v = ya + u;
+    const float f = floorf(v);
+    const float d = v - f;
+    exact = exact || !(fabsf(ya) <= 128.0f) || d < kAmbiguity || d > 1.0f - kAmbiguity;
+    return f;
+  } else {
+    const float t = __builtin_rintf(ya);
+    exact = exact || !(fabsf(ya) <= 128.0f) || fabsf(ya - t) > 0.5f - kAmbiguity;
+    return t;
+  }
+}
+
+// Four int32 values in [-128, 127] as the bytes of one word (byte i from the i-th).
+__device__ __forceinline__ uint32_t pack_bytes4(int b0, int b1, int b2, int b3) {
+  // v_perm_b32 selects bytes of {S0, S1} (S1 = bytes 0-3, S0 = bytes 4-7; 0x0c = zero)
+  const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(b1), static_cast<uint32_t>(b0),
+                                            0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(b3), static_cast<uint32_t>(b2),
+                                            0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 template <bool SR>
 __device__ __forceinline__ float round_quotient(float y, float s, float r, float u) {
   const float ya = y * r;
