@@ -344,6 +344,7 @@ def _per_dispatch_kib(csv_path: str, counter: str) -> list[tuple[str, float]]:
 def _stage_means(rows: list[tuple[str, float]]) -> tuple[dict, float]:
     """Mean KiB per launch of each stage (its kernels summed), and of the copy."""
     sums = {name: 0.0 for name in STAGE_KERNELS}
+    counts = {name: 0 for name in STAGE_KERNELS}
     copies = [kib for name, kib in rows if "copy" in name.lower() and "rk::" not in name]
     # the calibration copies (setup copies of small tensors excluded)
     copy = [kib for kib in copies if kib >= 0.25 * max(copies, default=0.0)]
@@ -351,8 +352,11 @@ def _stage_means(rows: list[tuple[str, float]]) -> tuple[dict, float]:
         for stage, frags in STAGE_KERNELS.items():
             if any(f in name for f in frags):
                 sums[stage] += kib
-    warm = 1  # the first launch of each stage precedes the timed repeats
-    return {k: v / (PROBE_REPEATS + warm) for k, v in sums.items()}, sum(copy) / max(len(copy), 1)
+                counts[stage] += 1
+    # every launch of a stage does the same work (the warm-up and the setup launches that
+    # produce later stages' inputs included): the mean over all of them
+    return ({k: v / max(counts[k], 1) for k, v in sums.items()},
+            sum(copy) / max(len(copy), 1))
 
 
 def traffic_summary(fetch_csv: str, write_csv: str) -> dict:
@@ -407,6 +411,27 @@ def write_traffic_file(summary: dict, fetch_csv: str, write_csv: str) -> None:
     TRAFFIC_FILE.write_text("\n".join(lines))
 
 
+# VALU issue peak: every SIMD issues one wave64 VALU instruction per 4 cycles (16 lanes per
+# cycle; packed float32 doubles the lanes of its own instructions only).
+PEAK_VALU_WAVE_INSTS = 1024 * 2.4e9 / 4
+COUNTERS_FILE = REPO / "profiles" / f"op_step_M{M_TOK}_K{K_IN}_N{N_OUT}_counters.md"
+
+
+def measured_valu_insts(kernel: str):
+    """VALU wave instructions per launch of `kernel` from the committed counter summary."""
+    if not COUNTERS_FILE.is_file():
+        return None
+    text = COUNTERS_FILE.read_text()
+    start = text.find("```json")
+    if start < 0:
+        return None
+    body = text[start + 7:text.find("```", start + 7)]
+    try:
+        return json.loads(body)[kernel]["VALU_insts"]
+    except (ValueError, KeyError):
+        return None
+
+
 def measured_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
     if not TRAFFIC_FILE.is_file():
@@ -442,10 +467,19 @@ def roofline_entry(kernels: dict) -> dict:
                     "alg_ops_per_launch": e["alg_ops"], "alg_bytes_per_launch": e["alg_bytes"],
                     "avg_us": e["avg_us"]}
     achieved = e["alg_bytes"] / sec / 1e9
-    return {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1),
-            "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
-            "frac": round(achieved * 1e9 / PEAK_HBM_BPS, 4), "traffic": traffic,
-            "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
+    entry = {"kernel": name, "bound": "hbm", "achieved": round(achieved, 1),
+             "peak": PEAK_HBM_BPS / 1e9, "unit": "GB/s",
+             "frac": round(achieved * 1e9 / PEAK_HBM_BPS, 4), "traffic": traffic,
+             "alg_bytes_per_launch": e["alg_bytes"], "avg_us": e["avg_us"]}
+    insts = measured_valu_insts(name)
+    if insts:
+        # the stochastic-rounding quant issues ~50 VALU instructions per element (Philox):
+        # its binding roofline is VALU issue, reported beside the HBM one
+        rate = insts / sec
+        entry["valu"] = {"insts_per_launch": insts, "achieved": round(rate / 1e9, 1),
+                         "peak": PEAK_VALU_WAVE_INSTS / 1e9, "unit": "G wave-instr/s",
+                         "frac": round(rate / PEAK_VALU_WAVE_INSTS, 4)}
+    return entry
 
 
 # ---------------------------------------------------------------------------
@@ -512,6 +546,8 @@ def counter_summary(csv_paths: list[str]) -> str:
             d["mfma_i8_ops"] = mean["SQ_INSTS_VALU_MFMA_MOPS_I8"] * 512
         if mean.get("SQ_INSTS_VALU_MFMA_MOPS_BF16"):
             d["mfma_bf16_flops"] = mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512
+        if "SQ_INSTS_VALU" in mean:
+            d["VALU_insts"] = round(mean["SQ_INSTS_VALU"])  # wave instructions per launch
         if mean.get("SQ_WAVES"):
             for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU",
                       "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR"):
