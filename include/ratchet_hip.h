@@ -420,13 +420,14 @@ int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* 
  * grad [T, D] float32 / bfloat16 with row stride ldg; ids int64 (ids_int64 = 1) or int32.
  * The sum order is fixed: tokens in chunks of 64 positions, token order within a chunk,
  * chunk order across chunks; no memset, no device-wide sort (legal under HIP-graph
- * capture). work holds rk_embedding_backward_workspace(T, D) bytes, 16-byte aligned;
- * nothing needs clearing between calls.
+ * capture). work holds rk_embedding_backward_workspace(T, V, D) bytes, 16-byte aligned
+ * (per-chunk partial rows and a V x chunks byte table the call clears itself); nothing
+ * needs clearing between calls.
  * D % 4 != 0 or D > 4096: RK_ERR_UNSUPPORTED.
  * Replaces: the backward of the model's token lookup, model.py:237 (an nn.Embedding,
  *           model.py:219, whose torch backward sorts the ids on the device).
  */
-int64_t rk_embedding_backward_workspace(int64_t T, int64_t D);
+int64_t rk_embedding_backward_workspace(int64_t T, int64_t V, int64_t D);
 int rk_embedding_backward(const void* grad, int grad_dtype, int64_t ldg, const void* ids,
                           int ids_int64, int64_t T, int64_t V, int64_t D, float* out,
                           int64_t ldo, void* work, int64_t work_bytes, void* stream);

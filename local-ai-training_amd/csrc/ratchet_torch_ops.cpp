@@ -706,7 +706,7 @@ Tensor embedding_backward(const Tensor& grad_in, const Tensor& ids_in, int64_t n
   const int64_t t = grad.size(0);
   const c10::DeviceGuard guard(grad.device());
   Tensor out = at::empty({num_weights, d}, grad.options().dtype(at::kFloat));
-  const int64_t bytes = rk_embedding_backward_workspace(t, d);
+  const int64_t bytes = rk_embedding_backward_workspace(t, num_weights, d);
   Tensor work = at::empty({std::max<int64_t>(bytes, 16)}, grad.options().dtype(at::kByte));
   check_status(rk_embedding_backward(grad.data_ptr(), dtype_code(grad, "grad"),
                                      t > 1 ? grad.stride(0) : d, ids.data_ptr(),

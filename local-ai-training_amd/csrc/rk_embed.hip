@@ -7,24 +7,28 @@
 // rows of one id are summed in token order; the per-chunk sums of an id are then summed in
 // chunk order. (torch's embedding_dense_backward sorts the ids with a device radix sort
 // whose temporary state is cleared by a memset; inside a captured HIP graph that clear is a
-// memset node. These kernels need no clear and no global sort.)
+// memset node. These kernels clear with a kernel and need no global sort.)
 //
+//   embed_clear_kernel   sets the [V, chunks] slot table to "absent" (0xff bytes);
 //   embed_chunk_kernel   one wavefront per (chunk, 256-column slice): ranks the chunk's ids
-//                        (id, then position) with lane shuffles, writes the chunk's sorted
-//                        ids, and streams the chunk's gradient rows in sorted order into one
-//                        partial row per distinct id (stored at the id's first sorted slot).
-//   embed_gather_kernel  one wavefront per vocabulary row: each lane binary-searches one
-//                        chunk's sorted ids; the hits are summed in chunk (lane) order.
+//                        (id, then position) with lane shuffles and streams the chunk's
+//                        gradient rows in sorted order into one partial row per distinct id,
+//                        stored at the id's first sorted slot j; the table gets slot[v][c] = j;
+//   embed_gather_kernel  one wavefront per (vocabulary row, 256-column block): lane c reads
+//                        slot[v][c] (a coalesced row of bytes), and the present chunks'
+//                        partial rows are added in chunk (lane) order, 16 rows' loads in
+//                        flight.
 //
 // Bytes: the gradient is read once, the partial rows (at most one per token) are written
-// once and read once, and the [V, D] result is written once.
+// once and read once, the [V, D] result is written once, and the V x chunks byte table is
+// cleared, written sparsely and read once.
 #include "rk_common.h"
 
 namespace rk {
 
 constexpr int kEmbChunk = 64;            // tokens per chunk (one lane each)
 constexpr int kEmbCols = kWave * 4;      // columns per wavefront pass (4 per lane)
-constexpr int kEmbMaxBlocks = 16;        // column passes held in registers: D <= 4096
+constexpr int kEmbMaxBlocks = 16;        // D <= 4096 (256-column blocks)
 constexpr int32_t kNoId = 0x7fffffff;    // sorts after every valid id
 
 struct EmbedArgs {
@@ -33,8 +37,8 @@ struct EmbedArgs {
   const void* ids;
   int64_t T, V, D;
   float* partial;     // [chunks * kEmbChunk, D]
-  int32_t* sorted;    // [chunks * kEmbChunk]
-  int64_t chunks;
+  uint8_t* slot;      // [V, ldslot]: slot of id v's partial row in chunk c, 0xff if absent
+  int64_t chunks, ldslot;
   float* out;
   int64_t ldo;
 };
@@ -80,8 +84,9 @@ __global__ __launch_bounds__(64) void embed_chunk_kernel(EmbedArgs a) {
   s_id[rank] = id;
   s_tok[rank] = static_cast<int32_t>(t);
   __syncthreads();
-  if (blockIdx.y == 0) a.sorted[c * kEmbChunk + lane] = s_id[lane];
   const int valid = __popcll(__ballot(id != kNoId));  // sorted slots 0..valid-1 hold ids
+  if (blockIdx.y == 0 && lane < valid && (lane == 0 || s_id[lane - 1] != s_id[lane]))
+    a.slot[static_cast<int64_t>(s_id[lane]) * a.ldslot + c] = static_cast<uint8_t>(lane);
   const int64_t col = static_cast<int64_t>(blockIdx.y) * kEmbCols + lane * 4;
   if (col >= a.D) return;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -107,48 +112,55 @@ __global__ __launch_bounds__(64) void embed_chunk_kernel(EmbedArgs a) {
   }
 }
 
-template <int NB>
-__global__ __launch_bounds__(256) void embed_gather_kernel(EmbedArgs a) {
+__global__ __launch_bounds__(256) void embed_clear_kernel(uint4* p, int64_t n16) {
+  const uint4 ff = make_uint4(0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    p[i] = ff;
+}
+
+// One wavefront per (vocabulary row, 256-column block). A frequent id has a partial row in
+// nearly every chunk, so its wavefront walks up to `chunks` rows in order: the loads of
+// kEmbBatch of them are issued before the first is added, in chunk order.
+constexpr int kEmbBatch = 16;
+
+__global__ __launch_bounds__(256) void embed_gather_kernel(EmbedArgs a, int nb) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t v = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t v = w / nb;
   if (v >= a.V) return;
-  const int32_t vid = static_cast<int32_t>(v);
-  float4 acc[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) acc[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t col = static_cast<int64_t>(w - v * nb) * kEmbCols + lane * 4;
+  const bool colok = col < a.D;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const uint8_t* srow = a.slot + v * a.ldslot;
   for (int64_t g = 0; g < a.chunks; g += kWave) {
     const int64_t c = g + lane;
-    int64_t row = -1;
-    if (c < a.chunks) {
-      // first slot of chunk c whose sorted id is >= v
-      const int32_t* ids = a.sorted + c * kEmbChunk;
-      int lo = 0, hi = kEmbChunk;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (ids[mid] < vid) lo = mid + 1;
-        else hi = mid;
-      }
-      if (lo < kEmbChunk && ids[lo] == vid) row = c * kEmbChunk + lo;
-    }
-    uint64_t hits = __ballot(row >= 0);
+    const int j = c < a.chunks ? srow[c] : 0xff;
+    uint64_t hits = __ballot(j != 0xff);
+    const int64_t row = c * kEmbChunk + j;
     while (hits) {
-      const int k = __ffsll(static_cast<unsigned long long>(hits)) - 1;
-      hits &= hits - 1;
-      const int64_t r = __shfl(row, k, kWave);
-      const float* src = a.partial + r * a.D;
+      int64_t rr[kEmbBatch];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int64_t col = static_cast<int64_t>(b) * kEmbCols + lane * 4;
-        if (col < a.D) add4(acc[b], *reinterpret_cast<const float4*>(src + col));
+      for (int u = 0; u < kEmbBatch; ++u) {
+        rr[u] = -1;
+        if (hits) {
+          const int k = __ffsll(static_cast<unsigned long long>(hits)) - 1;
+          hits &= hits - 1;
+          rr[u] = __shfl(row, k, kWave);
+        }
       }
+      float4 x[kEmbBatch];
+#pragma unroll
+      for (int u = 0; u < kEmbBatch; ++u)
+        x[u] = (rr[u] >= 0 && colok)
+                   ? *reinterpret_cast<const float4*>(a.partial + rr[u] * a.D + col)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < kEmbBatch; ++u)
+        if (rr[u] >= 0) add4(acc, x[u]);
     }
   }
-  float* dst = a.out + v * a.ldo;
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const int64_t col = static_cast<int64_t>(b) * kEmbCols + lane * 4;
-    if (col < a.D) *reinterpret_cast<float4*>(dst + col) = acc[b];
-  }
+  if (colok) *reinterpret_cast<float4*>(a.out + v * a.ldo + col) = acc;
 }
 
 static int64_t embed_chunks(int64_t T) { return (T + kEmbChunk - 1) / kEmbChunk; }
@@ -157,10 +169,13 @@ static int64_t embed_chunks(int64_t T) { return (T + kEmbChunk - 1) / kEmbChunk;
 
 using namespace rk;
 
-extern "C" int64_t rk_embedding_backward_workspace(int64_t T, int64_t D) {
-  if (T < 0 || D < 0) return -1;
+// slot-table row: one byte per chunk, padded to 16 bytes
+static int64_t embed_ldslot(int64_t T) { return (embed_chunks(T) + 15) / 16 * 16; }
+
+extern "C" int64_t rk_embedding_backward_workspace(int64_t T, int64_t V, int64_t D) {
+  if (T < 0 || V < 0 || D < 0) return -1;
   const int64_t slots = embed_chunks(T) * kEmbChunk;
-  return slots * D * 4 + slots * 4;
+  return slots * D * 4 + V * embed_ldslot(T);
 }
 
 extern "C" int rk_embedding_backward(const void* grad, int grad_dtype, int64_t ldg,
@@ -183,7 +198,7 @@ extern "C" int rk_embedding_backward(const void* grad, int grad_dtype, int64_t l
   const int gsz = dtype_size(grad_dtype);
   if ((reinterpret_cast<uintptr_t>(grad) % (4 * gsz)) != 0 || !aligned16(out) || !aligned16(work))
     return fail(RK_ERR_ARG, "grad, out and work must be aligned to 4 elements / 16 bytes");
-  const int64_t need = rk_embedding_backward_workspace(T, D);
+  const int64_t need = rk_embedding_backward_workspace(T, V, D);
   if (work_bytes < need)
     return fail(RK_ERR_ARG, "workspace of %lld bytes below the %lld needed",
                 static_cast<long long>(work_bytes), static_cast<long long>(need));
@@ -196,11 +211,17 @@ extern "C" int rk_embedding_backward(const void* grad, int grad_dtype, int64_t l
   a.D = D;
   a.chunks = embed_chunks(T);
   a.partial = static_cast<float*>(work);
-  a.sorted = reinterpret_cast<int32_t*>(static_cast<char*>(work) + a.chunks * kEmbChunk * D * 4);
+  a.slot = static_cast<uint8_t*>(work) + a.chunks * kEmbChunk * D * 4;
+  a.ldslot = embed_ldslot(T);
   a.out = out;
   a.ldo = ldo;
   hipStream_t st = as_stream(stream);
   if (a.chunks > 0) {
+    const int64_t n16 = V * a.ldslot / 16;
+    const int64_t cb = (n16 + 255) / 256;
+    embed_clear_kernel<<<static_cast<unsigned>(cb < 2048 ? cb : 2048), 256, 0, st>>>(
+        reinterpret_cast<uint4*>(a.slot), n16);
+    if (int e = launch_status("embedding_backward clear")) return e;
     const dim3 grid(static_cast<unsigned>(a.chunks),
                     static_cast<unsigned>((D + kEmbCols - 1) / kEmbCols));
     if (grad_dtype == RK_F32) {
@@ -213,12 +234,8 @@ extern "C" int rk_embedding_backward(const void* grad, int grad_dtype, int64_t l
     const int rc = launch_status("embedding_backward chunks");
     if (rc != RK_OK) return rc;
   }
-  const dim3 ggrid(static_cast<unsigned>((V + 3) / 4));
-  const int64_t nb = (D + kEmbCols - 1) / kEmbCols;
-  if (nb <= 1) embed_gather_kernel<1><<<ggrid, 256, 0, st>>>(a);
-  else if (nb <= 2) embed_gather_kernel<2><<<ggrid, 256, 0, st>>>(a);
-  else if (nb <= 4) embed_gather_kernel<4><<<ggrid, 256, 0, st>>>(a);
-  else if (nb <= 8) embed_gather_kernel<8><<<ggrid, 256, 0, st>>>(a);
-  else embed_gather_kernel<16><<<ggrid, 256, 0, st>>>(a);
+  const int nb = static_cast<int>((D + kEmbCols - 1) / kEmbCols);
+  const int64_t waves = V * nb;
+  embed_gather_kernel<<<static_cast<unsigned>((waves + 3) / 4), 256, 0, st>>>(a, nb);
   return launch_status("embedding_backward gather");
 }

@@ -65,7 +65,7 @@ def test_embedding_backward_through_the_c_abi_with_ids_outside_the_table(cuda):
     g = torch.randn(t, d, device=cuda)
     ids = torch.randint(-3, v + 3, (t,), device=cuda)
     out = torch.full((v, d), float("nan"), device=cuda)
-    nbytes = int(nat.load_library().rk_embedding_backward_workspace(t, d))
+    nbytes = int(nat.load_library().rk_embedding_backward_workspace(t, v, d))
     work = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
     nat.call("rk_embedding_backward", g.data_ptr(), nat.RK_F32, d, ids.data_ptr(), 1, t, v, d,
              out.data_ptr(), d, work.data_ptr(), nbytes, nat.stream_handle(cuda))
