@@ -401,6 +401,21 @@ int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg, const voi
                         int64_t K, void* grad_x, int64_t ldgx, float* grad_w, float* workspace,
                         int64_t workspace_floats, void* stream);
 
+/*
+ * rk_rmsnorm_backward for a float32 x whose rows also feed the residual stream:
+ *   grad_x = float32(bf16(dx)) + residual_grad
+ * (one float32 add per element, the add autograd performs where x has both uses), with
+ * residual_grad [M, K] float32, row stride ldr. residual_grad may be grad_x itself (same
+ * row stride); any other overlap is rejected. grad_w as rk_rmsnorm_backward.
+ * Replaces: rmsnorm_backward  int8_backward.py:7-51 plus the residual add of the block,
+ *           model.py:181-195 (inputs = inputs + self.attention(self.attention_norm(inputs))).
+ */
+int rk_rmsnorm_backward_residual(const void* grad_y, int gy_dtype, int64_t ldg, const float* x,
+                                 int64_t ldx, const float* w, float eps, int64_t M, int64_t K,
+                                 const float* residual_grad, int64_t ldr, float* grad_x,
+                                 int64_t ldgx, float* grad_w, float* workspace,
+                                 int64_t workspace_floats, void* stream);
+
 /* Number of grad_w partial rows rk_rmsnorm_backward uses for M rows (0 for M <= 0, at most 512). */
 int rk_rmsnorm_backward_parts(int64_t M);
 

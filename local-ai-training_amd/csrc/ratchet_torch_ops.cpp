@@ -649,7 +649,8 @@ std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in) {
 }
 
 std::tuple<Tensor, Tensor> rmsnorm_backward(const Tensor& gy_in, const Tensor& x_in,
-                                            const Tensor& w_in, double eps) {
+                                            const Tensor& w_in, double eps,
+                                            const OptTensor& residual_grad) {
   require_gpu(x_in, "RMSNorm backward");
   const Tensor x = float_rows(x_in);
   const Tensor gy = float_rows(gy_in);
@@ -662,6 +663,22 @@ std::tuple<Tensor, Tensor> rmsnorm_backward(const Tensor& gy_in, const Tensor& x
   if (k == 0) return {grad_x, grad_w};
   const int64_t parts = std::max<int64_t>(rk_rmsnorm_backward_parts(m), 1);
   Tensor work = at::empty({parts, k}, x.options().dtype(at::kFloat));
+  if (residual_grad.has_value()) {
+    // grad_x = bf16(dx) + residual_grad in one pass (float32 x: the residual stream)
+    TORCH_CHECK(x.scalar_type() == at::kFloat,
+                "RMSNorm backward with a residual gradient needs float32 x");
+    TORCH_CHECK(residual_grad->scalar_type() == at::kFloat && residual_grad->numel() == m * k,
+                "residual_grad must be float32 with x's shape");
+    same_device(*residual_grad, x, "RMSNorm backward");
+    const Tensor r = unit_columns(residual_grad->reshape({m, k}));
+    check_status(rk_rmsnorm_backward_residual(
+                     gy.data_ptr(), dtype_code(gy, "grad_y"), ld(gy), x.data_ptr<float>(), ld(x),
+                     w.data_ptr<float>(), static_cast<float>(eps), m, k, r.data_ptr<float>(),
+                     ld(r), static_cast<float*>(grad_x.data_ptr()), k, grad_w.data_ptr<float>(),
+                     work.data_ptr<float>(), work.numel(), stream_of(x)),
+                 "rk_rmsnorm_backward_residual");
+    return {grad_x, grad_w};
+  }
   check_status(rk_rmsnorm_backward(gy.data_ptr(), dtype_code(gy, "grad_y"), ld(gy),
                                    x.data_ptr(), dtype_code(x, "x"), ld(x), w.data_ptr<float>(),
                                    static_cast<float>(eps), m, k, grad_x.data_ptr(), k,
@@ -769,7 +786,9 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("rmsnorm_quantize(Tensor x, Tensor w, float eps) -> (Tensor, Tensor)");
   m.def("gelu_quantize(Tensor x) -> (Tensor, Tensor)");
   m.def("transpose_quantize(Tensor x) -> (Tensor, Tensor)");
-  m.def("rmsnorm_backward(Tensor grad_y, Tensor x, Tensor w, float eps) -> (Tensor, Tensor)");
+  m.def(
+      "rmsnorm_backward(Tensor grad_y, Tensor x, Tensor w, float eps, "
+      "Tensor? residual_grad=None) -> (Tensor, Tensor)");
   m.def("gelu_backward(Tensor grad_y, Tensor x) -> Tensor");
   m.def("embedding_backward(Tensor grad, Tensor ids, int num_weights) -> Tensor");
 }

@@ -98,6 +98,8 @@ struct NormBwdArgs {
   float* part;             // [gridDim.x][K] grad_w partial of each block
   int64_t rows_per_block;  // a multiple of 4
   int vec;                 // 4-element vector access is legal for x, grad_y, grad_x and w
+  const float* add;        // float32 x only: grad_x = float32(bf16(dx)) + add (may be grad_x)
+  int64_t lda;
 };
 
 template <int GDT, int XDT, int NC>
@@ -165,6 +167,25 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
         gw[c][i] = gw[c][i] + gv[c][i] * xv[c][i] * rs;
       }
       const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+      if constexpr (XDT == RK_F32) {
+        if (a.add && nv[c] > 0) {
+          // the residual stream's gradient joins here: one float32 add of the two
+          // contributions, the add autograd performs where x feeds both paths
+          float ad[kBwdV];
+          load4<RK_F32>(a.add, row * a.lda + e0, nv[c], a.vec, ad);
+#pragma unroll
+          for (int i = 0; i < kBwdV; ++i) dx[i] = round_bf16(dx[i]) + ad[i];
+          float* p = static_cast<float*>(a.gx) + row * a.ldgx + e0;
+          if (a.vec && nv[c] == 4) {
+            *reinterpret_cast<float4*>(p) = make_float4(dx[0], dx[1], dx[2], dx[3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < kBwdV; ++i)
+              if (i < nv[c]) p[i] = dx[i];
+          }
+          continue;
+        }
+      }
       if (nv[c] > 0) store4_bf16<XDT>(a.gx, row * a.ldgx + e0, nv[c], a.vec, dx);
     }
     if constexpr (PREFETCH) {
@@ -296,10 +317,11 @@ extern "C" int rk_rmsnorm_backward_parts(int64_t M) {
   return static_cast<int>((M + rpb - 1) / rpb);  // <= kBwdTargetBlocks
 }
 
-extern "C" int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
-                                   int x_dtype, int64_t ldx, const float* w, float eps, int64_t M,
-                                   int64_t K, void* grad_x, int64_t ldgx, float* grad_w,
-                                   float* workspace, int64_t workspace_floats, void* stream) {
+static int rmsnorm_backward_entry(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
+                                  int x_dtype, int64_t ldx, const float* w, float eps, int64_t M,
+                                  int64_t K, const float* add, int64_t lda, void* grad_x,
+                                  int64_t ldgx, float* grad_w, float* workspace,
+                                  int64_t workspace_floats, void* stream) {
   clear_error();
   if (M < 0 || K < 0) return fail(RK_ERR_ARG, "negative size M=%lld K=%lld", (long long)M,
                                   (long long)K);
@@ -322,12 +344,15 @@ extern "C" int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg
   if (workspace_floats < nparts * K)
     return fail(RK_ERR_ARG, "workspace holds %lld floats, needs %lld",
                 (long long)workspace_floats, (long long)(nparts * K));
+  if (add && lda < K) return fail(RK_ERR_ARG, "leading dimension below K");
   NormBwdArgs a{};
   a.gy = grad_y; a.ldg = ldg; a.x = x; a.ldx = ldx; a.w = w; a.eps = eps;
   a.M = M; a.K = K; a.gx = grad_x; a.ldgx = ldgx; a.part = workspace;
+  a.add = add; a.lda = lda;
   a.rows_per_block = norm_rows_per_block(M);
   a.vec = vec4_ok(grad_y, gy_dtype, ldg, K) && vec4_ok(x, x_dtype, ldx, K) &&
-          vec4_ok(grad_x, x_dtype, ldgx, K) && vec4_ok(w, RK_F32, K, K);
+          vec4_ok(grad_x, x_dtype, ldgx, K) && vec4_ok(w, RK_F32, K, K) &&
+          (!add || vec4_ok(add, RK_F32, lda, K));
   const dim3 grid(static_cast<unsigned>(nparts));
   int e;
   if (gy_dtype == RK_F32) {
@@ -340,6 +365,44 @@ extern "C" int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg
   if (e) return e;
   rmsnorm_gw_reduce_kernel<<<reduce_grid, dim3(256), 0, st>>>(workspace, nparts, K, grad_w);
   return launch_status("rmsnorm_backward_reduce");
+}
+
+extern "C" int rk_rmsnorm_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,
+                                   int x_dtype, int64_t ldx, const float* w, float eps, int64_t M,
+                                   int64_t K, void* grad_x, int64_t ldgx, float* grad_w,
+                                   float* workspace, int64_t workspace_floats, void* stream) {
+  return rmsnorm_backward_entry(grad_y, gy_dtype, ldg, x, x_dtype, ldx, w, eps, M, K, nullptr, 0,
+                                grad_x, ldgx, grad_w, workspace, workspace_floats, stream);
+}
+
+extern "C" int rk_rmsnorm_backward_residual(const void* grad_y, int gy_dtype, int64_t ldg,
+                                            const float* x, int64_t ldx, const float* w, float eps,
+                                            int64_t M, int64_t K, const float* residual_grad,
+                                            int64_t ldr, float* grad_x, int64_t ldgx,
+                                            float* grad_w, float* workspace,
+                                            int64_t workspace_floats, void* stream) {
+  if (M > 0 && K > 0 && !residual_grad) {
+    clear_error();
+    return fail(RK_ERR_ARG, "null residual gradient");
+  }
+  if (residual_grad && residual_grad != grad_x) {
+    // any overlap other than the same rows in place would let one row's store reach
+    // another row's unread residual gradient
+    const char* r0 = reinterpret_cast<const char*>(residual_grad);
+    const char* r1 = r0 + ((M > 0 ? M - 1 : 0) * ldr + K) * 4;
+    const char* g0 = reinterpret_cast<const char*>(grad_x);
+    const char* g1 = g0 + ((M > 0 ? M - 1 : 0) * ldgx + K) * 4;
+    if (M > 0 && K > 0 && r0 < g1 && g0 < r1) {
+      clear_error();
+      return fail(RK_ERR_ARG, "residual gradient partly overlaps grad_x");
+    }
+  } else if (residual_grad && ldr != ldgx) {
+    clear_error();
+    return fail(RK_ERR_ARG, "in place needs the same row stride");
+  }
+  return rmsnorm_backward_entry(grad_y, gy_dtype, ldg, x, RK_F32, ldx, w, eps, M, K,
+                                residual_grad, ldr, grad_x, ldgx, grad_w, workspace,
+                                workspace_floats, stream);
 }
 
 extern "C" int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, const void* x,

@@ -76,6 +76,8 @@ SIGNATURES: dict[str, list] = {
     "rk_rmsnorm_backward": [_p, _i32, _i64, _p, _i32, _i64, _p, _f32, _i64, _i64, _p, _i64, _p,
                             _p, _i64, _p],
     "rk_rmsnorm_backward_parts": [_i64],
+    "rk_rmsnorm_backward_residual": [_p, _i32, _i64, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p,
+                                     _i64, _p, _p, _i64, _p],
     "rk_gelu_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "rk_decode_gemv": [_p, _i64, _p, _i64, _p, _i32, _p, _f32, _p, _i64, _i32, _p, _p, _i32,
                        _i64, _i32, _i64, _i64, _i64, _p],

@@ -43,8 +43,10 @@ def _rmsnorm_backward_torch(gy: Tensor, x_flat: Tensor, w: Tensor, eps: float
     return dx.to(torch.bfloat16).to(x_flat.dtype), (gf * xf * rsqrt).sum(dim=0)
 
 
-def rmsnorm_backward(grad_y: Tensor, x: Tensor, w: Tensor, eps: float = 1e-5
-                     ) -> tuple[Tensor, Tensor]:
+def rmsnorm_backward(grad_y: Tensor, x: Tensor, w: Tensor, eps: float = 1e-5, *,
+                     residual_grad: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """``residual_grad`` (float32 x only): the gradient x also receives as the residual
+    stream, added to grad_x in the same pass (the float32 add autograd would do)."""
     if not x.is_cuda:
         raise RuntimeError("CUDA required (a ROCm GPU)")
     x_flat = _rows(_float_or_bf16(x))
@@ -53,11 +55,19 @@ def rmsnorm_backward(grad_y: Tensor, x: Tensor, w: Tensor, eps: float = 1e-5
     if gy.shape != x_flat.shape:
         raise ValueError(f"grad_y {tuple(grad_y.shape)} does not match x {tuple(x.shape)}")
     wf = w.float().contiguous()
+    fuse = residual_grad is not None and x_flat.dtype == torch.float32 and k <= _MAX_NORM_K \
+        and residual_grad.dtype == torch.float32
     if k > _MAX_NORM_K:
         grad_x, grad_w = _rmsnorm_backward_torch(gy, x_flat, wf, eps)
+    elif fuse:
+        grad_x, grad_w = _ops().rmsnorm_backward(gy, x_flat, wf, float(eps),
+                                                 _rows(residual_grad))
     else:
         grad_x, grad_w = _ops().rmsnorm_backward(gy, x_flat, wf, float(eps))
-    return grad_x.to(x.dtype).reshape(x.shape), grad_w.to(w.dtype)
+    grad_x = grad_x.to(x.dtype).reshape(x.shape)
+    if residual_grad is not None and not fuse:
+        grad_x = grad_x + residual_grad
+    return grad_x, grad_w.to(w.dtype)
 
 
 def gelu_backward(grad_y: Tensor, x: Tensor) -> Tensor:

@@ -73,6 +73,32 @@ class FusedRMSNormQuantizeFn(torch.autograd.Function):
         return grad_x, grad_w, None
 
 
+class FusedRMSNormQuantizeResidualFn(torch.autograd.Function):
+    """FusedRMSNormQuantizeFn for an x that also continues as the residual stream: returns
+    (int8, scale, dummy, x). Both of x's gradients then arrive in this backward, which adds
+    them in the RMSNorm backward kernel's store (the same float32 add autograd performs when
+    x feeds two separate uses) instead of a separate add kernel."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor, eps: float = 1e-5):
+        int8_out, scale_out = fused_rmsnorm_quantize(x, weight, eps)
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        _no_grad_outputs(ctx, int8_out, scale_out)
+        return int8_out, scale_out, torch.empty_like(x), x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, grad_int8, grad_scale, grad_dummy, grad_residual):
+        x, weight = ctx.saved_tensors
+        if grad_dummy is None:
+            return grad_residual, None, None
+        from .int8_backward import rmsnorm_backward
+
+        grad_x, grad_w = rmsnorm_backward(grad_dummy, x, weight, ctx.eps,
+                                          residual_grad=grad_residual)
+        return grad_x, grad_w, None
+
+
 class FusedGELUQuantizeFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor):

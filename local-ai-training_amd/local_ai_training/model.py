@@ -21,7 +21,12 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from .int8_fused import FusedGELUQuantizeFn, FusedRMSNormQuantizeFn, FusedTransposeQuantizeFn
+from .int8_fused import (
+    FusedGELUQuantizeFn,
+    FusedRMSNormQuantizeFn,
+    FusedRMSNormQuantizeResidualFn,
+    FusedTransposeQuantizeFn,
+)
 from .ratchet import DiscreteRatchetLinear, RatchetEmbedding, RatchetUpdateStats
 
 
@@ -322,6 +327,9 @@ class TransformerBlock(nn.Module):
     # int8 blocks hand the residual stream to the attention projection and the feed-forward
     # contraction, whose GEMMs add it in their epilogue (the same float32 add)
     fuse_residual: bool = True
+    # with fuse_residual: the block input's two gradients are added in the RMSNorm backward
+    # kernel's store instead of by autograd (the same float32 add)
+    fuse_residual_grad: bool = True
 
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -333,22 +341,38 @@ class TransformerBlock(nn.Module):
     def forward(self, inputs: Tensor, *, cache: KVCache | None = None, layer: int = 0,
                 decode: bool = False) -> Tensor:
         kv = dict(cache=cache, layer=layer, decode=decode) if cache is not None else {}
+        fuse_grad = self.fuse_residual and self.fuse_residual_grad
         if _is_int8(self.attention.qkv):
-            q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight, 1e-5)
-            if self.fuse_residual:
-                inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, residual=inputs,
+            if fuse_grad:
+                # the block input's two gradients (normalized path, residual stream) meet
+                # in the RMSNorm backward's store instead of a separate add
+                q, s, dummy, res = FusedRMSNormQuantizeResidualFn.apply(
+                    inputs, self.attention_norm.weight, 1e-5)
+                inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, residual=res,
                                         **kv)
             else:
-                inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s, **kv)
+                q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight,
+                                                           1e-5)
+                if self.fuse_residual:
+                    inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s,
+                                            residual=inputs, **kv)
+                else:
+                    inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s, **kv)
         else:
             inputs = inputs + self.attention(self.attention_norm(inputs), **kv)
         if _is_int8(self.feed_forward.expand):
-            q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
-                                                       1e-5)
-            if self.fuse_residual:
-                inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s, residual=inputs)
+            if fuse_grad:
+                q, s, dummy, res = FusedRMSNormQuantizeResidualFn.apply(
+                    inputs, self.feed_forward_norm.weight, 1e-5)
+                inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s, residual=res)
             else:
-                inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
+                q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
+                                                           1e-5)
+                if self.fuse_residual:
+                    inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s,
+                                               residual=inputs)
+                else:
+                    inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
         else:
             inputs = inputs + self.feed_forward(self.feed_forward_norm(inputs))
         return inputs

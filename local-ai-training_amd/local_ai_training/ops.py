@@ -140,7 +140,7 @@ def _register_fakes() -> None:
         return x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
 
     @fake("ratchet::rmsnorm_backward")
-    def _rmsnorm_backward(grad_y, x, w, eps):
+    def _rmsnorm_backward(grad_y, x, w, eps, residual_grad=None):
         return (x.new_empty((x.shape[0], x.shape[1]), dtype=float_dtype(x)),
                 x.new_empty((x.shape[1],), dtype=torch.float32))
 

@@ -122,10 +122,12 @@ def test_fused_transpose_quantize_is_exact(cuda, dtype):
     assert torch.equal(q2.cpu(), q.cpu()) and torch.equal(s2.cpu(), s.cpu())
 
 
-def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True):
+def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True,
+                fuse_grad: bool = True):
     from local_ai_training.model import FeedForward, TransformerBlock
 
     TransformerBlock.fuse_residual = fuse
+    TransformerBlock.fuse_residual_grad = fuse_grad
     FeedForward.bf16_expand = bf16_expand
     try:
         torch.manual_seed(0)
@@ -149,6 +151,7 @@ def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True):
         return losses, states, params
     finally:
         TransformerBlock.fuse_residual = True
+        TransformerBlock.fuse_residual_grad = True
         FeedForward.bf16_expand = True
 
 
@@ -200,6 +203,31 @@ def test_bf16_expansion_hand_off_changes_nothing(cuda, fuse):
         int8_backward.gelu_backward = gelu_bwd
     assert seen and all(d == (torch.bfloat16, torch.bfloat16) for d in seen)
     lb, sb, pb = _int8_steps(cuda, fuse=fuse, bf16_expand=False)
+    assert all(torch.equal(x, y) for x, y in zip(la, lb))
+    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
+    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
+
+
+def test_residual_gradient_added_in_the_rmsnorm_backward_changes_nothing(cuda):
+    # The block input's gradient from the residual stream added in the RMSNorm backward's
+    # store (FusedRMSNormQuantizeResidualFn) instead of by autograd: identical losses,
+    # ratchet states and float parameters over three steps, and no separate add runs.
+    from local_ai_training import int8_backward
+
+    calls = []
+    orig = int8_backward.rmsnorm_backward
+
+    def recording(*args, **kwargs):
+        calls.append(kwargs.get("residual_grad") is not None)
+        return orig(*args, **kwargs)
+
+    int8_backward.rmsnorm_backward = recording
+    try:
+        la, sa, pa = _int8_steps(cuda, fuse=True, fuse_grad=True)
+    finally:
+        int8_backward.rmsnorm_backward = orig
+    assert calls and all(calls)
+    lb, sb, pb = _int8_steps(cuda, fuse=True, fuse_grad=False)
     assert all(torch.equal(x, y) for x, y in zip(la, lb))
     assert all(torch.equal(x, y) for x, y in zip(sa, sb))
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))

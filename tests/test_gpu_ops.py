@@ -93,6 +93,8 @@ def cases(t, cuda):
         (R.gelu_quantize, (t["xb"],), {}),
         (R.transpose_quantize, (t["att"],), {}),
         (R.rmsnorm_backward, (t["xb"], t["xb"], torch.ones(K, device=cuda), 1e-5), {}),
+        (R.rmsnorm_backward, (t["xb"], t["x"], torch.ones(K, device=cuda), 1e-5, t["x"] * 0.5),
+         {}),
         (R.gelu_backward, (t["x"], t["x"]), {}),
         (R.embedding_backward, (t["x"], torch.randint(0, 40, (M,), generator=gen(5)).to(cuda),
                                 40), {}),

@@ -15,11 +15,17 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from local_ai_training import _native as nat
+from local_ai_training import ops
 from local_ai_training.int8_backward import gelu_backward, rmsnorm_backward
 
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.bfloat16]
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
 
 
 def _rms_reference(x: torch.Tensor, gy: torch.Tensor, w: torch.Tensor, eps: float):
@@ -96,6 +102,54 @@ def test_rmsnorm_backward_is_reproducible(cuda):
     b = rmsnorm_backward(gy, x, w)
     torch.cuda.synchronize()
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+@pytest.mark.parametrize("m,k,g_dtype", [(16384, 512, torch.bfloat16), (300, 2048, torch.float32),
+                                         (37, 200, torch.bfloat16), (8, 4096, torch.float32)])
+def test_rmsnorm_backward_with_residual_gradient_equals_backward_then_add(cuda, m, k, g_dtype):
+    # grad_x = bf16(dx) + residual_grad in the kernel's store: the same bits as the plain
+    # backward followed by the float32 add autograd performs for a block input with two uses;
+    # through the operator, and through the C ABI out of place and in place
+    x = (torch.randn(m, k, generator=gen(m + k)) * 2.0).to(cuda)
+    w = (torch.rand(k, generator=gen(3)) + 0.5).to(cuda)
+    gy = (torch.randn(m, k, generator=gen(4)) * 1e-2).to(g_dtype).to(cuda)
+    res = (torch.randn(m, k, generator=gen(5)) * 1e-2).to(cuda)
+    gx0, gw0 = rmsnorm_backward(gy, x, w, 1e-5)
+    want = gx0 + res
+    gx1, gw1 = rmsnorm_backward(gy, x, w, 1e-5, residual_grad=res)
+    assert torch.equal(gx1.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(gw1, gw0)
+    parts = int(nat.load_library().rk_rmsnorm_backward_parts(m))
+    work = torch.empty(parts, k, device=cuda)
+    gw2 = torch.empty(k, device=cuda)
+    out = torch.empty(m, k, device=cuda)
+    gdt = nat.RK_F32 if g_dtype == torch.float32 else nat.RK_BF16
+    args = (gy.data_ptr(), gdt, k, x.data_ptr(), k, w.data_ptr(), 1e-5, m, k)
+    tail = (gw2.data_ptr(), work.data_ptr(), work.numel(), nat.stream_handle(cuda))
+    nat.call("rk_rmsnorm_backward_residual", *args, res.data_ptr(), k, out.data_ptr(), k, *tail)
+    inplace = res.clone()
+    nat.call("rk_rmsnorm_backward_residual", *args, inplace.data_ptr(), k, inplace.data_ptr(),
+             k, *tail)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(inplace.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(gw2, gw0)
+
+
+def test_rmsnorm_backward_residual_rejects_partial_overlap_and_bf16_x(cuda):
+    m, k = 64, 256
+    x = torch.randn(m, k, device=cuda)
+    w = torch.ones(k, device=cuda)
+    gy = torch.randn(m, k, device=cuda)
+    buf = torch.randn(m + 1, k, device=cuda)
+    work = torch.empty(int(nat.load_library().rk_rmsnorm_backward_parts(m)), k, device=cuda)
+    gw = torch.empty(k, device=cuda)
+    with pytest.raises(nat.NativeError, match="overlap"):
+        nat.call("rk_rmsnorm_backward_residual", gy.data_ptr(), nat.RK_F32, k, x.data_ptr(), k,
+                 w.data_ptr(), 1e-5, m, k, buf[1:].data_ptr(), k, buf[:-1].data_ptr(), k,
+                 gw.data_ptr(), work.data_ptr(), work.numel(), nat.stream_handle(cuda))
+    with pytest.raises(RuntimeError, match="float32 x"):
+        ops.ratchet().rmsnorm_backward(gy, x.to(torch.bfloat16), w, 1e-5, gy)
 
 
 def test_rmsnorm_backward_wide_rows_use_the_tensor_formulas(cuda):
