@@ -396,6 +396,8 @@ class RatchetGPT(nn.Module):
     fused_decode: bool = True
     # the token embedding's weight gradient from the HIP kernels (False: torch's backward)
     hip_embedding_backward: bool = True
+    # the layers' move counts in one model-level buffer, summed and cleared once per step
+    shared_move_counts: bool = True
 
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -427,6 +429,8 @@ class RatchetGPT(nn.Module):
         sequence_length = tokens.shape[1]
         if sequence_length > self.config.block_size:
             raise ValueError("token sequence exceeds configured block_size")
+        if self.training and torch.is_grad_enabled() and self.shared_move_counts:
+            self._attach_count_slots()
         if self.hip_embedding_backward and _hip_lookup_supported(self.token_embedding, tokens):
             looked_up = _TokenLookup.apply(tokens, self.token_embedding.weight)
         else:
@@ -434,9 +438,9 @@ class RatchetGPT(nn.Module):
         hidden = looked_up + self.position_encoding[:sequence_length]
         for block in self.blocks:
             if self.config.gradient_checkpointing and self.training:
-                import torch.utils.checkpoint
+                from torch.utils.checkpoint import checkpoint
 
-                hidden = torch.utils.checkpoint.checkpoint(block, hidden, use_reentrant=False)
+                hidden = checkpoint(block, hidden, use_reentrant=False)
             else:
                 hidden = block(hidden)
         logits = self.lm_head(self.final_norm(hidden))
@@ -497,15 +501,56 @@ class RatchetGPT(nn.Module):
             hidden = block(hidden, cache=cache, layer=index, decode=True)
         return self.lm_head(self.final_norm(hidden))[:, 0]
 
+    def _attach_count_slots(self) -> None:
+        """One int64 [layers, 4] move-count buffer for every ratchet layer of the model (each
+        layer's update adds into its row): summed and cleared once per step by
+        ``ratchet_update`` instead of one zero-filled tensor per layer and step."""
+        layers = [m for m in self.modules() if isinstance(m, DiscreteRatchetLinear)]
+        if not layers:
+            return
+        device = layers[0].packed.device
+        buf = getattr(self, "_count_slots", None)
+        if (buf is not None and buf.device == device and buf.shape[0] == len(layers)
+                and all(m._counts_slot is not None for m in layers)):
+            return
+        buf = torch.zeros(len(layers), 4, dtype=torch.int64, device=device)
+        for i, m in enumerate(layers):
+            m._counts_slot = buf[i]
+            m._slot_dirty = False
+        self._count_slots = buf
+
     def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
-        updates = [m.ratchet_update(validate=validate) for m in self.modules()
-                   if isinstance(m, DiscreteRatchetLinear)]
+        layers = [m for m in self.modules() if isinstance(m, DiscreteRatchetLinear)]
+        buf = getattr(self, "_count_slots", None)
+        shared = (buf is not None and buf.shape[0] == len(layers)
+                  and all(m._counts_slot is not None and m._counts_slot.data_ptr()
+                          == buf[i].data_ptr() for i, m in enumerate(layers)))
+        if shared:
+            # slots whose counts a layer-level ratchet_update already reported
+            for i, m in enumerate(layers):
+                if m._slot_dirty:
+                    buf[i].zero_()
+                    m._slot_dirty = False
+        updates = [m.ratchet_update(validate=validate) for m in layers]
+        if shared:
+            # the layers' counts live in one buffer: one reduction for the four totals,
+            # then the buffer is cleared for the next step
+            totals = buf.sum(dim=0)
+            moves = (totals[0], totals[1], totals[2], totals[3])
+            buf.zero_()
+            for m in layers:
+                m._slot_dirty = False
+        else:
+            moves = (_total(u.positive_moves for u in updates),
+                     _total(u.negative_moves for u in updates),
+                     _total(u.blocked_positive_moves for u in updates),
+                     _total(u.blocked_negative_moves for u in updates))
         aggregated = RatchetUpdateStats(
             total_weights=sum(u.total_weights for u in updates),
-            positive_moves=_total(u.positive_moves for u in updates),
-            negative_moves=_total(u.negative_moves for u in updates),
-            blocked_positive_moves=_total(u.blocked_positive_moves for u in updates),
-            blocked_negative_moves=_total(u.blocked_negative_moves for u in updates),
+            positive_moves=moves[0],
+            negative_moves=moves[1],
+            blocked_positive_moves=moves[2],
+            blocked_negative_moves=moves[3],
             gradient_rms_mean=(_total(u.gradient_rms_mean for u in updates) / len(updates)
                                if updates else 0.0),
         )

@@ -538,6 +538,11 @@ class DiscreteRatchetLinear(nn.Module):
         self._effective_weight: Tensor | None = None
         self._pending_weight_gradient: Tensor | None = None
         self._generation = 0
+        # a model may hand the layer a [4] view of one counts buffer for all its layers
+        # (summed and cleared once per step by the model); `_slot_dirty`: the slot still
+        # holds counts a layer-level ratchet_update consumed
+        self._counts_slot: Tensor | None = None
+        self._slot_dirty = False
         self._reset_pending_stats()
 
     # -- state ----------------------------------------------------------------
@@ -590,7 +595,15 @@ class DiscreteRatchetLinear(nn.Module):
 
     def _counts(self) -> Tensor:
         if self._pending_counts is None:
-            self._pending_counts = torch.zeros(4, dtype=torch.int64, device=self.packed.device)
+            slot = self._counts_slot
+            if slot is not None and slot.device == self.packed.device:
+                if self._slot_dirty:
+                    slot.zero_()
+                    self._slot_dirty = False
+                self._pending_counts = slot
+            else:
+                self._pending_counts = torch.zeros(4, dtype=torch.int64,
+                                                   device=self.packed.device)
         return self._pending_counts
 
     def _nonfinite_flag(self) -> Tensor:
@@ -783,6 +796,8 @@ class DiscreteRatchetLinear(nn.Module):
                                    if self._pending_rms_means else 0.0),
             )
             nonfinite = self._nonfinite
+            if counts is not None and counts is self._counts_slot:
+                self._slot_dirty = True  # cleared by the model's sum, or before next use
             self._reset_pending_stats()
             self._nonfinite = nonfinite
         elif self.matmul_mode != "fp32":

@@ -231,3 +231,38 @@ def test_residual_gradient_added_in_the_rmsnorm_backward_changes_nothing(cuda):
     assert all(torch.equal(x, y) for x, y in zip(la, lb))
     assert all(torch.equal(x, y) for x, y in zip(sa, sb))
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))
+
+
+def test_shared_move_count_buffer_gives_the_per_layer_totals(cuda):
+    # The model's one [layers, 4] move-count buffer (summed and cleared once per step) gives
+    # the same step statistics as per-layer count tensors, step after step, and a
+    # layer-level ratchet_update in between (which leaves its slot to be cleared before its
+    # next use) does not leak counts into the next step.
+    from local_ai_training.model import RatchetGPT
+
+    def run(shared: bool):
+        RatchetGPT.shared_move_counts = shared
+        try:
+            torch.manual_seed(0)
+            config = ModelConfig(vocab_size=64, block_size=64, n_layer=2, n_head=4, n_embd=128,
+                                 matmul_mode="int8", int8_backward=True)
+            model = build_seeded_model(config, max_code=2, seed=1337).to(cuda).train()
+            gen = torch.Generator().manual_seed(3)
+            batch = torch.randint(0, 64, (8, 65), generator=gen).to(cuda)
+            out = []
+            for step in range(4):
+                with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                    _, loss = model(batch[:, :64], batch[:, 1:])
+                loss.backward()
+                if step == 2:
+                    first = next(m for m in model.modules()
+                                 if isinstance(m, DiscreteRatchetLinear))
+                    out.append(first.ratchet_update(validate=True))
+                out.append(model.ratchet_update(validate=True))
+            return out
+        finally:
+            RatchetGPT.shared_move_counts = True
+
+    shared, separate = run(True), run(False)
+    assert shared == separate
+    assert any(s.code_moves > 0 for s in shared)
