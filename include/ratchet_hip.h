@@ -86,6 +86,22 @@ int rk_quantize_rows_devseed(const void* x, int x_dtype, int64_t M, int64_t K, i
                              uint16_t* x_bf16, int64_t ld_xb, void* stream);
 
 /*
+ * rk_quantize_rows (unit column stride) over a row split by columns across nparts (1..3)
+ * separate tensors: row m is x0[m, :] | x1[m, :] | x2[m, :], each [M, part_cols] with row
+ * stride ldx, so K = nparts * part_cols (part_cols % 8 == 0). seed_dev, when not NULL, is
+ * read at kernel time as in rk_quantize_rows_devseed (stochastic only). Same results as
+ * concatenating the parts first.
+ * Replaces: the gradient concatenation autograd performs for the attention's q, k, v chunks
+ *           (model.py:106-110, qkv.chunk(3)) ahead of quantize_rows_colscaled
+ *           (ratchet.py:130-132).
+ */
+int rk_quantize_rows_parts(const void* x0, const void* x1, const void* x2, int nparts,
+                           int64_t part_cols, int x_dtype, int64_t M, int64_t ldx,
+                           const float* col_scale, int stochastic, uint64_t seed,
+                           const int64_t* seed_dev, int64_t row_offset, int8_t* q, int64_t ldq,
+                           float* scale, void* stream);
+
+/*
  * Random words of the stochastic rounding: out[i] = first output word of
  * Philox4x32-10 for counter ((counter0 + i) mod 2^32, 0, 0, 0) and key
  * (seed & 0xffffffff, seed >> 32), exactly the words rk_quantize_rows(stochastic=1)
@@ -216,6 +232,20 @@ int rk_dequant_transpose_bf16(const int8_t* q, int64_t ldq, const float* scale, 
 int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, const int8_t* q, int64_t ldq,
                         const float* s, int64_t M, int64_t N, int64_t K, float* workspace,
                         int nsplit, uint16_t* out, int64_t ldo, void* stream);
+
+/*
+ * rk_grad_weight_bf16 with the gradient's columns split across nparts (1..3) separate
+ * tensors g0 | g1 | g2, each [M, part_cols] with row stride ldg (N = nparts * part_cols;
+ * part_cols a multiple of the output tile: 128, or 256 where the large tiles apply;
+ * RK_ERR_UNSUPPORTED otherwise). Same results as concatenating the parts first.
+ * Replaces: the qkv gradient concatenation (model.py:106-110) ahead of the BF16 grad_weight
+ *           GEMM (ratchet.py:148-163).
+ */
+int rk_grad_weight_bf16_parts(const void* g0, const void* g1, const void* g2, int nparts,
+                              int64_t part_cols, int g_dtype, int64_t ldg, const int8_t* q,
+                              int64_t ldq, const float* s, int64_t M, int64_t N, int64_t K,
+                              float* workspace, int nsplit, uint16_t* out, int64_t ldo,
+                              void* stream);
 
 /*
  * The same BF16 weight gradient with the activation operand given directly:

@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <optional>
+#include <vector>
 
 #include "ratchet_hip.h"
 
@@ -431,6 +432,87 @@ void grad_weight_partials(const Tensor& g, const Tensor& q, const Tensor& s, Ten
   grad_weight_partials_common(g, q, true, s, work);
 }
 
+// The parts of one gradient row split by columns (the attention's q, k, v gradients), each
+// [M, C] with unit column stride and one shared row stride.
+struct Parts {
+  const void* p[3] = {nullptr, nullptr, nullptr};
+  int n = 0;
+  int64_t cols = 0, ld = 0, rows = 0;
+  int dtype = RK_F32;
+};
+
+Parts gradient_parts(const std::vector<Tensor>& parts, const char* what) {
+  TORCH_CHECK(parts.size() >= 1 && parts.size() <= 3, what, ": 1 to 3 parts");
+  Parts r;
+  r.n = static_cast<int>(parts.size());
+  for (int i = 0; i < r.n; ++i) {
+    const Tensor& t = parts[i];
+    require_gpu(t, what);
+    TORCH_CHECK(t.dim() == 2 && t.stride(1) == 1, what, ": parts must be [M, C] with unit column stride");
+    if (i == 0) {
+      r.rows = t.size(0);
+      r.cols = t.size(1);
+      r.ld = t.size(0) > 1 ? t.stride(0) : t.size(1);
+      r.dtype = dtype_code(t, what);
+    } else {
+      TORCH_CHECK(t.size(0) == r.rows && t.size(1) == r.cols && t.device() == parts[0].device() &&
+                      t.scalar_type() == parts[0].scalar_type() &&
+                      (t.size(0) <= 1 || t.stride(0) == r.ld),
+                  what, ": parts must share shape, dtype, device and row stride");
+    }
+    r.p[i] = t.data_ptr();
+  }
+  return r;
+}
+
+std::tuple<Tensor, Tensor> quantize_rows_parts(const std::vector<Tensor>& parts,
+                                               const OptTensor& col_scale, bool stochastic,
+                                               int64_t seed, const OptTensor& seed_slot,
+                                               int64_t row_offset) {
+  const Parts g = gradient_parts(parts, "row quantization");
+  const int64_t m = g.rows, k = g.n * g.cols;
+  const c10::DeviceGuard guard(parts[0].device());
+  Tensor q = at::empty({m, k}, parts[0].options().dtype(at::kChar));
+  Tensor scale = at::empty({m}, parts[0].options().dtype(at::kFloat));
+  const OptTensor cs = f32_vector(col_scale, k, "col_scale");
+  if (m == 0 || k == 0) return {q, scale};
+  const int64_t* slot = nullptr;
+  if (seed_slot.has_value()) {
+    TORCH_CHECK(stochastic, "a device seed applies to stochastic rounding only");
+    TORCH_CHECK(seed_slot->scalar_type() == at::kLong && seed_slot->numel() == 1 &&
+                    seed_slot->device() == parts[0].device(),
+                "seed_slot must be one int64 on the input's device");
+    slot = static_cast<const int64_t*>(seed_slot->data_ptr());
+  }
+  check_status(rk_quantize_rows_parts(g.p[0], g.p[1], g.p[2], g.n, g.cols, g.dtype, m, g.ld,
+                                      ptr<const float>(cs), stochastic ? 1 : 0,
+                                      static_cast<uint64_t>(seed), slot, row_offset,
+                                      q.data_ptr<int8_t>(), k, scale.data_ptr<float>(),
+                                      stream_of(parts[0])),
+               "rk_quantize_rows_parts");
+  return {q, scale};
+}
+
+void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& q_in,
+                                const Tensor& s, Tensor& work) {
+  const Parts g = gradient_parts(parts, "grad_weight");
+  int8_matrix(q_in, "q");
+  const Tensor q = unit_columns(q_in);
+  TORCH_CHECK(q.size(0) == g.rows, "activations must have the gradient's rows");
+  same_device(parts[0], q, "grad_weight");
+  const int64_t m = g.rows, n = g.n * g.cols, k = q.size(1);
+  check_workspace(work, n, k);
+  const c10::DeviceGuard guard(q.device());
+  if (n == 0 || k == 0) return;
+  const Tensor sv = f32_vector(s, m, "activation row scale");
+  check_status(rk_grad_weight_bf16_parts(g.p[0], g.p[1], g.p[2], g.n, g.cols, g.dtype, g.ld,
+                                         q.data_ptr<int8_t>(), ld(q), sv.data_ptr<float>(), m,
+                                         n, k, work.data_ptr<float>(),
+                                         static_cast<int>(work.size(0)), nullptr, k,
+                                         stream_of(q)),
+               "rk_grad_weight_bf16_parts");
+}
+
 void grad_weight_partials_x(const Tensor& g, const Tensor& x, Tensor& work) {
   TORCH_CHECK(x.dim() == 2, "activations must be a 2-D matrix");
   grad_weight_partials_common(g, x, false, std::nullopt, work);
@@ -767,6 +849,10 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("grad_weight_x(Tensor g, Tensor x, int nsplit=0) -> Tensor");
   m.def("grad_weight_partials(Tensor g, Tensor q, Tensor s, Tensor(a!) work) -> ()");
   m.def("grad_weight_partials_x(Tensor g, Tensor x, Tensor(a!) work) -> ()");
+  m.def("grad_weight_partials_parts(Tensor[] parts, Tensor q, Tensor s, Tensor(a!) work) -> ()");
+  m.def(
+      "quantize_rows_parts(Tensor[] parts, Tensor? col_scale=None, bool stochastic=False, "
+      "int seed=0, Tensor? seed_slot=None, int row_offset=0) -> (Tensor, Tensor)");
   m.def(
       "update_from_z(Tensor(a!) packed, Tensor z, int max_code, int threshold, float low, "
       "float high, Tensor(b!) counts) -> ()");
@@ -810,6 +896,8 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("grad_weight_x", &grad_weight_x);
   m.impl("grad_weight_partials", &grad_weight_partials);
   m.impl("grad_weight_partials_x", &grad_weight_partials_x);
+  m.impl("grad_weight_partials_parts", &grad_weight_partials_parts);
+  m.impl("quantize_rows_parts", &quantize_rows_parts);
   m.impl("update_from_z", &update_from_z);
   m.impl("update_from_grad", &update_from_grad);
   m.impl("update_from_partials", &update_from_partials);

@@ -39,6 +39,12 @@ enum { GW_X_Q8 = 0, GW_X_BF16 = 1, GW_X_F32 = 2 };
 struct GwArgs {
   const void* g;
   int64_t ldg;
+  // the gradient's columns split over up to three separate [M, part_cols] tensors (row
+  // stride ldg), nparts > 0; part_cols is a multiple of the output tile, so one tile's
+  // columns lie in one part
+  const void* g_parts[3];
+  int64_t part_cols;
+  int nparts;
   const void* x;    // int8 q, bf16 or f32 activations [M, K]
   int64_t ldx;
   const float* s;   // per-token scale (int8 form only)
@@ -198,9 +204,17 @@ void grad_weight_partial_kernel(GwArgs a) {
   // loads exactly and waits only for the ring slot it consumes. Per-thread offsets are
   // fixed; the step advances a scalar offset. The host guarantees offsets < 2^31.
   const int64_t rows = m_end - m_begin;
+  const void* gbase = a.g;
+  int64_t gcol0 = n0, gcols = a.N;
+  if (a.nparts > 0) {
+    const int64_t p = n0 / a.part_cols;  // uniform: scalar selects, no indexed kernarg array
+    gbase = p == 0 ? a.g_parts[0] : (p == 1 ? a.g_parts[1] : a.g_parts[2]);
+    gcol0 = n0 - p * a.part_cols;
+    gcols = a.part_cols;
+  }
   const __amdgpu_buffer_rsrc_t g_rsrc = make_buffer(
-      static_cast<const char*>(a.g) + (m_begin * a.ldg + n0) * GE,
-      rows > 0 ? ((rows - 1) * a.ldg + (a.N - n0)) * GE : 0);
+      static_cast<const char*>(gbase) + (m_begin * a.ldg + gcol0) * GE,
+      rows > 0 ? ((rows - 1) * a.ldg + (gcols - gcol0)) * GE : 0);
   const __amdgpu_buffer_rsrc_t x_rsrc = make_buffer(
       static_cast<const char*>(a.x) + (m_begin * a.ldx + k0) * XE,
       rows > 0 ? ((rows - 1) * a.ldx + (a.K - k0)) * XE : 0);
@@ -427,14 +441,15 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
                        int64_t ldx, const float* s, int64_t M, int64_t N, int64_t K,
                        float* workspace, int nsplit, uint16_t* out, int64_t ldo, void* stream,
                        const GradUpdateArgs* upd = nullptr, int32_t* counters = nullptr,
-                       float* rms_mean = nullptr) {
+                       float* rms_mean = nullptr, const void* const* g_parts = nullptr,
+                       int nparts = 0, int64_t part_cols = 0) {
   if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
   if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
   if (N == 0 || K == 0) return RK_OK;
   if (!g || !x || (x_kind == GW_X_Q8 && !s) || !workspace)
     return fail(RK_ERR_ARG, "null pointer");
   if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
-  if (ldg < N || ldx < K || (out && ldo < K))
+  if ((nparts == 0 && ldg < N) || ldx < K || (out && ldo < K))
     return fail(RK_ERR_ARG, "leading dimension too small");
   const int ge = g_dtype == RK_F32 ? 4 : 2;
   const int xe = x_kind == GW_X_Q8 ? 1 : (x_kind == GW_X_BF16 ? 2 : 4);
@@ -445,6 +460,16 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
                 "grad_weight needs N %% 8 == 0, K %% 16 == 0 and 16-byte aligned rows");
   const bool big = gw_big_tiles(N, K);
   const int64_t feat = big ? GwBig::FEAT : GwSmall::FEAT;
+  if (nparts > 0) {
+    if (nparts > 3 || part_cols <= 0 || nparts * part_cols != N || part_cols % feat != 0)
+      return fail(RK_ERR_UNSUPPORTED,
+                  "grad_weight parts: N must be parts x columns, columns a multiple of %lld",
+                  static_cast<long long>(feat));
+    for (int i = 0; i < nparts; ++i)
+      if (!g_parts[i] || !aligned16(g_parts[i]))
+        return fail(RK_ERR_ARG, "gradient parts must be non-null and 16-byte aligned");
+    if (ldg < part_cols) return fail(RK_ERR_ARG, "leading dimension too small");
+  }
   const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
   const int64_t chunk = ((M + nsplit - 1) / nsplit + GW_BM - 1) / GW_BM * GW_BM;
   // Buffer offsets are 32-bit: the furthest load of a block (ring padding and prefetch
@@ -465,6 +490,9 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   a.K = K;
   a.m_chunk = chunk > 0 ? chunk : GW_BM;
   a.nsplit = nsplit;
+  a.nparts = nparts;
+  a.part_cols = part_cols;
+  for (int i = 0; i < nparts; ++i) a.g_parts[i] = g_parts[i];
   const int64_t blocks = tiles * nsplit;
   if (blocks > 0x7fffffff) return fail(RK_ERR_ARG, "grid too large");
   hipStream_t st = as_stream(stream);
@@ -579,6 +607,19 @@ extern "C" int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, cons
   clear_error();
   return grad_weight_launch(g, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, workspace, nsplit,
                             out, ldo, stream);
+}
+
+extern "C" int rk_grad_weight_bf16_parts(const void* g0, const void* g1, const void* g2,
+                                         int nparts, int64_t part_cols, int g_dtype, int64_t ldg,
+                                         const int8_t* q, int64_t ldq, const float* s, int64_t M,
+                                         int64_t N, int64_t K, float* workspace, int nsplit,
+                                         uint16_t* out, int64_t ldo, void* stream) {
+  clear_error();
+  if (nparts < 1 || nparts > 3) return fail(RK_ERR_ARG, "nparts must be 1, 2 or 3");
+  const void* parts[3] = {g0, g1, g2};
+  return grad_weight_launch(g0, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, workspace, nsplit,
+                            out, ldo, stream, nullptr, nullptr, nullptr, parts, nparts,
+                            part_cols);
 }
 
 extern "C" int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x,

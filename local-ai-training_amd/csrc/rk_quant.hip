@@ -37,6 +37,12 @@ struct QuantArgs {
   int64_t ldxb;
   int vec_ok;                 // 16-byte vector loads are legal for every chunk
   int round_bf16;             // plain float32 source: each value is taken as bf16(x) first
+  // plain source split by columns over up to three [M, part_cols] tensors (row stride sxm,
+  // unit column stride), nparts > 0; part_cols is a multiple of 8, so no vector or element
+  // group crosses a part
+  const void* xp[3];
+  int64_t part_cols;
+  int nparts;
 };
 
 constexpr int kMaxChunks = 8;
@@ -58,6 +64,20 @@ template <int DT, int SRC, bool VEC>
 __device__ __forceinline__ void load_chunk(const QuantArgs& a, int64_t row, int64_t e0,
                                            float* v) {
   constexpr int V = Vec<DT>::N;
+  if constexpr (SRC == SRC_PLAIN) {
+    if (a.nparts > 0) {
+      const int64_t p = e0 / a.part_cols;
+      const void* base = p == 0 ? a.xp[0] : (p == 1 ? a.xp[1] : a.xp[2]);
+      const int64_t idx = row * a.sxm + (e0 - p * a.part_cols);
+      if (VEC || (a.vec_ok && e0 + V <= a.K)) {
+        load_vec16<DT>(base, idx, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[i] = e0 + i < a.K ? load_elem<DT>(base, idx + i) : 0.0f;
+      }
+      return;
+    }
+  }
   if (VEC || (a.vec_ok && e0 + V <= a.K)) {
     load_vec16<DT>(a.x, src_offset<DT, SRC>(a, row, e0), v);
   } else {
@@ -366,6 +386,50 @@ static int quantize_rows_entry(const void* x, int x_dtype, int64_t M, int64_t K,
   a.vec_ok = (rows_vec_ok(x, x_dtype, K, sxm, sxk) && (!col_scale || aligned16(col_scale))) ? 1 : 0;
   if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(x_dtype, a, as_stream(stream));
   return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
+}
+
+extern "C" int rk_quantize_rows_parts(const void* x0, const void* x1, const void* x2, int nparts,
+                                      int64_t part_cols, int x_dtype, int64_t M, int64_t ldx,
+                                      const float* col_scale, int stochastic, uint64_t seed,
+                                      const int64_t* seed_dev, int64_t row_offset, int8_t* q,
+                                      int64_t ldq, float* scale, void* stream) {
+  clear_error();
+  if (nparts < 1 || nparts > 3) return fail(RK_ERR_ARG, "nparts must be 1, 2 or 3");
+  if (part_cols <= 0 || part_cols % 8 != 0)
+    return fail(RK_ERR_ARG, "part columns must be a positive multiple of 8");
+  if (ldx < part_cols) return fail(RK_ERR_ARG, "ldx < part columns");
+  if (seed_dev && !stochastic) return fail(RK_ERR_ARG, "a device seed applies to stochastic rounding only");
+  const void* parts[3] = {x0, x1, x2};
+  const int64_t K = nparts * part_cols;
+  const int dt = x_dtype == RK_F32_AS_BF16 ? RK_F32 : x_dtype;
+  if (int st = check_common(x0, dt, M, K, q, ldq, scale)) return st;
+  if (M == 0) return RK_OK;
+  bool vec = (!col_scale || aligned16(col_scale));
+  for (int i = 0; i < nparts; ++i) {
+    if (!parts[i]) return fail(RK_ERR_ARG, "null part");
+    vec = vec && rows_vec_ok(parts[i], dt, part_cols, ldx, 1);
+  }
+  QuantArgs a{};
+  a.x = x0;
+  a.M = M;
+  a.K = K;
+  a.sxm = ldx;
+  a.sxk = 1;
+  a.col_scale = col_scale;
+  a.key0 = static_cast<uint32_t>(seed & 0xffffffffu);
+  a.key1 = static_cast<uint32_t>(seed >> 32);
+  a.seed_dev = seed_dev;
+  a.row_offset = row_offset;
+  a.q = q;
+  a.ldq = ldq;
+  a.scale = scale;
+  a.vec_ok = vec ? 1 : 0;
+  a.round_bf16 = x_dtype == RK_F32_AS_BF16 ? 1 : 0;
+  a.nparts = nparts;
+  a.part_cols = part_cols;
+  for (int i = 0; i < nparts; ++i) a.xp[i] = parts[i];
+  if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(dt, a, as_stream(stream));
+  return dispatch_dtype<SRC_PLAIN, false>(dt, a, as_stream(stream));
 }
 
 extern "C" int rk_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,

@@ -78,6 +78,10 @@ SIGNATURES: dict[str, list] = {
     "rk_rmsnorm_backward_parts": [_i64],
     "rk_rmsnorm_backward_residual": [_p, _i32, _i64, _p, _i64, _p, _f32, _i64, _i64, _p, _i64, _p,
                                      _i64, _p, _p, _i64, _p],
+    "rk_quantize_rows_parts": [_p, _p, _p, _i32, _i64, _i32, _i64, _i64, _p, _i32, _u64, _p,
+                               _i64, _p, _i64, _p, _p],
+    "rk_grad_weight_bf16_parts": [_p, _p, _p, _i32, _i64, _i32, _i64, _p, _i64, _p, _i64, _i64,
+                                  _i64, _p, _i32, _p, _i64, _p],
     "rk_gelu_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "rk_decode_gemv": [_p, _i64, _p, _i64, _p, _i32, _p, _f32, _p, _i64, _i32, _p, _p, _i32,
                        _i64, _i32, _i64, _i64, _i64, _p],

@@ -122,6 +122,16 @@ def quantize_rows_sr(values: Tensor, col_scale: Tensor | None = None, *,
     return q, s, (slot if slot is not None else seed)
 
 
+def quantize_rows_sr_parts(parts: list[Tensor], col_scale: Tensor | None = None
+                           ) -> tuple[Tensor, Tensor, int | Tensor]:
+    """quantize_rows_sr of the row concatenation of ``parts`` (each [M, C], unit column
+    stride, one shared row stride) without building it: the same seed draw, codes and
+    scales as quantizing ``torch.cat(parts, dim=-1)``."""
+    seed, slot = sr_seed_args(parts[0].device)
+    q, s = _ops().quantize_rows_parts(list(parts), col_scale, True, seed, slot, 0)
+    return q, s, (slot if slot is not None else seed)
+
+
 def _quantize_rows_fused(values: Tensor, col_scale: Tensor | None = None, *,
                          stochastic: bool = False) -> tuple[Tensor, Tensor]:
     """HIP row quantization; bit-exact with the reference's torch formula
@@ -323,6 +333,29 @@ def grad_weight_bf16_x(grad: Tensor, x: Tensor, nsplit: int | None = None, *,
         return _ops().grad_weight_x(grad, x, nsplit or 0)
     work = _partials_workspace(grad, x.shape[1], nsplit, work)
     _ops().grad_weight_partials_x(grad, x, work)
+    return work
+
+
+def grad_weight_parts_supported(parts: list[Tensor], q: Tensor) -> bool:
+    """Shapes rk_grad_weight_bf16_parts takes: every part's columns a multiple of the output
+    tile the kernel picks for [N, K] (256 where the large tiles apply, else 128)."""
+    c, k = parts[0].shape[1], q.shape[1]
+    n = c * len(parts)
+    big = n >= 256 and k >= 256 and ((n + 255) // 256) * ((k + 255) // 256) >= 64
+    feat = 256 if big else 128
+    ld = parts[0].stride(0)
+    return (c % feat == 0 and k % 16 == 0 and q.stride(-1) == 1
+            and all(p.stride(-1) == 1 and p.stride(0) == ld and p.data_ptr() % 16 == 0
+                    for p in parts)
+            and (ld * parts[0].element_size()) % 16 == 0
+            and (q.stride(0) * q.element_size()) % 16 == 0 and q.data_ptr() % 16 == 0)
+
+
+def grad_weight_bf16_parts(parts: list[Tensor], q: Tensor, s: Tensor, *,
+                           work: Tensor) -> Tensor:
+    """grad_weight's float32 split partials for the gradient ``torch.cat(parts, dim=-1)``,
+    read from the parts in place (the same partials as from the concatenation)."""
+    _ops().grad_weight_partials_parts(list(parts), q, s, work)
     return work
 
 

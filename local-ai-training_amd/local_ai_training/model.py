@@ -210,6 +210,9 @@ def _autocast_bf16(t: Tensor) -> torch.dtype | None:
 
 
 class CausalSelfAttention(nn.Module):
+    # int8 qkv: the layer returns q, k, v as chunks whose gradients it reads in place
+    split_qkv_grad: bool = True
+
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
         self.qkv = _linear(config, config.n_embd, 3 * config.n_embd, max_code)
@@ -228,12 +231,14 @@ class CausalSelfAttention(nn.Module):
         if inputs_int8 is not None:
             # Under bf16 autocast the attention casts q, k, v to bf16 (and their gradients
             # back): take the GEMM's bf16 result directly instead (the same values; no cast
-            # kernels, half the bytes for the gradient concatenation)
+            # kernels). The layer returns the three chunks itself, so their gradients reach
+            # its backward separately and are read there in place (no concatenation).
+            kw = {"split": 3} if self.split_qkv_grad else {}
             qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale,
-                           out_dtype=_autocast_bf16(inputs))
+                           out_dtype=_autocast_bf16(inputs), **kw)
         else:
             qkv = self.qkv(inputs)
-        query, key, value = qkv.chunk(3, dim=-1)
+        query, key, value = qkv if isinstance(qkv, tuple) else qkv.chunk(3, dim=-1)
 
         def heads(t: Tensor) -> Tensor:
             return t.view(batch_size, sequence_length, self.n_head, self.head_size).transpose(1, 2)

@@ -148,6 +148,17 @@ def _register_fakes() -> None:
     def _gelu_backward(grad_y, x):
         return x.new_empty((x.shape[0], x.shape[1]), dtype=float_dtype(x))
 
+    @fake("ratchet::quantize_rows_parts")
+    def _quantize_rows_parts(parts, col_scale=None, stochastic=False, seed=0, seed_slot=None,
+                             row_offset=0):
+        m, k = parts[0].shape[0], parts[0].shape[1] * len(parts)
+        return (parts[0].new_empty((m, k), dtype=torch.int8),
+                parts[0].new_empty((m,), dtype=torch.float32))
+
+    @fake("ratchet::grad_weight_partials_parts")
+    def _grad_weight_partials_parts(parts, q, s, work):
+        return None
+
     @fake("ratchet::embedding_backward")
     def _embedding_backward(grad, ids, num_weights):
         return grad.new_empty((num_weights, grad.shape[-1]), dtype=torch.float32)
@@ -161,5 +172,6 @@ OPERATORS = (
     "grad_weight_x", "grad_weight_partials", "grad_weight_partials_x", "update_from_z",
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
-    "rmsnorm_backward", "gelu_backward", "embedding_backward",
+    "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
+    "grad_weight_partials_parts",
 )

@@ -37,7 +37,9 @@ from .int8_matmul import (
     dequant_transpose_bf16,
     effective_bf16,
     grad_weight_bf16,
+    grad_weight_bf16_parts,
     grad_weight_bf16_x,
+    grad_weight_parts_supported,
     grad_weight_splits,
     int8_mm_nt,
     packed_int8_mm,
@@ -45,6 +47,7 @@ from .int8_matmul import (
     packed_int8_mm_t,
     packed_t_supported,
     quantize_rows_sr,
+    quantize_rows_sr_parts,
     residual_supported,
     transpose_bf16,
     unpack_transpose,
@@ -201,7 +204,8 @@ class _RatchetMatmul(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype=None,
-                residual=None):
+                residual=None, split=1):
+        ctx.split = split
         input_shape = inputs.shape
         flat_inputs = inputs.flatten(0, -2)
         mode = layer.matmul_mode
@@ -255,10 +259,13 @@ class _RatchetMatmul(torch.autograd.Function):
         output = output.reshape(*input_shape[:-1], out_features)
         if requested is None and output.dtype != inputs.dtype:
             output = output.to(inputs.dtype)
-        return output if residual is None else residual + output
+        output = output if residual is None else residual + output
+        # split > 1: the output's equal column chunks (views), whose gradients reach backward
+        # separately and are read there in place instead of being concatenated first
+        return tuple(output.chunk(split, dim=-1)) if split > 1 else output
 
     @staticmethod
-    def backward(ctx, grad_output: Tensor):
+    def backward(ctx, *grad_outputs: Tensor):
         layer = ctx.layer
         if layer._generation != ctx.generation:
             raise RuntimeError(
@@ -266,6 +273,13 @@ class _RatchetMatmul(torch.autograd.Function):
                 "(the layer was applied twice before backward; weight sharing is unsupported "
                 "with the fused update)"
             )
+        if ctx.split > 1:
+            parts = _gradient_parts(ctx, layer, grad_outputs)
+            if parts is not None:
+                return _RatchetMatmul._backward_parts(ctx, layer, parts)
+            grad_output = torch.cat(grad_outputs, dim=-1)
+        else:
+            grad_output = grad_outputs[0]
         packed = layer.packed
         mode = layer.matmul_mode
         if ctx.used_fused_int8:
@@ -310,7 +324,7 @@ class _RatchetMatmul(torch.autograd.Function):
             if needs_scale:
                 grad_scale = (grad_weight_fp32 * layer.code.float()).sum(dim=1)
             return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-                grad_scale, None, None, grad_residual
+                grad_scale, None, None, grad_residual, None
 
         m, n = flat_gradient.shape
         gradient_bf16 = None
@@ -418,7 +432,77 @@ class _RatchetMatmul(torch.autograd.Function):
         else:
             grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-            grad_scale, None, None, grad_residual
+            grad_scale, None, None, grad_residual, None
+
+    @staticmethod
+    def _backward_parts(ctx, layer, parts: list[Tensor]):
+        """The int8-backward path for a gradient that arrives as the output's column chunks
+        (``split``): the SR quant and grad_weight read the chunks in place, as one row, with
+        the results of the concatenated gradient (same seed draw, codes, scales and
+        partials)."""
+        q, s, scale = ctx.saved_tensors
+        packed = layer.packed
+        m = parts[0].shape[0]
+        scale_d = scale.detach()
+        needs_scale = ctx.needs_input_grad[4]
+        partials = None
+        side = None
+        if layer.overlap_weight_gradient and torch.cuda.is_current_stream_capturing():
+            # grad_weight on the side stream, as in the single-gradient path
+            main = torch.cuda.current_stream(q.device)
+            side = _side_stream(q.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                partials = grad_weight_bf16_parts(parts, q, s,
+                                                  work=layer._split_workspace(m, q.device))
+            for t in (*parts, *ctx.saved_tensors):
+                t.record_stream(side)
+        grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr_parts(
+            parts, scale_d.float().contiguous())
+        out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
+            else torch.bfloat16
+        if packed_t_supported(grad_q, packed):
+            grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
+                                          out_dtype)
+        else:
+            code_t = unpack_transpose(packed, layer.max_code)
+            grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
+        if partials is None:
+            partials = grad_weight_bf16_parts(parts, q, s,
+                                              work=layer._split_workspace(m, q.device))
+        if side is not None:
+            torch.cuda.current_stream(partials.device).wait_stream(side)
+            partials.record_stream(torch.cuda.current_stream(partials.device))
+        grad_scale = layer._fused_update(partials, want_grad_scale=needs_scale,
+                                         from_partials=True)
+        return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
+            grad_scale, None, None, None, None
+
+
+def _gradient_parts(ctx, layer, grads) -> list[Tensor] | None:
+    """The chunk gradients as [M, C] row views for the in-place parts path, or None when
+    it does not apply (then they are concatenated): the fused int8-backward layer path, no
+    residual, every chunk's gradient present with one dtype and one row layout, and shapes
+    the parts kernels take."""
+    if not (layer.fuse_backward_update and layer.matmul_mode == "int8" and layer.int8_backward
+            and ctx.used_fused_int8 and ctx.residual_dtype is None):
+        return None
+    if any(g is None for g in grads):
+        return None
+    dtype = grads[0].dtype
+    if dtype not in (torch.float32, torch.bfloat16) or any(g.dtype != dtype for g in grads):
+        return None
+    parts = []
+    for g in grads:
+        flat = g.reshape(-1, g.shape[-1])  # a view when the chunk gradient has row layout
+        if flat.stride(-1) != 1 or (flat.shape[0] > 1 and flat.data_ptr() != g.data_ptr()):
+            return None
+        parts.append(flat)
+    if len({(p.shape, p.stride()) for p in parts}) != 1 or parts[0].shape[1] % 8 != 0:
+        return None
+    if not grad_weight_parts_supported(parts, ctx.saved_tensors[0]):
+        return None
+    return parts
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -615,14 +699,16 @@ class DiscreteRatchetLinear(nn.Module):
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None,
                 out_dtype: torch.dtype | None = None,
-                residual: Tensor | None = None) -> Tensor:
+                residual: Tensor | None = None, split: int = 1):
         """``out_dtype`` (int8 mode only): the output dtype in place of the input's, for a
         caller that would cast the result anyway (same values). ``residual``: return
         ``residual + output`` (added in the GEMM's epilogue where the shapes allow, the same
-        float32 add)."""
+        float32 add). ``split`` > 1: return ``output.chunk(split, dim=-1)``; on the fused
+        int8-backward path the chunks' gradients are then read in place rather than
+        concatenated (the same results)."""
         if self.matmul_mode != "fp32" or self.fuse_backward_update:
             return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
-                                        self.scale, self, out_dtype, residual)
+                                        self.scale, self, out_dtype, residual, split)
         effective = self.effective_weight().to(dtype=inputs.dtype)
         if self.training and torch.is_grad_enabled():
             if self.trainable_scale:
@@ -631,7 +717,8 @@ class DiscreteRatchetLinear(nn.Module):
                 effective = effective.detach().requires_grad_(True)
             self._effective_weight = effective
         output = F.linear(inputs, effective)
-        return output if residual is None else residual + output
+        output = output if residual is None else residual + output
+        return output.chunk(split, dim=-1) if split > 1 else output
 
     # -- gradient capture and the fused update --------------------------------
     def _capture_weight_gradient(self, gradient: Tensor) -> None:

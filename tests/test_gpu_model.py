@@ -123,12 +123,13 @@ def test_fused_transpose_quantize_is_exact(cuda, dtype):
 
 
 def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True,
-                fuse_grad: bool = True):
-    from local_ai_training.model import FeedForward, TransformerBlock
+                fuse_grad: bool = True, split_qkv: bool = True):
+    from local_ai_training.model import CausalSelfAttention, FeedForward, TransformerBlock
 
     TransformerBlock.fuse_residual = fuse
     TransformerBlock.fuse_residual_grad = fuse_grad
     FeedForward.bf16_expand = bf16_expand
+    CausalSelfAttention.split_qkv_grad = split_qkv
     try:
         torch.manual_seed(0)
         config = ModelConfig(vocab_size=64, block_size=64, n_layer=2, n_head=4, n_embd=128,
@@ -153,6 +154,7 @@ def _int8_steps(cuda, fuse: bool, steps: int = 3, bf16_expand: bool = True,
         TransformerBlock.fuse_residual = True
         TransformerBlock.fuse_residual_grad = True
         FeedForward.bf16_expand = True
+        CausalSelfAttention.split_qkv_grad = True
 
 
 def test_residual_fused_into_the_gemm_epilogue_changes_nothing(cuda):
@@ -228,6 +230,32 @@ def test_residual_gradient_added_in_the_rmsnorm_backward_changes_nothing(cuda):
         int8_backward.rmsnorm_backward = orig
     assert calls and all(calls)
     lb, sb, pb = _int8_steps(cuda, fuse=True, fuse_grad=False)
+    assert all(torch.equal(x, y) for x, y in zip(la, lb))
+    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
+    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
+
+
+def test_qkv_gradients_read_in_parts_change_nothing(cuda):
+    # The qkv layer returning q, k, v itself, so that its backward quantizes dq, dk, dv and
+    # forms the weight gradient from them in place instead of from their concatenation:
+    # identical losses, ratchet states and float parameters over three steps.
+    from local_ai_training import ratchet
+
+    calls = []
+    cls = ratchet._RatchetMatmul
+    orig = cls.__dict__["_backward_parts"]
+
+    def recording(*args, **kwargs):
+        calls.append(1)
+        return orig.__func__(*args, **kwargs)
+
+    cls._backward_parts = staticmethod(recording)
+    try:
+        la, sa, pa = _int8_steps(cuda, fuse=True, split_qkv=True)
+    finally:
+        cls._backward_parts = orig
+    assert len(calls) == 3 * 2  # both layers' qkv, every step
+    lb, sb, pb = _int8_steps(cuda, fuse=True, split_qkv=False)
     assert all(torch.equal(x, y) for x, y in zip(la, lb))
     assert all(torch.equal(x, y) for x, y in zip(sa, sb))
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))

@@ -57,6 +57,9 @@ def cases(t, cuda):
     partials = torch.randn(nsplit, N, K, generator=gen(9)).mul_(1e-3).to(cuda)
     seed = torch.tensor([1234], dtype=torch.int64, device=cuda)
     rule = (MC, 8, 0.5, 1.5, 1e-8)
+    whole = (torch.randn(M, 3 * N, generator=gen(11)) * 1e-2).to(torch.bfloat16).to(cuda)
+    parts = list(whole.chunk(3, dim=-1))
+    work3 = torch.zeros(R.grad_weight_splits(M, 3 * N, K), 3 * N, K, device=cuda)
     return [
         (R.quantize_rows, (t["x"],), {}),
         (R.quantize_rows, (t["gf"], t["scale"], True, 77), {"x_bf16": torch.empty_like(t["g"])}),
@@ -98,15 +101,22 @@ def cases(t, cuda):
         (R.gelu_backward, (t["x"], t["x"]), {}),
         (R.embedding_backward, (t["x"], torch.randint(0, 40, (M,), generator=gen(5)).to(cuda),
                                 40), {}),
+        (R.quantize_rows_parts, (parts, t["scale"].repeat(3), True, 5), {}),
+        (R.quantize_rows_parts, ([p.contiguous() for p in parts[:2]],), {}),
+        (R.grad_weight_partials_parts, (parts, t["q"], t["s"], work3), {}),
     ]
+
+
+N_CASES = 36
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):
     covered = {op._qualified_op_name.split("::")[1] for op, _, _ in cases(t, cuda)}
     assert covered == set(ops.OPERATORS) - {"grad_weight_splits"}
+    assert len(cases(t, cuda)) == N_CASES
 
 
-@pytest.mark.parametrize("index", range(31))
+@pytest.mark.parametrize("index", range(N_CASES))
 def test_opcheck(t, cuda, index):
     op, args, kwargs = cases(t, cuda)[index]
     print(f"opcheck {op._qualified_op_name} case {index}", flush=True)

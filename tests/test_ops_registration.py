@@ -17,6 +17,7 @@ MUTATED = {
     "packed_mm_accumulate": {"acc"},
     "grad_weight_partials": {"work"},
     "grad_weight_partials_x": {"work"},
+    "grad_weight_partials_parts": {"work"},
     "update_from_z": {"packed", "counts"},
     "update_from_grad": {"packed", "rms_ema", "counts", "row_rms", "grad_scale", "nonfinite",
                          "rms_mean"},
@@ -94,6 +95,10 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
     emb = R.embedding_backward(meta(2, m // 2, k, dtype=torch.bfloat16),
                                meta(2, m // 2, dtype=torch.int64), 50)
     assert emb.shape == (50, k) and emb.dtype == torch.float32
+    parts = [meta(m, n, dtype=torch.bfloat16) for _ in range(3)]
+    qp, sp = R.quantize_rows_parts(parts, meta(3 * n), True, 7)
+    assert (qp.shape, qp.dtype, sp.shape, sp.dtype) == ((m, 3 * n), torch.int8, (m,),
+                                                          torch.float32)
 
 
 def test_split_count_query_runs_on_the_host(R):
