@@ -170,6 +170,28 @@ int rk_int8_gemm_packed_t(const int8_t* A, int64_t lda, const uint8_t* packed, i
                           void* stream);
 
 /*
+ * The int8 grad_input with the gradient's stochastic-rounding quantization fused into the
+ * GEMM's operand staging: for the gradient g [M, K] (up to 3 column parts as in
+ * rk_quantize_rows_parts; nparts = 1 with part_cols = K for one tensor) and the packed state
+ * [K, N] (the layer's weight, read as the K x N operand as in rk_int8_gemm_packed_t):
+ *   scale[m], q = rk_quantize_rows(g, col_scale, stochastic=1, seed | *seed_dev, row_offset)
+ *   out = bf16(float(q @ code) * scale[m])          (c_dtype RK_BF16, or RK_F32 widened)
+ * bit for bit, without writing q (q, when not NULL, receives the codes; g_bf16, when not
+ * NULL, receives bf16(g) like rk_quantize_rows' x_bf16). g_dtype RK_F32, RK_BF16 or
+ * RK_F32_AS_BF16. Requires N in {128, 256, 512}, K <= 4096, part_cols % 64 == 0, 16-byte
+ * aligned rows (RK_ERR_UNSUPPORTED otherwise: use the two calls).
+ * Replaces: quantize_rows_colscaled(grad_output * weight_scale, stochastic) followed by
+ *           scaled_int8_mm(grad_int8, code, ...)  ratchet.py:125-134, int8_matmul.py:262-277,
+ *           289-343.
+ */
+int rk_grad_input_sr(const void* g0, const void* g1, const void* g2, int nparts,
+                     int64_t part_cols, int g_dtype, int64_t ldg, const float* col_scale,
+                     uint64_t seed, const int64_t* seed_dev, int64_t row_offset,
+                     const uint8_t* packed, int64_t ldp, int max_code, int64_t M, int64_t K,
+                     int64_t N, float* scale, int8_t* q, int64_t ldq, uint16_t* g_bf16,
+                     int64_t ld_gb, void* out, int c_dtype, int64_t ldo, void* stream);
+
+/*
  * Decode + transpose the packed state: codeT[k, n] = (packed[n, k] & 15) - max_code.
  *   packed [N, K] (row stride ldp) -> codeT int8 [K, N] (row stride ldt).
  * Feeds the int8 grad_input GEMM (contraction over the output features), replacing
@@ -234,18 +256,20 @@ int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, const int8_t* q
                         int nsplit, uint16_t* out, int64_t ldo, void* stream);
 
 /*
- * rk_grad_weight_bf16 with the gradient's columns split across nparts (1..3) separate
- * tensors g0 | g1 | g2, each [M, part_cols] with row stride ldg (N = nparts * part_cols;
- * part_cols a multiple of the output tile: 128, or 256 where the large tiles apply;
- * RK_ERR_UNSUPPORTED otherwise). Same results as concatenating the parts first.
+ * rk_grad_weight_bf16 / rk_grad_weight_bf16_x with the gradient's columns split across
+ * nparts (1..3) separate tensors g0 | g1 | g2, each [M, part_cols] with row stride ldg
+ * (N = nparts * part_cols; part_cols a multiple of the output tile: 128, or 256 where the
+ * large tiles apply; RK_ERR_UNSUPPORTED otherwise). The activations x: x_dtype RK_I8 (int8
+ * with the per-row scale s) or RK_BF16 / RK_F32 (s unused). Same results as concatenating
+ * the parts first.
  * Replaces: the qkv gradient concatenation (model.py:106-110) ahead of the BF16 grad_weight
  *           GEMM (ratchet.py:148-163).
  */
 int rk_grad_weight_bf16_parts(const void* g0, const void* g1, const void* g2, int nparts,
-                              int64_t part_cols, int g_dtype, int64_t ldg, const int8_t* q,
-                              int64_t ldq, const float* s, int64_t M, int64_t N, int64_t K,
-                              float* workspace, int nsplit, uint16_t* out, int64_t ldo,
-                              void* stream);
+                              int64_t part_cols, int g_dtype, int64_t ldg, const void* x,
+                              int x_dtype, int64_t ldx, const float* s, int64_t M, int64_t N,
+                              int64_t K, float* workspace, int nsplit, uint16_t* out,
+                              int64_t ldo, void* stream);
 
 /*
  * The same BF16 weight gradient with the activation operand given directly:
@@ -414,6 +438,32 @@ int rk_gelu_quantize(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t
 int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
                           int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t sd,
                           int8_t* q, int64_t ldq, float* scale, void* stream);
+
+/*
+ * The activation quantizations above (and rk_quantize_rows' round-to-nearest form, without a
+ * column scale) that also write the dequantized activations
+ *   x_dq[m, k] = bf16(bf16(q[m, k]) * bf16(scale[m]))
+ * in the same pass: the bf16 operand the backward's grad_weight reads (rk_grad_weight_bf16_x
+ * with RK_BF16), which then needs no int8 -> bf16 conversion per output tile. x_dq is NULL
+ * (no output) or a 16-byte aligned bf16 [M, K] matrix whose row stride ld_dq >= K is a
+ * multiple of 8. Same q and scale as the functions without the suffix.
+ * Replaces: the dequantized copy of the saved activations, inputs_int8.to(bf16) *
+ *           inputs_scale.to(bf16)  ratchet.py:71-76 (made once in the forward instead of by
+ *           every output tile of grad_weight).
+ */
+int rk_quantize_rows_dq(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
+                        int64_t sxk, int8_t* q, int64_t ldq, float* scale, uint16_t* x_dq,
+                        int64_t ld_dq, void* stream);
+int rk_rmsnorm_quantize_dq(const void* x, int x_dtype, int64_t ldx, const float* w, float eps,
+                           int8_t* q, int64_t ldq, float* scale, int64_t M, int64_t K,
+                           uint16_t* x_dq, int64_t ld_dq, void* stream);
+int rk_gelu_quantize_dq(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                        float* scale, int64_t M, int64_t K, uint16_t* x_dq, int64_t ld_dq,
+                        void* stream);
+int rk_transpose_quantize_dq(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
+                             int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t sd,
+                             int8_t* q, int64_t ldq, float* scale, uint16_t* x_dq,
+                             int64_t ld_dq, void* stream);
 
 /*
  * Backward of the RMSNorm prologue, per row of x [M, K] and grad_y [M, K]:

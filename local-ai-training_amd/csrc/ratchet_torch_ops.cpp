@@ -24,6 +24,7 @@
 
 #include <algorithm>
 #include <optional>
+#include <utility>
 #include <vector>
 
 #include "ratchet_hip.h"
@@ -97,10 +98,24 @@ void packed_matrix(const Tensor& t) {
 // ---------------------------------------------------------------------------------------
 // Row quantization (int8_matmul.py:106-150, 181-207, 251-277)
 // ---------------------------------------------------------------------------------------
+// The optional dequantized output of the activation quantizations: a bfloat16 [M, K]
+// row-major matrix on the input's device (16-byte aligned rows, checked by the library).
+std::pair<uint16_t*, int64_t> dq_out(const OptTensor& x_dq, int64_t m, int64_t k,
+                                     const Tensor& x) {
+  if (!x_dq.has_value()) return {nullptr, 0};
+  TORCH_CHECK(x_dq->scalar_type() == at::kBFloat16 && x_dq->dim() == 2 && x_dq->size(0) == m &&
+                  x_dq->size(1) == k && (x_dq->stride(1) == 1 || k <= 1) &&
+                  x_dq->device() == x.device(),
+              "x_dq must be a bfloat16 [M, K] matrix with unit column stride on the input's "
+              "device");
+  return {static_cast<uint16_t*>(x_dq->data_ptr()), ld(*x_dq)};
+}
+
 std::tuple<Tensor, Tensor> quantize_rows(const Tensor& x, const OptTensor& col_scale,
                                          bool stochastic, int64_t seed,
                                          const OptTensor& seed_slot, int64_t row_offset,
-                                         const OptTensor& x_bf16, bool round_bf16) {
+                                         const OptTensor& x_bf16, bool round_bf16,
+                                         const OptTensor& x_dq) {
   require_gpu(x, "row quantization");
   TORCH_CHECK(x.dim() == 2, "row quantization requires a 2D tensor");
   int code = dtype_code(x, "row quantization input");
@@ -121,7 +136,19 @@ std::tuple<Tensor, Tensor> quantize_rows(const Tensor& x, const OptTensor& col_s
     xb = static_cast<uint16_t*>(x_bf16->data_ptr());
     ld_xb = ld(*x_bf16);
   }
+  const auto dq = dq_out(x_dq, m, k, x);
+  if (dq.first) {
+    TORCH_CHECK(!stochastic && !col_scale.has_value() && !x_bf16.has_value() && !round_bf16,
+                "x_dq applies to the plain round-to-nearest quantization");
+  }
   if (m == 0 || k == 0) return {q, scale};
+  if (dq.first) {
+    check_status(rk_quantize_rows_dq(x.data_ptr(), code, m, k, x.stride(0), x.stride(1),
+                                     q.data_ptr<int8_t>(), k, scale.data_ptr<float>(), dq.first,
+                                     dq.second, stream_of(x)),
+                 "rk_quantize_rows_dq");
+    return {q, scale};
+  }
   if (seed_slot.has_value()) {
     TORCH_CHECK(stochastic, "a device seed applies to stochastic rounding only");
     TORCH_CHECK(seed_slot->scalar_type() == at::kLong && seed_slot->numel() == 1 &&
@@ -493,23 +520,90 @@ std::tuple<Tensor, Tensor> quantize_rows_parts(const std::vector<Tensor>& parts,
   return {q, scale};
 }
 
-void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& q_in,
-                                const Tensor& s, Tensor& work) {
+// The int8 grad_input with the SR quantization of the gradient in its operand staging
+// (ratchet.py:125-134): (grad_input, row scale), the results of quantize_rows(stochastic)
+// followed by packed_mm_t. q_out / g_bf16 optionally receive the int8 codes / bf16(g).
+std::tuple<Tensor, Tensor> grad_input_sr(const std::vector<Tensor>& parts, const Tensor& packed,
+                                         int64_t max_code, const OptTensor& col_scale,
+                                         int64_t seed, const OptTensor& seed_slot,
+                                         int64_t row_offset, at::ScalarType out_dtype,
+                                         bool round_bf16, const OptTensor& q_out,
+                                         const OptTensor& g_bf16) {
+  const Parts g = gradient_parts(parts, "grad_input_sr");
+  packed_matrix(packed);
+  same_device(parts[0], packed, "grad_input_sr");
+  const int64_t m = g.rows, k = g.n * g.cols, n = packed.size(1);
+  TORCH_CHECK(packed.size(0) == k, "grad_input_sr: the gradient has ", k,
+              " columns, the packed state ", packed.size(0), " rows");
+  TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16,
+              "grad_input_sr: output dtype must be float32 or bfloat16");
+  TORCH_CHECK(!round_bf16 || g.dtype == RK_F32, "round_bf16 applies to a float32 gradient");
+  const c10::DeviceGuard guard(parts[0].device());
+  Tensor out = at::empty({m, n}, parts[0].options().dtype(out_dtype));
+  Tensor scale = at::empty({m}, parts[0].options().dtype(at::kFloat));
+  const OptTensor cs = f32_vector(col_scale, k, "col_scale");
+  const int64_t* slot = nullptr;
+  if (seed_slot.has_value()) {
+    TORCH_CHECK(seed_slot->scalar_type() == at::kLong && seed_slot->numel() == 1 &&
+                    seed_slot->device() == parts[0].device(),
+                "seed_slot must be one int64 on the input's device");
+    slot = static_cast<const int64_t*>(seed_slot->data_ptr());
+  }
+  int8_t* qp = nullptr;
+  int64_t ldq = k;
+  if (q_out.has_value()) {
+    TORCH_CHECK(q_out->scalar_type() == at::kChar && q_out->dim() == 2 && q_out->size(0) == m &&
+                    q_out->size(1) == k && q_out->stride(1) == 1 &&
+                    q_out->device() == parts[0].device(),
+                "q_out must be an int8 [M, K] row-major tensor on the gradient's device");
+    qp = q_out->data_ptr<int8_t>();
+    ldq = q_out->size(0) > 1 ? q_out->stride(0) : k;
+  }
+  uint16_t* xb = nullptr;
+  int64_t ldxb = k;
+  if (g_bf16.has_value()) {
+    TORCH_CHECK(g_bf16->scalar_type() == at::kBFloat16 && g_bf16->dim() == 2 &&
+                    g_bf16->size(0) == m && g_bf16->size(1) == k && g_bf16->stride(1) == 1 &&
+                    g_bf16->device() == parts[0].device(),
+                "g_bf16 must be a bfloat16 [M, K] row-major tensor on the gradient's device");
+    xb = static_cast<uint16_t*>(g_bf16->data_ptr());
+    ldxb = g_bf16->size(0) > 1 ? g_bf16->stride(0) : k;
+  }
+  if (m == 0 || n == 0) return {out, scale};
+  check_status(rk_grad_input_sr(g.p[0], g.p[1], g.p[2], g.n, g.cols,
+                                round_bf16 ? RK_F32_AS_BF16 : g.dtype, g.ld,
+                                ptr<const float>(cs), static_cast<uint64_t>(seed), slot,
+                                row_offset, packed.data_ptr<uint8_t>(), ld(packed),
+                                static_cast<int>(max_code), m, k, n, scale.data_ptr<float>(), qp,
+                                ldq, xb, ldxb, out.data_ptr(), dtype_code(out_dtype), n,
+                                stream_of(parts[0])),
+               "rk_grad_input_sr");
+  return {out, scale};
+}
+
+// x: int8 activations with their row scale s, or float32 / bfloat16 activations (s None)
+void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& x_in,
+                                const OptTensor& s, Tensor& work) {
   const Parts g = gradient_parts(parts, "grad_weight");
-  int8_matrix(q_in, "q");
-  const Tensor q = unit_columns(q_in);
-  TORCH_CHECK(q.size(0) == g.rows, "activations must have the gradient's rows");
-  same_device(parts[0], q, "grad_weight");
-  const int64_t m = g.rows, n = g.n * g.cols, k = q.size(1);
+  TORCH_CHECK(x_in.dim() == 2, "activations must be a 2-D matrix");
+  const bool int8_act = x_in.scalar_type() == at::kChar;
+  TORCH_CHECK(int8_act == s.has_value(),
+              "grad_weight: int8 activations take a row scale, float activations none");
+  const Tensor x = unit_columns(x_in);
+  TORCH_CHECK(x.size(0) == g.rows, "activations must have the gradient's rows");
+  same_device(parts[0], x, "grad_weight");
+  const int64_t m = g.rows, n = g.n * g.cols, k = x.size(1);
   check_workspace(work, n, k);
-  const c10::DeviceGuard guard(q.device());
+  const c10::DeviceGuard guard(x.device());
   if (n == 0 || k == 0) return;
-  const Tensor sv = f32_vector(s, m, "activation row scale");
+  const OptTensor sv = int8_act ? OptTensor(f32_vector(*s, m, "activation row scale"))
+                                : OptTensor();
   check_status(rk_grad_weight_bf16_parts(g.p[0], g.p[1], g.p[2], g.n, g.cols, g.dtype, g.ld,
-                                         q.data_ptr<int8_t>(), ld(q), sv.data_ptr<float>(), m,
-                                         n, k, work.data_ptr<float>(),
+                                         x.data_ptr(),
+                                         int8_act ? RK_I8 : dtype_code(x, "activations"), ld(x),
+                                         ptr<const float>(sv), m, n, k, work.data_ptr<float>(),
                                          static_cast<int>(work.size(0)), nullptr, k,
-                                         stream_of(q)),
+                                         stream_of(x)),
                "rk_grad_weight_bf16_parts");
 }
 
@@ -680,7 +774,8 @@ Tensor float_rows(const Tensor& x) {
   return unit_columns(f);
 }
 
-std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_in, double eps) {
+std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_in, double eps,
+                                            const OptTensor& x_dq) {
   require_gpu(x_in, "fused RMSNorm quantization");
   const Tensor x = float_rows(x_in);
   const int64_t m = x.size(0), k = x.size(1);
@@ -688,30 +783,33 @@ std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({m, k}, x.options().dtype(at::kChar));
   Tensor s = at::empty({m}, x.options().dtype(at::kFloat));
+  const auto dq = dq_out(x_dq, m, k, x);
   if (m == 0 || k == 0) return {q, s};
-  check_status(rk_rmsnorm_quantize(x.data_ptr(), dtype_code(x, "RMSNorm input"), ld(x),
-                                   w.data_ptr<float>(), static_cast<float>(eps),
-                                   q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k,
-                                   stream_of(x)),
+  check_status(rk_rmsnorm_quantize_dq(x.data_ptr(), dtype_code(x, "RMSNorm input"), ld(x),
+                                      w.data_ptr<float>(), static_cast<float>(eps),
+                                      q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k,
+                                      dq.first, dq.second, stream_of(x)),
                "rk_rmsnorm_quantize");
   return {q, s};
 }
 
-std::tuple<Tensor, Tensor> gelu_quantize(const Tensor& x_in) {
+std::tuple<Tensor, Tensor> gelu_quantize(const Tensor& x_in, const OptTensor& x_dq) {
   require_gpu(x_in, "fused GELU quantization");
   const Tensor x = float_rows(x_in);
   const int64_t m = x.size(0), k = x.size(1);
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({m, k}, x.options().dtype(at::kChar));
   Tensor s = at::empty({m}, x.options().dtype(at::kFloat));
+  const auto dq = dq_out(x_dq, m, k, x);
   if (m == 0 || k == 0) return {q, s};
-  check_status(rk_gelu_quantize(x.data_ptr(), dtype_code(x, "GELU input"), ld(x),
-                                q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k, stream_of(x)),
+  check_status(rk_gelu_quantize_dq(x.data_ptr(), dtype_code(x, "GELU input"), ld(x),
+                                   q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k, dq.first,
+                                   dq.second, stream_of(x)),
                "rk_gelu_quantize");
   return {q, s};
 }
 
-std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in) {
+std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in, const OptTensor& x_dq) {
   require_gpu(x_in, "fused transpose quantization");
   TORCH_CHECK(x_in.dim() == 4, "transpose quantization takes [B, H, S, D]");
   const Tensor x = (x_in.scalar_type() == at::kFloat || x_in.scalar_type() == at::kBFloat16)
@@ -721,11 +819,12 @@ std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in) {
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({b * s, h * d}, x.options().dtype(at::kChar));
   Tensor scale = at::empty({b * s}, x.options().dtype(at::kFloat));
+  const auto dq = dq_out(x_dq, b * s, h * d, x);
   if (b * s == 0 || h * d == 0) return {q, scale};
-  check_status(rk_transpose_quantize(x.data_ptr(), dtype_code(x, "attention output"), b, h, s, d,
-                                     x.stride(0), x.stride(1), x.stride(2), x.stride(3),
-                                     q.data_ptr<int8_t>(), h * d, scale.data_ptr<float>(),
-                                     stream_of(x)),
+  check_status(rk_transpose_quantize_dq(x.data_ptr(), dtype_code(x, "attention output"), b, h, s,
+                                        d, x.stride(0), x.stride(1), x.stride(2), x.stride(3),
+                                        q.data_ptr<int8_t>(), h * d, scale.data_ptr<float>(),
+                                        dq.first, dq.second, stream_of(x)),
                "rk_transpose_quantize");
   return {q, scale};
 }
@@ -822,7 +921,7 @@ TORCH_LIBRARY(ratchet, m) {
   m.def(
       "quantize_rows(Tensor x, Tensor? col_scale=None, bool stochastic=False, int seed=0, "
       "Tensor? seed_slot=None, int row_offset=0, Tensor(a!)? x_bf16=None, "
-      "bool round_bf16=False) -> (Tensor, Tensor)");
+      "bool round_bf16=False, Tensor(b!)? x_dq=None) -> (Tensor, Tensor)");
   m.def(
       "int8_mm_nt(Tensor a, Tensor b, Tensor a_scale, Tensor? b_scale, ScalarType out_dtype) "
       "-> Tensor");
@@ -849,7 +948,13 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("grad_weight_x(Tensor g, Tensor x, int nsplit=0) -> Tensor");
   m.def("grad_weight_partials(Tensor g, Tensor q, Tensor s, Tensor(a!) work) -> ()");
   m.def("grad_weight_partials_x(Tensor g, Tensor x, Tensor(a!) work) -> ()");
-  m.def("grad_weight_partials_parts(Tensor[] parts, Tensor q, Tensor s, Tensor(a!) work) -> ()");
+  m.def(
+      "grad_weight_partials_parts(Tensor[] parts, Tensor x, Tensor? s, Tensor(a!) work) -> ()");
+  m.def(
+      "grad_input_sr(Tensor[] parts, Tensor packed, int max_code, Tensor? col_scale=None, "
+      "int seed=0, Tensor? seed_slot=None, int row_offset=0, ScalarType out_dtype=bfloat16, "
+      "bool round_bf16=False, Tensor(a!)? q_out=None, Tensor(b!)? g_bf16=None) "
+      "-> (Tensor, Tensor)");
   m.def(
       "quantize_rows_parts(Tensor[] parts, Tensor? col_scale=None, bool stochastic=False, "
       "int seed=0, Tensor? seed_slot=None, int row_offset=0) -> (Tensor, Tensor)");
@@ -869,9 +974,9 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("normalize_rows(Tensor g, float eps, Tensor(a!)? rms_ema, float beta) -> Tensor");
   m.def("pressure_leak(Tensor(a!) packed, int max_code) -> ()");
   m.def("validate_state(Tensor packed, int max_code, Tensor? scale) -> Tensor");
-  m.def("rmsnorm_quantize(Tensor x, Tensor w, float eps) -> (Tensor, Tensor)");
-  m.def("gelu_quantize(Tensor x) -> (Tensor, Tensor)");
-  m.def("transpose_quantize(Tensor x) -> (Tensor, Tensor)");
+  m.def("rmsnorm_quantize(Tensor x, Tensor w, float eps, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
+  m.def("gelu_quantize(Tensor x, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
+  m.def("transpose_quantize(Tensor x, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
   m.def(
       "rmsnorm_backward(Tensor grad_y, Tensor x, Tensor w, float eps, "
       "Tensor? residual_grad=None) -> (Tensor, Tensor)");
@@ -897,6 +1002,7 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("grad_weight_partials", &grad_weight_partials);
   m.impl("grad_weight_partials_x", &grad_weight_partials_x);
   m.impl("grad_weight_partials_parts", &grad_weight_partials_parts);
+  m.impl("grad_input_sr", &grad_input_sr);
   m.impl("quantize_rows_parts", &quantize_rows_parts);
   m.impl("update_from_z", &update_from_z);
   m.impl("update_from_grad", &update_from_grad);

@@ -611,15 +611,17 @@ extern "C" int rk_grad_weight_bf16(const void* g, int g_dtype, int64_t ldg, cons
 
 extern "C" int rk_grad_weight_bf16_parts(const void* g0, const void* g1, const void* g2,
                                          int nparts, int64_t part_cols, int g_dtype, int64_t ldg,
-                                         const int8_t* q, int64_t ldq, const float* s, int64_t M,
-                                         int64_t N, int64_t K, float* workspace, int nsplit,
-                                         uint16_t* out, int64_t ldo, void* stream) {
+                                         const void* x, int x_dtype, int64_t ldx, const float* s,
+                                         int64_t M, int64_t N, int64_t K, float* workspace,
+                                         int nsplit, uint16_t* out, int64_t ldo, void* stream) {
   clear_error();
   if (nparts < 1 || nparts > 3) return fail(RK_ERR_ARG, "nparts must be 1, 2 or 3");
+  if (x_dtype != RK_F32 && x_dtype != RK_BF16 && x_dtype != RK_I8)
+    return fail(RK_ERR_ARG, "unsupported activation dtype");
+  const int kind = x_dtype == RK_I8 ? GW_X_Q8 : (x_dtype == RK_BF16 ? GW_X_BF16 : GW_X_F32);
   const void* parts[3] = {g0, g1, g2};
-  return grad_weight_launch(g0, g_dtype, ldg, q, GW_X_Q8, ldq, s, M, N, K, workspace, nsplit,
-                            out, ldo, stream, nullptr, nullptr, nullptr, parts, nparts,
-                            part_cols);
+  return grad_weight_launch(g0, g_dtype, ldg, x, kind, ldx, s, M, N, K, workspace, nsplit, out,
+                            ldo, stream, nullptr, nullptr, nullptr, parts, nparts, part_cols);
 }
 
 extern "C" int rk_grad_weight_bf16_x(const void* g, int g_dtype, int64_t ldg, const void* x,

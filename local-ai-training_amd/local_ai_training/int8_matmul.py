@@ -161,6 +161,20 @@ def quantize_rows(values: Tensor) -> tuple[Tensor, Tensor]:
     return _quantize_rows_fused(values)
 
 
+def quantize_rows_dq(values: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """quantize_rows, and the dequantized activations bf16(bf16(q) * bf16(s)) the backward's
+    grad_weight reads (ratchet.py:73-75), written by the same kernel."""
+    if not values.is_cuda:
+        raise RuntimeError("quantize_rows requires CUDA (a ROCm GPU); the int8 path is GPU-only")
+    if values.ndim != 2:
+        raise ValueError("row quantization requires a 2D tensor")
+    if values.dtype not in (torch.float32, torch.bfloat16):
+        values = values.float()
+    xd = torch.empty(values.shape, device=values.device, dtype=torch.bfloat16)
+    q, s = _ops().quantize_rows(values, x_dq=xd)
+    return q, s, xd
+
+
 def quantize_rows_colscaled(values: Tensor, col_scale: Tensor, *,
                             stochastic: bool = False) -> tuple[Tensor, Tensor]:
     """Row-quantize values * col_scale[None, :] in one pass (no M x N float temp)."""
@@ -234,6 +248,37 @@ def packed_t_supported(a: Tensor, packed: Tensor) -> bool:
     return (k % 64 == 0 and n % 8 == 0 and a.stride(-1) == 1 and packed.stride(-1) == 1
             and _ld(a) % 16 == 0 and _ld(packed) % 16 == 0 and a.data_ptr() % 16 == 0
             and packed.data_ptr() % 16 == 0)
+
+
+def grad_input_sr_supported(parts: list[Tensor], packed: Tensor,
+                            col_scale: Tensor | None = None) -> bool:
+    """Whether grad_input_sr takes these operands: 128, 256 or 512 output columns, at most
+    4096 gradient columns in parts of a multiple of 64, 16-byte aligned rows."""
+    k, n = packed.shape
+    c = parts[0].shape[1]
+    ld = parts[0].stride(0) if parts[0].shape[0] > 1 else c
+    return (n in (128, 256, 512) and c * len(parts) == k and k <= 4096 and c % 64 == 0
+            and parts[0].dtype in (torch.float32, torch.bfloat16)
+            and all(p.stride(-1) == 1 and p.data_ptr() % 16 == 0 and p.dtype == parts[0].dtype
+                    and (p.shape[0] <= 1 or p.stride(0) == ld) for p in parts)
+            and (ld * parts[0].element_size()) % 16 == 0
+            and packed.stride(-1) == 1 and _ld(packed) % 16 == 0
+            and packed.data_ptr() % 16 == 0
+            and (col_scale is None or col_scale.data_ptr() % 16 == 0))
+
+
+def grad_input_sr(parts: list[Tensor], packed: Tensor, max_code: int,
+                  col_scale: Tensor | None, out_dtype: torch.dtype, *,
+                  bf16_out: Tensor | None = None, round_bf16: bool = False
+                  ) -> tuple[Tensor, Tensor, int | Tensor]:
+    """grad_input = packed_int8_mm_t(q, packed, max_code, s) for (q, s) the stochastically
+    rounded row quantization of the gradient torch.cat(parts, -1) * col_scale, in one kernel
+    (q never reaches memory). Returns (grad_input, s, seed) with the seed drawn as
+    quantize_rows_sr draws it; ``bf16_out`` / ``round_bf16`` as in quantize_rows_sr."""
+    seed, slot = sr_seed_args(parts[0].device)
+    out, s = _ops().grad_input_sr(list(parts), packed, max_code, col_scale, seed, slot, 0,
+                                  out_dtype, round_bf16, None, bf16_out)
+    return out, s, (slot if slot is not None else seed)
 
 
 def packed_int8_mm_t(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
@@ -351,11 +396,12 @@ def grad_weight_parts_supported(parts: list[Tensor], q: Tensor) -> bool:
             and (q.stride(0) * q.element_size()) % 16 == 0 and q.data_ptr() % 16 == 0)
 
 
-def grad_weight_bf16_parts(parts: list[Tensor], q: Tensor, s: Tensor, *,
+def grad_weight_bf16_parts(parts: list[Tensor], x: Tensor, s: Tensor | None, *,
                            work: Tensor) -> Tensor:
     """grad_weight's float32 split partials for the gradient ``torch.cat(parts, dim=-1)``,
-    read from the parts in place (the same partials as from the concatenation)."""
-    _ops().grad_weight_partials_parts(list(parts), q, s, work)
+    read from the parts in place (the same partials as from the concatenation). x: the int8
+    activations with their row scale s, or bf16 / float32 activations (s None)."""
+    _ops().grad_weight_partials_parts(list(parts), x, s, work)
     return work
 
 

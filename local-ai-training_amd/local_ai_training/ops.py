@@ -54,7 +54,7 @@ def _register_fakes() -> None:
 
     @fake("ratchet::quantize_rows")
     def _quantize_rows(x, col_scale=None, stochastic=False, seed=0, seed_slot=None,
-                       row_offset=0, x_bf16=None, round_bf16=False):
+                       row_offset=0, x_bf16=None, round_bf16=False, x_dq=None):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::int8_mm_nt")
@@ -123,15 +123,15 @@ def _register_fakes() -> None:
         return packed.new_empty((3,), dtype=torch.int32)
 
     @fake("ratchet::rmsnorm_quantize")
-    def _rmsnorm_quantize(x, w, eps):
+    def _rmsnorm_quantize(x, w, eps, x_dq=None):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::gelu_quantize")
-    def _gelu_quantize(x):
+    def _gelu_quantize(x, x_dq=None):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::transpose_quantize")
-    def _transpose_quantize(x):
+    def _transpose_quantize(x, x_dq=None):
         b, h, s, d = x.shape
         return (x.new_empty((b * s, h * d), dtype=torch.int8),
                 x.new_empty((b * s,), dtype=torch.float32))
@@ -155,8 +155,16 @@ def _register_fakes() -> None:
         return (parts[0].new_empty((m, k), dtype=torch.int8),
                 parts[0].new_empty((m,), dtype=torch.float32))
 
+    @fake("ratchet::grad_input_sr")
+    def _grad_input_sr(parts, packed, max_code, col_scale=None, seed=0, seed_slot=None,
+                       row_offset=0, out_dtype=torch.bfloat16, round_bf16=False, q_out=None,
+                       g_bf16=None):
+        m = parts[0].shape[0]
+        return (parts[0].new_empty((m, packed.shape[1]), dtype=out_dtype),
+                parts[0].new_empty((m,), dtype=torch.float32))
+
     @fake("ratchet::grad_weight_partials_parts")
-    def _grad_weight_partials_parts(parts, q, s, work):
+    def _grad_weight_partials_parts(parts, x, s, work):
         return None
 
     @fake("ratchet::embedding_backward")
@@ -173,5 +181,5 @@ OPERATORS = (
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
-    "grad_weight_partials_parts",
+    "grad_weight_partials_parts", "grad_input_sr",
 )

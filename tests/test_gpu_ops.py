@@ -64,6 +64,8 @@ def cases(t, cuda):
         (R.quantize_rows, (t["x"],), {}),
         (R.quantize_rows, (t["gf"], t["scale"], True, 77), {"x_bf16": torch.empty_like(t["g"])}),
         (R.quantize_rows, (t["g"], t["scale"], True, 0, seed), {}),
+        (R.quantize_rows, (t["x"],), {"x_dq": torch.empty(M, K, dtype=torch.bfloat16,
+                                                          device=cuda)}),
         (R.int8_mm_nt, (t["q"], t["b"], t["s"], t["scale"], torch.bfloat16), {}),
         (R.packed_mm, (t["q"], t["packed"], MC, t["s"], t["scale"], torch.float32), {}),
         (R.packed_mm_residual, (t["q"], t["packed"], MC, t["s"], t["scale"], t["res"]), {}),
@@ -93,8 +95,13 @@ def cases(t, cuda):
         (R.pressure_leak, (t["packed"].clone(), MC), {}),
         (R.validate_state, (t["packed"], MC, t["scale"]), {}),
         (R.rmsnorm_quantize, (t["x"], torch.ones(K, device=cuda), 1e-5), {}),
+        (R.rmsnorm_quantize, (t["x"], torch.ones(K, device=cuda), 1e-5,
+                              torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
         (R.gelu_quantize, (t["xb"],), {}),
+        (R.gelu_quantize, (t["xb"], torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
         (R.transpose_quantize, (t["att"],), {}),
+        (R.transpose_quantize, (t["att"], torch.empty(96, 128, dtype=torch.bfloat16,
+                                                      device=cuda)), {}),
         (R.rmsnorm_backward, (t["xb"], t["xb"], torch.ones(K, device=cuda), 1e-5), {}),
         (R.rmsnorm_backward, (t["xb"], t["x"], torch.ones(K, device=cuda), 1e-5, t["x"] * 0.5),
          {}),
@@ -104,10 +111,16 @@ def cases(t, cuda):
         (R.quantize_rows_parts, (parts, t["scale"].repeat(3), True, 5), {}),
         (R.quantize_rows_parts, ([p.contiguous() for p in parts[:2]],), {}),
         (R.grad_weight_partials_parts, (parts, t["q"], t["s"], work3), {}),
+        (R.grad_weight_partials_parts, (parts, t["xb"], None, work3.clone()), {}),
+        (R.grad_input_sr, ([t["xb"]], t["packed_kn"], MC, t["scale"][:K].contiguous(), 5), {}),
+        (R.grad_input_sr, ([t["x"][:, :64], t["x"][:, 64:]], t["packed_kn"], MC, None, 6, None,
+                           3, torch.float32, True,
+                           torch.empty(M, K, dtype=torch.int8, device=cuda),
+                           torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
     ]
 
 
-N_CASES = 36
+N_CASES = 43
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):

@@ -97,8 +97,12 @@ def test_grad_weight_partials_parts_equal_those_of_the_concatenation(cuda, m, c,
     work_ref = torch.full_like(work, float("nan"))
     R.grad_weight_partials_parts(parts, q, s, work)
     R.grad_weight_partials(whole, q, s, work_ref)
+    # the dequantized bf16 activations give the same partials
+    xd = R.dequant_bf16(q, s)
+    work_x = torch.full_like(work, float("nan"))
+    R.grad_weight_partials_parts(parts, xd, None, work_x)
     torch.cuda.synchronize()
-    assert torch.equal(work, work_ref)
+    assert torch.equal(work, work_ref) and torch.equal(work_x, work_ref)
 
 
 def test_parts_through_the_c_abi(cuda):
@@ -117,7 +121,7 @@ def test_parts_through_the_c_abi(cuda):
     out = torch.empty(3 * c, k, dtype=torch.bfloat16, device=cuda)
     nsplit = ratchet().grad_weight_splits(m, 3 * c, k)
     work = torch.empty(nsplit, 3 * c, k, device=cuda)
-    nat.call("rk_grad_weight_bf16_parts", *p, 3, c, nat.RK_BF16, c, a.data_ptr(), k,
+    nat.call("rk_grad_weight_bf16_parts", *p, 3, c, nat.RK_BF16, c, a.data_ptr(), nat.RK_I8, k,
              sa.data_ptr(), m, 3 * c, k, work.data_ptr(), nsplit, out.data_ptr(), k, stream)
     torch.cuda.synchronize()
     assert torch.equal(q, q_ref) and torch.equal(s, s_ref)
@@ -142,6 +146,8 @@ def test_parts_reject_bad_arguments(cuda):
     assert not grad_weight_parts_supported(odd, q)
     with pytest.raises(RuntimeError):
         R.grad_weight_partials_parts(odd, q, s, work)
+    with pytest.raises(RuntimeError, match="row scale"):
+        R.grad_weight_partials_parts(parts, q, None, work)
     stream = nat.stream_handle(cuda)
     out = torch.empty(8, 384, dtype=torch.int8, device=cuda)
     with pytest.raises(nat.NativeError):
