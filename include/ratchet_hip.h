@@ -496,7 +496,7 @@ int rk_rmsnorm_backward_residual(const void* grad_y, int gy_dtype, int64_t ldg, 
                                  int64_t ldgx, float* grad_w, float* workspace,
                                  int64_t workspace_floats, void* stream);
 
-/* Number of grad_w partial rows rk_rmsnorm_backward uses for M rows (0 for M <= 0, at most 512). */
+/* Number of grad_w partial rows rk_rmsnorm_backward uses for M rows (0 for M <= 0, at most 1024). */
 int rk_rmsnorm_backward_parts(int64_t M);
 
 /*
@@ -581,6 +581,33 @@ int rk_decode_attention(const void* qkv, int qkv_dtype, int64_t ld_qkv, void* k_
 int rk_decode_embed(const int64_t* tokens, int64_t B, const float* table, int64_t vocab,
                     int64_t C, const float* pos_table, int64_t n_pos, const int64_t* pos,
                     float* hidden, int64_t ldh, void* stream);
+
+/*
+ * Token cross-entropy, mean over the rows whose target is not ignore_index: per row of
+ * logits [M, V] (float32 / bfloat16, row stride ldl, 16-byte aligned rows, V a multiple of
+ * 4 / 8), m = max x, logsum = log(sum exp(x - m)), loss_row = -((x_t - m) - logsum);
+ * *loss = (sum of loss_row in a fixed order) / count, *count = the number of rows counted
+ * (float; 0 gives NaN). A target outside [0, V) other than ignore_index gives a NaN loss.
+ * stats [3, M] float32 receives (m, logsum, loss_row) for rk_cross_entropy_backward.
+ * targets int64 [M]. Shapes outside the aligned form: RK_ERR_UNSUPPORTED.
+ * Replaces: F.cross_entropy(logits.flatten(0, 1), targets.flatten()), model.py:249
+ *           (log_softmax + nll_loss forward).
+ */
+int rk_cross_entropy_forward(const void* logits, int dtype, int64_t ldl, const int64_t* targets,
+                             int64_t M, int64_t V, int64_t ignore_index, float* stats,
+                             float* loss, float* count, void* stream);
+
+/*
+ * Its backward: with g_t = -(*grad_loss / *count) for a counted row (0 for an ignored one),
+ * grad[j] = [j == t] g_t - exp((x_j - m) - logsum) * g_t, stored as grad_dtype (float32 or
+ * bfloat16, 16-byte aligned rows: ldg a multiple of 16 bytes); grad_loss and count are
+ * device scalars (count from the forward). Nothing else is written.
+ * Replaces: the backward of model.py:249 (nll_loss and log_softmax backward).
+ */
+int rk_cross_entropy_backward(const void* logits, int dtype, int64_t ldl, const int64_t* targets,
+                              int64_t M, int64_t V, int64_t ignore_index, const float* stats,
+                              const float* count, const float* grad_loss, void* grad,
+                              int grad_dtype, int64_t ldg, void* stream);
 
 /* HBM streaming probe (measurement only; no counterpart in the reference): reads `bytes`
  * (a multiple of 16) from src in 16-byte vectors, `unroll` (1, 2, 4, 8) loads in flight

@@ -915,6 +915,66 @@ Tensor embedding_backward(const Tensor& grad_in, const Tensor& ids_in, int64_t n
   return out;
 }
 
+// F.cross_entropy(logits, targets) (mean, ignore_index) in two launches: per-row max, log
+// of the sum of exponentials and loss (kept in `stats` for the backward), then the mean in
+// a fixed order. Returns (loss, stats [3, M], count), loss and count 0-d float32.
+std::tuple<Tensor, Tensor, Tensor> cross_entropy_forward(const Tensor& logits_in,
+                                                         const Tensor& targets_in,
+                                                         int64_t ignore_index) {
+  require_gpu(logits_in, "cross entropy");
+  same_device(logits_in, targets_in, "cross entropy");
+  TORCH_CHECK(logits_in.dim() == 2, "cross entropy: logits must be 2-D, got ",
+              logits_in.sizes());
+  TORCH_CHECK(targets_in.scalar_type() == at::kLong, "cross entropy: targets must be int64");
+  TORCH_CHECK(targets_in.dim() == 1 && targets_in.size(0) == logits_in.size(0),
+              "cross entropy: targets must be 1-D with one entry per row");
+  const Tensor logits = unit_columns(logits_in);
+  const Tensor targets = targets_in.contiguous();
+  const int64_t m = logits.size(0), v = logits.size(1);
+  const c10::DeviceGuard guard(logits.device());
+  const auto f32 = logits.options().dtype(at::kFloat);
+  Tensor stats = at::empty({3, m}, f32);
+  Tensor loss = at::empty({}, f32);
+  Tensor count = at::empty({}, f32);
+  check_status(rk_cross_entropy_forward(logits.data_ptr(), dtype_code(logits, "logits"),
+                                        ld(logits), targets.data_ptr<int64_t>(), m, v,
+                                        ignore_index, stats.data_ptr<float>(),
+                                        loss.data_ptr<float>(), count.data_ptr<float>(),
+                                        stream_of(logits)),
+               "rk_cross_entropy_forward");
+  return {loss, stats, count};
+}
+
+// The gradient of cross_entropy_forward's loss with respect to the logits, in the logits'
+// dtype (for bfloat16 logits: the float32 gradient rounded once, as a bfloat16 consumer
+// casts it).
+Tensor cross_entropy_backward(const Tensor& grad_loss_in, const Tensor& logits_in,
+                              const Tensor& targets_in, const Tensor& stats,
+                              const Tensor& count, int64_t ignore_index) {
+  require_gpu(logits_in, "cross entropy backward");
+  TORCH_CHECK(logits_in.dim() == 2, "cross entropy backward: logits must be 2-D");
+  TORCH_CHECK(targets_in.scalar_type() == at::kLong, "cross entropy backward: targets must be int64");
+  const Tensor logits = unit_columns(logits_in);
+  const Tensor targets = targets_in.contiguous();
+  const int64_t m = logits.size(0), v = logits.size(1);
+  TORCH_CHECK(targets.numel() == m, "cross entropy backward: one target per row");
+  TORCH_CHECK(stats.scalar_type() == at::kFloat && stats.is_contiguous() && stats.numel() == 3 * m,
+              "cross entropy backward: stats must be the forward's float32 [3, M]");
+  TORCH_CHECK(count.numel() == 1 && count.scalar_type() == at::kFloat,
+              "cross entropy backward: count must be the forward's float32 scalar");
+  const Tensor grad_loss = grad_loss_in.to(at::kFloat).reshape({}).contiguous();
+  const c10::DeviceGuard guard(logits.device());
+  Tensor grad = at::empty({m, v}, logits.options());
+  check_status(rk_cross_entropy_backward(logits.data_ptr(), dtype_code(logits, "logits"),
+                                         ld(logits), targets.data_ptr<int64_t>(), m, v,
+                                         ignore_index, stats.data_ptr<float>(),
+                                         count.data_ptr<float>(), grad_loss.data_ptr<float>(),
+                                         grad.data_ptr(), dtype_code(grad, "grad"), v,
+                                         stream_of(logits)),
+               "rk_cross_entropy_backward");
+  return grad;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(ratchet, m) {
@@ -982,6 +1042,10 @@ TORCH_LIBRARY(ratchet, m) {
       "Tensor? residual_grad=None) -> (Tensor, Tensor)");
   m.def("gelu_backward(Tensor grad_y, Tensor x) -> Tensor");
   m.def("embedding_backward(Tensor grad, Tensor ids, int num_weights) -> Tensor");
+  m.def("cross_entropy_forward(Tensor logits, Tensor targets, int ignore_index=-100) -> "
+        "(Tensor, Tensor, Tensor)");
+  m.def("cross_entropy_backward(Tensor grad_loss, Tensor logits, Tensor targets, Tensor stats, "
+        "Tensor count, int ignore_index=-100) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
@@ -1016,4 +1080,6 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("rmsnorm_backward", &rmsnorm_backward);
   m.impl("gelu_backward", &gelu_backward);
   m.impl("embedding_backward", &embedding_backward);
+  m.impl("cross_entropy_forward", &cross_entropy_forward);
+  m.impl("cross_entropy_backward", &cross_entropy_backward);
 }

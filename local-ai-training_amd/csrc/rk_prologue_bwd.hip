@@ -9,7 +9,8 @@
 // gelu_backward, int8_backward.py:53-89, elementwise:
 //   t  = tanh(sqrt(2/pi) * (x + 0.044715 * x * x^2))
 //   dx = grad_y * (0.5 * (1 + t) + 0.5 * x * (1 - t^2) * sqrt(2/pi) * (1 + 0.134145 * x^2))
-//   -> rounded to bf16, stored in x's dtype.
+//   -> rounded to bf16, stored in x's dtype. tanh is evaluated as 1 - 2 / (exp(2u) + 1) from
+//   the hardware exp2 and reciprocal (absolute error < 3e-7, see tanh_fast).
 //
 // Both are HBM-bound streams. The RMSNorm kernel keeps a whole row in registers (one
 // wavefront per row, 4 columns per lane per 256-column chunk, K <= 4096), so x and
@@ -24,7 +25,8 @@ namespace {
 constexpr int kBwdV = 4;                   // columns per lane per chunk
 constexpr int kBwdSpan = kWave * kBwdV;    // 256 columns per chunk
 constexpr int kBwdMaxChunks = 16;          // K <= 4096 on the register-resident path
-constexpr int kBwdTargetBlocks = 512;      // grid size the row split aims for
+constexpr int kBwdTargetBlocks = 1024;     // grid size the row split aims for
+constexpr int kGeluG = 8;                  // GELU backward: columns per thread
 
 // Valid columns (0..4) of the 4-column group starting at e0 in a row of K.
 __device__ __forceinline__ int quad_valid(int64_t K, int64_t e0) {
@@ -102,15 +104,21 @@ struct NormBwdArgs {
   int64_t lda;
 };
 
+// One row's x, grad_y and (float32 x with a residual gradient) the residual gradient, all
+// requested before any is used.
 template <int GDT, int XDT, int NC>
 __device__ __forceinline__ void norm_load_row(const NormBwdArgs& a, int64_t row, int lane,
-                                              float (&xv)[NC][kBwdV], float (&gv)[NC][kBwdV]) {
+                                              float (&xv)[NC][kBwdV], float (&gv)[NC][kBwdV],
+                                              float (&av)[NC][kBwdV]) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int64_t e0 = c * kBwdSpan + lane * kBwdV;
     const int n = quad_valid(a.K, e0);
     load4<XDT>(a.x, row * a.ldx + e0, n, a.vec, xv[c]);
     load4<GDT>(a.gy, row * a.ldg + e0, n, a.vec, gv[c]);
+    if constexpr (XDT == RK_F32) {
+      if (a.add) load4<RK_F32>(a.add, row * a.lda + e0, n, a.vec, av[c]);
+    }
   }
 }
 
@@ -138,13 +146,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
   }
 
   int64_t row = r0 + wave;
-  float xv[NC][kBwdV], gv[NC][kBwdV];
-  if (row < r1) norm_load_row<GDT, XDT, NC>(a, row, lane, xv, gv);
+  float xv[NC][kBwdV], gv[NC][kBwdV], av[NC][kBwdV];
+  if (row < r1) norm_load_row<GDT, XDT, NC>(a, row, lane, xv, gv, av);
   while (row < r1) {
     const int64_t next = row + 4;
-    float xn[NC][kBwdV], gn[NC][kBwdV];
+    float xn[NC][kBwdV], gn[NC][kBwdV], an[NC][kBwdV];
     if constexpr (PREFETCH) {
-      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xn, gn);
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xn, gn, an);
     }
     float sxx = 0.0f, sgx = 0.0f;
 #pragma unroll
@@ -171,10 +179,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
         if (a.add && nv[c] > 0) {
           // the residual stream's gradient joins here: one float32 add of the two
           // contributions, the add autograd performs where x feeds both paths
-          float ad[kBwdV];
-          load4<RK_F32>(a.add, row * a.lda + e0, nv[c], a.vec, ad);
 #pragma unroll
-          for (int i = 0; i < kBwdV; ++i) dx[i] = round_bf16(dx[i]) + ad[i];
+          for (int i = 0; i < kBwdV; ++i) dx[i] = round_bf16(dx[i]) + av[c][i];
           float* p = static_cast<float*>(a.gx) + row * a.ldgx + e0;
           if (a.vec && nv[c] == 4) {
             *reinterpret_cast<float4*>(p) = make_float4(dx[0], dx[1], dx[2], dx[3]);
@@ -195,9 +201,10 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
         for (int i = 0; i < kBwdV; ++i) {
           xv[c][i] = xn[c][i];
           gv[c][i] = gn[c][i];
+          av[c][i] = an[c][i];
         }
     } else {
-      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xv, gv);
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xv, gv, av);
     }
     row = next;
   }
@@ -244,9 +251,39 @@ struct GeluBwdArgs {
   void* gx;
   int64_t ldgx;
   int64_t M, K;
-  int64_t quads;  // ceil(K / 4) column groups per row
-  int vec;
+  int64_t groups;  // ceil(K / kGeluG) column groups per row
+  int vec;         // 4-element vector access is legal for x, grad_y and grad_x
+  int vec8;        // ... and every 8-column group starts 16-byte aligned
 };
+
+// 8 elements at a 16-byte aligned address, widened to float32.
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t idx, float* v) {
+  if constexpr (DT == RK_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + idx);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+}
+
+// tanh(u) = 1 - 2 / (exp(2u) + 1) from the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32). Absolute error below 3e-7 everywhere (the exponent's argument rounding, one
+// ulp each of exp2 and rcp, the final subtraction); exp overflow gives 1, underflow -1.
+// The derivative below uses t only through 0.5 (1 + t) and 1 - t^2, where an absolute
+// error that size is below a millionth of the result, far under the bf16 rounding of dx.
+__device__ __forceinline__ float tanh_fast(float u) {
+  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // 2 log2(e) u
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
 
 // The derivative of the tanh-GELU, evaluated in the operation order of
 // int8_backward.py:65-72.
@@ -254,28 +291,47 @@ __device__ __forceinline__ float gelu_tanh_grad(float x) {
   const float k = 0.7978845608028654f;
   const float x_sq = x * x;
   const float inner = k * (x + 0.044715f * x * x_sq);
-  const float t = tanhf(inner);
+  const float t = tanh_fast(inner);
   const float term1 = 0.5f * (1.0f + t);
   const float term2 = 0.5f * x * (1.0f - t * t) * k * (1.0f + 0.134145f * x_sq);
   return term1 + term2;
 }
 
-// One thread = 4 consecutive columns of one row; grid-stride over M * quads groups.
+// One thread = kGeluG consecutive columns of one row (two 4-column groups: 16-byte bf16 or
+// 2 x 16-byte float32 accesses); grid-stride over M * groups.
 template <int GDT, int XDT>
 __global__ __launch_bounds__(256) void gelu_bwd_kernel(GeluBwdArgs a) {
-  const int64_t total = a.M * a.quads;
+  const int64_t total = a.M * a.groups;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   for (int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; u < total;
        u += stride) {
-    const int64_t row = u / a.quads;
-    const int64_t e0 = (u - row * a.quads) * kBwdV;
-    const int n = quad_valid(a.K, e0);
-    float xv[kBwdV], gv[kBwdV], dx[kBwdV];
-    load4<XDT>(a.x, row * a.ldx + e0, n, a.vec, xv);
-    load4<GDT>(a.gy, row * a.ldg + e0, n, a.vec, gv);
+    const int64_t row = u / a.groups;
+    const int64_t e0 = (u - row * a.groups) * kGeluG;
+    if (a.vec8) {
+      float xv[kGeluG], gv[kGeluG], dx[kGeluG];
+      load8<XDT>(a.x, row * a.ldx + e0, xv);
+      load8<GDT>(a.gy, row * a.ldg + e0, gv);
 #pragma unroll
-    for (int i = 0; i < kBwdV; ++i) dx[i] = gv[i] * gelu_tanh_grad(xv[i]);
-    store4_bf16<XDT>(a.gx, row * a.ldgx + e0, n, a.vec, dx);
+      for (int i = 0; i < kGeluG; ++i) dx[i] = gv[i] * gelu_tanh_grad(xv[i]);
+      store4_bf16<XDT>(a.gx, row * a.ldgx + e0, kBwdV, true, dx);
+      store4_bf16<XDT>(a.gx, row * a.ldgx + e0 + kBwdV, kBwdV, true, dx + kBwdV);
+      continue;
+    }
+    float xv[2][kBwdV], gv[2][kBwdV];
+    int n[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      n[h] = quad_valid(a.K, e0 + h * kBwdV);
+      load4<XDT>(a.x, row * a.ldx + e0 + h * kBwdV, n[h], a.vec, xv[h]);
+      load4<GDT>(a.gy, row * a.ldg + e0 + h * kBwdV, n[h], a.vec, gv[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float dx[kBwdV];
+#pragma unroll
+      for (int i = 0; i < kBwdV; ++i) dx[i] = gv[h][i] * gelu_tanh_grad(xv[h][i]);
+      if (n[h] > 0) store4_bf16<XDT>(a.gx, row * a.ldgx + e0 + h * kBwdV, n[h], a.vec, dx);
+    }
   }
 }
 
@@ -418,10 +474,12 @@ extern "C" int rk_gelu_backward(const void* grad_y, int gy_dtype, int64_t ldg, c
   if (ldg < K || ldx < K || ldgx < K) return fail(RK_ERR_ARG, "leading dimension below K");
   GeluBwdArgs a{};
   a.gy = grad_y; a.ldg = ldg; a.x = x; a.ldx = ldx; a.gx = grad_x; a.ldgx = ldgx;
-  a.M = M; a.K = K; a.quads = (K + kBwdV - 1) / kBwdV;
+  a.M = M; a.K = K; a.groups = (K + kGeluG - 1) / kGeluG;
   a.vec = vec4_ok(grad_y, gy_dtype, ldg, K) && vec4_ok(x, x_dtype, ldx, K) &&
           vec4_ok(grad_x, x_dtype, ldgx, K);
-  const int64_t total = M * a.quads;
+  a.vec8 = a.vec && K % kGeluG == 0 && ldg % kGeluG == 0 && ldx % kGeluG == 0 &&
+           ldgx % kGeluG == 0 && aligned16(grad_y) && aligned16(x) && aligned16(grad_x);
+  const int64_t total = M * a.groups;
   const int64_t want = (total + 255) / 256;
   const int64_t blocks = want < (int64_t{1} << 20) ? want : (int64_t{1} << 20);
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);

@@ -21,6 +21,7 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
+from .cross_entropy import cross_entropy
 from .int8_fused import (
     FusedGELUQuantizeFn,
     FusedRMSNormQuantizeFn,
@@ -419,6 +420,9 @@ class RatchetGPT(nn.Module):
     hip_embedding_backward: bool = True
     # the layers' move counts in one model-level buffer, summed and cleared once per step
     shared_move_counts: bool = True
+    # the training loss from the HIP cross-entropy kernels (False: F.cross_entropy); with an
+    # int8 lm_head the logits of a forward with targets are then bfloat16 (the same values)
+    fused_cross_entropy: bool = True
 
     def __init__(self, config: ModelConfig, *, max_code: int | None) -> None:
         super().__init__()
@@ -464,11 +468,20 @@ class RatchetGPT(nn.Module):
                 hidden = checkpoint(block, hidden, use_reentrant=False)
             else:
                 hidden = block(hidden)
-        logits = self.lm_head(self.final_norm(hidden))
+        if targets is not None and targets.shape != tokens.shape:
+            raise ValueError("targets must have the same shape as tokens")
+        fused_loss = (targets is not None and self.fused_cross_entropy and hidden.is_cuda
+                      and targets.dtype == torch.int64)
+        if fused_loss and _is_int8(self.lm_head):
+            # the int8 lm_head's float32 output is its bf16 result widened: the loss reads
+            # the bf16 logits (the same values) and hands their gradient back as bf16
+            logits = self.lm_head(self.final_norm(hidden), out_dtype=torch.bfloat16)
+        else:
+            logits = self.lm_head(self.final_norm(hidden))
         loss = None
-        if targets is not None:
-            if targets.shape != tokens.shape:
-                raise ValueError("targets must have the same shape as tokens")
+        if fused_loss:
+            loss = cross_entropy(logits.flatten(0, 1), targets.flatten())
+        elif targets is not None:
             loss = F.cross_entropy(logits.flatten(0, 1), targets.flatten())
         return logits, loss
 

@@ -171,6 +171,16 @@ def _register_fakes() -> None:
     def _embedding_backward(grad, ids, num_weights):
         return grad.new_empty((num_weights, grad.shape[-1]), dtype=torch.float32)
 
+    @fake("ratchet::cross_entropy_forward")
+    def _cross_entropy_forward(logits, targets, ignore_index=-100):
+        f32 = torch.float32
+        return (logits.new_empty((), dtype=f32), logits.new_empty((3, logits.shape[0]), dtype=f32),
+                logits.new_empty((), dtype=f32))
+
+    @fake("ratchet::cross_entropy_backward")
+    def _cross_entropy_backward(grad_loss, logits, targets, stats, count, ignore_index=-100):
+        return logits.new_empty((logits.shape[0], logits.shape[1]))
+
 
 # every operator the library defines (the opcheck tests walk this list)
 OPERATORS = (
@@ -181,5 +191,6 @@ OPERATORS = (
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
-    "grad_weight_partials_parts", "grad_input_sr",
+    "grad_weight_partials_parts", "grad_input_sr", "cross_entropy_forward",
+    "cross_entropy_backward",
 )

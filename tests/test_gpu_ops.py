@@ -58,6 +58,10 @@ def cases(t, cuda):
     seed = torch.tensor([1234], dtype=torch.int64, device=cuda)
     rule = (MC, 8, 0.5, 1.5, 1e-8)
     whole = (torch.randn(M, 3 * N, generator=gen(11)) * 1e-2).to(torch.bfloat16).to(cuda)
+    tgt = torch.randint(0, K, (M,), generator=gen(12)).to(cuda)
+    tgt_ignored = torch.where(torch.arange(M, device=cuda) % 7 == 0, -1, tgt)
+    xent_b = R.cross_entropy_forward(t["xb"], tgt)
+    xent_f = R.cross_entropy_forward(t["x"], tgt_ignored, -1)
     parts = list(whole.chunk(3, dim=-1))
     work3 = torch.zeros(R.grad_weight_splits(M, 3 * N, K), 3 * N, K, device=cuda)
     return [
@@ -117,10 +121,15 @@ def cases(t, cuda):
                            3, torch.float32, True,
                            torch.empty(M, K, dtype=torch.int8, device=cuda),
                            torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
+        (R.cross_entropy_forward, (t["xb"], tgt), {}),
+        (R.cross_entropy_forward, (t["x"], tgt_ignored, -1), {}),
+        (R.cross_entropy_backward, (torch.ones((), device=cuda), t["xb"], tgt, *xent_b[1:]), {}),
+        (R.cross_entropy_backward, (torch.full((), 0.5, device=cuda), t["x"], tgt_ignored,
+                                    *xent_f[1:], -1), {}),
     ]
 
 
-N_CASES = 43
+N_CASES = 47
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):

@@ -110,6 +110,12 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
     qp, sp = R.quantize_rows_parts(parts, meta(3 * n), True, 7)
     assert (qp.shape, qp.dtype, sp.shape, sp.dtype) == ((m, 3 * n), torch.int8, (m,),
                                                           torch.float32)
+    tg = meta(m, dtype=torch.int64)
+    loss, stats, count = R.cross_entropy_forward(x, tg)
+    assert (loss.shape, stats.shape, count.shape) == ((), (3, m), ())
+    assert loss.dtype == stats.dtype == count.dtype == torch.float32
+    grad = R.cross_entropy_backward(meta(), x, tg, stats, count)
+    assert grad.shape == (m, k) and grad.dtype == torch.bfloat16
 
 
 def test_split_count_query_runs_on_the_host(R):
