@@ -112,6 +112,15 @@ __device__ __forceinline__ void load_vec16(const void* base, int64_t idx, float*
   }
 }
 
+// tanh(u) = 1 - 2 / (exp(2u) + 1) from the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32), about 5 instructions against ~25 for the correctly rounded tanhf. Absolute
+// error below 3e-7 everywhere (the exponent argument's rounding, one ulp each of exp2 and
+// rcp, the final subtraction); exp overflow gives 1, underflow -1, NaN stays NaN.
+__device__ __forceinline__ float tanh_fast(float u) {
+  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // 2 log2(e) u
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront reductions (xor butterfly; every lane ends with the same value).
 // The float sum's association order is fixed: offsets 32, 16, 8, 4, 2, 1 with

@@ -275,18 +275,9 @@ __device__ __forceinline__ void load8(const void* base, int64_t idx, float* v) {
   }
 }
 
-// tanh(u) = 1 - 2 / (exp(2u) + 1) from the hardware exp2 and reciprocal (v_exp_f32,
-// v_rcp_f32). Absolute error below 3e-7 everywhere (the exponent's argument rounding, one
-// ulp each of exp2 and rcp, the final subtraction); exp overflow gives 1, underflow -1.
-// The derivative below uses t only through 0.5 (1 + t) and 1 - t^2, where an absolute
-// error that size is below a millionth of the result, far under the bf16 rounding of dx.
-__device__ __forceinline__ float tanh_fast(float u) {
-  const float e = __builtin_amdgcn_exp2f(u * 2.8853900817779268f);  // 2 log2(e) u
-  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-}
-
 // The derivative of the tanh-GELU, evaluated in the operation order of
-// int8_backward.py:65-72.
+// int8_backward.py:65-72. It uses t only through 0.5 (1 + t) and 1 - t^2, where tanh_fast's
+// absolute error is below a millionth of the result, far under the bf16 rounding of dx.
 __device__ __forceinline__ float gelu_tanh_grad(float x) {
   const float k = 0.7978845608028654f;
   const float x_sq = x * x;

@@ -9,9 +9,11 @@ namespace rk {
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), evaluated in the
-  // operation order of int8_fused.py:72-75.
+  // operation order of int8_fused.py:72-75. tanh_fast's absolute error (< 3e-7) moves the
+  // result by under 1.5e-7 |x|, a ten-thousandth of an int8 step for rows whose absmax
+  // exceeds 0.2 |x|: quantized values change only where they sit on a rounding boundary.
   const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  const float t = tanhf(inner);
+  const float t = tanh_fast(inner);
   return 0.5f * x * (1.0f + t);
 }
 
