@@ -385,6 +385,19 @@ int rk_ratchet_update_partials(uint8_t* packed, int64_t ldp, const float* partia
                                void* stream);
 
 /*
+ * Means of segments of a row-rms buffer: means[s] = mean of row_rms[offsets[s] ..
+ * offsets[s + 1]) for s < nseg (offsets: nseg + 1 device int64, non-decreasing; an empty
+ * segment gives NaN), each summed in the order the update entry points use for their
+ * rms_mean, so a layer's mean here equals the one its update launch would have written.
+ * One launch for every layer of a model whose updates wrote their row rms into one buffer
+ * with rms_mean = NULL.
+ * Replaces: the per-layer mean of the row rms, ratchet.py:570 / 637 (gradient_rms_mean),
+ *           averaged over layers in model.py:265-267.
+ */
+int rk_row_rms_means(const float* row_rms, const int64_t* offsets, int64_t nseg, float* means,
+                     void* stream);
+
+/*
  * Row normalization alone: z = g / (rms + eps) with rms = sqrt(sum_k g^2 / K) in the
  * same fixed order as rk_ratchet_update_grad (or sqrt of the per-row EMA, which is
  * updated in place when rms_ema is non-NULL). z float32 [rows, K] (row stride ldz);

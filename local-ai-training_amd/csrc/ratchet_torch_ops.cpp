@@ -915,6 +915,24 @@ Tensor embedding_backward(const Tensor& grad_in, const Tensor& ids_in, int64_t n
   return out;
 }
 
+// Means of segments [offsets[s], offsets[s + 1]) of a float32 row-rms buffer (rk_row_rms_means).
+Tensor row_rms_means(const Tensor& row_rms, const Tensor& offsets) {
+  require_gpu(row_rms, "row rms means");
+  same_device(row_rms, offsets, "row rms means");
+  TORCH_CHECK(row_rms.scalar_type() == at::kFloat && row_rms.dim() == 1 && row_rms.is_contiguous(),
+              "row rms means: row_rms must be a contiguous float32 vector");
+  TORCH_CHECK(offsets.scalar_type() == at::kLong && offsets.dim() == 1 && offsets.size(0) >= 1 &&
+                  offsets.is_contiguous(),
+              "row rms means: offsets must be a contiguous int64 vector of nseg + 1 entries");
+  const int64_t nseg = offsets.size(0) - 1;
+  const c10::DeviceGuard guard(row_rms.device());
+  Tensor means = at::empty({nseg}, row_rms.options());
+  check_status(rk_row_rms_means(row_rms.data_ptr<float>(), offsets.data_ptr<int64_t>(), nseg,
+                                means.data_ptr<float>(), stream_of(row_rms)),
+               "rk_row_rms_means");
+  return means;
+}
+
 // F.cross_entropy(logits, targets) (mean, ignore_index) in two launches: per-row max, log
 // of the sum of exponentials and loss (kept in `stats` for the backward), then the mean in
 // a fixed order. Returns (loss, stats [3, M], count), loss and count 0-d float32.
@@ -1042,6 +1060,7 @@ TORCH_LIBRARY(ratchet, m) {
       "Tensor? residual_grad=None) -> (Tensor, Tensor)");
   m.def("gelu_backward(Tensor grad_y, Tensor x) -> Tensor");
   m.def("embedding_backward(Tensor grad, Tensor ids, int num_weights) -> Tensor");
+  m.def("row_rms_means(Tensor row_rms, Tensor offsets) -> Tensor");
   m.def("cross_entropy_forward(Tensor logits, Tensor targets, int ignore_index=-100) -> "
         "(Tensor, Tensor, Tensor)");
   m.def("cross_entropy_backward(Tensor grad_loss, Tensor logits, Tensor targets, Tensor stats, "
@@ -1080,6 +1099,7 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("rmsnorm_backward", &rmsnorm_backward);
   m.impl("gelu_backward", &gelu_backward);
   m.impl("embedding_backward", &embedding_backward);
+  m.impl("row_rms_means", &row_rms_means);
   m.impl("cross_entropy_forward", &cross_entropy_forward);
   m.impl("cross_entropy_backward", &cross_entropy_backward);
 }

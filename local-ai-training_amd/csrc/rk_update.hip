@@ -53,18 +53,36 @@ __global__ __launch_bounds__(256) void ratchet_update_z_kernel(
 }
 
 
-__global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms, int64_t rows,
-                                                            float* mean) {
-  __shared__ float part[256];
+// Mean of rows values with one 256-thread block, in a fixed order: thread t adds rows t,
+// t + 256, ... in order, then a halving tree (t += t + w for w = 128 .. 1). Thread 0 gets it.
+__device__ __forceinline__ float block_mean_256(const float* x, int64_t rows, float* part) {
   float acc = 0.0f;
-  for (int64_t r = threadIdx.x; r < rows; r += 256) acc = acc + row_rms[r];
+  for (int64_t r = threadIdx.x; r < rows; r += 256) acc = acc + x[r];
   part[threadIdx.x] = acc;
   __syncthreads();
   for (int w = 128; w >= 1; w >>= 1) {
     if (static_cast<int>(threadIdx.x) < w) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) mean[0] = part[0] / static_cast<float>(rows);
+  return part[0] / static_cast<float>(rows);
+}
+
+__global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms, int64_t rows,
+                                                            float* mean) {
+  __shared__ float part[256];
+  const float m = block_mean_256(row_rms, rows, part);
+  if (threadIdx.x == 0) mean[0] = m;
+}
+
+// One block per segment [offsets[s], offsets[s + 1]) of a buffer holding several layers'
+// row rms: the same order as row_rms_mean_kernel, so each mean equals that kernel's.
+__global__ __launch_bounds__(256) void row_rms_segment_means_kernel(const float* row_rms,
+                                                                     const int64_t* offsets,
+                                                                     float* means) {
+  __shared__ float part[256];
+  const int64_t b = offsets[blockIdx.x], e = offsets[blockIdx.x + 1];
+  const float m = block_mean_256(row_rms + b, e - b, part);
+  if (threadIdx.x == 0) means[blockIdx.x] = m;
 }
 // Element i of a 16-byte gradient vector held as four words (4 fp32, or 8 bf16 in pairs,
 // element 2j in the low half of word j).
@@ -270,4 +288,15 @@ extern "C" int rk_normalize_rows(const void* g, int g_dtype, int64_t ldg, int64_
   const int V = g_dtype == RK_F32 ? 4 : 8;
   a.vec_g = aligned16(g) && (ldg % V) == 0 && (K % V) == 0;
   return launch_grad_kernel<true>(a, g_dtype, as_stream(stream));
+}
+
+extern "C" int rk_row_rms_means(const float* row_rms, const int64_t* offsets, int64_t nseg,
+                                float* means, void* stream) {
+  clear_error();
+  if (nseg < 0 || nseg > 0x7fffffff) return fail(RK_ERR_ARG, "segment count out of range");
+  if (nseg == 0) return RK_OK;
+  if (!row_rms || !offsets || !means) return fail(RK_ERR_ARG, "null pointer");
+  row_rms_segment_means_kernel<<<static_cast<unsigned>(nseg), 256, 0, as_stream(stream)>>>(
+      row_rms, offsets, means);
+  return launch_status("row_rms_means");
 }

@@ -552,6 +552,18 @@ class RatchetGPT(nn.Module):
             m._counts_slot = buf[i]
             m._slot_dirty = False
         self._count_slots = buf
+        # the layers' row rms in one buffer too, segment s = layer s: one launch takes every
+        # layer's mean row rms for the step's statistics
+        sizes = [m.out_features for m in layers]
+        bounds = [0]
+        for n in sizes:
+            bounds.append(bounds[-1] + n)
+        rms = torch.zeros(bounds[-1], dtype=torch.float32, device=device)
+        self._rms_slots = rms
+        self._rms_offsets = torch.tensor(bounds, dtype=torch.int64, device=device)
+        for i, m in enumerate(layers):
+            m._rms_slot = rms[bounds[i]:bounds[i + 1]]
+            m._rms_slot_bounds = torch.tensor([0, sizes[i]], dtype=torch.int64, device=device)
 
     def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
         layers = [m for m in self.modules() if isinstance(m, DiscreteRatchetLinear)]
@@ -565,6 +577,18 @@ class RatchetGPT(nn.Module):
                 if m._slot_dirty:
                     buf[i].zero_()
                     m._slot_dirty = False
+        # every layer's first launch of the step left its row rms in the shared buffer: one
+        # launch for all their means (each equal to the per-layer launch's)
+        rms = getattr(self, "_rms_slots", None)
+        slot_means = None
+        if (rms is not None and rms.shape[0] == sum(m.out_features for m in layers)
+                and all(m._rms_slot is not None and len(m._pending_rms_means) == 1
+                        and m._pending_rms_means[0] is None for m in layers)):
+            from .ops import ratchet as _ratchet_ops
+
+            slot_means = _ratchet_ops().row_rms_means(rms, self._rms_offsets)
+            for i, m in enumerate(layers):
+                m._rms_slot_mean = slot_means[i]
         updates = [m.ratchet_update(validate=validate) for m in layers]
         if shared:
             # the layers' counts live in one buffer: one reduction for the four totals,
@@ -585,7 +609,11 @@ class RatchetGPT(nn.Module):
             negative_moves=moves[1],
             blocked_positive_moves=moves[2],
             blocked_negative_moves=moves[3],
-            gradient_rms_mean=(_total(u.gradient_rms_mean for u in updates) / len(updates)
+            # unvalidated, the layers' means are views of one vector: its sum is the sum of
+            # their stack (validated, they are host floats, added as floats)
+            gradient_rms_mean=(slot_means.sum() / len(updates)
+                               if slot_means is not None and not validate
+                               else _total(u.gradient_rms_mean for u in updates) / len(updates)
                                if updates else 0.0),
         )
         return aggregated.materialize() if validate else aggregated

@@ -171,6 +171,10 @@ def _register_fakes() -> None:
     def _embedding_backward(grad, ids, num_weights):
         return grad.new_empty((num_weights, grad.shape[-1]), dtype=torch.float32)
 
+    @fake("ratchet::row_rms_means")
+    def _row_rms_means(row_rms, offsets):
+        return row_rms.new_empty((offsets.shape[0] - 1,))
+
     @fake("ratchet::cross_entropy_forward")
     def _cross_entropy_forward(logits, targets, ignore_index=-100):
         f32 = torch.float32
@@ -192,5 +196,5 @@ OPERATORS = (
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
     "grad_weight_partials_parts", "grad_input_sr", "cross_entropy_forward",
-    "cross_entropy_backward",
+    "cross_entropy_backward", "row_rms_means",
 )

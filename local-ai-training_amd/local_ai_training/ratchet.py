@@ -673,15 +673,24 @@ class DiscreteRatchetLinear(nn.Module):
         # holds counts a layer-level ratchet_update consumed
         self._counts_slot: Tensor | None = None
         self._slot_dirty = False
+        # likewise an [out_features] view of one row-rms buffer for all its layers, with
+        # this layer's [2] int64 segment bounds [0, out_features): the first fused update of
+        # a step writes its row rms there and leaves the mean to one launch for the whole
+        # model (``row_rms_means``) instead of one per layer
+        self._rms_slot: Tensor | None = None
+        self._rms_slot_bounds: Tensor | None = None
         self._reset_pending_stats()
 
     # -- state ----------------------------------------------------------------
     def _reset_pending_stats(self) -> None:
         self._pending_stats_total_weights = 0
         self._pending_counts: Tensor | None = None
-        # per launch: mean row rms over all out_features rows (a device scalar)
-        self._pending_rms_means: list[Tensor] = []
+        # per launch: mean row rms over all out_features rows (a device scalar), or None for
+        # the launch whose row rms sits in the row-rms slot (its mean taken later)
+        self._pending_rms_means: list[Tensor | None] = []
         self._nonfinite: Tensor | None = None
+        # the slot's mean, when the model computed every layer's in one launch
+        self._rms_slot_mean: Tensor | None = None
 
     @classmethod
     def from_reference(cls, reference: Tensor, *, max_code: int, pressure_threshold: int = 8,
@@ -794,7 +803,7 @@ class DiscreteRatchetLinear(nn.Module):
 
     def _launch_update(self, gradient: Tensor, counts: Tensor, row_rms: Tensor | None,
                        grad_scale: Tensor | None, nonfinite: Tensor | None, *,
-                       from_partials: bool = False) -> None:
+                       from_partials: bool = False, defer_mean: bool = False) -> None:
         """One update launch from a weight gradient [N, K], or (``from_partials``) from the
         grad_weight GEMM's float32 split partials [nsplit, N, K], reduced inside the update
         with the same arithmetic. With ``keep_weight_gradient`` set, the bf16 gradient the
@@ -802,9 +811,10 @@ class DiscreteRatchetLinear(nn.Module):
         _require_gpu(gradient, self.packed, what="the ratchet update")
         ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
         beta = self.rms_ema_beta
-        # the launch also writes the mean of row_rms (the stats' gradient_rms_mean)
+        # the launch also writes the mean of row_rms (the stats' gradient_rms_mean), unless
+        # that mean is taken later from the row-rms slot
         rms_mean = (torch.empty((), device=self.packed.device, dtype=torch.float32)
-                    if row_rms is not None else None)
+                    if row_rms is not None and not defer_mean else None)
         rule = (self.max_code, self.pressure_threshold, self.bucket_low, self.bucket_high,
                 self.eps, ema, beta, counts, row_rms, grad_scale, nonfinite, rms_mean)
         if from_partials:
@@ -828,14 +838,32 @@ class DiscreteRatchetLinear(nn.Module):
         ``grad_weight`` is the gradient, or its split partials with ``from_partials``."""
         if grad_weight.shape[-2:] != (self.out_features, self.in_features):
             raise ValueError("fused gradient shape mismatch")
-        row_rms = torch.empty(self.out_features, device=grad_weight.device, dtype=torch.float32)
+        slot = self._rms_slot
+        defer = (slot is not None and slot.device == grad_weight.device
+                 and None not in self._pending_rms_means)
+        row_rms = slot if defer else torch.empty(self.out_features, device=grad_weight.device,
+                                                 dtype=torch.float32)
         grad_scale = (torch.empty(self.out_features, device=grad_weight.device,
                                   dtype=torch.float32) if want_grad_scale else None)
         self._launch_update(grad_weight, self._counts(), row_rms, grad_scale,
-                            self._nonfinite_flag(), from_partials=from_partials)
+                            self._nonfinite_flag(), from_partials=from_partials,
+                            defer_mean=defer)
         self._pending_stats_total_weights += self.out_features * self.in_features
-        self._pending_rms_means.append(self._last_rms_mean)
+        self._pending_rms_means.append(None if defer else self._last_rms_mean)
         return grad_scale
+
+    def _pending_rms_mean(self) -> Tensor | float:
+        means = [self._slot_rms_mean() if m is None else m for m in self._pending_rms_means]
+        if not means:
+            return 0.0
+        return means[0] if len(means) == 1 else torch.stack(means).sum()
+
+    def _slot_rms_mean(self) -> Tensor:
+        """Mean of the row rms in this layer's slot: the one the model computed for all its
+        layers, else one launch for this layer (the same summation order either way)."""
+        if self._rms_slot_mean is not None:
+            return self._rms_slot_mean
+        return _ops().row_rms_means(self._rms_slot, self._rms_slot_bounds)[0]
 
     @torch.no_grad()
     def _normalize(self, gradient: Tensor, row_start: int, row_end: int) -> Tensor:
@@ -927,10 +955,7 @@ class DiscreteRatchetLinear(nn.Module):
                 blocked_negative_moves=bneg,
                 # sum over launches of sum(row_rms) / out_features; each launch covers all
                 # out_features rows, so that is the sum of the launches' mean row rms
-                gradient_rms_mean=(self._pending_rms_means[0]
-                                   if len(self._pending_rms_means) == 1
-                                   else torch.stack(self._pending_rms_means).sum()
-                                   if self._pending_rms_means else 0.0),
+                gradient_rms_mean=self._pending_rms_mean(),
             )
             nonfinite = self._nonfinite
             if counts is not None and counts is self._counts_slot:

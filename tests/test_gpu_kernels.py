@@ -8,6 +8,7 @@ tests' ragged cases, the BASELINE op shape (M=16384, K=512, N=2048) and 1B-class
 
 from __future__ import annotations
 
+import math
 import numpy as np
 import pytest
 import torch
@@ -576,6 +577,21 @@ def test_update_writes_the_mean_row_rms(cuda, rows, k):
         nat.call("rk_ratchet_update_grad", pd.data_ptr(), k, g.data_ptr(), nat.RK_F32, k, rows,
                  k, 2, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(), None, None, None,
                  mean.data_ptr(), nat.stream_handle(cuda))
+    # the same row rms as one segment among others of a shared buffer: rk_row_rms_means
+    # gives the update's rms_mean bit for bit, every segment its own float64 mean, an
+    # empty segment NaN
+    other = torch.rand(3000, generator=gen(7)).to(cuda)
+    buf = torch.cat([other[:1000], row_rms, torch.empty(0, device=cuda), other[1000:]])
+    bounds = [0, 1000, 1000 + rows, 1000 + rows, buf.numel()]
+    offsets = torch.tensor(bounds, dtype=torch.int64, device=cuda)
+    seg = torch.empty(4, device=cuda)
+    nat.call("rk_row_rms_means", buf.data_ptr(), offsets.data_ptr(), 4, seg.data_ptr(),
+             nat.stream_handle(cuda))
+    assert seg[1].view(torch.int32).item() == means[0]
+    for i in (0, 3):
+        want = buf[bounds[i]:bounds[i + 1]].double().mean().item()
+        assert abs(seg[i].item() - want) <= 1e-6 * abs(want)
+    assert math.isnan(seg[2].item())
 
 
 # 4100 and 9000 rows take the pipelined row loop (several rows per wavefront, the next

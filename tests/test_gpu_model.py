@@ -321,7 +321,10 @@ def test_shared_move_count_buffer_gives_the_per_layer_totals(cuda):
     # The model's one [layers, 4] move-count buffer (summed and cleared once per step) gives
     # the same step statistics as per-layer count tensors, step after step, and a
     # layer-level ratchet_update in between (which leaves its slot to be cleared before its
-    # next use) does not leak counts into the next step.
+    # next use) does not leak counts into the next step. The same for the row-rms buffer
+    # whose per-layer means one launch takes: gradient_rms_mean equal bit for bit, also
+    # for a layer-level ratchet_update (its own mean launch) and for a step with two
+    # backward passes (the second launch of each layer keeps its own row rms).
     from local_ai_training.model import RatchetGPT
 
     def run(shared: bool):
@@ -334,10 +337,11 @@ def test_shared_move_count_buffer_gives_the_per_layer_totals(cuda):
             gen = torch.Generator().manual_seed(3)
             batch = torch.randint(0, 64, (8, 65), generator=gen).to(cuda)
             out = []
-            for step in range(4):
-                with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
-                    _, loss = model(batch[:, :64], batch[:, 1:])
-                loss.backward()
+            for step in range(5):
+                for _ in range(2 if step == 3 else 1):
+                    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                        _, loss = model(batch[:, :64], batch[:, 1:])
+                    loss.backward()
                 if step == 2:
                     first = next(m for m in model.modules()
                                  if isinstance(m, DiscreteRatchetLinear))

@@ -121,6 +121,8 @@ def cases(t, cuda):
                            3, torch.float32, True,
                            torch.empty(M, K, dtype=torch.int8, device=cuda),
                            torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
+        (R.row_rms_means, (t["x"][0].abs().contiguous(),
+                           torch.tensor([0, 5, 100, K], dtype=torch.int64, device=cuda)), {}),
         (R.cross_entropy_forward, (t["xb"], tgt), {}),
         (R.cross_entropy_forward, (t["x"], tgt_ignored, -1), {}),
         (R.cross_entropy_backward, (torch.ones((), device=cuda), t["xb"], tgt, *xent_b[1:]), {}),
@@ -129,7 +131,7 @@ def cases(t, cuda):
     ]
 
 
-N_CASES = 47
+N_CASES = 48
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):

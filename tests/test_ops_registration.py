@@ -110,6 +110,7 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
     qp, sp = R.quantize_rows_parts(parts, meta(3 * n), True, 7)
     assert (qp.shape, qp.dtype, sp.shape, sp.dtype) == ((m, 3 * n), torch.int8, (m,),
                                                           torch.float32)
+    assert R.row_rms_means(meta(n), meta(5, dtype=torch.int64)).shape == (4,)
     tg = meta(m, dtype=torch.int64)
     loss, stats, count = R.cross_entropy_forward(x, tg)
     assert (loss.shape, stats.shape, count.shape) == ((), (3, m), ())
