@@ -654,9 +654,11 @@ def train_bench(shape: dict, steps: int, warmup: int, device, graph: bool):
                          ffn_hidden=shape["ffn"], matmul_mode="int8", int8_backward=True)
     model = build_seeded_model(config, max_code=shape["max_code"], seed=1337).to(device).train()
     # capturable (device-side step count) in both modes: the same AdamW arithmetic, so the
-    # eager and graph runs of the same steps end at the same loss
+    # eager and graph runs of the same steps end at the same loss; torch's fused AdamW (one
+    # kernel for every parameter; the same update as the reference's foreach AdamW up to
+    # float rounding)
     optimizer = torch.optim.AdamW(model.parameters(), lr=3e-4, weight_decay=0.0,
-                                  capturable=True)
+                                  capturable=True, fused=True)
     rng = np.random.default_rng(1337)
     ids = (rng.zipf(1.1, size=batch * (block + 1)) - 1) % vocab  # Zipf(s=1.1) token ids
     tokens = torch.from_numpy(ids.astype(np.uint16).astype(np.int64)).view(batch, block + 1)

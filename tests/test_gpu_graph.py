@@ -111,10 +111,12 @@ def test_replays_with_different_seeds_round_differently(cuda):
     assert not torch.equal(a, b)
 
 
-def test_captured_training_step_equals_eager_steps(cuda):
+@pytest.mark.parametrize("fused_adamw", [False, True])
+def test_captured_training_step_equals_eager_steps(cuda, fused_adamw):
     # The model's whole training step (autocast forward, backward with the fused updates,
-    # ratchet_update, capturable AdamW) replayed as a graph: losses, every ratchet state and
-    # every float parameter equal an eager run of the same steps with the same host RNG.
+    # ratchet_update, capturable AdamW: torch's foreach form, or its fused kernel as the
+    # benchmark uses) replayed as a graph: losses, every ratchet state and every float
+    # parameter equal an eager run of the same steps with the same host RNG.
     from local_ai_training.model import ModelConfig, build_seeded_model
     from local_ai_training.training import CapturedTrainingStep, training_step
 
@@ -126,7 +128,7 @@ def test_captured_training_step_equals_eager_steps(cuda):
     for graphed in (False, True):
         model = build_seeded_model(config, max_code=2, seed=21).to(cuda).train()
         optimizer = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.0,
-                                      capturable=True)
+                                      capturable=True, fused=fused_adamw)
         torch.manual_seed(8)
         losses = []
         if graphed:
