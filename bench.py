@@ -575,13 +575,13 @@ STEP_CLASSES = [
     ("SR gradient quant (Philox)", r"quant_rows_kernel<\d+, \d+, true"),
     ("activation quant prologues (RMSNorm/GELU/transpose)", r"quant_rows_kernel<\d+, \d+, false"),
     ("bf16 grad_weight (MFMA)", r"grad_weight_(partial|reduce)_kernel"),
-    ("fused ratchet update", r"ratchet_update|row_rms_mean"),
+    ("fused ratchet update", r"ratchet_update|row_rms_(segment_)?mean"),
     ("prologue backward (RMSNorm/GELU)", r"rmsnorm_bwd|rmsnorm_gw_reduce|gelu_bwd"),
     ("attention (SDPA)", r"attn|fmha|flash"),
     ("bf16 GEMM (hipBLASLt, lm_head grad_input)", r"Cijk_|gemm"),
     ("effective bf16 weights", r"effective_bf16"),
     ("optimizer (AdamW)", r"multi_tensor|adam"),
-    ("loss / reductions", r"reduce|softmax|nll|cross_entropy"),
+    ("loss (cross-entropy) / reductions", r"xent|reduce|softmax|nll|cross_entropy"),
     ("elementwise / cast / copy", r"elementwise|copy|cast|fill|vectorized|index|embedding"),
 ]
 
