@@ -622,6 +622,24 @@ int rk_cross_entropy_backward(const void* logits, int dtype, int64_t ldl, const 
                               const float* count, const float* grad_loss, void* grad,
                               int grad_dtype, int64_t ldg, void* stream);
 
+/*
+ * Causal self-attention forward (flash form): for bf16 q, k, v [B, H, S, D] with element
+ * strides (batch, head, position; the feature stride is 1), D = 64 or 128,
+ *   o[b, h, i, :] = sum_{j <= i} softmax_j(s_ij) v[b, h, j, :],  s_ij = (q_i . k_j) * scale,
+ *   lse[b, h, i] = log(sum_{j <= i} exp(s_ij))  (float32 [B, H, S], contiguous),
+ * o bf16 with its own strides (8-byte aligned rows). The scores and the softmax run in float32;
+ * the probabilities enter the value product rounded to bf16. q, k, v 16-byte aligned, strides
+ * multiples of 8 elements, one head's positions under 2^30 bytes; otherwise
+ * RK_ERR_UNSUPPORTED. (o, lse) is the pair torch's memory-efficient attention backward takes.
+ * Replaces: the forward of F.scaled_dot_product_attention(q, k, v, is_causal=True),
+ *           model.py:117-123.
+ */
+int rk_attention_forward(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqs,
+                         const uint16_t* k, int64_t skb, int64_t skh, int64_t sks,
+                         const uint16_t* v, int64_t svb, int64_t svh, int64_t svs, int64_t B,
+                         int64_t H, int64_t S, int64_t D, float scale, uint16_t* o, int64_t sob,
+                         int64_t soh, int64_t sos, float* lse, void* stream);
+
 /* HBM streaming probe (measurement only; no counterpart in the reference): reads `bytes`
  * (a multiple of 16) from src in 16-byte vectors, `unroll` (1, 2, 4, 8) loads in flight
  * per thread, `blocks` blocks of 256 threads in a grid-stride loop; copy != 0 writes them

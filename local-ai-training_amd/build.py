@@ -51,9 +51,18 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libratchet_hip.so)")
 
 
+# Per-source flags. rk_attention.hip: MFMA results in VGPRs (the attention's softmax and
+# output rescale read every accumulator with VALU instructions; in AGPRs each read and write
+# back is an extra copy, about as many instructions as the softmax itself).
+SOURCE_FLAGS = {
+    "rk_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o",
+           str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"compile failed: {src.name}\n{proc.stdout}\n{proc.stderr}")

@@ -915,6 +915,37 @@ Tensor embedding_backward(const Tensor& grad_in, const Tensor& ids_in, int64_t n
   return out;
 }
 
+// Causal attention forward (rk_attention_forward) on bf16 q, k, v [B, H, S, D]: returns
+// (o, lse), o as a [B, H, S, D] view of [B, S, H, D] memory (rows of the heads' outputs side
+// by side, the layout torch's memory-efficient forward writes), lse float32 [B, H, S].
+std::tuple<Tensor, Tensor> attention_forward(const Tensor& q, const Tensor& k, const Tensor& v,
+                                             double scale) {
+  require_gpu(q, "attention");
+  same_device(q, k, "attention");
+  same_device(q, v, "attention");
+  TORCH_CHECK(q.dim() == 4 && k.sizes() == q.sizes() && v.sizes() == q.sizes(),
+              "attention: q, k, v must share a [B, H, S, D] shape");
+  TORCH_CHECK(q.scalar_type() == at::kBFloat16 && k.scalar_type() == at::kBFloat16 &&
+                  v.scalar_type() == at::kBFloat16,
+              "attention: q, k, v must be bfloat16");
+  const auto unit = [](const Tensor& t) { return t.stride(3) == 1 ? t : t.contiguous(); };
+  const Tensor qq = unit(q), kk = unit(k), vv = unit(v);
+  const int64_t B = q.size(0), H = q.size(1), S = q.size(2), D = q.size(3);
+  const c10::DeviceGuard guard(q.device());
+  Tensor o = at::empty({B, S, H, D}, q.options()).permute({0, 2, 1, 3});
+  Tensor lse = at::empty({B, H, S}, q.options().dtype(at::kFloat));
+  const auto p16 = [](const Tensor& t) { return static_cast<const uint16_t*>(t.data_ptr()); };
+  check_status(rk_attention_forward(p16(qq), qq.stride(0), qq.stride(1), qq.stride(2), p16(kk),
+                                    kk.stride(0), kk.stride(1), kk.stride(2), p16(vv),
+                                    vv.stride(0), vv.stride(1), vv.stride(2), B, H, S, D,
+                                    static_cast<float>(scale),
+                                    static_cast<uint16_t*>(o.data_ptr()), o.stride(0),
+                                    o.stride(1), o.stride(2), lse.data_ptr<float>(),
+                                    stream_of(q)),
+               "rk_attention_forward");
+  return {o, lse};
+}
+
 // Means of segments [offsets[s], offsets[s + 1]) of a float32 row-rms buffer (rk_row_rms_means).
 Tensor row_rms_means(const Tensor& row_rms, const Tensor& offsets) {
   require_gpu(row_rms, "row rms means");
@@ -1061,6 +1092,7 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("gelu_backward(Tensor grad_y, Tensor x) -> Tensor");
   m.def("embedding_backward(Tensor grad, Tensor ids, int num_weights) -> Tensor");
   m.def("row_rms_means(Tensor row_rms, Tensor offsets) -> Tensor");
+  m.def("attention_forward(Tensor q, Tensor k, Tensor v, float scale) -> (Tensor, Tensor)");
   m.def("cross_entropy_forward(Tensor logits, Tensor targets, int ignore_index=-100) -> "
         "(Tensor, Tensor, Tensor)");
   m.def("cross_entropy_backward(Tensor grad_loss, Tensor logits, Tensor targets, Tensor stats, "
@@ -1100,6 +1132,7 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("gelu_backward", &gelu_backward);
   m.impl("embedding_backward", &embedding_backward);
   m.impl("row_rms_means", &row_rms_means);
+  m.impl("attention_forward", &attention_forward);
   m.impl("cross_entropy_forward", &cross_entropy_forward);
   m.impl("cross_entropy_backward", &cross_entropy_backward);
 }

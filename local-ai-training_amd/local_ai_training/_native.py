@@ -105,6 +105,8 @@ SIGNATURES: dict[str, list] = {
     "rk_cross_entropy_backward": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i32,
                                   _i64, _p],
     "rk_row_rms_means": [_p, _p, _i64, _p, _p],
+    "rk_attention_forward": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
+                             _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _i64, _p, _p],
     "rk_version": [],
     "rk_last_error": [],
 }

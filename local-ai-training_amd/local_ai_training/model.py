@@ -21,6 +21,7 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
+from .attention import CausalAttentionFn, attention_supported
 from .cross_entropy import cross_entropy
 from .int8_fused import (
     FusedGELUQuantizeFn,
@@ -156,6 +157,9 @@ class KVCache:
         self.pos.add_(steps)
 
 
+# causal training attention: the HIP forward (rk_attention_forward) where it applies, with
+# torch's memory-efficient backward (False: torch's forward too)
+hip_attention_forward = True
 _FAST_ATTENTION = [SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]
 _DETERMINISTIC_ATTENTION = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
 
@@ -170,8 +174,13 @@ def _attend(q: Tensor, k: Tensor, v: Tensor, **kwargs) -> Tensor:
     the output repeat bit for bit, dq does not; the flash kernel repeats at both shapes), so
     under torch.use_deterministic_algorithms(True) the flash kernel comes first."""
     if q.is_cuda and q.dtype in (torch.bfloat16, torch.float16):
-        order = (_DETERMINISTIC_ATTENTION if torch.are_deterministic_algorithms_enabled()
-                 else _FAST_ATTENTION)
+        deterministic = torch.are_deterministic_algorithms_enabled()
+        if (hip_attention_forward and not deterministic and kwargs.get("is_causal")
+                and not kwargs.get("dropout_p") and kwargs.keys() <= {"is_causal", "dropout_p"}
+                and attention_supported(q, k, v)):
+            # the HIP forward with torch's memory-efficient backward (attention.py)
+            return CausalAttentionFn.apply(q, k, v)
+        order = _DETERMINISTIC_ATTENTION if deterministic else _FAST_ATTENTION
         with sdpa_kernel(order, set_priority=True):
             return F.scaled_dot_product_attention(q, k, v, **kwargs)
     return F.scaled_dot_product_attention(q, k, v, **kwargs)

@@ -171,6 +171,12 @@ def _register_fakes() -> None:
     def _embedding_backward(grad, ids, num_weights):
         return grad.new_empty((num_weights, grad.shape[-1]), dtype=torch.float32)
 
+    @fake("ratchet::attention_forward")
+    def _attention_forward(q, k, v, scale):
+        b, h, sl, d = q.shape
+        o = q.new_empty((b, sl, h, d)).permute(0, 2, 1, 3)
+        return o, q.new_empty((b, h, sl), dtype=torch.float32)
+
     @fake("ratchet::row_rms_means")
     def _row_rms_means(row_rms, offsets):
         return row_rms.new_empty((offsets.shape[0] - 1,))
@@ -196,5 +202,5 @@ OPERATORS = (
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
     "grad_weight_partials_parts", "grad_input_sr", "cross_entropy_forward",
-    "cross_entropy_backward", "row_rms_means",
+    "cross_entropy_backward", "row_rms_means", "attention_forward",
 )

@@ -60,6 +60,8 @@ def cases(t, cuda):
     whole = (torch.randn(M, 3 * N, generator=gen(11)) * 1e-2).to(torch.bfloat16).to(cuda)
     tgt = torch.randint(0, K, (M,), generator=gen(12)).to(cuda)
     tgt_ignored = torch.where(torch.arange(M, device=cuda) % 7 == 0, -1, tgt)
+    att_qkv = tuple(torch.randn(2, 2, 48, 64, generator=gen(13 + i)).to(torch.bfloat16).to(cuda)
+                    for i in range(3))
     xent_b = R.cross_entropy_forward(t["xb"], tgt)
     xent_f = R.cross_entropy_forward(t["x"], tgt_ignored, -1)
     parts = list(whole.chunk(3, dim=-1))
@@ -123,6 +125,7 @@ def cases(t, cuda):
                            torch.empty(M, K, dtype=torch.bfloat16, device=cuda)), {}),
         (R.row_rms_means, (t["x"][0].abs().contiguous(),
                            torch.tensor([0, 5, 100, K], dtype=torch.int64, device=cuda)), {}),
+        (R.attention_forward, (*att_qkv, 0.125), {}),
         (R.cross_entropy_forward, (t["xb"], tgt), {}),
         (R.cross_entropy_forward, (t["x"], tgt_ignored, -1), {}),
         (R.cross_entropy_backward, (torch.ones((), device=cuda), t["xb"], tgt, *xent_b[1:]), {}),
@@ -131,7 +134,7 @@ def cases(t, cuda):
     ]
 
 
-N_CASES = 48
+N_CASES = 49
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):

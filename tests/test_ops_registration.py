@@ -111,6 +111,10 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
     assert (qp.shape, qp.dtype, sp.shape, sp.dtype) == ((m, 3 * n), torch.int8, (m,),
                                                           torch.float32)
     assert R.row_rms_means(meta(n), meta(5, dtype=torch.int64)).shape == (4,)
+    ao, alse = R.attention_forward(*(meta(2, 3, 40, 64, dtype=torch.bfloat16) for _ in range(3)),
+                                   0.125)
+    assert ao.shape == (2, 3, 40, 64) and ao.stride() == (7680, 64, 192, 1)
+    assert alse.shape == (2, 3, 40) and alse.dtype == torch.float32
     tg = meta(m, dtype=torch.int64)
     loss, stats, count = R.cross_entropy_forward(x, tg)
     assert (loss.shape, stats.shape, count.shape) == ((), (3, m), ())
