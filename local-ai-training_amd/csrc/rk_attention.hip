@@ -18,8 +18,8 @@
 // (h = lane / 32, the accumulator's own row order), and the first operand reads V^T with
 // the same slot order. The probabilities enter the product rounded to bf16; their sum
 // stays float32. Causal blocks above a wavefront's diagonal are skipped; the diagonal
-// block is masked per element. Every global access goes through a buffer descriptor
-// bounded by the (batch, head) extent, so positions past S read zeros.
+// block is masked per element. Every global load goes through a buffer descriptor bounded
+// by the (batch, head) extent, so positions past S read zeros without a test.
 #include "rk_common.h"
 
 namespace rk {
@@ -69,32 +69,35 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t sk2[2][BN * KP];
   __shared__ __attribute__((aligned(16))) uint8_t sv2[2][D * VP];
 
-  const int64_t S = a.S;
-  const int nqb = static_cast<int>((S + BM - 1) / BM);
+  // positions fit 32 bits (checked by the host, with the row offsets of S + BN rows)
+  const int S = static_cast<int>(a.S);
+  const int sqs = static_cast<int>(a.sqs), sks = static_cast<int>(a.sks),
+            svs = static_cast<int>(a.svs);
+  const int nqb = (S + BM - 1) / BM;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // longest causal rows first
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh - b * a.H;
   const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int64_t q0 = static_cast<int64_t>(qb) * BM;
-  const int64_t qw0 = q0 + 32 * wave;  // this wavefront's first query
-  const int64_t qi = qw0 + l32;        // this lane's query
+  const int q0 = qb * BM;
+  const int qw0 = q0 + 32 * wave;  // this wavefront's first query
+  const int qi = qw0 + l32;        // this lane's query
 
+  // descriptors end at the head's last position: rows past S read zeros (their offsets,
+  // up to S + BN rows, stay below 2^31)
   const __amdgpu_buffer_rsrc_t qbuf =
-      make_buffer(a.q + b * a.sqb + h * a.sqh, ((S - 1) * a.sqs + D) * 2);
+      make_buffer(a.q + b * a.sqb + h * a.sqh, (static_cast<int64_t>(S - 1) * sqs + D) * 2);
   const __amdgpu_buffer_rsrc_t kbuf =
-      make_buffer(a.k + b * a.skb + h * a.skh, ((S - 1) * a.sks + D) * 2);
+      make_buffer(a.k + b * a.skb + h * a.skh, (static_cast<int64_t>(S - 1) * sks + D) * 2);
   const __amdgpu_buffer_rsrc_t vbuf =
-      make_buffer(a.v + b * a.svb + h * a.svh, ((S - 1) * a.svs + D) * 2);
+      make_buffer(a.v + b * a.svb + h * a.svh, (static_cast<int64_t>(S - 1) * svs + D) * 2);
 
   // Q of this lane's query, features 16 s + 8 hh .. + 7: the second MFMA operand
   v8bf_a qf[D / 16];
 #pragma unroll
-  for (int s = 0; s < D / 16; ++s) {
-    const int off = static_cast<int>((qi * a.sqs + 16 * s + 8 * hh) * 2);
-    qf[s] = as_v8bf(__builtin_bit_cast(
-        uint4, __builtin_amdgcn_raw_buffer_load_b128(qbuf, qi < S ? off : 0x7ffffff0, 0, 0)));
-  }
+  for (int s = 0; s < D / 16; ++s)
+    qf[s] = as_v8bf(__builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  qbuf, (qi * sqs + 16 * s + 8 * hh) * 2, 0, 0)));
 
   // staging. K: piece c = tid + 256 i is row c / (D / 8), features 8 (c % (D / 8)) .. + 7.
   // V: thread tid takes keys 4 (tid / DG) .. + 3, features 4 (tid % DG) .. + 3 (8-byte loads),
@@ -106,18 +109,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < PIECES; ++i) {
       const int c = tid + 256 * i, row = c / (D / 8), col = 8 * (c % (D / 8));
-      const int64_t key = static_cast<int64_t>(kb) * BN + row;
       kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                            kbuf, key < S ? static_cast<int>((key * a.sks + col) * 2)
-                                                          : 0x7ffffff0, 0, 0));
+                                            kbuf, ((kb * BN + row) * sks + col) * 2, 0, 0));
     }
 #pragma unroll
-    for (int i = 0; i < VKEYS; ++i) {
-      const int64_t key = static_cast<int64_t>(kb) * BN + vk0 + i;
+    for (int i = 0; i < VKEYS; ++i)
       vr[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                            vbuf, key < S ? static_cast<int>((key * a.svs + vd0) * 2)
-                                                          : 0x7ffffff0, 0, 0));
-    }
+                                            vbuf, ((kb * BN + vk0 + i) * svs + vd0) * 2, 0, 0));
   };
   auto lstore = [&](int buf) {
     uint8_t* sk = sk2[buf];
@@ -143,8 +141,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) o[dt] = v16f_a{};
 
-  const int64_t last_key = (q0 + BM - 1 < S - 1) ? q0 + BM - 1 : S - 1;
-  const int nkb = static_cast<int>(last_key / BN) + 1;
+  const int last_key = (q0 + BM - 1 < S - 1) ? q0 + BM - 1 : S - 1;
+  const int nkb = last_key / BN + 1;
   gload(0);
   lstore(0);
   if (nkb > 1) gload(1);
@@ -152,7 +150,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   for (int kb = 0; kb < nkb; ++kb) {
     const uint8_t* sk = sk2[kb & 1];
     const uint8_t* sv = sv2[kb & 1];
-    const int64_t k0 = static_cast<int64_t>(kb) * BN;
+    const int k0 = kb * BN;
     if (k0 <= qw0 + 31) {  // else the block lies above this wavefront's diagonal
 
       // S^T for two 32-key tiles: lane holds keys k0 + 32 kt + 8 (e / 4) + 4 hh + e % 4
@@ -174,7 +172,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int64_t key = k0 + 32 * kt + 8 * (e / 4) + 4 * hh + (e % 4);
+            const int key = k0 + 32 * kt + 8 * (e / 4) + 4 * hh + (e % 4);
             if (key > qi) st[kt][e] = -INFINITY;
           }
       }
@@ -241,7 +239,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   // o[dt][e] = O[qi][32 dt + 8 (e / 4) + 4 hh + e % 4] * l
   if (qi < S) {
     const float inv = 1.0f / l;
-    uint16_t* orow = a.o + b * a.sob + h * a.soh + qi * a.sos;
+    uint16_t* orow = a.o + b * a.sob + h * a.soh + static_cast<int64_t>(qi) * a.sos;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
@@ -277,10 +275,12 @@ extern "C" int rk_attention_forward(const uint16_t* q, int64_t sqb, int64_t sqh,
   for (int64_t st : strides)
     if (st < 0 || st % 8 != 0)
       return fail(RK_ERR_UNSUPPORTED, "strides must be non-negative multiples of 8 elements");
-  // buffer offsets are 32-bit: one (batch, head)'s positions must span under 2^30 bytes
-  if ((S * sqs + D) * 2 >= (int64_t{1} << 30) || (S * sks + D) * 2 >= (int64_t{1} << 30) ||
-      (S * svs + D) * 2 >= (int64_t{1} << 30))
-    return fail(RK_ERR_UNSUPPORTED, "sequence extent exceeds 2^30 bytes per head");
+  // buffer offsets are 32-bit: the rows of one (batch, head) up to S + 128 (the last key
+  // block's padding) must lie below 2^31 bytes
+  const int64_t rows = S + 128;
+  if ((rows * sqs + D) * 2 >= (int64_t{1} << 31) || (rows * sks + D) * 2 >= (int64_t{1} << 31) ||
+      (rows * svs + D) * 2 >= (int64_t{1} << 31))
+    return fail(RK_ERR_UNSUPPORTED, "sequence extent exceeds 2^31 bytes per head");
   if (B * H > 0x7fffffff || (S + kAttnBM - 1) / kAttnBM > 0x7fffffff)
     return fail(RK_ERR_ARG, "grid too large");
   AttnArgs a{q, k, v, sqb, sqh, sqs, skb, skh, sks, svb, svh, svs, o, sob, soh, sos, lse,
