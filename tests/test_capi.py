@@ -65,3 +65,23 @@ def test_zero_sized_calls_are_no_ops(lib):
     assert lib.rk_int8_gemm_nt(None, 1, None, 1, None, None, None, 1, 1, 0, 5, 5, None) == 0
     assert lib.rk_unpack(None, 0, 2, None, None, None) == 0
     assert lib.rk_pressure_leak(None, 0, 2, None) == 0
+
+
+def test_attention_forward_rejects_before_device_work(lib):
+    """Head sizes other than 64 / 128 and unaligned strides return a status, no launch."""
+    i64 = ctypes.c_int64
+    args = [None, i64(0), i64(0), i64(64)] * 3
+    status = lib.rk_attention_forward(*args, i64(1), i64(1), i64(16), i64(32),
+                                      ctypes.c_float(0.125), None, i64(0), i64(0), i64(32),
+                                      None, None)
+    assert status == 3 and b"head size" in lib.rk_last_error()
+    bad = [None, i64(0), i64(0), i64(68)] * 3
+    fake = ctypes.c_void_p(1 << 12)  # never dereferenced: the stride check comes first
+    bad[0] = bad[4] = bad[8] = fake
+    status = lib.rk_attention_forward(*bad, i64(1), i64(1), i64(16), i64(64),
+                                      ctypes.c_float(0.125), fake, i64(0), i64(0), i64(64),
+                                      fake, None)
+    assert status == 3 and b"multiples of 8" in lib.rk_last_error()
+    assert lib.rk_attention_forward(*args, i64(1), i64(1), i64(0), i64(64),
+                                    ctypes.c_float(0.125), None, i64(0), i64(0), i64(64),
+                                    None, None) == 0
