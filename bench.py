@@ -577,7 +577,7 @@ STEP_CLASSES = [
     ("bf16 grad_weight (MFMA)", r"grad_weight_(partial|reduce)_kernel"),
     ("fused ratchet update", r"ratchet_update|row_rms_(segment_)?mean"),
     ("prologue backward (RMSNorm/GELU)", r"rmsnorm_bwd|rmsnorm_gw_reduce|gelu_bwd"),
-    ("attention (SDPA)", r"attn|fmha|flash"),
+    ("attention (HIP forward, torch memory-efficient backward)", r"attn|fmha|flash|bwd_preprocess|bwd_postprocess"),
     ("bf16 GEMM (hipBLASLt, lm_head grad_input)", r"Cijk_|gemm"),
     ("effective bf16 weights", r"effective_bf16"),
     ("optimizer (AdamW)", r"multi_tensor|adam"),
