@@ -279,10 +279,13 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   static_assert(CFG::WM % CFG::EROUNDS == 0, "whole wave rows per epilogue round");
   constexpr int BSTAGE = BT ? BK * BTP : BN * BK;  // bytes of one B stage
   constexpr int TILES = 2 * BM * BK + 2 * BSTAGE;
-  constexpr int SMEM = EROWS * EPITCH > TILES ? EROWS * EPITCH : TILES;
+  constexpr int BODY = EROWS * EPITCH > TILES ? EROWS * EPITCH : TILES;
+  constexpr int SMEM = BODY + BN * 4;  // + the tile's column scales
+  static_assert(THREADS >= BN, "one column scale per thread");
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
   uint8_t* As = smem;
   uint8_t* Bs = smem + 2 * BM * BK;
+  float* const rs_lds = reinterpret_cast<float*>(smem + BODY);
 
   const int64_t tiles_n = (g.N + BN - 1) / BN;
   int64_t b = blockIdx.x;
@@ -367,12 +370,27 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   // issued right after step kt is written to LDS. Pairs of k-steps run without a branch;
   // an odd last step follows. Loads past the last k-step are never consumed (past the
   // last row's end they read zeros, elsewhere the next row: always in bounds).
+  // The epilogue's row and column scales are requested first, so their latency passes
+  // under the main loop's; the column scales go to LDS once the first k-steps are issued.
+  const int r32 = lane & 31, hh = lane >> 5;
+  const __amdgpu_buffer_rsrc_t ls_rsrc = make_buffer(g.ls + m0, rows_a * 4);
+  float lsv[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+    lsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                           ls_rsrc, (arow0 + 32 * i + r32) * 4, 0, 0));
+  float rsv = 1.0f;
+  if constexpr (HAS_RS) {
+    const __amdgpu_buffer_rsrc_t rs_rsrc = make_buffer(g.rs + n0, rows_b * 4);
+    rsv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_rsrc, tid * 4, 0, 0));
+  }
   const int nk = static_cast<int>(g.K / BK);
   if constexpr (S == 2) {
     load(ring[0], 0);
     __builtin_amdgcn_sched_barrier(0);
     load(ring[1], 1);
     __builtin_amdgcn_sched_barrier(0);
+    if (HAS_RS && tid < BN) rs_lds[tid] = rsv;
     const int nk_pairs = nk & ~1;
     for (int kb = 0; kb < nk_pairs; kb += S) {
 #pragma unroll
@@ -393,6 +411,7 @@ void int8_gemm_m32_kernel(GemmArgs g) {
     // one k-step in registers: the loads of step kt + 1 are issued right after step kt is
     // written to LDS (the same LDS ping-pong and one barrier per step)
     load(ring[0], 0);
+    if (HAS_RS && tid < BN) rs_lds[tid] = rsv;
     for (int kt = 0; kt < nk; ++kt) {
       const int buf = kt & 1;
       store(ring[0], buf);
@@ -408,14 +427,6 @@ void int8_gemm_m32_kernel(GemmArgs g) {
   // n = brow0 + 32 j + 8 q + 4 (lane >> 5) + (e % 4), q = e / 4. In round r the waves
   // whose rows lie in [r EROWS, (r + 1) EROWS) stage them as bf16, then the whole block
   // copies them out.
-  const int r32 = lane & 31, hh = lane >> 5;
-  const __amdgpu_buffer_rsrc_t ls_rsrc = make_buffer(g.ls + m0, rows_a * 4);
-  float lsv[MI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-    lsv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                           ls_rsrc, (arow0 + 32 * i + r32) * 4, 0, 0));
-  const __amdgpu_buffer_rsrc_t rs_rsrc = make_buffer(HAS_RS ? g.rs + n0 : g.ls, HAS_RS ? rows_b * 4 : 0);
   constexpr int ES = CDT == RK_BF16 ? 2 : 4;
   constexpr int CHUNKS = BN / 8;             // 8-column chunks per row
   constexpr int RSTEP = THREADS / CHUNKS;    // rows copied per pass
@@ -442,9 +453,7 @@ void int8_gemm_m32_kernel(GemmArgs g) {
           for (int q = 0; q < 4; ++q) {
             float4 rs4 = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
             if constexpr (HAS_RS)
-              rs4 = __builtin_bit_cast(
-                  float4, __builtin_amdgcn_raw_buffer_load_b128(
-                              rs_rsrc, (brow0 + 32 * j + 8 * q + 4 * hh) * 4, 0, 0));
+              rs4 = *reinterpret_cast<const float4*>(rs_lds + brow0 + 32 * j + 8 * q + 4 * hh);
             float v0 = static_cast<float>(acc[i][j][4 * q]) * lsv[i];
             float v1 = static_cast<float>(acc[i][j][4 * q + 1]) * lsv[i];
             float v2 = static_cast<float>(acc[i][j][4 * q + 2]) * lsv[i];
@@ -526,14 +535,15 @@ void int8_gemm_m32_kernel(GemmArgs g) {
 // store writes 16 bytes of 32-lane-contiguous 512-byte rows (stores straight from the MFMA
 // layout scatter 8 bytes over 32 rows per instruction and cost 18 of 45 us at
 // 16384 x 2048 x 512). Out-of-range columns are stored to an offset past the output
-// descriptor (dropped by the hardware) instead of behind a branch. Tiles are walked in
+// descriptor (2^31, dropped by the hardware) instead of behind a branch. Tiles are walked in
 // groups of 8 row tiles (n-major inside a group), so the 32 tiles an XCD runs at once
 // share 8 A panels and 4 B panels in its L2 (8192^3: 626 -> 534 us against row-major).
 //
-// Synchronization per k-step: each wavefront waits (vmcnt) for its own DMA loads of the
-// stage, then one s_barrier (no fence: LDS-DMA completion is what vmcnt tracks) makes every
-// wavefront's part visible; the stage refilled after the barrier is the one every
-// wavefront finished reading before it arrived. The DMA loads are inline assembly, which
+// Synchronization per k-step: each wavefront waits for its own DMA loads of the stage
+// (vmcnt, and lgkmcnt(0): the LDS write of an LDS-DMA load is tracked on the LDS counter, and
+// with vmcnt alone a wavefront on a busy CU was measured reading stale stage bytes), then
+// one s_barrier makes every wavefront's part visible; the stage refilled after the barrier
+// is the one every wavefront finished reading before it arrived. The DMA loads are inline assembly, which
 // the compiler does not track: its own vmcnt waits (the residual loads) only become
 // stricter, never too weak, with loads it cannot see in flight.
 // ---------------------------------------------------------------------------
@@ -669,9 +679,9 @@ void int8_gemm_pipe_kernel(GemmArgs g, PipeSched p) {
     // flight (2 CH per step; the scale loads and stores issued after them only make the
     // wait stricter)
     const int ahead = total - 1 - step;
-    if (ahead >= S - 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH * (S - 2)));
-    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if (ahead >= S - 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH * (S - 2)) & ~0x0F00);
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CH) & ~0x0F00);
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~0x0F00);
     asm volatile("s_barrier" ::: "memory");
     if (step + S - 1 < total) issue();
 
@@ -777,21 +787,22 @@ void int8_gemm_pipe_kernel(GemmArgs g, PipeSched p) {
           const int ml = 64 * round + row;
           const bool in = n0 + 8 * seg < g.N;
           if constexpr (CDT == RK_BF16) {
-            const int off = in ? static_cast<int>((ml * g.ldc + 8 * seg) * 2) : 0x7ffffff0;
+            const uint32_t off = in ? static_cast<uint32_t>((ml * g.ldc + 8 * seg) * 2) : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_r, off, 0, 0);
+                __builtin_bit_cast(v4i, make_uint4(lo.x, lo.y, hi.x, hi.y)), c_r,
+                static_cast<int>(off), 0, 0);
           } else {
-            const int off = in ? static_cast<int>((ml * g.ldc + 8 * seg) * 4) : 0x7ffffff0;
+            const uint32_t off = in ? static_cast<uint32_t>((ml * g.ldc + 8 * seg) * 4) : 0x80000000u;
             uint4 w0 = make_uint4(lo.x << 16, lo.x & 0xffff0000u, lo.y << 16, lo.y & 0xffff0000u);
             uint4 w1 = make_uint4(hi.x << 16, hi.x & 0xffff0000u, hi.y << 16, hi.y & 0xffff0000u);
             if (has_r) {
               // C = R + widened bf16, the float add of adding the tensors afterwards (R may
               // be C itself: each thread reads the residual it then overwrites)
-              const int roff = in ? static_cast<int>((ml * g.ldr + 8 * seg) * 4) : 0x7ffffff0;
+              const uint32_t roff = in ? static_cast<uint32_t>((ml * g.ldr + 8 * seg) * 4) : 0x80000000u;
               const float4 r0 = __builtin_bit_cast(
-                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, roff, 0, 0));
+                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, static_cast<int>(roff), 0, 0));
               const float4 r1 = __builtin_bit_cast(
-                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, roff + 16, 0, 0));
+                  float4, __builtin_amdgcn_raw_buffer_load_b128(r_r, static_cast<int>(roff + 16u), 0, 0));
               w0.x = __float_as_uint(r0.x + __uint_as_float(w0.x));
               w0.y = __float_as_uint(r0.y + __uint_as_float(w0.y));
               w0.z = __float_as_uint(r0.z + __uint_as_float(w0.z));
@@ -801,8 +812,10 @@ void int8_gemm_pipe_kernel(GemmArgs g, PipeSched p) {
               w1.z = __float_as_uint(r1.z + __uint_as_float(w1.z));
               w1.w = __float_as_uint(r1.w + __uint_as_float(w1.w));
             }
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w0), c_r, off, 0, 0);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w1), c_r, off + 16, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w0), c_r,
+                                                   static_cast<int>(off), 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, w1), c_r,
+                                                   static_cast<int>(off + 16u), 0, 0);
           }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): staging reads done
