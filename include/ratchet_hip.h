@@ -170,28 +170,6 @@ int rk_int8_gemm_packed_t(const int8_t* A, int64_t lda, const uint8_t* packed, i
                           void* stream);
 
 /*
- * The int8 grad_input with the gradient's stochastic-rounding quantization fused into the
- * GEMM's operand staging: for the gradient g [M, K] (up to 3 column parts as in
- * rk_quantize_rows_parts; nparts = 1 with part_cols = K for one tensor) and the packed state
- * [K, N] (the layer's weight, read as the K x N operand as in rk_int8_gemm_packed_t):
- *   scale[m], q = rk_quantize_rows(g, col_scale, stochastic=1, seed | *seed_dev, row_offset)
- *   out = bf16(float(q @ code) * scale[m])          (c_dtype RK_BF16, or RK_F32 widened)
- * bit for bit, without writing q (q, when not NULL, receives the codes; g_bf16, when not
- * NULL, receives bf16(g) like rk_quantize_rows' x_bf16). g_dtype RK_F32, RK_BF16 or
- * RK_F32_AS_BF16. Requires N in {128, 256, 512}, K <= 4096, part_cols % 64 == 0, 16-byte
- * aligned rows (RK_ERR_UNSUPPORTED otherwise: use the two calls).
- * Replaces: quantize_rows_colscaled(grad_output * weight_scale, stochastic) followed by
- *           scaled_int8_mm(grad_int8, code, ...)  ratchet.py:125-134, int8_matmul.py:262-277,
- *           289-343.
- */
-int rk_grad_input_sr(const void* g0, const void* g1, const void* g2, int nparts,
-                     int64_t part_cols, int g_dtype, int64_t ldg, const float* col_scale,
-                     uint64_t seed, const int64_t* seed_dev, int64_t row_offset,
-                     const uint8_t* packed, int64_t ldp, int max_code, int64_t M, int64_t K,
-                     int64_t N, float* scale, int8_t* q, int64_t ldq, uint16_t* g_bf16,
-                     int64_t ld_gb, void* out, int c_dtype, int64_t ldo, void* stream);
-
-/*
  * Decode + transpose the packed state: codeT[k, n] = (packed[n, k] & 15) - max_code.
  *   packed [N, K] (row stride ldp) -> codeT int8 [K, N] (row stride ldt).
  * Feeds the int8 grad_input GEMM (contraction over the output features), replacing
@@ -394,8 +372,8 @@ int rk_ratchet_update_partials(uint8_t* packed, int64_t ldp, const float* partia
  * Replaces: the per-layer mean of the row rms, ratchet.py:570 / 637 (gradient_rms_mean),
  *           averaged over layers in model.py:265-267.
  */
-int rk_row_rms_means(const float* row_rms, const int64_t* offsets, int64_t nseg, float* means,
-                     void* stream);
+int rk_row_rms_means(const float* row_rms, int64_t n, const int64_t* offsets, int64_t nseg,
+                     float* means, void* stream);
 
 /*
  * Row normalization alone: z = g / (rms + eps) with rms = sqrt(sum_k g^2 / K) in the

@@ -520,67 +520,6 @@ std::tuple<Tensor, Tensor> quantize_rows_parts(const std::vector<Tensor>& parts,
   return {q, scale};
 }
 
-// The int8 grad_input with the SR quantization of the gradient in its operand staging
-// (ratchet.py:125-134): (grad_input, row scale), the results of quantize_rows(stochastic)
-// followed by packed_mm_t. q_out / g_bf16 optionally receive the int8 codes / bf16(g).
-std::tuple<Tensor, Tensor> grad_input_sr(const std::vector<Tensor>& parts, const Tensor& packed,
-                                         int64_t max_code, const OptTensor& col_scale,
-                                         int64_t seed, const OptTensor& seed_slot,
-                                         int64_t row_offset, at::ScalarType out_dtype,
-                                         bool round_bf16, const OptTensor& q_out,
-                                         const OptTensor& g_bf16) {
-  const Parts g = gradient_parts(parts, "grad_input_sr");
-  packed_matrix(packed);
-  same_device(parts[0], packed, "grad_input_sr");
-  const int64_t m = g.rows, k = g.n * g.cols, n = packed.size(1);
-  TORCH_CHECK(packed.size(0) == k, "grad_input_sr: the gradient has ", k,
-              " columns, the packed state ", packed.size(0), " rows");
-  TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16,
-              "grad_input_sr: output dtype must be float32 or bfloat16");
-  TORCH_CHECK(!round_bf16 || g.dtype == RK_F32, "round_bf16 applies to a float32 gradient");
-  const c10::DeviceGuard guard(parts[0].device());
-  Tensor out = at::empty({m, n}, parts[0].options().dtype(out_dtype));
-  Tensor scale = at::empty({m}, parts[0].options().dtype(at::kFloat));
-  const OptTensor cs = f32_vector(col_scale, k, "col_scale");
-  const int64_t* slot = nullptr;
-  if (seed_slot.has_value()) {
-    TORCH_CHECK(seed_slot->scalar_type() == at::kLong && seed_slot->numel() == 1 &&
-                    seed_slot->device() == parts[0].device(),
-                "seed_slot must be one int64 on the input's device");
-    slot = static_cast<const int64_t*>(seed_slot->data_ptr());
-  }
-  int8_t* qp = nullptr;
-  int64_t ldq = k;
-  if (q_out.has_value()) {
-    TORCH_CHECK(q_out->scalar_type() == at::kChar && q_out->dim() == 2 && q_out->size(0) == m &&
-                    q_out->size(1) == k && q_out->stride(1) == 1 &&
-                    q_out->device() == parts[0].device(),
-                "q_out must be an int8 [M, K] row-major tensor on the gradient's device");
-    qp = q_out->data_ptr<int8_t>();
-    ldq = q_out->size(0) > 1 ? q_out->stride(0) : k;
-  }
-  uint16_t* xb = nullptr;
-  int64_t ldxb = k;
-  if (g_bf16.has_value()) {
-    TORCH_CHECK(g_bf16->scalar_type() == at::kBFloat16 && g_bf16->dim() == 2 &&
-                    g_bf16->size(0) == m && g_bf16->size(1) == k && g_bf16->stride(1) == 1 &&
-                    g_bf16->device() == parts[0].device(),
-                "g_bf16 must be a bfloat16 [M, K] row-major tensor on the gradient's device");
-    xb = static_cast<uint16_t*>(g_bf16->data_ptr());
-    ldxb = g_bf16->size(0) > 1 ? g_bf16->stride(0) : k;
-  }
-  if (m == 0 || n == 0) return {out, scale};
-  check_status(rk_grad_input_sr(g.p[0], g.p[1], g.p[2], g.n, g.cols,
-                                round_bf16 ? RK_F32_AS_BF16 : g.dtype, g.ld,
-                                ptr<const float>(cs), static_cast<uint64_t>(seed), slot,
-                                row_offset, packed.data_ptr<uint8_t>(), ld(packed),
-                                static_cast<int>(max_code), m, k, n, scale.data_ptr<float>(), qp,
-                                ldq, xb, ldxb, out.data_ptr(), dtype_code(out_dtype), n,
-                                stream_of(parts[0])),
-               "rk_grad_input_sr");
-  return {out, scale};
-}
-
 // x: int8 activations with their row scale s, or float32 / bfloat16 activations (s None)
 void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& x_in,
                                 const OptTensor& s, Tensor& work) {
@@ -958,8 +897,9 @@ Tensor row_rms_means(const Tensor& row_rms, const Tensor& offsets) {
   const int64_t nseg = offsets.size(0) - 1;
   const c10::DeviceGuard guard(row_rms.device());
   Tensor means = at::empty({nseg}, row_rms.options());
-  check_status(rk_row_rms_means(row_rms.data_ptr<float>(), offsets.data_ptr<int64_t>(), nseg,
-                                means.data_ptr<float>(), stream_of(row_rms)),
+  check_status(rk_row_rms_means(row_rms.data_ptr<float>(), row_rms.numel(),
+                                offsets.data_ptr<int64_t>(), nseg, means.data_ptr<float>(),
+                                stream_of(row_rms)),
                "rk_row_rms_means");
   return means;
 }
@@ -1060,11 +1000,6 @@ TORCH_LIBRARY(ratchet, m) {
   m.def(
       "grad_weight_partials_parts(Tensor[] parts, Tensor x, Tensor? s, Tensor(a!) work) -> ()");
   m.def(
-      "grad_input_sr(Tensor[] parts, Tensor packed, int max_code, Tensor? col_scale=None, "
-      "int seed=0, Tensor? seed_slot=None, int row_offset=0, ScalarType out_dtype=bfloat16, "
-      "bool round_bf16=False, Tensor(a!)? q_out=None, Tensor(b!)? g_bf16=None) "
-      "-> (Tensor, Tensor)");
-  m.def(
       "quantize_rows_parts(Tensor[] parts, Tensor? col_scale=None, bool stochastic=False, "
       "int seed=0, Tensor? seed_slot=None, int row_offset=0) -> (Tensor, Tensor)");
   m.def(
@@ -1117,7 +1052,6 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("grad_weight_partials", &grad_weight_partials);
   m.impl("grad_weight_partials_x", &grad_weight_partials_x);
   m.impl("grad_weight_partials_parts", &grad_weight_partials_parts);
-  m.impl("grad_input_sr", &grad_input_sr);
   m.impl("quantize_rows_parts", &quantize_rows_parts);
   m.impl("update_from_z", &update_from_z);
   m.impl("update_from_grad", &update_from_grad);

@@ -75,12 +75,16 @@ __global__ __launch_bounds__(256) void row_rms_mean_kernel(const float* row_rms,
 }
 
 // One block per segment [offsets[s], offsets[s + 1]) of a buffer holding several layers'
-// row rms: the same order as row_rms_mean_kernel, so each mean equals that kernel's.
+// row rms: the same order as row_rms_mean_kernel, so each mean equals that kernel's. The
+// bounds are clamped to [0, n] (and e >= b), so offsets past the buffer read nothing outside.
 __global__ __launch_bounds__(256) void row_rms_segment_means_kernel(const float* row_rms,
+                                                                     int64_t n,
                                                                      const int64_t* offsets,
                                                                      float* means) {
   __shared__ float part[256];
-  const int64_t b = offsets[blockIdx.x], e = offsets[blockIdx.x + 1];
+  int64_t b = offsets[blockIdx.x], e = offsets[blockIdx.x + 1];
+  b = b < 0 ? 0 : (b > n ? n : b);
+  e = e < b ? b : (e > n ? n : e);
   const float m = block_mean_256(row_rms + b, e - b, part);
   if (threadIdx.x == 0) means[blockIdx.x] = m;
 }
@@ -290,13 +294,14 @@ extern "C" int rk_normalize_rows(const void* g, int g_dtype, int64_t ldg, int64_
   return launch_grad_kernel<true>(a, g_dtype, as_stream(stream));
 }
 
-extern "C" int rk_row_rms_means(const float* row_rms, const int64_t* offsets, int64_t nseg,
-                                float* means, void* stream) {
+extern "C" int rk_row_rms_means(const float* row_rms, int64_t n, const int64_t* offsets,
+                                int64_t nseg, float* means, void* stream) {
   clear_error();
   if (nseg < 0 || nseg > 0x7fffffff) return fail(RK_ERR_ARG, "segment count out of range");
+  if (n < 0) return fail(RK_ERR_ARG, "negative row rms length");
   if (nseg == 0) return RK_OK;
-  if (!row_rms || !offsets || !means) return fail(RK_ERR_ARG, "null pointer");
+  if (!offsets || !means || (n > 0 && !row_rms)) return fail(RK_ERR_ARG, "null pointer");
   row_rms_segment_means_kernel<<<static_cast<unsigned>(nseg), 256, 0, as_stream(stream)>>>(
-      row_rms, offsets, means);
+      row_rms, n, offsets, means);
   return launch_status("row_rms_means");
 }

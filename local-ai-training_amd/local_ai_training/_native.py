@@ -86,8 +86,6 @@ SIGNATURES: dict[str, list] = {
                                      _i64, _p, _p, _i64, _p],
     "rk_quantize_rows_parts": [_p, _p, _p, _i32, _i64, _i32, _i64, _i64, _p, _i32, _u64, _p,
                                _i64, _p, _i64, _p, _p],
-    "rk_grad_input_sr": [_p, _p, _p, _i32, _i64, _i32, _i64, _p, _u64, _p, _i64, _p, _i64, _i32,
-                         _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p, _i32, _i64, _p],
     "rk_grad_weight_bf16_parts": [_p, _p, _p, _i32, _i64, _i32, _i64, _p, _i32, _i64, _p, _i64,
                                   _i64, _i64, _p, _i32, _p, _i64, _p],
     "rk_gelu_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
@@ -104,7 +102,7 @@ SIGNATURES: dict[str, list] = {
     "rk_cross_entropy_forward": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p],
     "rk_cross_entropy_backward": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i32,
                                   _i64, _p],
-    "rk_row_rms_means": [_p, _p, _i64, _p, _p],
+    "rk_row_rms_means": [_p, _i64, _p, _i64, _p, _p],
     "rk_attention_forward": [_p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64,
                              _i64, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _i64, _p, _p],
     "rk_version": [],

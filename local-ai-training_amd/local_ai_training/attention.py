@@ -34,6 +34,14 @@ def _philox_placeholders() -> tuple[Tensor, Tensor]:
     return _NO_DROPOUT_SEED[key]
 
 
+def _extent_fits(shape: tuple[int, ...], stride: tuple[int, ...]) -> bool:
+    """The kernel's 32-bit buffer offsets: one (batch, head)'s rows up to S + 128 (the last
+    key block's padding) within 2^31 bytes of bf16, and at most 2^31 - 1 (batch, head)
+    pairs (the same limits ``rk_attention_forward`` checks before launching)."""
+    b, h, s, d = shape
+    return ((s + 128) * stride[2] + d) * 2 < 2**31 and b * h <= 0x7FFFFFFF
+
+
 def attention_supported(q: Tensor, k: Tensor, v: Tensor) -> bool:
     if not (q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 4):
         return False
@@ -43,6 +51,8 @@ def attention_supported(q: Tensor, k: Tensor, v: Tensor) -> bool:
         return False
     for t in (q, k, v):
         if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):
+            return False
+        if not _extent_fits(tuple(t.shape), t.stride()):
             return False
     return True
 

@@ -250,37 +250,6 @@ def packed_t_supported(a: Tensor, packed: Tensor) -> bool:
             and packed.data_ptr() % 16 == 0)
 
 
-def grad_input_sr_supported(parts: list[Tensor], packed: Tensor,
-                            col_scale: Tensor | None = None) -> bool:
-    """Whether grad_input_sr takes these operands: 128, 256 or 512 output columns, at most
-    4096 gradient columns in parts of a multiple of 64, 16-byte aligned rows."""
-    k, n = packed.shape
-    c = parts[0].shape[1]
-    ld = parts[0].stride(0) if parts[0].shape[0] > 1 else c
-    return (n in (128, 256, 512) and c * len(parts) == k and k <= 4096 and c % 64 == 0
-            and parts[0].dtype in (torch.float32, torch.bfloat16)
-            and all(p.stride(-1) == 1 and p.data_ptr() % 16 == 0 and p.dtype == parts[0].dtype
-                    and (p.shape[0] <= 1 or p.stride(0) == ld) for p in parts)
-            and (ld * parts[0].element_size()) % 16 == 0
-            and packed.stride(-1) == 1 and _ld(packed) % 16 == 0
-            and packed.data_ptr() % 16 == 0
-            and (col_scale is None or col_scale.data_ptr() % 16 == 0))
-
-
-def grad_input_sr(parts: list[Tensor], packed: Tensor, max_code: int,
-                  col_scale: Tensor | None, out_dtype: torch.dtype, *,
-                  bf16_out: Tensor | None = None, round_bf16: bool = False
-                  ) -> tuple[Tensor, Tensor, int | Tensor]:
-    """grad_input = packed_int8_mm_t(q, packed, max_code, s) for (q, s) the stochastically
-    rounded row quantization of the gradient torch.cat(parts, -1) * col_scale, in one kernel
-    (q never reaches memory). Returns (grad_input, s, seed) with the seed drawn as
-    quantize_rows_sr draws it; ``bf16_out`` / ``round_bf16`` as in quantize_rows_sr."""
-    seed, slot = sr_seed_args(parts[0].device)
-    out, s = _ops().grad_input_sr(list(parts), packed, max_code, col_scale, seed, slot, 0,
-                                  out_dtype, round_bf16, None, bf16_out)
-    return out, s, (slot if slot is not None else seed)
-
-
 def packed_int8_mm_t(a: Tensor, packed: Tensor, max_code: int, a_scale: Tensor,
                      row_scale: Tensor | None, out_dtype: torch.dtype = torch.bfloat16
                      ) -> Tensor:

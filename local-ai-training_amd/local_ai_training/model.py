@@ -208,14 +208,22 @@ class _TokenLookup(torch.autograd.Function):
         return None, grad.to(ctx.weight_dtype)
 
 
-def _hip_lookup_supported(embedding: nn.Module, tokens: Tensor) -> bool:
+def _hip_lookup_config_ok(embedding: nn.Module) -> bool:
+    """Whether the HIP embedding-gradient kernels take this embedding (devices aside): a
+    plain nn.Embedding in float32 or bf16 without padding_idx, max_norm, sparse gradients or
+    scale_grad_by_freq, rows of a multiple of 4 and at most 4096 columns."""
     if type(embedding) is not nn.Embedding:
         return False
     w = embedding.weight
-    return (w.is_cuda and tokens.is_cuda and w.dtype in (torch.float32, torch.bfloat16)
+    return (w.dtype in (torch.float32, torch.bfloat16)
             and embedding.padding_idx is None and embedding.max_norm is None
             and not embedding.sparse and not embedding.scale_grad_by_freq
             and w.shape[1] % 4 == 0 and w.shape[1] <= 4096 and w.shape[0] < 2**31 - 1)
+
+
+def _hip_lookup_supported(embedding: nn.Module, tokens: Tensor) -> bool:
+    return (embedding.weight.is_cuda and tokens.is_cuda
+            and _hip_lookup_config_ok(embedding))
 
 
 def _autocast_bf16(t: Tensor) -> torch.dtype | None:
@@ -455,6 +463,21 @@ class RatchetGPT(nn.Module):
         )
         self.final_norm = nn.RMSNorm(config.n_embd)
         self.lm_head = _linear(config, config.n_embd, config.vocab_size, max_code)
+
+    def embedding_backward_is_sort_based(self) -> bool:
+        """Whether a training step takes the token embedding's weight gradient from torch's
+        sort-based embedding backward (``embedding_dense_backward``) instead of the HIP
+        kernels: a ratchet embedding (its effective weight goes through F.embedding), the
+        HIP path switched off, or an embedding those kernels do not take (padding_idx,
+        max_norm, sparse or scale_grad_by_freq, width not a multiple of 4 or above 4096).
+        Under graph capture that backward records a memset node that clears its sort's
+        state, which is not safe on replays."""
+        emb = self.token_embedding
+        if type(emb) is not nn.Embedding:
+            return True
+        if not emb.weight.requires_grad:
+            return False
+        return not (self.hip_embedding_backward and _hip_lookup_config_ok(emb))
 
     def forward(self, tokens: Tensor, targets: Tensor | None = None
                 ) -> tuple[Tensor, Tensor | None]:

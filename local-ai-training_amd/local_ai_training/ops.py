@@ -155,14 +155,6 @@ def _register_fakes() -> None:
         return (parts[0].new_empty((m, k), dtype=torch.int8),
                 parts[0].new_empty((m,), dtype=torch.float32))
 
-    @fake("ratchet::grad_input_sr")
-    def _grad_input_sr(parts, packed, max_code, col_scale=None, seed=0, seed_slot=None,
-                       row_offset=0, out_dtype=torch.bfloat16, round_bf16=False, q_out=None,
-                       g_bf16=None):
-        m = parts[0].shape[0]
-        return (parts[0].new_empty((m, packed.shape[1]), dtype=out_dtype),
-                parts[0].new_empty((m,), dtype=torch.float32))
-
     @fake("ratchet::grad_weight_partials_parts")
     def _grad_weight_partials_parts(parts, x, s, work):
         return None
@@ -201,6 +193,6 @@ OPERATORS = (
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
-    "grad_weight_partials_parts", "grad_input_sr", "cross_entropy_forward",
+    "grad_weight_partials_parts", "cross_entropy_forward",
     "cross_entropy_backward", "row_rms_means", "attention_forward",
 )

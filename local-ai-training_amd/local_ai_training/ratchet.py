@@ -41,8 +41,6 @@ from .int8_matmul import (
     grad_weight_bf16_x,
     grad_weight_parts_supported,
     grad_weight_splits,
-    grad_input_sr,
-    grad_input_sr_supported,
     int8_mm_nt,
     packed_int8_mm,
     packed_int8_mm_residual,
@@ -407,23 +405,15 @@ class _RatchetMatmul(torch.autograd.Function):
             col_scale = scale_d.float().contiguous()
             out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
                 else torch.bfloat16
-            if g.stride(-1) == 1 and layer.fuse_sr_grad_input \
-                    and grad_input_sr_supported([g], packed, col_scale):
-                # the SR quant inside the grad_input GEMM's operand staging (same results;
-                # the int8 gradient never reaches memory)
-                grad_input, grad_s, layer.last_sr_seed = grad_input_sr(
-                    [g], packed, layer.max_code, col_scale, out_dtype, bf16_out=gradient_bf16,
-                    round_bf16=round_bf16)
+            grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr(
+                g, col_scale, bf16_out=gradient_bf16, round_bf16=round_bf16)
+            if packed_t_supported(grad_q, packed):
+                # contraction over the packed rows, read in place (no unpacked copy)
+                grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
+                                              out_dtype)
             else:
-                grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr(
-                    g, col_scale, bf16_out=gradient_bf16, round_bf16=round_bf16)
-                if packed_t_supported(grad_q, packed):
-                    # contraction over the packed rows, read in place (no unpacked copy)
-                    grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
-                                                  out_dtype)
-                else:
-                    code_t = unpack_transpose(packed, layer.max_code)
-                    grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
+                code_t = unpack_transpose(packed, layer.max_code)
+                grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
         else:
             gradient_bf16 = flat_gradient.to(torch.bfloat16)
             grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)
@@ -487,17 +477,13 @@ class _RatchetMatmul(torch.autograd.Function):
         col_scale = scale_d.float().contiguous()
         out_dtype = ctx.input_dtype if ctx.input_dtype in (torch.float32, torch.bfloat16) \
             else torch.bfloat16
-        if layer.fuse_sr_grad_input and grad_input_sr_supported(parts, packed, col_scale):
-            grad_input, grad_s, layer.last_sr_seed = grad_input_sr(
-                parts, packed, layer.max_code, col_scale, out_dtype)
+        grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr_parts(parts, col_scale)
+        if packed_t_supported(grad_q, packed):
+            grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
+                                          out_dtype)
         else:
-            grad_q, grad_s, layer.last_sr_seed = quantize_rows_sr_parts(parts, col_scale)
-            if packed_t_supported(grad_q, packed):
-                grad_input = packed_int8_mm_t(grad_q, packed, layer.max_code, grad_s, None,
-                                              out_dtype)
-            else:
-                code_t = unpack_transpose(packed, layer.max_code)
-                grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
+            code_t = unpack_transpose(packed, layer.max_code)
+            grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
         if partials is None:
             partials = grad_weight_bf16_parts(parts, q, None if ctx.x_dq else s,
                                               work=layer._split_workspace(m, q.device))
@@ -556,13 +542,6 @@ class DiscreteRatchetLinear(nn.Module):
     # fused backward under HIP-graph capture: grad_weight on a side stream, concurrent with
     # grad_input (False: one stream, e.g. to compare the two)
     overlap_weight_gradient: bool = True
-    # int8 backward: the gradient's SR quant inside the grad_input GEMM where the shapes
-    # allow (rk_grad_input_sr; the same results as the quant kernel followed by the GEMM on
-    # its int8 output). Off by default: on MI355X the fused kernel measured slower than the
-    # two kernels (91.5 vs 63.1 + 25.7 us at 16384 x 2048 -> 512), since its absmax pass
-    # re-reads the gradient with the VALU idle and its rounding and MFMA phases alternate
-    # at every k-step barrier (VALU busy 0.58 against the quant kernel's 0.80).
-    fuse_sr_grad_input: bool = False
     # int8 inputs handed over with their dequantized bf16 copy (written by the same
     # quantization kernel): the backward's grad_weight reads that copy instead of
     # converting the int8 rows for every output tile (the same operand values). Off by
@@ -946,7 +925,11 @@ class DiscreteRatchetLinear(nn.Module):
             if counts is None:
                 pos = neg = bpos = bneg = 0
             else:
-                pos, neg, bpos, bneg = counts[0], counts[1], counts[2], counts[3]
+                # the model's shared count slot is cleared by its sum and reused next step:
+                # the stats own a copy (32 bytes), as the reference's per-layer stats own
+                # their tensors
+                own = counts.clone() if counts is self._counts_slot else counts
+                pos, neg, bpos, bneg = own[0], own[1], own[2], own[3]
             stats = RatchetUpdateStats(
                 total_weights=self._pending_stats_total_weights,
                 positive_moves=pos,

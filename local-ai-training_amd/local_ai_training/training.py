@@ -19,6 +19,10 @@ What a replay keeps identical to an eager step:
 * the numerics: autocast runs with its cast cache off (``cache_enabled=False``), which
   changes no value.
 
+A model whose token-embedding gradient would come from torch's sort-based backward is
+refused before anything runs (``RatchetGPT.embedding_backward_is_sort_based``): that
+backward records a memset node in the graph, and such nodes are not safe on replays.
+
 The warm-up steps that precede the capture are real training steps.
 """
 
@@ -62,6 +66,15 @@ class CapturedTrainingStep:
 
     def __init__(self, model: RatchetGPT, optimizer: torch.optim.Optimizer, inputs: Tensor,
                  targets: Tensor, *, warmup_steps: int = 2) -> None:
+        if model.embedding_backward_is_sort_based():
+            # checked before any step runs: the capture would record that backward's memset
+            # node (see RatchetGPT.embedding_backward_is_sort_based)
+            raise RuntimeError(
+                "CapturedTrainingStep refuses this model: its token-embedding gradient would "
+                "come from torch's sort-based embedding backward, whose memset node is not "
+                "safe in a replayed graph; use an nn.Embedding with hip_embedding_backward "
+                "(no padding_idx, max_norm, sparse or scale_grad_by_freq; width a multiple "
+                "of 4, at most 4096) or run the step eagerly")
         if not inputs.is_cuda:
             raise RuntimeError("CapturedTrainingStep requires CUDA (a ROCm GPU)")
         if not all(group.get("capturable", False) for group in optimizer.param_groups):

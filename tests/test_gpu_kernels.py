@@ -585,13 +585,27 @@ def test_update_writes_the_mean_row_rms(cuda, rows, k):
     bounds = [0, 1000, 1000 + rows, 1000 + rows, buf.numel()]
     offsets = torch.tensor(bounds, dtype=torch.int64, device=cuda)
     seg = torch.empty(4, device=cuda)
-    nat.call("rk_row_rms_means", buf.data_ptr(), offsets.data_ptr(), 4, seg.data_ptr(),
-             nat.stream_handle(cuda))
+    nat.call("rk_row_rms_means", buf.data_ptr(), buf.numel(), offsets.data_ptr(), 4,
+             seg.data_ptr(), nat.stream_handle(cuda))
     assert seg[1].view(torch.int32).item() == means[0]
     for i in (0, 3):
         want = buf[bounds[i]:bounds[i + 1]].double().mean().item()
         assert abs(seg[i].item() - want) <= 1e-6 * abs(want)
     assert math.isnan(seg[2].item())
+    # offsets past the buffer (or reversed, or negative) are clamped to [0, n]: the last
+    # segment reads up to the end only, a segment wholly past the end is empty (NaN)
+    n = buf.numel()
+    bad = torch.tensor([1000, n + 5000, n + 9000, -7, 1000 + rows], dtype=torch.int64,
+                       device=cuda)
+    seg4 = torch.empty(4, device=cuda)
+    nat.call("rk_row_rms_means", buf.data_ptr(), n, bad.data_ptr(), 4, seg4.data_ptr(),
+             nat.stream_handle(cuda))
+    want = buf[1000:].double().mean().item()
+    assert abs(seg4[0].item() - want) <= 1e-6 * abs(want)
+    assert math.isnan(seg4[1].item()) and math.isnan(seg4[2].item())
+    want = buf[0:1000 + rows].double().mean().item()
+    assert abs(seg4[3].item() - want) <= 1e-6 * abs(want)
+    torch.cuda.synchronize()
 
 
 # 4100 and 9000 rows take the pipelined row loop (several rows per wavefront, the next

@@ -261,33 +261,6 @@ def test_qkv_gradients_read_in_parts_change_nothing(cuda):
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))
 
 
-def test_sr_quant_fused_into_grad_input_changes_nothing(cuda):
-    # The gradient's SR quant done inside the grad_input GEMM (rk_grad_input_sr) instead of
-    # the quant kernel followed by the GEMM on its int8 output: identical losses, ratchet
-    # states and float parameters over three steps.
-    from local_ai_training import ratchet
-
-    calls = []
-    orig = ratchet.grad_input_sr
-
-    def recording(*args, **kwargs):
-        calls.append(1)
-        return orig(*args, **kwargs)
-
-    ratchet.grad_input_sr = recording
-    DiscreteRatchetLinear.fuse_sr_grad_input = True
-    try:
-        la, sa, pa = _int8_steps(cuda, fuse=True)
-    finally:
-        ratchet.grad_input_sr = orig
-        DiscreteRatchetLinear.fuse_sr_grad_input = False
-    assert calls
-    lb, sb, pb = _int8_steps(cuda, fuse=True)
-    assert all(torch.equal(x, y) for x, y in zip(la, lb))
-    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
-    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
-
-
 def test_dequantized_activations_for_the_backward_change_nothing(cuda):
     # The prologues also writing the dequantized bf16 rows, which the layers' backward
     # reads for grad_weight instead of converting q and s per output tile: identical losses,
@@ -354,3 +327,38 @@ def test_shared_move_count_buffer_gives_the_per_layer_totals(cuda):
     shared, separate = run(True), run(False)
     assert shared == separate
     assert any(s.code_moves > 0 for s in shared)
+
+
+def test_layer_stats_keep_their_counts_across_model_updates(cuda):
+    # A layer's RatchetUpdateStats (from its own ratchet_update, counts in the model's shared
+    # slot) keep their values after the model's update sums and clears that slot and the
+    # next step reuses it, as the reference's per-layer stats own their tensors.
+    from local_ai_training.ratchet import pack_code_pressure
+
+    torch.manual_seed(0)
+    config = ModelConfig(vocab_size=64, block_size=64, n_layer=2, n_head=4, n_embd=128,
+                         matmul_mode="int8", int8_backward=True)
+    model = build_seeded_model(config, max_code=2, seed=1337).to(cuda).train()
+    first = next(m for m in model.modules() if isinstance(m, DiscreteRatchetLinear))
+    gen = torch.Generator().manual_seed(4)
+    near = (torch.randint(0, 2, tuple(first.packed.shape), generator=gen,
+                          dtype=torch.int8) * 14 - 7)
+    first.packed.copy_(pack_code_pressure(first.code.cpu(), near, 2).to(cuda))
+    batch = torch.randint(0, 64, (8, 65), generator=gen).to(cuda)
+
+    def step():
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            _, loss = model(batch[:, :64], batch[:, 1:])
+        loss.backward()
+
+    step()
+    kept = first.ratchet_update(validate=True)
+    fields = ("positive_moves", "negative_moves", "blocked_positive_moves",
+              "blocked_negative_moves")
+    before = [int(getattr(kept, f)) for f in fields]
+    model.ratchet_update(validate=True)
+    step()
+    model.ratchet_update(validate=True)
+    torch.cuda.synchronize()
+    assert [int(getattr(kept, f)) for f in fields] == before
+    assert sum(before) > 0

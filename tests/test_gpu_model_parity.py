@@ -97,12 +97,6 @@ class StepRecorder:
             self.grad_input[name] = (a[r], a_scale[r], out[r])
             return out
 
-        def record_fused(name, values, round_bf16, seed, q, s, out):
-            r = self.rows(values.shape[0], values.device)
-            consumed = values[r].to(torch.bfloat16) if round_bf16 else values[r].clone()
-            self.sr.append([name, consumed, seed, q[r], s[r]])
-            self.grad_input[name] = (q[r], s[r], out[r])
-
         def sr_parts(parts, col_scale=None):
             q, s, seed = orig_sr_parts(parts, col_scale)
             r = self.rows(q.shape[0], q.device)
@@ -110,23 +104,8 @@ class StepRecorder:
             self.sr.append([None, torch.cat(parts, dim=-1)[r], seed, q[r], s[r]])
             return q, s, seed
 
-        def gi(parts, packed, max_code, col_scale, out_dtype, *, bf16_out=None,
-               round_bf16=False):
-            # the fused SR quant + grad_input, run with its optional code output so that the
-            # codes it rounded are checked too (the same seed draw as the wrapper's)
-            seed, slot = int8_matmul.sr_seed_args(parts[0].device)
-            m, k = parts[0].shape[0], sum(p.shape[1] for p in parts)
-            q = torch.empty(m, k, dtype=torch.int8, device=parts[0].device)
-            out, s = ops.ratchet().grad_input_sr(list(parts), packed, max_code, col_scale, seed,
-                                                 slot, 0, out_dtype, round_bf16, q, bf16_out)
-            seed = slot if slot is not None else seed
-            values = torch.cat(parts, dim=-1) if len(parts) > 1 else parts[0]
-            record_fused(self.by_ptr[packed.data_ptr()], values, round_bf16, seed, q, s, out)
-            return out, s, seed
-
         orig_sr_parts = ratchet_mod.quantize_rows_sr_parts
         monkeypatch.setattr(ratchet_mod, "quantize_rows_sr_parts", sr_parts)
-        monkeypatch.setattr(ratchet_mod, "grad_input_sr", gi)
         monkeypatch.setattr(ratchet_mod, "packed_int8_mm", mm)
         monkeypatch.setattr(ratchet_mod, "packed_int8_mm_residual", mm_residual)
         monkeypatch.setattr(ratchet_mod, "packed_int8_mm_t", mm_t)
@@ -250,18 +229,6 @@ def test_tiny_config_hundred_steps_every_row_bit_exact(cuda, monkeypatch):
     torch.manual_seed(1234)
     losses = run_parity(cuda, monkeypatch, model, tokens, 100, 2, None, None)
     assert np.mean(losses[-10:]) < np.mean(losses[:10])
-
-
-def test_tiny_config_fused_sr_grad_input_every_row_bit_exact(cuda, monkeypatch):
-    # the same check with the gradient's SR quant done inside the grad_input GEMM
-    # (rk_grad_input_sr, opt-in), its int8 codes captured through its optional output
-    monkeypatch.setattr(DiscreteRatchetLinear, "fuse_sr_grad_input", True)
-    model = make_model(cuda, vocab=256, block=64, n_layer=2, n_head=4, n_embd=128, ffn=512,
-                       max_code=2, seed=1338, random_pressure=True)
-    gen = torch.Generator().manual_seed(21)
-    tokens = torch.randint(0, 256, (8, 65), generator=gen).to(cuda)
-    torch.manual_seed(4321)
-    run_parity(cuda, monkeypatch, model, tokens, 10, 2, None, None)
 
 
 def zipf_tokens(batch, block, vocab, seed, device):

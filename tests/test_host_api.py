@@ -126,3 +126,60 @@ def test_model_config_validation():
         RatchetGPT(tiny_config(), max_code=2)(torch.zeros((1, 9), dtype=torch.long))
     assert ModelConfig(vocab_size=8, n_embd=2048, n_head=16, ffn_hidden=5632).hidden_size == 5632
     assert ModelConfig(vocab_size=8, n_embd=64, n_head=4).hidden_size == 256
+
+
+def test_captured_step_refuses_sort_based_embedding_backward():
+    """The captured training step is refused, before any step runs, wherever the token
+    embedding's weight gradient would come from torch's sort-based embedding backward (the
+    backward whose memset node a replayed graph must not hold); the HIP path is accepted."""
+    from local_ai_training.training import CapturedTrainingStep
+
+    def model(**kw):
+        m = RatchetGPT(tiny_config(**kw), max_code=2)
+        return m
+
+    plain = model()
+    assert not plain.embedding_backward_is_sort_based()
+    off = model()
+    off.hip_embedding_backward = False
+    assert off.embedding_backward_is_sort_based()
+    ratchet_emb = model(ratchet_embedding=True)
+    assert ratchet_emb.embedding_backward_is_sort_based()
+    padded = model()
+    padded.token_embedding.padding_idx = 0
+    assert padded.embedding_backward_is_sort_based()
+    for attr, value in (("max_norm", 1.0), ("sparse", True), ("scale_grad_by_freq", True)):
+        m = model()
+        setattr(m.token_embedding, attr, value)
+        assert m.embedding_backward_is_sort_based(), attr
+    wide = RatchetGPT(ModelConfig(vocab_size=11, block_size=8, n_layer=1, n_head=2,
+                                  n_embd=4098), max_code=2)
+    assert wide.embedding_backward_is_sort_based()
+    frozen = model()
+    frozen.token_embedding.weight.requires_grad_(False)
+    frozen.hip_embedding_backward = False
+    assert not frozen.embedding_backward_is_sort_based()
+
+    tokens = torch.zeros((1, 8), dtype=torch.long)
+    for bad in (off, ratchet_emb, padded):
+        opt = torch.optim.AdamW([p for p in bad.parameters() if p.requires_grad], lr=1e-3)
+        with pytest.raises(RuntimeError, match="sort-based embedding backward"):
+            CapturedTrainingStep(bad, opt, tokens, tokens)
+
+
+def test_attention_gate_repeats_the_kernel_extent_check():
+    """attention_supported sends inputs whose per-head extent would overflow the kernel's
+    32-bit offsets to torch's attention instead of letting the HIP op raise (the gate alone,
+    on shapes and strides; no allocation)."""
+    from local_ai_training.attention import _extent_fits
+
+    # the 25M and 1B shapes as the model's strided views ([B, S, 3, H, D] -> [B, H, S, D])
+    assert _extent_fits((32, 8, 512, 64), (512 * 3 * 512, 64, 3 * 512, 1))
+    assert _extent_fits((8, 16, 1024, 128), (1024 * 3 * 2048, 128, 3 * 2048, 1))
+    # a row stride whose (S + 128) rows pass 2^31 bytes, just under and just over
+    d = 128
+    s = 4096
+    limit = (2**31 // 2 - d) // (s + 128)
+    assert _extent_fits((1, 1, s, d), (0, 0, limit, 1))
+    assert not _extent_fits((1, 1, s, d), (0, 0, limit + 1, 1))
+    assert not _extent_fits((2**16, 2**15 + 1, 1, 64), (0, 0, 64, 1))

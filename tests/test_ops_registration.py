@@ -29,7 +29,6 @@ MUTATED = {
     "rmsnorm_quantize": {"x_dq"},
     "gelu_quantize": {"x_dq"},
     "transpose_quantize": {"x_dq"},
-    "grad_input_sr": {"q_out", "g_bf16"},
 }
 
 
@@ -53,7 +52,7 @@ def test_schema_declares_exactly_the_written_arguments(R, name):
     assert written == MUTATED.get(name, set())
     if written:
         assert not schema.returns or name in ("quantize_rows", "normalize_rows",
-                                              "grad_input_sr", "rmsnorm_quantize",
+                                              "rmsnorm_quantize",
                                               "gelu_quantize", "transpose_quantize")
 
 
@@ -102,11 +101,6 @@ def test_fake_kernels_give_result_shapes_on_meta_tensors(R):
                                meta(2, m // 2, dtype=torch.int64), 50)
     assert emb.shape == (50, k) and emb.dtype == torch.float32
     parts = [meta(m, n, dtype=torch.bfloat16) for _ in range(3)]
-    gi, gs = R.grad_input_sr(parts, meta(3 * n, k, dtype=torch.uint8), 2, meta(3 * n), 7)
-    assert (gi.shape, gi.dtype, gs.shape) == ((m, k), torch.bfloat16, (m,))
-    gi, _ = R.grad_input_sr(parts, meta(3 * n, k, dtype=torch.uint8), 2, None, 7, None, 0,
-                            torch.float32)
-    assert gi.dtype == torch.float32
     qp, sp = R.quantize_rows_parts(parts, meta(3 * n), True, 7)
     assert (qp.shape, qp.dtype, sp.shape, sp.dtype) == ((m, 3 * n), torch.int8, (m,),
                                                           torch.float32)
