@@ -743,9 +743,11 @@ def hbm_probe(device, gib: float = 1.0) -> dict:
 def update_1b_bench(device, iters: int) -> dict:
     """The fused update of one 1B training step at full scale: every ratchet layer of the 1B
     septenary model (24 x qkv 6144x2048, proj 2048x2048, expand 5632x2048, contract
-    2048x5632, then lm_head 8192x2048; 973 M weights) updated from its grad_weight split
-    partials (the split counts of 8192 tokens), in model order. The partials (4 B per
-    weight and split) and packed states (1 B read + 1 B write) total more than the
+    2048x5632, then lm_head 8192x2048; 973 M weights), in model order, from what the
+    training step hands it: the bf16 gradient grad_weight writes itself where it takes one
+    split of 8192 tokens (2 B per weight), its float32 split partials elsewhere (4 B per
+    weight and split). Packed states are 1 B read + 1 B written per weight. Beside it, the
+    same sweep with every layer fed float32 partials (the earlier path). The data exceed the
     last-level cache, so every sweep streams them from HBM."""
     import torch
 
@@ -755,41 +757,59 @@ def update_1b_bench(device, iters: int) -> dict:
     tokens, mc = 8192, 3
     shapes = [(6144, 2048), (2048, 2048), (5632, 2048), (2048, 5632)] * 24 + [(8192, 2048)]
     gen = torch.Generator().manual_seed(11)
-    layers = []
-    for n, k in shapes:
-        nsplit = grad_weight_splits(tokens, n, k)
-        code = torch.randint(-mc, mc + 1, (n, k), generator=gen, dtype=torch.int8)
-        packed = (((code + mc) & 0x0F) | (7 << 4)).to(torch.uint8).to(device)
-        part = torch.empty(nsplit, n, k, device=device).normal_(0.0, 1e-3)
-        layers.append((packed, part, nsplit, n, k, torch.empty(n, device=device)))
     counts = torch.zeros(4, dtype=torch.int64, device=device)
     flag = torch.zeros(1, dtype=torch.int32, device=device)
     stream = nat.stream_handle(device)
 
-    def sweep():
-        for packed, part, nsplit, n, k, row_rms in layers:
-            nat.call("rk_ratchet_update_partials", packed.data_ptr(), k, part.data_ptr(),
-                     nsplit, n, k, mc, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0, counts.data_ptr(),
-                     row_rms.data_ptr(), None, flag.data_ptr(), None, None, k, stream)
+    def run(all_partials: bool) -> dict:
+        layers = []
+        for n, k in shapes:
+            nsplit = grad_weight_splits(tokens, n, k)
+            code = torch.randint(-mc, mc + 1, (n, k), generator=gen, dtype=torch.int8)
+            packed = (((code + mc) & 0x0F) | (7 << 4)).to(torch.uint8).to(device)
+            if nsplit == 1 and not all_partials:
+                grad = torch.empty(n, k, device=device).normal_(0.0, 1e-3).to(torch.bfloat16)
+            else:
+                grad = torch.empty(nsplit, n, k, device=device).normal_(0.0, 1e-3)
+            layers.append((packed, grad, nsplit, n, k, torch.empty(n, device=device)))
 
-    sweep()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(iters):
+        def sweep():
+            for packed, grad, nsplit, n, k, row_rms in layers:
+                if grad.dtype == torch.bfloat16:
+                    nat.call("rk_ratchet_update_grad", packed.data_ptr(), k, grad.data_ptr(),
+                             nat.RK_BF16, k, n, k, mc, 8, 0.5, 1.5, 1e-8, None, 0.0, 1.0,
+                             counts.data_ptr(), row_rms.data_ptr(), None, flag.data_ptr(),
+                             None, stream)
+                else:
+                    nat.call("rk_ratchet_update_partials", packed.data_ptr(), k,
+                             grad.data_ptr(), nsplit, n, k, mc, 8, 0.5, 1.5, 1e-8, None, 0.0,
+                             1.0, counts.data_ptr(), row_rms.data_ptr(), None, flag.data_ptr(),
+                             None, None, k, stream)
+
         sweep()
-    e1.record()
-    torch.cuda.synchronize()
-    sweep_s = e0.elapsed_time(e1) * 1e-3 / iters
-    weights = sum(n * k for n, k in shapes)
-    alg = sum(n * k * (2 + 4 * nsp) + 4 * n for _, _, nsp, n, k, _ in layers)
-    del layers
-    torch.cuda.empty_cache()
-    return {"workload": "fused update of every 1B ratchet layer from grad_weight split partials",
-            "weights": weights, "launches": len(shapes), "alg_bytes": alg,
-            "ms": round(sweep_s * 1e3, 3), "GB_s": round(alg / sweep_s / 1e9, 1),
-            "frac_hbm": round(alg / sweep_s / PEAK_HBM_BPS, 4)}
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            sweep()
+        e1.record()
+        torch.cuda.synchronize()
+        sweep_s = e0.elapsed_time(e1) * 1e-3 / iters
+        alg = sum(n * k * (2 + (2 if g.dtype == torch.bfloat16 else 4 * nsp)) + 4 * n
+                  for _, g, nsp, n, k, _ in layers)
+        del layers
+        torch.cuda.empty_cache()
+        return {"alg_bytes": alg, "ms": round(sweep_s * 1e3, 3),
+                "GB_s": round(alg / sweep_s / 1e9, 1),
+                "frac_hbm": round(alg / sweep_s / PEAK_HBM_BPS, 4)}
+
+    step = run(False)
+    partials = run(True)
+    return {"workload": "fused update of every 1B ratchet layer from what its backward hands "
+                        "it (bf16 gradient at one split, float32 split partials otherwise)",
+            "weights": sum(n * k for n, k in shapes), "launches": len(shapes), **step,
+            "all_partials": {"workload": "every layer from float32 split partials", **partials}}
 
 
 DECODE_LAYERS = dict(vocab=8192, block=1024, n_layer=24, n_head=16, n_embd=2048, ffn=5632)

@@ -224,7 +224,9 @@ int rk_dequant_transpose_bf16(const int8_t* q, int64_t ldq, const float* scale, 
  *   s  [M] float32, out [N, K] bf16 (row stride ldo).
  * The token axis is split into nsplit ranges (rk_grad_weight_splits gives the default);
  * workspace is float32 [nsplit, N, K] (caller-allocated, fully overwritten). Partial
- * sums are added in split order, so the result is reproducible. Requires N % 8 == 0,
+ * sums are added in split order, so the result is reproducible. With nsplit == 1 and out
+ * given, the GEMM writes the bf16 gradient itself (the same values) and workspace may be
+ * NULL (it is not touched). Requires N % 8 == 0,
  * K % 16 == 0 and 16-byte aligned rows (RK_ERR_UNSUPPORTED otherwise).
  * Replaces: grad_weight_tile = grad_out_tile.to(bf16) @ inputs_bf16 over the 256-row
  *           tiles of ratchet.py:148-163, with inputs_bf16 from ratchet.py:71-76.

@@ -397,23 +397,38 @@ void check_workspace(const Tensor& work, int64_t n, int64_t k) {
               "grad_weight workspace must be a contiguous float32 [nsplit, N, K] tensor");
 }
 
+// The work tensor of the partials operators: float32 [nsplit, N, K] split partials, or a
+// bfloat16 [1, N, K] tensor that receives the gradient itself (one split, written by the
+// GEMM's epilogue: the values rk_ratchet_update_partials would form from one split).
+bool direct_workspace(const Tensor& work, int64_t n, int64_t k) {
+  if (work.scalar_type() != at::kBFloat16) {
+    check_workspace(work, n, k);
+    return false;
+  }
+  TORCH_CHECK(work.dim() == 3 && work.size(0) == 1 && work.size(1) == n && work.size(2) == k &&
+                  work.is_contiguous(),
+              "a bfloat16 grad_weight work tensor must be a contiguous [1, N, K] tensor");
+  return true;
+}
+
+// work: float32 split partials (out, when given, receives their bf16 sum), or null with one
+// split and out given (the bf16 gradient written directly)
 void grad_weight_launch(const Tensor& g_in, const Tensor& act, bool int8_act,
-                        const OptTensor& s, const Tensor& work, uint16_t* out) {
+                        const OptTensor& s, float* work, int nsplit, uint16_t* out) {
   const Tensor g = unit_columns(g_in);
   const Tensor x = unit_columns(act);
   const int64_t m = g.size(0), n = g.size(1), k = x.size(1);
-  const int nsplit = static_cast<int>(work.size(0));
   const int gcode = dtype_code(g, "upstream gradient");
   if (int8_act) {
     const Tensor sv = f32_vector(*s, m, "activation row scale");
     check_status(rk_grad_weight_bf16(g.data_ptr(), gcode, ld(g), x.data_ptr<int8_t>(), ld(x),
-                                     sv.data_ptr<float>(), m, n, k, work.data_ptr<float>(),
-                                     nsplit, out, k, stream_of(g)),
+                                     sv.data_ptr<float>(), m, n, k, work, nsplit, out, k,
+                                     stream_of(g)),
                  "rk_grad_weight_bf16");
   } else {
     check_status(rk_grad_weight_bf16_x(g.data_ptr(), gcode, ld(g), x.data_ptr(),
-                                       dtype_code(x, "activations"), ld(x), m, n, k,
-                                       work.data_ptr<float>(), nsplit, out, k, stream_of(g)),
+                                       dtype_code(x, "activations"), ld(x), m, n, k, work,
+                                       nsplit, out, k, stream_of(g)),
                  "rk_grad_weight_bf16_x");
   }
 }
@@ -428,8 +443,10 @@ Tensor grad_weight_common(const Tensor& g, const Tensor& act, bool int8_act, con
   Tensor out = at::empty({n, k}, g.options().dtype(at::kBFloat16));
   if (n == 0 || k == 0) return out;
   const int64_t splits = nsplit > 0 ? nsplit : grad_weight_splits(m, n, k);
-  Tensor work = at::empty({splits, n, k}, g.options().dtype(at::kFloat));
-  grad_weight_launch(g, act, int8_act, s, work, static_cast<uint16_t*>(out.data_ptr()));
+  // one split writes the bf16 gradient directly and needs no float32 workspace
+  Tensor work = splits > 1 ? at::empty({splits, n, k}, g.options().dtype(at::kFloat)) : Tensor();
+  grad_weight_launch(g, act, int8_act, s, splits > 1 ? work.data_ptr<float>() : nullptr,
+                     static_cast<int>(splits), static_cast<uint16_t*>(out.data_ptr()));
   return out;
 }
 
@@ -448,10 +465,14 @@ void grad_weight_partials_common(const Tensor& g, const Tensor& act, bool int8_a
   require_gpu(g, "grad_weight");
   same_device(g, act, "grad_weight");
   check_gradient(g, act.size(0));
-  check_workspace(work, g.size(1), act.size(1));
+  const bool direct = direct_workspace(work, g.size(1), act.size(1));
   const c10::DeviceGuard guard(g.device());
   if (g.size(1) == 0 || act.size(1) == 0) return;
-  grad_weight_launch(g, act, int8_act, s, work, nullptr);
+  if (direct)
+    grad_weight_launch(g, act, int8_act, s, nullptr, 1, static_cast<uint16_t*>(work.data_ptr()));
+  else
+    grad_weight_launch(g, act, int8_act, s, work.data_ptr<float>(),
+                       static_cast<int>(work.size(0)), nullptr);
 }
 
 void grad_weight_partials(const Tensor& g, const Tensor& q, const Tensor& s, Tensor& work) {
@@ -532,7 +553,7 @@ void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& 
   TORCH_CHECK(x.size(0) == g.rows, "activations must have the gradient's rows");
   same_device(parts[0], x, "grad_weight");
   const int64_t m = g.rows, n = g.n * g.cols, k = x.size(1);
-  check_workspace(work, n, k);
+  const bool direct = direct_workspace(work, n, k);
   const c10::DeviceGuard guard(x.device());
   if (n == 0 || k == 0) return;
   const OptTensor sv = int8_act ? OptTensor(f32_vector(*s, m, "activation row scale"))
@@ -540,9 +561,11 @@ void grad_weight_partials_parts(const std::vector<Tensor>& parts, const Tensor& 
   check_status(rk_grad_weight_bf16_parts(g.p[0], g.p[1], g.p[2], g.n, g.cols, g.dtype, g.ld,
                                          x.data_ptr(),
                                          int8_act ? RK_I8 : dtype_code(x, "activations"), ld(x),
-                                         ptr<const float>(sv), m, n, k, work.data_ptr<float>(),
-                                         static_cast<int>(work.size(0)), nullptr, k,
-                                         stream_of(x)),
+                                         ptr<const float>(sv), m, n, k,
+                                         direct ? nullptr : work.data_ptr<float>(),
+                                         direct ? 1 : static_cast<int>(work.size(0)),
+                                         direct ? static_cast<uint16_t*>(work.data_ptr()) : nullptr,
+                                         k, stream_of(x)),
                "rk_grad_weight_bf16_parts");
 }
 

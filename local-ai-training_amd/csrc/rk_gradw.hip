@@ -49,6 +49,8 @@ struct GwArgs {
   int64_t ldx;
   const float* s;   // per-token scale (int8 form only)
   float* part;      // [nsplit][N][K] fp32
+  uint16_t* out;    // one split: the bf16 gradient [N, K] (row stride ldo) written directly
+  int64_t ldo;
   int64_t M, N, K;
   int64_t m_chunk;  // tokens per split, a multiple of GW_BM
   int nsplit;
@@ -161,15 +163,17 @@ __device__ __forceinline__ void block_row_rms_mean(const float* row_rms, int64_t
   if (t == 0) mean[0] = part[0] / static_cast<float>(rows);
 }
 
-// UNC < 0: partial sums only. UNC >= 0 (rk_grad_weight_update): after writing its partial
+// UNC < 0: partial sums only, or with BF16OUT (one split) the bf16 gradient itself, rounded
+// by the reduce kernel's conversion. UNC >= 0 (rk_grad_weight_update): after writing its partial
 // tile, each block publishes it (device-scope release: the XCDs' L2s are not coherent) and
 // counts its arrival for its row block; the block that completes a row block acquires and
 // runs the fused update (update_row with the split-partial source, UNC chunks in registers)
 // on those rows, then resets the row block's counter for the next launch. The block that
 // completes the last row block writes the mean row rms the same way.
-template <int GDT, int XK, int S, int BM, class CFG, int UNC = -1>
+template <int GDT, int XK, int S, int BM, class CFG, int UNC = -1, bool BF16OUT = false>
 __global__ __launch_bounds__(CFG::THREADS) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void grad_weight_partial_kernel(GwArgs a) {
+  static_assert(!BF16OUT || UNC < 0, "the fused update reads split partials");
   constexpr int GE = GDT == RK_F32 ? 4 : 2;                          // g element bytes
   constexpr int XE = XK == GW_X_Q8 ? 1 : (XK == GW_X_BF16 ? 2 : 4);  // X element bytes
   constexpr int FEAT = CFG::FEAT, THREADS = CFG::THREADS, PITCH = CFG::PITCH;
@@ -348,8 +352,25 @@ void grad_weight_partial_kernel(GwArgs a) {
 
   // Partial sums: acc[i][j][e] is C[n][k] with k = k0 + kw0 + 32 j + lane % 32 and
   // n = n0 + nw0 + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4.
-  float* out = a.part + static_cast<int64_t>(split) * a.N * a.K;
   const int lk = lane & 31, lh = lane >> 5;
+  if constexpr (BF16OUT) {
+    // one split: the sum is complete; round it as grad_weight_reduce_kernel does (the same
+    // packed conversion) and store the bf16 gradient, half the bytes of a float32 partial
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t k = k0 + kw0 + 32 * j + lk;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t n = n0 + nw0 + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
+          if (n < a.N && k < a.K)
+            a.out[n * a.ldo + k] = static_cast<uint16_t>(gw_pack_bf16x2(acc[i][j][e], 0.0f));
+        }
+      }
+    return;
+  }
+  float* out = a.part + static_cast<int64_t>(split) * a.N * a.K;
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -414,12 +435,14 @@ __global__ __launch_bounds__(256) void grad_weight_reduce_kernel(const float* pa
 
 // Ring depth 2 and 32-token steps: ring depths 4 and 6 and 64-token steps (BM = 64, 80 KB
 // of LDS) measure the same or slower on MI355X at the op and model shapes.
-template <int XK, class CFG, int UNC = -1>
+template <int XK, class CFG, int UNC = -1, bool BF16OUT = false>
 void launch_partial_g(const GwArgs& a, int g_dtype, dim3 grid, hipStream_t st) {
   if (g_dtype == RK_F32)
-    grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM, CFG, UNC><<<grid, CFG::THREADS, 0, st>>>(a);
+    grad_weight_partial_kernel<RK_F32, XK, 2, GW_BM, CFG, UNC, BF16OUT>
+        <<<grid, CFG::THREADS, 0, st>>>(a);
   else
-    grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM, CFG, UNC><<<grid, CFG::THREADS, 0, st>>>(a);
+    grad_weight_partial_kernel<RK_BF16, XK, 2, GW_BM, CFG, UNC, BF16OUT>
+        <<<grid, CFG::THREADS, 0, st>>>(a);
 }
 
 // The fused form: the update's row chunks in registers for rows of up to 512 columns (one
@@ -446,7 +469,9 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   if (g_dtype != RK_F32 && g_dtype != RK_BF16) return fail(RK_ERR_ARG, "unsupported gradient dtype");
   if (M < 0 || N < 0 || K < 0) return fail(RK_ERR_ARG, "negative size");
   if (N == 0 || K == 0) return RK_OK;
-  if (!g || !x || (x_kind == GW_X_Q8 && !s) || !workspace)
+  // one split with an output needs no workspace: the kernel writes the bf16 gradient itself
+  const bool direct = nsplit == 1 && out != nullptr && upd == nullptr;
+  if (!g || !x || (x_kind == GW_X_Q8 && !s) || (!workspace && !direct))
     return fail(RK_ERR_ARG, "null pointer");
   if (nsplit < 1 || nsplit > 64) return fail(RK_ERR_ARG, "nsplit must be in 1..64");
   if ((nparts == 0 && ldg < N) || ldx < K || (out && ldo < K))
@@ -454,7 +479,7 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   const int ge = g_dtype == RK_F32 ? 4 : 2;
   const int xe = x_kind == GW_X_Q8 ? 1 : (x_kind == GW_X_BF16 ? 2 : 4);
   if ((N % 8) != 0 || (K % 16) != 0 || ((ldg * ge) % 16) != 0 || ((ldx * xe) % 16) != 0 ||
-      (ldo % 4) != 0 || !aligned16(g) || !aligned16(x) || !aligned16(workspace) ||
+      (ldo % 4) != 0 || !aligned16(g) || !aligned16(x) || (workspace && !aligned16(workspace)) ||
       (reinterpret_cast<uintptr_t>(out) % 8) != 0)
     return fail(RK_ERR_UNSUPPORTED,
                 "grad_weight needs N %% 8 == 0, K %% 16 == 0 and 16-byte aligned rows");
@@ -485,6 +510,8 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   a.ldx = ldx;
   a.s = s;
   a.part = workspace;
+  a.out = out;
+  a.ldo = ldo;
   a.M = M;
   a.N = N;
   a.K = K;
@@ -518,6 +545,18 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
       else launch_partial_upd<GW_X_F32, GwSmall>(a, g_dtype, grid, st);
     }
     return launch_status("grad_weight_update");
+  }
+  if (direct) {
+    if (big) {
+      if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwBig, -1, true>(a, g_dtype, grid, st);
+      else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16, GwBig, -1, true>(a, g_dtype, grid, st);
+      else launch_partial_g<GW_X_F32, GwBig, -1, true>(a, g_dtype, grid, st);
+    } else {
+      if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwSmall, -1, true>(a, g_dtype, grid, st);
+      else if (x_kind == GW_X_BF16) launch_partial_g<GW_X_BF16, GwSmall, -1, true>(a, g_dtype, grid, st);
+      else launch_partial_g<GW_X_F32, GwSmall, -1, true>(a, g_dtype, grid, st);
+    }
+    return launch_status("grad_weight_bf16");
   }
   if (big) {
     if (x_kind == GW_X_Q8) launch_partial_g<GW_X_Q8, GwBig>(a, g_dtype, grid, st);

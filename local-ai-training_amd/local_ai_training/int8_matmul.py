@@ -328,7 +328,8 @@ def grad_weight_bf16(grad: Tensor, q: Tensor, s: Tensor, nsplit: int | None = No
     activations (q [M, K], s [M]) and the upstream gradient grad [M, N] (float32 or
     bfloat16), with no transposed copies. ``reduce=False`` stops at the float32 split
     partials [nsplit, N, K], written to ``work`` (allocated when not given) and returned, for
-    the update that reduces them itself.
+    the update that reduces them itself; a bfloat16 [1, N, K] ``work`` receives the gradient
+    itself (one split, written by the GEMM's epilogue).
     """
     if reduce:
         return _ops().grad_weight(grad, q, s, nsplit or 0)

@@ -769,14 +769,18 @@ class DiscreteRatchetLinear(nn.Module):
         self._pending_weight_gradient = gradient
 
     def _split_workspace(self, tokens: int, device: torch.device) -> Tensor:
-        """float32 [nsplit, out, in] split-partial workspace of the grad_weight GEMM, kept
-        across steps (reused in stream order: each backward's GEMM follows the previous
-        update that read it)."""
+        """The grad_weight GEMM's output for the update, kept across steps (reused in stream
+        order: each backward's GEMM follows the previous update that read it): float32
+        [nsplit, out, in] split partials, or with one split a bfloat16 [1, out, in] tensor
+        that receives the gradient itself (2 bytes per weight written and read instead of
+        4; the values the update forms from one split)."""
         nsplit = grad_weight_splits(tokens, self.out_features, self.in_features)
         shape = (nsplit, self.out_features, self.in_features)
+        dtype = torch.bfloat16 if nsplit == 1 else torch.float32
         work = self._gw_workspace
-        if work is None or work.shape != shape or work.device != device:
-            work = torch.empty(shape, device=device, dtype=torch.float32)
+        if (work is None or work.shape != shape or work.device != device
+                or work.dtype != dtype):
+            work = torch.empty(shape, device=device, dtype=dtype)
             self._gw_workspace = work
         return work
 
@@ -796,7 +800,13 @@ class DiscreteRatchetLinear(nn.Module):
                     if row_rms is not None and not defer_mean else None)
         rule = (self.max_code, self.pressure_threshold, self.bucket_low, self.bucket_high,
                 self.eps, ema, beta, counts, row_rms, grad_scale, nonfinite, rms_mean)
-        if from_partials:
+        if from_partials and gradient.dtype == torch.bfloat16:
+            # one split, written as the bf16 gradient by the GEMM: the update from the
+            # gradient itself gives what the update from one split's partials gives
+            gradient = gradient[0]
+            _ops().update_from_grad(self.packed, gradient, *rule)
+            self.last_weight_gradient = gradient.clone() if self.keep_weight_gradient else None
+        elif from_partials:
             kept = None
             if self.keep_weight_gradient:
                 kept = torch.empty(gradient.shape[1:], device=gradient.device,

@@ -21,6 +21,7 @@ from local_ai_training.int8_matmul import (
     dequant_transpose_bf16,
     effective_bf16,
     grad_weight_bf16,
+    grad_weight_bf16_parts,
     grad_weight_bf16_x,
     int8_mm_nt,
     packed_int8_mm,
@@ -697,6 +698,84 @@ def test_grad_weight_partials_reduce_to_the_entry_point_result(cuda):
     assert part.dtype == torch.float32 and part.shape[1:] == (n, k)
     want = grad_weight_bf16(g, q, s, part.shape[0])
     assert torch.equal(_reduce_partials(part).view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("shape,form", [
+    (shape, form) for shape in [(2048, 384, 512), (4096, 1024, 1024), (1000, 264, 272)]
+    for form in ("q8", "bf16", "f32")] + [((2048, 384, 512), "parts"),
+                                          ((1000, 768, 1024), "parts")])
+def test_one_split_gradient_written_directly_equals_the_reduced_partial(cuda, shape, form):
+    # One split: the GEMM's epilogue writes the bf16 gradient itself (the entry point with
+    # nsplit = 1, and the partials operators on a bf16 [1, N, K] work tensor). It equals
+    # the split's float32 partial rounded by the reduction, bit for bit: the three
+    # activation forms and a gradient in three column parts, both tile configurations
+    # (1024 x 1024 takes the 256 x 256 tiles) and ragged tiles.
+    m, n, k = shape
+    q = torch.randint(-127, 128, (m, k), generator=gen(51), dtype=torch.int8).to(cuda)
+    s = (torch.rand(m, generator=gen(52)) * 0.05 + 1e-3).to(cuda)
+    g = (torch.randn(m, n, generator=gen(53)) * 1e-2).to(torch.bfloat16).to(cuda)
+    x = (torch.randn(m, k, generator=gen(54))).to(cuda)
+    f32 = torch.empty(1, n, k, device=cuda)
+    direct = torch.empty(1, n, k, dtype=torch.bfloat16, device=cuda)
+    if form == "q8":
+        grad_weight_bf16(g, q, s, reduce=False, work=f32)
+        grad_weight_bf16(g, q, s, reduce=False, work=direct)
+        entry = grad_weight_bf16(g, q, s, 1)
+    elif form == "parts":
+        parts = list(g.chunk(3, dim=1))
+        grad_weight_bf16_parts(parts, q, s, work=f32)
+        grad_weight_bf16_parts(parts, q, s, work=direct)
+        entry = grad_weight_bf16(g, q, s, 1)
+    else:
+        xx = x.to(torch.bfloat16) if form == "bf16" else x
+        grad_weight_bf16_x(g, xx, reduce=False, work=f32)
+        grad_weight_bf16_x(g, xx, reduce=False, work=direct)
+        entry = grad_weight_bf16_x(g, xx, 1)
+    want = _reduce_partials(f32)
+    assert torch.equal(direct[0].view(torch.int16), want.view(torch.int16))
+    assert torch.equal(entry.view(torch.int16), want.view(torch.int16))
+
+
+def test_one_split_layer_update_equals_the_partials_update(cuda):
+    # A layer whose grad_weight takes one split (4096 x 2048: 128 large tiles) hands the
+    # update the bf16 gradient written by the GEMM; forcing the float32 partials path gives
+    # the same state, counts, row rms and mean, over two steps.
+    from local_ai_training import ratchet as ratchet_mod
+    from local_ai_training.int8_matmul import grad_weight_splits, quantize_rows
+
+    m, k, n = 4096, 2048, 4096
+    assert grad_weight_splits(m, n, k) == 1
+    outs = []
+    for force_f32 in (False, True):
+        torch.manual_seed(0)
+        layer = ratchet_mod.DiscreteRatchetLinear(
+            k, n, max_code=3, matmul_mode="int8", int8_backward=True,
+            fuse_backward_update=True).to(cuda).train()
+        layer.keep_weight_gradient = True
+        # pressures one step short of the threshold, so the steps move codes
+        near = (torch.randint(0, 2, (n, k), generator=gen(59), dtype=torch.int8) * 14 - 7)
+        layer.packed.copy_(ratchet_mod.pack_code_pressure(layer.code.cpu(), near, 3).to(cuda))
+        if force_f32:
+            layer._split_workspace = lambda tokens, device: torch.empty(
+                1, n, k, device=device, dtype=torch.float32)
+        rec = []
+        for step in range(2):
+            x = torch.randn(m, k, generator=gen(60 + step)).to(torch.bfloat16).to(cuda)
+            gout = (torch.randn(m, n, generator=gen(70 + step)) * 1e-2).to(torch.bfloat16)
+            q, qs = quantize_rows(x)
+            out = layer(x.requires_grad_(True), inputs_int8=q, inputs_scale=qs)
+            torch.manual_seed(5 + step)
+            out.backward(gout.to(cuda))
+            st = layer.ratchet_update(validate=True)
+            rec.append((layer.packed.clone(), [int(st.positive_moves), int(st.negative_moves),
+                                               int(st.blocked_positive_moves),
+                                               int(st.blocked_negative_moves)],
+                        float(st.gradient_rms_mean), layer.last_weight_gradient.clone()))
+        outs.append(rec)
+    for (pa, ca, ra, ga), (pb, cb, rb, gb) in zip(*outs):
+        assert torch.equal(pa, pb) and ca == cb and ra == rb
+        assert torch.equal(ga.view(torch.int16), gb.view(torch.int16))
+    assert sum(outs[0][0][1]) > 0
 
 
 def test_fused_update_rms_ema_bit_exact(cuda):
