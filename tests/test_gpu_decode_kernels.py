@@ -56,10 +56,11 @@ def _gemv(layer, out, prologue, epilogue, x=None, xq=None, xs=None, w=None, eps=
 
 
 # (1, 5632, 2048) and (1, 6144, 32): one token row over rows longer than 2048, the
-# 8-wavefront split of K (the batch-1 contraction of the 1B model)
+# 8-wavefront split of K (the batch-1 contraction of the 1B model); (16, 2048, 6144) and
+# (16, 2048, 8192): the 1B qkv and lm_head at batch 16
 SHAPES = [(1, 2048, 6144), (1, 64, 16), (3, 2048, 5632), (4, 5632, 2048), (5, 320, 48),
           (16, 2048, 2048), (16, 5632, 2048), (11, 6144, 32), (1, 2048, 8192),
-          (1, 5632, 2048), (1, 6144, 32)]
+          (1, 5632, 2048), (1, 6144, 32), (16, 2048, 6144), (16, 2048, 8192)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
