@@ -187,6 +187,25 @@ int rk_unpack(const uint8_t* packed, int64_t n, int max_code, int8_t* code,
               int8_t* pressure, void* stream);
 
 /*
+ * BF16 grad_input against the packed state:
+ *   out[m, k] = bf16( sum_n G[m, n] * E[n, k] ),  E[n, k] = bf16( bf16(code[n, k]) * bf16(scale[n]) )
+ *   G bf16 [M, N] (row stride ldg), packed [N, K] uint8 (row stride ldp), scale [N] fp32,
+ *   out [M, K] (row stride ldo) bf16, or fp32 holding the bf16 value (out_dtype RK_F32).
+ * float32 accumulation. E is decoded once into `work` (rk_grad_input_bf16_workspace(N, K)
+ * bytes, 16-byte aligned, contents overwritten) in MFMA operand order, then read by the
+ * GEMM. Requires N a positive multiple of 8, K % 8 == 0 and 16-byte aligned rows
+ * (RK_ERR_UNSUPPORTED otherwise).
+ * Replaces: effective = code.to(bf16) * scale.to(bf16)[:, None]; grad_input =
+ *           gradient_bf16 @ effective  ratchet.py:136-141 (the lm_head's backward, and every
+ *           layer's with int8_backward off).
+ */
+int64_t rk_grad_input_bf16_workspace(int64_t N, int64_t K);
+int rk_grad_input_bf16(const uint16_t* g, int64_t ldg, const uint8_t* packed, int64_t ldp,
+                       int max_code, const float* scale, void* out, int out_dtype, int64_t ldo,
+                       int64_t M, int64_t N, int64_t K, void* work, int64_t work_bytes,
+                       void* stream);
+
+/*
  * Effective BF16 weight: W[n, k] = bf16(code[n,k]) * bf16(scale[n]) rounded to bf16.
  * Replaces: effective = code.to(bf16) * scale.to(bf16)[:, None]  ratchet.py:140, 61.
  */

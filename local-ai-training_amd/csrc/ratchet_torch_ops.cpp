@@ -334,6 +334,37 @@ Tensor effective_bf16(const Tensor& packed, int64_t max_code, const Tensor& scal
   return out;
 }
 
+// The bf16 grad_input against the packed state (rk_grad_input_bf16): out =
+// bf16(g @ (bf16(code) * bf16(scale)[:, None])), the effective weight decoded into a
+// workspace from torch's allocator in the GEMM's operand order.
+Tensor grad_input_bf16(const Tensor& g_in, const Tensor& packed, int64_t max_code,
+                       const Tensor& scale, at::ScalarType out_dtype) {
+  require_gpu(g_in, "bf16 grad_input");
+  packed_matrix(packed);
+  same_device(g_in, packed, "bf16 grad_input");
+  TORCH_CHECK(g_in.scalar_type() == at::kBFloat16 && g_in.dim() == 2,
+              "bf16 grad_input: the gradient must be a bfloat16 matrix");
+  TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16,
+              "bf16 grad_input: output dtype must be float32 or bfloat16");
+  const Tensor g = unit_columns(g_in);
+  const int64_t m = g.size(0), n = g.size(1), k = packed.size(1);
+  TORCH_CHECK(packed.size(0) == n, "bf16 grad_input: the gradient has ", n,
+              " columns, the packed state ", packed.size(0), " rows");
+  const Tensor s = f32_vector(scale, n, "row scale");
+  const c10::DeviceGuard guard(g.device());
+  Tensor out = at::empty({m, k}, g.options().dtype(out_dtype));
+  if (m == 0 || k == 0) return out;
+  const int64_t work_bytes = rk_grad_input_bf16_workspace(n, k);
+  const Tensor work = at::empty({work_bytes > 0 ? work_bytes : 1}, g.options().dtype(at::kByte));
+  check_status(rk_grad_input_bf16(static_cast<const uint16_t*>(g.data_ptr()), ld(g),
+                                  packed.data_ptr<uint8_t>(), ld(packed),
+                                  static_cast<int>(max_code), s.data_ptr<float>(),
+                                  out.data_ptr(), dtype_code(out_dtype), k, m, n, k,
+                                  work.data_ptr(), work_bytes, stream_of(g)),
+               "rk_grad_input_bf16");
+  return out;
+}
+
 Tensor dequant_bf16(const Tensor& q_in, const Tensor& s_in) {
   require_gpu(q_in, "dequant_bf16");
   int8_matrix(q_in, "q");
@@ -1012,6 +1043,9 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("unpack_transpose(Tensor packed, int max_code) -> Tensor");
   m.def("unpack(Tensor packed, int max_code) -> (Tensor, Tensor)");
   m.def("effective_bf16(Tensor packed, int max_code, Tensor scale) -> Tensor");
+  m.def(
+      "grad_input_bf16(Tensor g, Tensor packed, int max_code, Tensor scale, "
+      "ScalarType out_dtype=bfloat16) -> Tensor");
   m.def("dequant_bf16(Tensor q, Tensor s) -> Tensor");
   m.def("transpose_bf16(Tensor x) -> Tensor");
   m.def("dequant_transpose_bf16(Tensor q, Tensor s) -> Tensor");
@@ -1066,6 +1100,7 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("packed_mm_t", &packed_mm_t);
   m.impl("unpack_transpose", &unpack_transpose);
   m.impl("unpack", &unpack);
+  m.impl("grad_input_bf16", &grad_input_bf16);
   m.impl("effective_bf16", &effective_bf16);
   m.impl("dequant_bf16", &dequant_bf16);
   m.impl("transpose_bf16", &transpose_bf16);

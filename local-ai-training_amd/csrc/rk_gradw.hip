@@ -23,15 +23,13 @@
 #include <mutex>
 
 #include "rk_common.h"
+#include "rk_tr16.h"
 #include "rk_update_row.h"
 
 namespace rk {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef short v4s __attribute__((ext_vector_type(4)));
 typedef unsigned int gw_u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
 
 // Forms of the activation operand X.
 enum { GW_X_Q8 = 0, GW_X_BF16 = 1, GW_X_F32 = 2 };
@@ -127,22 +125,6 @@ struct GwSlot {
   gw_u32x4 x[XV];
   float s[XV];
 };
-
-// Fragment of 8 consecutive tokens for feature column `col0 + lane % 16` (+16 for the
-// upper half of each 32-lane half) from a staged [token][feature] tile.
-template <int PITCH>
-__device__ __forceinline__ v8bf gw_fragment(const uint8_t* tile, int tok0, int col0, int lane) {
-  const int grp = lane >> 4, sl = lane & 15;
-  const int row = tok0 + 8 * (grp >> 1) + (sl >> 2);
-  const int col = col0 + 16 * (grp & 1) + 4 * (sl & 3);
-  const uint8_t* p = tile + row * PITCH + col * 2;
-  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(p));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s_ptr)(p + 4 * PITCH));
-  const v4s both[2] = {lo, hi};
-  v8bf f;
-  __builtin_memcpy(&f, both, sizeof(f));
-  return f;
-}
 
 // mean[0] = mean of row_rms[0 .. rows) by threads 0..255 of the block: each a strided
 // partial sum in row order, then a fixed LDS tree (the order of row_rms_mean_kernel).
@@ -336,9 +318,9 @@ void grad_weight_partial_kernel(GwArgs a) {
         for (int u = 0; u < BM / 16; ++u) {
           v8bf fa[MI], fb[NJ];
 #pragma unroll
-          for (int i = 0; i < MI; ++i) fa[i] = gw_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
+          for (int i = 0; i < MI; ++i) fa[i] = tr16_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) fb[j] = gw_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
+          for (int j = 0; j < NJ; ++j) fb[j] = tr16_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
 #pragma unroll
           for (int i = 0; i < MI; ++i)
 #pragma unroll

@@ -47,6 +47,9 @@ SIGNATURES: dict[str, list] = {
     "rk_unpack_transpose": [_p, _i64, _i32, _p, _i64, _i64, _i64, _p],
     "rk_unpack": [_p, _i64, _i32, _p, _p, _p],
     "rk_effective_bf16": [_p, _i64, _i32, _p, _p, _i64, _i64, _i64, _p],
+    "rk_grad_input_bf16": [_p, _i64, _p, _i64, _i32, _p, _p, _i32, _i64, _i64, _i64, _i64, _p,
+                           _i64, _p],
+    "rk_grad_input_bf16_workspace": [_i64, _i64],
     "rk_dequant_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "rk_transpose_bf16": [_p, _i32, _i64, _p, _i64, _i64, _i64, _p],
     "rk_dequant_transpose_bf16": [_p, _i64, _p, _p, _i64, _i64, _i64, _p],
@@ -115,6 +118,7 @@ RESTYPES = {
     "rk_decode_attention_splits": ctypes.c_int64,
     "rk_grad_weight_update_counters": ctypes.c_int64,
     "rk_embedding_backward_workspace": ctypes.c_int64,
+    "rk_grad_input_bf16_workspace": ctypes.c_int64,
 }
 
 _lib: ctypes.CDLL | None = None

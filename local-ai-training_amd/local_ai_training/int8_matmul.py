@@ -300,6 +300,23 @@ def effective_bf16(packed: Tensor, max_code: int, scale: Tensor) -> Tensor:
     return _ops().effective_bf16(packed, max_code, scale.float())
 
 
+def grad_input_bf16_supported(g: Tensor, packed: Tensor) -> bool:
+    """Whether grad_input_bf16 takes these operands: a bf16 gradient [M, N] with unit column
+    stride, N a positive multiple of 8, K % 8 == 0, 16-byte aligned rows."""
+    n, k = packed.shape
+    return (g.dtype == torch.bfloat16 and g.dim() == 2 and g.shape[1] == n and n > 0
+            and n % 8 == 0 and k % 8 == 0 and g.stride(-1) == 1 and _ld(g) % 8 == 0
+            and g.data_ptr() % 16 == 0 and packed.stride(-1) == 1 and _ld(packed) % 16 == 0
+            and packed.data_ptr() % 16 == 0)
+
+
+def grad_input_bf16(g: Tensor, packed: Tensor, max_code: int, scale: Tensor,
+                    out_dtype: torch.dtype = torch.bfloat16) -> Tensor:
+    """bf16(g @ (bf16(code) * bf16(scale)[:, None])): the bf16 grad_input of ratchet.py:136-141,
+    the effective weight decoded once into a workspace in the GEMM's operand order."""
+    return _ops().grad_input_bf16(g, packed, max_code, scale.float(), out_dtype)
+
+
 def dequant_bf16(q: Tensor, s: Tensor) -> Tensor:
     """bf16(q) * bf16(s)[:, None] rounded to bf16, as ratchet.py:73-75 computes it."""
     return _ops().dequant_bf16(q, s)

@@ -90,6 +90,10 @@ def _register_fakes() -> None:
     def _effective_bf16(packed, max_code, scale):
         return rows(packed, torch.bfloat16)
 
+    @fake("ratchet::grad_input_bf16")
+    def _grad_input_bf16(g, packed, max_code, scale, out_dtype=torch.bfloat16):
+        return g.new_empty((g.shape[0], packed.shape[1]), dtype=out_dtype)
+
     @fake("ratchet::dequant_bf16")
     def _dequant_bf16(q, s):
         return rows(q, torch.bfloat16)
@@ -187,7 +191,8 @@ def _register_fakes() -> None:
 # every operator the library defines (the opcheck tests walk this list)
 OPERATORS = (
     "quantize_rows", "int8_mm_nt", "packed_mm", "packed_mm_residual", "packed_mm_accumulate",
-    "packed_mm_t", "unpack_transpose", "unpack", "effective_bf16", "dequant_bf16",
+    "packed_mm_t", "unpack_transpose", "unpack", "effective_bf16", "grad_input_bf16",
+    "dequant_bf16",
     "transpose_bf16", "dequant_transpose_bf16", "grad_weight_splits", "grad_weight",
     "grad_weight_x", "grad_weight_partials", "grad_weight_partials_x", "update_from_z",
     "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",

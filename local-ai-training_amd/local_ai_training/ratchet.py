@@ -36,6 +36,8 @@ from .int8_matmul import (
     dequant_bf16,
     dequant_transpose_bf16,
     effective_bf16,
+    grad_input_bf16,
+    grad_input_bf16_supported,
     grad_weight_bf16,
     grad_weight_bf16_parts,
     grad_weight_bf16_x,
@@ -329,8 +331,8 @@ class _RatchetMatmul(torch.autograd.Function):
                 if inputs_bf16 is None:
                     inputs_bf16 = flat_inputs.to(torch.bfloat16)
                 gradient_bf16 = flat_gradient.to(torch.bfloat16)
-                effective = effective_bf16(packed, layer.max_code, scale_d)
-                grad_input = gradient_bf16 @ effective
+                grad_input = _bf16_grad_input(gradient_bf16, packed, layer.max_code, scale_d,
+                                              ctx.input_dtype)
                 grad_weight_fp32 = (gradient_bf16.t() @ inputs_bf16).float()
             layer._capture_weight_gradient(grad_weight_fp32)
             grad_scale = None
@@ -416,7 +418,8 @@ class _RatchetMatmul(torch.autograd.Function):
                 grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
         else:
             gradient_bf16 = flat_gradient.to(torch.bfloat16)
-            grad_input = gradient_bf16 @ effective_bf16(packed, layer.max_code, scale_d)
+            grad_input = _bf16_grad_input(gradient_bf16, packed, layer.max_code, scale_d,
+                                          ctx.input_dtype)
 
         if mode == "fp32":
             grad_weight = gradient_fp32.t() @ inputs_fp32
@@ -494,6 +497,18 @@ class _RatchetMatmul(torch.autograd.Function):
                                          from_partials=True)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
             grad_scale, None, None, None, None, None
+
+
+def _bf16_grad_input(gradient_bf16: Tensor, packed: Tensor, max_code: int, scale: Tensor,
+                     input_dtype: torch.dtype) -> Tensor:
+    """gradient_bf16 @ (code.bf16 * scale.bf16[:, None]) (ratchet.py:136-141): one HIP kernel
+    that forms the effective weight while staging, written in the input's dtype when that is
+    float32 (the bf16 result widened: the cast the caller makes); torch's GEMM on the
+    materialized effective weight for shapes the kernel does not take."""
+    if gradient_bf16.is_cuda and grad_input_bf16_supported(gradient_bf16, packed):
+        out_dtype = torch.float32 if input_dtype == torch.float32 else torch.bfloat16
+        return grad_input_bf16(gradient_bf16, packed, max_code, scale, out_dtype)
+    return gradient_bf16 @ effective_bf16(packed, max_code, scale)
 
 
 def _gradient_parts(ctx, layer, grads) -> list[Tensor] | None:

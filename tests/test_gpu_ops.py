@@ -81,6 +81,7 @@ def cases(t, cuda):
         (R.unpack_transpose, (t["packed"], MC), {}),
         (R.unpack, (t["packed"], MC), {}),
         (R.effective_bf16, (t["packed"], MC, t["scale"]), {}),
+        (R.grad_input_bf16, (t["g"], t["packed"], MC, t["scale"], torch.float32), {}),
         (R.dequant_bf16, (t["q"], t["s"]), {}),
         (R.transpose_bf16, (t["x"],), {}),
         (R.dequant_transpose_bf16, (t["q"], t["s"]), {}),
@@ -129,7 +130,7 @@ def cases(t, cuda):
     ]
 
 
-N_CASES = 47
+N_CASES = 48
 
 
 def test_every_operator_has_an_opcheck_case(t, cuda):
