@@ -117,19 +117,14 @@ def synthetic_layer(device):
 def op_bench(args, device):
     import torch
 
-    from local_ai_training.int8_matmul import CapturedSeeds, quantize_rows, quantize_rows_dq
+    from local_ai_training.int8_matmul import CapturedSeeds, quantize_rows
 
     layer, x, g = synthetic_layer(device)
     x.requires_grad_(True)
 
     def step():
-        # the activation quant also writes the dequantized rows the backward's grad_weight
-        # reads (as the model's prologues do), unless the layer is set not to use them
-        if layer.save_dequantized_inputs:
-            q, s, xd = quantize_rows_dq(x.detach())
-        else:
-            (q, s), xd = quantize_rows(x.detach()), None
-        out = layer(x, inputs_int8=q, inputs_scale=s, inputs_dq=xd)
+        q, s = quantize_rows(x.detach())
+        out = layer(x, inputs_int8=q, inputs_scale=s)
         out.backward(g)
         x.grad = None
         layer.ratchet_update(validate=False)

@@ -452,32 +452,6 @@ int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int6
                           int8_t* q, int64_t ldq, float* scale, void* stream);
 
 /*
- * The activation quantizations above (and rk_quantize_rows' round-to-nearest form, without a
- * column scale) that also write the dequantized activations
- *   x_dq[m, k] = bf16(bf16(q[m, k]) * bf16(scale[m]))
- * in the same pass: the bf16 operand the backward's grad_weight reads (rk_grad_weight_bf16_x
- * with RK_BF16), which then needs no int8 -> bf16 conversion per output tile. x_dq is NULL
- * (no output) or a 16-byte aligned bf16 [M, K] matrix whose row stride ld_dq >= K is a
- * multiple of 8. Same q and scale as the functions without the suffix.
- * Replaces: the dequantized copy of the saved activations, inputs_int8.to(bf16) *
- *           inputs_scale.to(bf16)  ratchet.py:71-76 (made once in the forward instead of by
- *           every output tile of grad_weight).
- */
-int rk_quantize_rows_dq(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
-                        int64_t sxk, int8_t* q, int64_t ldq, float* scale, uint16_t* x_dq,
-                        int64_t ld_dq, void* stream);
-int rk_rmsnorm_quantize_dq(const void* x, int x_dtype, int64_t ldx, const float* w, float eps,
-                           int8_t* q, int64_t ldq, float* scale, int64_t M, int64_t K,
-                           uint16_t* x_dq, int64_t ld_dq, void* stream);
-int rk_gelu_quantize_dq(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
-                        float* scale, int64_t M, int64_t K, uint16_t* x_dq, int64_t ld_dq,
-                        void* stream);
-int rk_transpose_quantize_dq(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
-                             int64_t D, int64_t sb, int64_t sh, int64_t ss, int64_t sd,
-                             int8_t* q, int64_t ldq, float* scale, uint16_t* x_dq,
-                             int64_t ld_dq, void* stream);
-
-/*
  * Backward of the RMSNorm prologue, per row of x [M, K] and grad_y [M, K]:
  *   rsqrt = 1 / sqrt(sum(x^2) / K + eps);  dvar = sum(grad_y * w * x) * -0.5 * rsqrt^3
  *   grad_x = bf16(grad_y * w * rsqrt + dvar * 2 * x / K)   (stored in x_dtype)

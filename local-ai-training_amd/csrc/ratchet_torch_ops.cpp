@@ -98,24 +98,10 @@ void packed_matrix(const Tensor& t) {
 // ---------------------------------------------------------------------------------------
 // Row quantization (int8_matmul.py:106-150, 181-207, 251-277)
 // ---------------------------------------------------------------------------------------
-// The optional dequantized output of the activation quantizations: a bfloat16 [M, K]
-// row-major matrix on the input's device (16-byte aligned rows, checked by the library).
-std::pair<uint16_t*, int64_t> dq_out(const OptTensor& x_dq, int64_t m, int64_t k,
-                                     const Tensor& x) {
-  if (!x_dq.has_value()) return {nullptr, 0};
-  TORCH_CHECK(x_dq->scalar_type() == at::kBFloat16 && x_dq->dim() == 2 && x_dq->size(0) == m &&
-                  x_dq->size(1) == k && (x_dq->stride(1) == 1 || k <= 1) &&
-                  x_dq->device() == x.device(),
-              "x_dq must be a bfloat16 [M, K] matrix with unit column stride on the input's "
-              "device");
-  return {static_cast<uint16_t*>(x_dq->data_ptr()), ld(*x_dq)};
-}
-
 std::tuple<Tensor, Tensor> quantize_rows(const Tensor& x, const OptTensor& col_scale,
                                          bool stochastic, int64_t seed,
                                          const OptTensor& seed_slot, int64_t row_offset,
-                                         const OptTensor& x_bf16, bool round_bf16,
-                                         const OptTensor& x_dq) {
+                                         const OptTensor& x_bf16, bool round_bf16) {
   require_gpu(x, "row quantization");
   TORCH_CHECK(x.dim() == 2, "row quantization requires a 2D tensor");
   int code = dtype_code(x, "row quantization input");
@@ -136,19 +122,7 @@ std::tuple<Tensor, Tensor> quantize_rows(const Tensor& x, const OptTensor& col_s
     xb = static_cast<uint16_t*>(x_bf16->data_ptr());
     ld_xb = ld(*x_bf16);
   }
-  const auto dq = dq_out(x_dq, m, k, x);
-  if (dq.first) {
-    TORCH_CHECK(!stochastic && !col_scale.has_value() && !x_bf16.has_value() && !round_bf16,
-                "x_dq applies to the plain round-to-nearest quantization");
-  }
   if (m == 0 || k == 0) return {q, scale};
-  if (dq.first) {
-    check_status(rk_quantize_rows_dq(x.data_ptr(), code, m, k, x.stride(0), x.stride(1),
-                                     q.data_ptr<int8_t>(), k, scale.data_ptr<float>(), dq.first,
-                                     dq.second, stream_of(x)),
-                 "rk_quantize_rows_dq");
-    return {q, scale};
-  }
   if (seed_slot.has_value()) {
     TORCH_CHECK(stochastic, "a device seed applies to stochastic rounding only");
     TORCH_CHECK(seed_slot->scalar_type() == at::kLong && seed_slot->numel() == 1 &&
@@ -767,8 +741,7 @@ Tensor float_rows(const Tensor& x) {
   return unit_columns(f);
 }
 
-std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_in, double eps,
-                                            const OptTensor& x_dq) {
+std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_in, double eps) {
   require_gpu(x_in, "fused RMSNorm quantization");
   const Tensor x = float_rows(x_in);
   const int64_t m = x.size(0), k = x.size(1);
@@ -776,33 +749,30 @@ std::tuple<Tensor, Tensor> rmsnorm_quantize(const Tensor& x_in, const Tensor& w_
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({m, k}, x.options().dtype(at::kChar));
   Tensor s = at::empty({m}, x.options().dtype(at::kFloat));
-  const auto dq = dq_out(x_dq, m, k, x);
   if (m == 0 || k == 0) return {q, s};
-  check_status(rk_rmsnorm_quantize_dq(x.data_ptr(), dtype_code(x, "RMSNorm input"), ld(x),
-                                      w.data_ptr<float>(), static_cast<float>(eps),
-                                      q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k,
-                                      dq.first, dq.second, stream_of(x)),
+  check_status(rk_rmsnorm_quantize(x.data_ptr(), dtype_code(x, "RMSNorm input"), ld(x),
+                                   w.data_ptr<float>(), static_cast<float>(eps),
+                                   q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k,
+                                   stream_of(x)),
                "rk_rmsnorm_quantize");
   return {q, s};
 }
 
-std::tuple<Tensor, Tensor> gelu_quantize(const Tensor& x_in, const OptTensor& x_dq) {
+std::tuple<Tensor, Tensor> gelu_quantize(const Tensor& x_in) {
   require_gpu(x_in, "fused GELU quantization");
   const Tensor x = float_rows(x_in);
   const int64_t m = x.size(0), k = x.size(1);
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({m, k}, x.options().dtype(at::kChar));
   Tensor s = at::empty({m}, x.options().dtype(at::kFloat));
-  const auto dq = dq_out(x_dq, m, k, x);
   if (m == 0 || k == 0) return {q, s};
-  check_status(rk_gelu_quantize_dq(x.data_ptr(), dtype_code(x, "GELU input"), ld(x),
-                                   q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k, dq.first,
-                                   dq.second, stream_of(x)),
+  check_status(rk_gelu_quantize(x.data_ptr(), dtype_code(x, "GELU input"), ld(x),
+                                q.data_ptr<int8_t>(), k, s.data_ptr<float>(), m, k, stream_of(x)),
                "rk_gelu_quantize");
   return {q, s};
 }
 
-std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in, const OptTensor& x_dq) {
+std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in) {
   require_gpu(x_in, "fused transpose quantization");
   TORCH_CHECK(x_in.dim() == 4, "transpose quantization takes [B, H, S, D]");
   const Tensor x = (x_in.scalar_type() == at::kFloat || x_in.scalar_type() == at::kBFloat16)
@@ -812,12 +782,11 @@ std::tuple<Tensor, Tensor> transpose_quantize(const Tensor& x_in, const OptTenso
   const c10::DeviceGuard guard(x.device());
   Tensor q = at::empty({b * s, h * d}, x.options().dtype(at::kChar));
   Tensor scale = at::empty({b * s}, x.options().dtype(at::kFloat));
-  const auto dq = dq_out(x_dq, b * s, h * d, x);
   if (b * s == 0 || h * d == 0) return {q, scale};
-  check_status(rk_transpose_quantize_dq(x.data_ptr(), dtype_code(x, "attention output"), b, h, s,
-                                        d, x.stride(0), x.stride(1), x.stride(2), x.stride(3),
-                                        q.data_ptr<int8_t>(), h * d, scale.data_ptr<float>(),
-                                        dq.first, dq.second, stream_of(x)),
+  check_status(rk_transpose_quantize(x.data_ptr(), dtype_code(x, "attention output"), b, h, s, d,
+                                     x.stride(0), x.stride(1), x.stride(2), x.stride(3),
+                                     q.data_ptr<int8_t>(), h * d, scale.data_ptr<float>(),
+                                     stream_of(x)),
                "rk_transpose_quantize");
   return {q, scale};
 }
@@ -1024,7 +993,7 @@ TORCH_LIBRARY(ratchet, m) {
   m.def(
       "quantize_rows(Tensor x, Tensor? col_scale=None, bool stochastic=False, int seed=0, "
       "Tensor? seed_slot=None, int row_offset=0, Tensor(a!)? x_bf16=None, "
-      "bool round_bf16=False, Tensor(b!)? x_dq=None) -> (Tensor, Tensor)");
+      "bool round_bf16=False) -> (Tensor, Tensor)");
   m.def(
       "int8_mm_nt(Tensor a, Tensor b, Tensor a_scale, Tensor? b_scale, ScalarType out_dtype) "
       "-> Tensor");
@@ -1075,9 +1044,9 @@ TORCH_LIBRARY(ratchet, m) {
   m.def("normalize_rows(Tensor g, float eps, Tensor(a!)? rms_ema, float beta) -> Tensor");
   m.def("pressure_leak(Tensor(a!) packed, int max_code) -> ()");
   m.def("validate_state(Tensor packed, int max_code, Tensor? scale) -> Tensor");
-  m.def("rmsnorm_quantize(Tensor x, Tensor w, float eps, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
-  m.def("gelu_quantize(Tensor x, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
-  m.def("transpose_quantize(Tensor x, Tensor(a!)? x_dq=None) -> (Tensor, Tensor)");
+  m.def("rmsnorm_quantize(Tensor x, Tensor w, float eps) -> (Tensor, Tensor)");
+  m.def("gelu_quantize(Tensor x) -> (Tensor, Tensor)");
+  m.def("transpose_quantize(Tensor x) -> (Tensor, Tensor)");
   m.def(
       "rmsnorm_backward(Tensor grad_y, Tensor x, Tensor w, float eps, "
       "Tensor? residual_grad=None) -> (Tensor, Tensor)");

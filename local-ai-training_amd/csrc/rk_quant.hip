@@ -36,8 +36,6 @@ struct QuantArgs {
   float* scale;
   uint16_t* xb;               // plain only: bf16 side output, may be null
   int64_t ldxb;
-  uint16_t* xd;               // dequantized bf16(bf16(q) * bf16(s)) output, may be null
-  int64_t ldxd;
   int vec_ok;                 // 16-byte vector loads are legal for every chunk
   int round_bf16;             // plain float32 source: each value is taken as bf16(x) first
   // plain source split by columns over up to three [M, part_cols] tensors (row stride sxm,
@@ -125,8 +123,7 @@ template <int DT, bool SR, bool ALL>
 __device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, uint32_t ctr_row,
                                                   const PhiloxKey& key, int64_t e0,
                                                   const float* y, float s, float r,
-                                                  int8_t* qrow, bool vec_store,
-                                                  uint16_t* xdrow = nullptr) {
+                                                  int8_t* qrow, bool vec_store) {
   constexpr int V = Vec<DT>::N;
   float t[V], u[V];
   bool exact = false;
@@ -149,30 +146,6 @@ __device__ __forceinline__ void quant_store_chunk(const QuantArgs& a, uint32_t c
   int qi[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) qi[i] = static_cast<int>(fminf(fmaxf(t[i], -127.0f), 127.0f));
-  if (xdrow) {
-    // the activations as the backward's bf16 grad_weight consumes them (ratchet.py:73-75):
-    // q is exact in bf16, so this is one float32 product with the bf16-rounded scale,
-    // rounded to bf16 (the product of two bf16 values is exact in float32)
-    const float sm = round_bf16(s);
-    uint16_t h[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) h[i] = f32_to_bf16(static_cast<float>(qi[i]) * sm);
-    if (vec_store && (ALL || e0 + V <= a.K)) {
-      uint32_t w[V / 2];
-#pragma unroll
-      for (int j = 0; j < V / 2; ++j)
-        w[j] = static_cast<uint32_t>(h[2 * j]) | (static_cast<uint32_t>(h[2 * j + 1]) << 16);
-      if constexpr (V == 8) {
-        *reinterpret_cast<uint4*>(xdrow + e0) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        *reinterpret_cast<uint2*>(xdrow + e0) = make_uint2(w[0], w[1]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; ++i)
-        if (e0 + i < a.K) xdrow[e0 + i] = h[i];
-    }
-  }
   if (vec_store && (ALL || e0 + V <= a.K)) {
     uint32_t w[V / 4];
 #pragma unroll
@@ -232,7 +205,6 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
   int8_t* qrow = a.q + row * a.ldq;
   const bool vec_store = (a.ldq % V) == 0 && ((reinterpret_cast<uintptr_t>(a.q) % V) == 0);
   uint16_t* xbrow = (SRC == SRC_PLAIN && a.xb) ? a.xb + row * a.ldxb : nullptr;
-  uint16_t* xdrow = a.xd ? a.xd + row * a.ldxd : nullptr;
   PhiloxKey key{};
   if constexpr (SR) {
     uint32_t k0 = a.key0, k1 = a.key1;
@@ -288,8 +260,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     for (int c = 0; c < NC; ++c) {
       const int64_t e0 = c * SPAN + lane0;
       if (c < nchunks && e0 < a.K)
-        quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, xr[c], s, r, qrow, vec_store,
-                                       xdrow);
+        quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, xr[c], s, r, qrow, vec_store);
     }
   } else {
     // Streaming row: re-read per pass (the row stays cache-resident).
@@ -326,7 +297,7 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
       load_chunk<DT, SRC, VEC>(a, row, e0, v);
       if (xbrow) store_bf16_chunk<DT>(xbrow, e0, a.K, v);
       transform_chunk<DT, SRC, VEC>(a, e0, v, row_factor);
-      quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, v, s, r, qrow, vec_store, xdrow);
+      quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, v, s, r, qrow, vec_store);
     }
   }
 }
@@ -397,12 +368,6 @@ static int check_common(const void* x, int dt, int64_t M, int64_t K, const int8_
 
 // The dequantized output of the activation quantizations: NULL, or a 16-byte aligned
 // bf16 matrix with a row stride that is a multiple of 8 elements and at least K.
-static int check_dq(const uint16_t* x_dq, int64_t ld_dq, int64_t K) {
-  if (!x_dq) return RK_OK;
-  if (ld_dq < K || ld_dq % 8 != 0 || !aligned16(x_dq))
-    return fail(RK_ERR_ARG, "x_dq needs a 16-byte aligned base and a row stride >= K, a multiple of 8");
-  return RK_OK;
-}
 
 }  // namespace rk
 
@@ -438,28 +403,6 @@ static int quantize_rows_entry(const void* x, int x_dtype, int64_t M, int64_t K,
   a.ldxb = ld_xb;
   a.vec_ok = (rows_vec_ok(x, x_dtype, K, sxm, sxk) && (!col_scale || aligned16(col_scale))) ? 1 : 0;
   if (stochastic) return dispatch_dtype<SRC_PLAIN, true>(x_dtype, a, as_stream(stream));
-  return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
-}
-
-extern "C" int rk_quantize_rows_dq(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
-                                   int64_t sxk, int8_t* q, int64_t ldq, float* scale,
-                                   uint16_t* x_dq, int64_t ld_dq, void* stream) {
-  clear_error();
-  if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
-  if (int st = check_dq(x_dq, ld_dq, K)) return st;
-  if (M == 0) return RK_OK;
-  QuantArgs a{};
-  a.x = x;
-  a.M = M;
-  a.K = K;
-  a.sxm = sxm;
-  a.sxk = sxk;
-  a.q = q;
-  a.ldq = ldq;
-  a.scale = scale;
-  a.xd = x_dq;
-  a.ldxd = ld_dq;
-  a.vec_ok = rows_vec_ok(x, x_dtype, K, sxm, sxk) ? 1 : 0;
   return dispatch_dtype<SRC_PLAIN, false>(x_dtype, a, as_stream(stream));
 }
 
@@ -530,10 +473,9 @@ extern "C" int rk_quantize_rows_devseed(const void* x, int x_dtype, int64_t M, i
 
 static int rmsnorm_quantize_entry(const void* x, int x_dtype, int64_t ldx, const float* w,
                                   float eps, int8_t* q, int64_t ldq, float* scale, int64_t M,
-                                  int64_t K, uint16_t* x_dq, int64_t ld_dq, void* stream) {
+                                  int64_t K, void* stream) {
   clear_error();
   if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
-  if (int st = check_dq(x_dq, ld_dq, K)) return st;
   if (M > 0 && !w) return fail(RK_ERR_ARG, "null RMSNorm weight");
   if (M == 0) return RK_OK;
   QuantArgs a{};
@@ -547,8 +489,6 @@ static int rmsnorm_quantize_entry(const void* x, int x_dtype, int64_t ldx, const
   a.q = q;
   a.ldq = ldq;
   a.scale = scale;
-  a.xd = x_dq;
-  a.ldxd = ld_dq;
   a.vec_ok = rows_vec_ok(x, x_dtype, K, ldx, 1) ? 1 : 0;
   return dispatch_dtype<SRC_RMSNORM, false>(x_dtype, a, as_stream(stream));
 }
@@ -556,23 +496,13 @@ static int rmsnorm_quantize_entry(const void* x, int x_dtype, int64_t ldx, const
 extern "C" int rk_rmsnorm_quantize(const void* x, int x_dtype, int64_t ldx, const float* w,
                                    float eps, int8_t* q, int64_t ldq, float* scale, int64_t M,
                                    int64_t K, void* stream) {
-  return rmsnorm_quantize_entry(x, x_dtype, ldx, w, eps, q, ldq, scale, M, K, nullptr, 0,
-                                stream);
-}
-
-extern "C" int rk_rmsnorm_quantize_dq(const void* x, int x_dtype, int64_t ldx, const float* w,
-                                      float eps, int8_t* q, int64_t ldq, float* scale, int64_t M,
-                                      int64_t K, uint16_t* x_dq, int64_t ld_dq, void* stream) {
-  return rmsnorm_quantize_entry(x, x_dtype, ldx, w, eps, q, ldq, scale, M, K, x_dq, ld_dq,
-                                stream);
+  return rmsnorm_quantize_entry(x, x_dtype, ldx, w, eps, q, ldq, scale, M, K, stream);
 }
 
 static int gelu_quantize_entry(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
-                               float* scale, int64_t M, int64_t K, uint16_t* x_dq,
-                               int64_t ld_dq, void* stream) {
+                               float* scale, int64_t M, int64_t K, void* stream) {
   clear_error();
   if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
-  if (int st = check_dq(x_dq, ld_dq, K)) return st;
   if (M == 0) return RK_OK;
   QuantArgs a{};
   a.x = x;
@@ -583,32 +513,23 @@ static int gelu_quantize_entry(const void* x, int x_dtype, int64_t ldx, int8_t* 
   a.q = q;
   a.ldq = ldq;
   a.scale = scale;
-  a.xd = x_dq;
-  a.ldxd = ld_dq;
   a.vec_ok = rows_vec_ok(x, x_dtype, K, ldx, 1) ? 1 : 0;
   return dispatch_dtype<SRC_GELU, false>(x_dtype, a, as_stream(stream));
 }
 
 extern "C" int rk_gelu_quantize(const void* x, int x_dtype, int64_t ldx, int8_t* q,
                                 int64_t ldq, float* scale, int64_t M, int64_t K, void* stream) {
-  return gelu_quantize_entry(x, x_dtype, ldx, q, ldq, scale, M, K, nullptr, 0, stream);
-}
-
-extern "C" int rk_gelu_quantize_dq(const void* x, int x_dtype, int64_t ldx, int8_t* q,
-                                   int64_t ldq, float* scale, int64_t M, int64_t K,
-                                   uint16_t* x_dq, int64_t ld_dq, void* stream) {
-  return gelu_quantize_entry(x, x_dtype, ldx, q, ldq, scale, M, K, x_dq, ld_dq, stream);
+  return gelu_quantize_entry(x, x_dtype, ldx, q, ldq, scale, M, K, stream);
 }
 
 static int transpose_quantize_entry(const void* x, int x_dtype, int64_t B, int64_t H,
                                     int64_t S, int64_t D, int64_t sb, int64_t sh, int64_t ss,
                                     int64_t sd, int8_t* q, int64_t ldq, float* scale,
-                                    uint16_t* x_dq, int64_t ld_dq, void* stream) {
+                                    void* stream) {
   clear_error();
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return fail(RK_ERR_ARG, "invalid [B,H,S,D] shape");
   const int64_t M = B * S, K = H * D;
   if (int st = check_common(x, x_dtype, M, K, q, ldq, scale)) return st;
-  if (int st = check_dq(x_dq, ld_dq, K)) return st;
   if (M == 0) return RK_OK;
   QuantArgs a{};
   a.x = x;
@@ -624,8 +545,6 @@ static int transpose_quantize_entry(const void* x, int x_dtype, int64_t B, int64
   a.q = q;
   a.ldq = ldq;
   a.scale = scale;
-  a.xd = x_dq;
-  a.ldxd = ld_dq;
   const int V = 16 / dtype_size(x_dtype);
   a.vec_ok = (sd == 1 && aligned16(x) && D % V == 0 && sb % V == 0 && sh % V == 0 &&
               ss % V == 0)
@@ -638,17 +557,7 @@ extern "C" int rk_transpose_quantize(const void* x, int x_dtype, int64_t B, int6
                                      int64_t S, int64_t D, int64_t sb, int64_t sh, int64_t ss,
                                      int64_t sd, int8_t* q, int64_t ldq, float* scale,
                                      void* stream) {
-  return transpose_quantize_entry(x, x_dtype, B, H, S, D, sb, sh, ss, sd, q, ldq, scale, nullptr,
-                                  0, stream);
-}
-
-extern "C" int rk_transpose_quantize_dq(const void* x, int x_dtype, int64_t B, int64_t H,
-                                        int64_t S, int64_t D, int64_t sb, int64_t sh,
-                                        int64_t ss, int64_t sd, int8_t* q, int64_t ldq,
-                                        float* scale, uint16_t* x_dq, int64_t ld_dq,
-                                        void* stream) {
-  return transpose_quantize_entry(x, x_dtype, B, H, S, D, sb, sh, ss, sd, q, ldq, scale, x_dq,
-                                  ld_dq, stream);
+  return transpose_quantize_entry(x, x_dtype, B, H, S, D, sb, sh, ss, sd, q, ldq, scale, stream);
 }
 
 namespace rk {

@@ -73,12 +73,6 @@ SIGNATURES: dict[str, list] = {
     "rk_pressure_leak": [_p, _i64, _i32, _p],
     "rk_validate_state": [_p, _i64, _i32, _p, _i64, _p, _p],
     "rk_rmsnorm_quantize": [_p, _i32, _i64, _p, _f32, _p, _i64, _p, _i64, _i64, _p],
-    "rk_quantize_rows_dq": [_p, _i32, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p],
-    "rk_rmsnorm_quantize_dq": [_p, _i32, _i64, _p, _f32, _p, _i64, _p, _i64, _i64, _p, _i64,
-                               _p],
-    "rk_gelu_quantize_dq": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p],
-    "rk_transpose_quantize_dq": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
-                                 _i64, _p, _p, _i64, _p],
     "rk_gelu_quantize": [_p, _i32, _i64, _p, _i64, _p, _i64, _i64, _p],
     "rk_transpose_quantize": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,
                               _i64, _p, _p],

@@ -161,20 +161,6 @@ def quantize_rows(values: Tensor) -> tuple[Tensor, Tensor]:
     return _quantize_rows_fused(values)
 
 
-def quantize_rows_dq(values: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """quantize_rows, and the dequantized activations bf16(bf16(q) * bf16(s)) the backward's
-    grad_weight reads (ratchet.py:73-75), written by the same kernel."""
-    if not values.is_cuda:
-        raise RuntimeError("quantize_rows requires CUDA (a ROCm GPU); the int8 path is GPU-only")
-    if values.ndim != 2:
-        raise ValueError("row quantization requires a 2D tensor")
-    if values.dtype not in (torch.float32, torch.bfloat16):
-        values = values.float()
-    xd = torch.empty(values.shape, device=values.device, dtype=torch.bfloat16)
-    q, s = _ops().quantize_rows(values, x_dq=xd)
-    return q, s, xd
-
-
 def quantize_rows_colscaled(values: Tensor, col_scale: Tensor, *,
                             stochastic: bool = False) -> tuple[Tensor, Tensor]:
     """Row-quantize values * col_scale[None, :] in one pass (no M x N float temp)."""

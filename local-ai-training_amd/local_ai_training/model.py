@@ -101,13 +101,6 @@ def _is_int8(layer: nn.Module) -> bool:
     return getattr(layer, "matmul_mode", "fp32") == "int8"
 
 
-def _dequant(layer: nn.Module) -> bool:
-    """Whether the quantization ahead of this int8 ratchet layer also writes the
-    dequantized bf16 rows its backward's grad_weight reads (a training step only)."""
-    return (getattr(layer, "save_dequantized_inputs", False) and layer.training
-            and torch.is_grad_enabled())
-
-
 class KVCache:
     """Per-layer keys/values [B, H, max_len, D] for incremental decoding, plus the number of
     filled positions. ``pos`` is that number as a device tensor, so a decode step (which
@@ -249,10 +242,9 @@ class CausalSelfAttention(nn.Module):
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None, cache: KVCache | None = None,
                 layer: int = 0, decode: bool = False,
-                residual: Tensor | None = None, inputs_dq: Tensor | None = None) -> Tensor:
+                residual: Tensor | None = None) -> Tensor:
         """``residual``: return residual + attention output (int8 projection: added in the
-        GEMM epilogue). ``inputs_dq``: the dequantized copy of ``inputs_int8`` (for the qkv
-        layer's backward)."""
+        GEMM epilogue)."""
         batch_size, sequence_length, channels = inputs.shape
         if inputs_int8 is not None:
             # Under bf16 autocast the attention casts q, k, v to bf16 (and their gradients
@@ -261,7 +253,7 @@ class CausalSelfAttention(nn.Module):
             # its backward separately and are read there in place (no concatenation).
             kw = {"split": 3} if self.split_qkv_grad else {}
             qkv = self.qkv(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale,
-                           inputs_dq=inputs_dq, out_dtype=_autocast_bf16(inputs), **kw)
+                           out_dtype=_autocast_bf16(inputs), **kw)
         else:
             qkv = self.qkv(inputs)
         query, key, value = qkv if isinstance(qkv, tuple) else qkv.chunk(3, dim=-1)
@@ -276,10 +268,9 @@ class CausalSelfAttention(nn.Module):
         else:
             attended = _attend(q, k, v, dropout_p=dropout_p, is_causal=True)
         if _is_int8(self.projection):
-            attn_int8, attn_scale, dummy, attn_dq = FusedTransposeQuantizeFn.apply(
-                attended, _dequant(self.projection))
+            attn_int8, attn_scale, dummy = FusedTransposeQuantizeFn.apply(attended)
             return self.projection(dummy, inputs_int8=attn_int8, inputs_scale=attn_scale,
-                                   inputs_dq=attn_dq, residual=residual)
+                                   residual=residual)
         joined = attended.transpose(1, 2).contiguous().view(batch_size, sequence_length, channels)
         out = self.projection(joined)
         return out if residual is None else residual + out
@@ -329,28 +320,26 @@ class FeedForward(nn.Module):
 
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None,
-                residual: Tensor | None = None, inputs_dq: Tensor | None = None) -> Tensor:
+                residual: Tensor | None = None) -> Tensor:
         """``residual``: return residual + feed-forward output (int8 contraction without
-        active dropout: added in the GEMM epilogue). ``inputs_dq``: the dequantized copy of
-        ``inputs_int8`` (for the expansion's backward)."""
+        active dropout: added in the GEMM epilogue)."""
         int8_contract = _is_int8(self.contract)
         bf16_out = _autocast_bf16(inputs) if int8_contract and self.bf16_expand else None
         kw = {"out_dtype": bf16_out} if bf16_out is not None else {}
         if inputs_int8 is not None:
             expanded = self.expand(inputs, inputs_int8=inputs_int8, inputs_scale=inputs_scale,
-                                   inputs_dq=inputs_dq, **kw)
+                                   **kw)
         else:
             expanded = self.expand(inputs, **kw)
         no_dropout = self.dropout == 0.0 or not self.training
         if int8_contract:
-            gelu_int8, gelu_scale, dummy, gelu_dq = FusedGELUQuantizeFn.apply(
-                expanded, _dequant(self.contract))
+            gelu_int8, gelu_scale, dummy = FusedGELUQuantizeFn.apply(expanded)
             kw = {"out_dtype": inputs.dtype} if expanded.dtype != inputs.dtype else {}
             if no_dropout:
                 return self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale,
-                                     inputs_dq=gelu_dq, residual=residual, **kw)
+                                     residual=residual, **kw)
             contracted = self.contract(dummy, inputs_int8=gelu_int8, inputs_scale=gelu_scale,
-                                       inputs_dq=gelu_dq, **kw)
+                                       **kw)
         else:
             contracted = self.contract(F.gelu(expanded))
         out = F.dropout(contracted, p=self.dropout, training=self.training)
@@ -380,38 +369,34 @@ class TransformerBlock(nn.Module):
             if fuse_grad:
                 # the block input's two gradients (normalized path, residual stream) meet
                 # in the RMSNorm backward's store instead of a separate add
-                q, s, dummy, res, dq = FusedRMSNormQuantizeResidualFn.apply(
-                    inputs, self.attention_norm.weight, 1e-5, _dequant(self.attention.qkv))
-                inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, inputs_dq=dq,
-                                        residual=res, **kv)
+                q, s, dummy, res = FusedRMSNormQuantizeResidualFn.apply(
+                    inputs, self.attention_norm.weight, 1e-5)
+                inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, residual=res,
+                                        **kv)
             else:
-                q, s, dummy, dq = FusedRMSNormQuantizeFn.apply(
-                    inputs, self.attention_norm.weight, 1e-5, _dequant(self.attention.qkv))
+                q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.attention_norm.weight,
+                                                           1e-5)
                 if self.fuse_residual:
-                    inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s, inputs_dq=dq,
+                    inputs = self.attention(dummy, inputs_int8=q, inputs_scale=s,
                                             residual=inputs, **kv)
                 else:
                     inputs = inputs + self.attention(dummy, inputs_int8=q, inputs_scale=s,
-                                                     inputs_dq=dq, **kv)
+                                                     **kv)
         else:
             inputs = inputs + self.attention(self.attention_norm(inputs), **kv)
         if _is_int8(self.feed_forward.expand):
             if fuse_grad:
-                q, s, dummy, res, dq = FusedRMSNormQuantizeResidualFn.apply(
-                    inputs, self.feed_forward_norm.weight, 1e-5,
-                    _dequant(self.feed_forward.expand))
-                inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s, inputs_dq=dq,
-                                           residual=res)
+                q, s, dummy, res = FusedRMSNormQuantizeResidualFn.apply(
+                    inputs, self.feed_forward_norm.weight, 1e-5)
+                inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s, residual=res)
             else:
-                q, s, dummy, dq = FusedRMSNormQuantizeFn.apply(
-                    inputs, self.feed_forward_norm.weight, 1e-5,
-                    _dequant(self.feed_forward.expand))
+                q, s, dummy = FusedRMSNormQuantizeFn.apply(inputs, self.feed_forward_norm.weight,
+                                                           1e-5)
                 if self.fuse_residual:
                     inputs = self.feed_forward(dummy, inputs_int8=q, inputs_scale=s,
-                                               inputs_dq=dq, residual=inputs)
+                                               residual=inputs)
                 else:
-                    inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s,
-                                                        inputs_dq=dq)
+                    inputs = inputs + self.feed_forward(dummy, inputs_int8=q, inputs_scale=s)
         else:
             inputs = inputs + self.feed_forward(self.feed_forward_norm(inputs))
         return inputs

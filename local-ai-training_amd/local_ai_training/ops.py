@@ -54,7 +54,7 @@ def _register_fakes() -> None:
 
     @fake("ratchet::quantize_rows")
     def _quantize_rows(x, col_scale=None, stochastic=False, seed=0, seed_slot=None,
-                       row_offset=0, x_bf16=None, round_bf16=False, x_dq=None):
+                       row_offset=0, x_bf16=None, round_bf16=False):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::int8_mm_nt")
@@ -127,15 +127,15 @@ def _register_fakes() -> None:
         return packed.new_empty((3,), dtype=torch.int32)
 
     @fake("ratchet::rmsnorm_quantize")
-    def _rmsnorm_quantize(x, w, eps, x_dq=None):
+    def _rmsnorm_quantize(x, w, eps):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::gelu_quantize")
-    def _gelu_quantize(x, x_dq=None):
+    def _gelu_quantize(x):
         return rows(x, torch.int8), x.new_empty((x.shape[0],), dtype=torch.float32)
 
     @fake("ratchet::transpose_quantize")
-    def _transpose_quantize(x, x_dq=None):
+    def _transpose_quantize(x):
         b, h, s, d = x.shape
         return (x.new_empty((b * s, h * d), dtype=torch.int8),
                 x.new_empty((b * s,), dtype=torch.float32))

@@ -206,9 +206,8 @@ class _RatchetMatmul(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, inputs, inputs_int8, inputs_scale, packed, scale, layer, out_dtype=None,
-                residual=None, split=1, inputs_dq=None):
+                residual=None, split=1):
         ctx.split = split
-        ctx.x_dq = False
         input_shape = inputs.shape
         flat_inputs = inputs.flatten(0, -2)
         mode = layer.matmul_mode
@@ -227,16 +226,7 @@ class _RatchetMatmul(torch.autograd.Function):
             s = inputs_scale.flatten(0, -1).float()
             if q.stride(-1) != 1:
                 q = q.contiguous()
-            xd = None if inputs_dq is None else inputs_dq.flatten(0, -2)
-            if xd is not None and xd.shape == q.shape and xd.stride(-1) == 1 \
-                    and xd.dtype == torch.bfloat16:
-                # the dequantized activations bf16(bf16(q) * bf16(s)), written by the
-                # quantization: the backward reads them instead of q and s (grad_weight's
-                # operand without a conversion per output tile)
-                ctx.save_for_backward(xd, s, scale)
-                ctx.x_dq = True
-            else:
-                ctx.save_for_backward(q, s, scale)
+            ctx.save_for_backward(q, s, scale)
             ctx.used_fused_int8 = True
             output = None
         else:
@@ -295,11 +285,10 @@ class _RatchetMatmul(torch.autograd.Function):
         packed = layer.packed
         mode = layer.matmul_mode
         if ctx.used_fused_int8:
-            # q: the saved int8 activations, or their dequantized bf16 copy (ctx.x_dq)
-            q, s, scale = ctx.saved_tensors
+            q, s, scale = ctx.saved_tensors  # the saved int8 activations and their scales
             inputs_bf16 = None
             if not layer.fuse_backward_update:
-                inputs_bf16 = q if ctx.x_dq else dequant_bf16(q, s)
+                inputs_bf16 = dequant_bf16(q, s)
             inputs_fp32 = None
         else:
             flat_inputs, scale = ctx.saved_tensors
@@ -339,7 +328,7 @@ class _RatchetMatmul(torch.autograd.Function):
             if needs_scale:
                 grad_scale = (grad_weight_fp32 * layer.code.float()).sum(dim=1)
             return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-                grad_scale, None, None, grad_residual, None, None
+                grad_scale, None, None, grad_residual, None
 
         m, n = flat_gradient.shape
         gradient_bf16 = None
@@ -352,9 +341,6 @@ class _RatchetMatmul(torch.autograd.Function):
             if ctx.used_fused_int8:
                 if not _grad_weight_supported(g, q):
                     return None
-                if ctx.x_dq:
-                    return grad_weight_bf16_x(g, q, reduce=False,
-                                              work=layer._split_workspace(m, g.device))
                 return grad_weight_bf16(g, q, s, reduce=False,
                                         work=layer._split_workspace(m, g.device))
             x_direct = flat_inputs if flat_inputs.dtype in (torch.float32, torch.bfloat16) \
@@ -436,7 +422,7 @@ class _RatchetMatmul(torch.autograd.Function):
                 # NT GEMM on transposed bf16 copies (both operands contiguous along tokens)
                 grad_t = transpose_bf16(g)
                 if ctx.used_fused_int8:
-                    inputs_t = transpose_bf16(q) if ctx.x_dq else dequant_transpose_bf16(q, s)
+                    inputs_t = dequant_transpose_bf16(q, s)
                 else:
                     x_direct = flat_inputs if flat_inputs.dtype in (torch.float32,
                                                                     torch.bfloat16) \
@@ -452,7 +438,7 @@ class _RatchetMatmul(torch.autograd.Function):
         else:
             grad_scale = layer._fused_update(grad_weight, want_grad_scale=needs_scale)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-            grad_scale, None, None, grad_residual, None, None
+            grad_scale, None, None, grad_residual, None
 
     @staticmethod
     def _backward_parts(ctx, layer, parts: list[Tensor]):
@@ -473,7 +459,7 @@ class _RatchetMatmul(torch.autograd.Function):
             side = _side_stream(q.device)
             side.wait_stream(main)
             with torch.cuda.stream(side):
-                partials = grad_weight_bf16_parts(parts, q, None if ctx.x_dq else s,
+                partials = grad_weight_bf16_parts(parts, q, s,
                                                   work=layer._split_workspace(m, q.device))
             for t in (*parts, *ctx.saved_tensors):
                 t.record_stream(side)
@@ -488,7 +474,7 @@ class _RatchetMatmul(torch.autograd.Function):
             code_t = unpack_transpose(packed, layer.max_code)
             grad_input = int8_mm_nt(grad_q, code_t, grad_s, None, out_dtype)
         if partials is None:
-            partials = grad_weight_bf16_parts(parts, q, None if ctx.x_dq else s,
+            partials = grad_weight_bf16_parts(parts, q, s,
                                               work=layer._split_workspace(m, q.device))
         if side is not None:
             torch.cuda.current_stream(partials.device).wait_stream(side)
@@ -496,7 +482,7 @@ class _RatchetMatmul(torch.autograd.Function):
         grad_scale = layer._fused_update(partials, want_grad_scale=needs_scale,
                                          from_partials=True)
         return grad_input.reshape(ctx.input_shape).to(ctx.input_dtype), None, None, None, \
-            grad_scale, None, None, None, None, None
+            grad_scale, None, None, None, None
 
 
 def _bf16_grad_input(gradient_bf16: Tensor, packed: Tensor, max_code: int, scale: Tensor,
@@ -557,14 +543,6 @@ class DiscreteRatchetLinear(nn.Module):
     # fused backward under HIP-graph capture: grad_weight on a side stream, concurrent with
     # grad_input (False: one stream, e.g. to compare the two)
     overlap_weight_gradient: bool = True
-    # int8 inputs handed over with their dequantized bf16 copy (written by the same
-    # quantization kernel): the backward's grad_weight reads that copy instead of
-    # converting the int8 rows for every output tile (the same operand values). Off by
-    # default: the copy's extra forward write costs more than grad_weight gains (graph
-    # step 0.196-0.205 vs 0.195-0.199 ms at 16384 x 512 -> 2048, 25M 10.13 vs 9.91 ms,
-    # 1B 64.4 vs 63.8 ms on MI355X), although grad_weight alone drops from 7.65M to 2.14M
-    # VALU instructions at the op shape and overlaps the SR quant better (100 -> 90 us).
-    save_dequantized_inputs: bool = False
 
     def __init__(
         self,
@@ -747,21 +725,17 @@ class DiscreteRatchetLinear(nn.Module):
     # -- forward --------------------------------------------------------------
     def forward(self, inputs: Tensor, *, inputs_int8: Tensor | None = None,
                 inputs_scale: Tensor | None = None,
-                inputs_dq: Tensor | None = None,
                 out_dtype: torch.dtype | None = None,
                 residual: Tensor | None = None, split: int = 1):
-        """``inputs_dq`` (with ``inputs_int8`` / ``inputs_scale``): their dequantized bf16
-        copy, written by the same quantization, which the backward then reads in place of
-        the int8 rows (the same values). ``out_dtype`` (int8 mode only): the output dtype in
-        place of the input's, for a caller that would cast the result anyway (same values).
+        """``out_dtype`` (int8 mode only): the output dtype in place of the input's, for a
+        caller that would cast the result anyway (same values).
         ``residual``: return ``residual + output`` (added in the GEMM's epilogue where the
         shapes allow, the same float32 add). ``split`` > 1: return
         ``output.chunk(split, dim=-1)``; on the fused int8-backward path the chunks'
         gradients are then read in place rather than concatenated (the same results)."""
         if self.matmul_mode != "fp32" or self.fuse_backward_update:
             return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
-                                        self.scale, self, out_dtype, residual, split,
-                                        inputs_dq)
+                                        self.scale, self, out_dtype, residual, split)
         effective = self.effective_weight().to(dtype=inputs.dtype)
         if self.training and torch.is_grad_enabled():
             if self.trainable_scale:

@@ -261,35 +261,6 @@ def test_qkv_gradients_read_in_parts_change_nothing(cuda):
     assert all(torch.equal(x, y) for x, y in zip(pa, pb))
 
 
-def test_dequantized_activations_for_the_backward_change_nothing(cuda):
-    # The prologues also writing the dequantized bf16 rows, which the layers' backward
-    # reads for grad_weight instead of converting q and s per output tile: identical losses,
-    # ratchet states and float parameters over three steps.
-    from local_ai_training import ratchet
-
-    calls = []
-    orig = ratchet.grad_weight_bf16_x
-
-    def recording(*args, **kwargs):
-        calls.append(args[1].dtype)
-        return orig(*args, **kwargs)
-
-    ratchet.grad_weight_bf16_x = recording
-    DiscreteRatchetLinear.save_dequantized_inputs = True
-    try:
-        la, sa, pa = _int8_steps(cuda, fuse=True)
-    finally:
-        ratchet.grad_weight_bf16_x = orig
-        DiscreteRatchetLinear.save_dequantized_inputs = False
-    # projection, expansion and contraction of both blocks, every step (qkv reads its
-    # gradient in parts through grad_weight_bf16_parts)
-    assert calls.count(torch.bfloat16) >= 3 * 2 * 3
-    lb, sb, pb = _int8_steps(cuda, fuse=True)
-    assert all(torch.equal(x, y) for x, y in zip(la, lb))
-    assert all(torch.equal(x, y) for x, y in zip(sa, sb))
-    assert all(torch.equal(x, y) for x, y in zip(pa, pb))
-
-
 def test_shared_move_count_buffer_gives_the_per_layer_totals(cuda):
     # The model's one [layers, 4] move-count buffer (summed and cleared once per step) gives
     # the same step statistics as per-layer count tensors, step after step, and a

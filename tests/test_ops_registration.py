@@ -25,10 +25,7 @@ MUTATED = {
                              "nonfinite", "rms_mean", "grad_out"},
     "normalize_rows": {"rms_ema"},
     "pressure_leak": {"packed"},
-    "quantize_rows": {"x_bf16", "x_dq"},
-    "rmsnorm_quantize": {"x_dq"},
-    "gelu_quantize": {"x_dq"},
-    "transpose_quantize": {"x_dq"},
+    "quantize_rows": {"x_bf16"},
 }
 
 
