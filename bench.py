@@ -7,8 +7,11 @@ BF16 activations N(0,1) quantized per token, BF16 upstream gradient N(0, 1e-2):
 per-token quant -> W8A8 forward GEMM (packed codes) -> SR gradient quant ->
 int8 grad_input GEMM -> BF16 grad_weight GEMM -> fused normalize+update. It runs
 through the drop-in DiscreteRatchetLinear autograd path. ``value`` is the step's
-TOPS over its three GEMMs (3 x 2*M*N*K ops; the int8 and bf16 halves are also
-reported separately), inputs resident in HBM.
+operations per second over its three GEMMs (3 x 2*M*N*K: two int8 GEMMs and one bf16
+GEMM), inputs resident in HBM. ``split`` reports the two kinds against their own peaks:
+int8 TOPS of the forward and grad_input GEMMs against the int8 MFMA peak, bf16 TFLOP/s of
+grad_weight against the bf16 MFMA peak, each over the step time and over the kernels' own
+launch times.
 
 Also reported on the same line:
   kernels        per-kernel average launch time (HIP events on the launch stream) and
@@ -445,6 +448,32 @@ def measured_traffic(kernel: str):
         return json.loads(body)["kernels"][kernel]["traffic_bytes"]
     except (ValueError, KeyError):
         return None
+
+
+def headline_split(step_s: float, kernels: dict) -> dict:
+    """The step's GEMM work by arithmetic: int8 (forward + grad_input, 2 x 2MNK ops) against
+    the int8 MFMA peak and bf16 (grad_weight, 2MNK FLOPs) against the bf16 MFMA peak, per
+    step time and per the kernels' own average launch times."""
+    mnk2 = 2.0 * M_TOK * N_OUT * K_IN
+    int8_us = kernels["fwd_gemm_packed"]["avg_us"] + kernels["grad_input_gemm"]["avg_us"]
+    bf16_us = kernels["grad_weight_partials"]["avg_us"]
+    int8_ops, bf16_flops = 2 * mnk2, mnk2
+    return {
+        "int8": {"ops_per_step": int8_ops, "kernels": ["fwd_gemm_packed", "grad_input_gemm"],
+                 "TOPS_over_step": round(int8_ops / step_s / 1e12, 1),
+                 "frac_int8_peak_over_step": round(int8_ops / step_s / PEAK_INT8_OPS, 4),
+                 "kernel_us": round(int8_us, 2),
+                 "TOPS_over_kernels": round(int8_ops / (int8_us * 1e-6) / 1e12, 1),
+                 "frac_int8_peak_over_kernels": round(int8_ops / (int8_us * 1e-6) / PEAK_INT8_OPS,
+                                                      4)},
+        "bf16": {"flops_per_step": bf16_flops, "kernels": ["grad_weight_partials"],
+                 "TFLOPs_over_step": round(bf16_flops / step_s / 1e12, 1),
+                 "frac_bf16_peak_over_step": round(bf16_flops / step_s / PEAK_BF16_FLOPS, 4),
+                 "kernel_us": round(bf16_us, 2),
+                 "TFLOPs_over_kernels": round(bf16_flops / (bf16_us * 1e-6) / 1e12, 1),
+                 "frac_bf16_peak_over_kernels": round(
+                     bf16_flops / (bf16_us * 1e-6) / PEAK_BF16_FLOPS, 4)},
+    }
 
 
 def roofline_entry(kernels: dict) -> dict:
@@ -1166,7 +1195,7 @@ def main() -> int:
         "config": {"workload": "int8 ratchet linear fwd+bwd+fused update (int8_backward)",
                    "M": M_TOK, "K": K_IN, "N": N_OUT, "codes": "quinary",
                    "batch": 32, "seq_len": 512, "parallelism": "none"},
-        "pct_int8_mfma_peak": round(tops * 1e12 / PEAK_INT8_OPS * 100, 2),
+        "split": headline_split(step_s, kernels),
         "kernels": kernels,
         "roofline": roofline_entry(kernels),
     }
