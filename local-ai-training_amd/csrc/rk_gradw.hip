@@ -285,48 +285,75 @@ void grad_weight_partial_kernel(GwArgs a) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = v16f{};
 
-  // Register ring of S steps: the global loads of step st + S are issued right after
-  // step st is written to LDS, so S steps of g and X stream in while the MFMAs run. The
-  // step count is padded to a multiple of S (even, so a slot's LDS buffer is fixed);
-  // padded steps stage zeros.
+  // Register ring of S steps over an LDS ping-pong, one barrier per step at its top. Step
+  // st reads its tiles from buffer st % 2 (staged during step st - 1) and, in the same
+  // barrier interval, stages step st + 1 (held in slot (st + 1) % S) into the other buffer,
+  // whose last reader was step st - 1, and refills that slot with step st + 1 + S. So one
+  // interval holds a step's MFMAs, the next step's staging writes and the loads S steps
+  // ahead, and sched_group_barrier interleaves them: the second 16-token half's fragment
+  // reads during the first half's MFMAs, the staging writes and the loads during the
+  // second half's. The step count is padded to a multiple of S (even, so a slot's LDS
+  // buffer is fixed); padded steps stage zeros, and adding +0 products to an accumulator
+  // that started at +0 leaves it bit-for-bit unchanged, so no step branches.
   static_assert(S % 2 == 0 && S <= kGwMaxRing, "ring depth must be even and <= 6");
   if (steps > 0) {
+    constexpr int U = BM / 16;                // 16-token halves per step
+    constexpr int R = (MI + NJ) * 2;          // transposing reads per half
+    constexpr int NM = MI * NJ;               // MFMAs per half
+    constexpr int DSW = GV + XV * (XK == GW_X_Q8 ? 2 : 1);  // staging writes per step
+    constexpr int VM = GV + XV * (XK == GW_X_Q8 ? 2 : 1);   // loads per step
     const int steps_pad = ((steps + S - 1) / S) * S;
     GwSlot<GV, XV> ring[S];
     // Issue the first S steps in slot order (the scheduler barrier keeps them so): the
-    // loop body waits for slot i with S - 1 slots still in flight only if slot i's loads
-    // are older than those of the later slots on every path into the loop.
+    // loop body waits for a slot with the later slots still in flight only if its loads
+    // are older than theirs on every path into the loop.
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       load_slot(ring[i], i);
       __builtin_amdgcn_sched_barrier(0);
     }
+    store_slot(ring[0], smem);
+    load_slot(ring[0], S);
     for (int st = 0; st < steps_pad; st += S) {
 #pragma unroll
       for (int slot = 0; slot < S; ++slot) {
         const int step = st + slot;
-        uint8_t* gt = smem + (slot & 1) * 2 * TILE;
-        uint8_t* xt = gt + TILE;
-        store_slot(ring[slot], gt);
-        load_slot(ring[slot], step + S);
         __syncthreads();
-        // No branch for padded steps: their tiles are zeros, and adding +0 products to
-        // an accumulator that started at +0 leaves it bit-for-bit unchanged. One basic
-        // block per step lets the scheduler overlap these MFMAs with the next step's
-        // staging.
+        const uint8_t* gt = smem + (slot & 1) * 2 * TILE;
+        const uint8_t* xt = gt + TILE;
+        v8bf fa[U][MI], fb[U][NJ];
 #pragma unroll
-        for (int u = 0; u < BM / 16; ++u) {
-          v8bf fa[MI], fb[NJ];
+        for (int u = 0; u < U; ++u) {
 #pragma unroll
-          for (int i = 0; i < MI; ++i) fa[i] = tr16_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
+          for (int i = 0; i < MI; ++i)
+            fa[u][i] = tr16_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
 #pragma unroll
-          for (int j = 0; j < NJ; ++j) fb[j] = tr16_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
+          for (int j = 0; j < NJ; ++j)
+            fb[u][j] = tr16_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
-              acc[i][j] =
-                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[u][i], fb[u][j], acc[i][j],
+                                                                  0, 0, 0);
+        store_slot(ring[(slot + 1) % S], smem + ((slot + 1) & 1) * 2 * TILE);
+        load_slot(ring[(slot + 1) % S], step + 1 + S);
+        __builtin_amdgcn_sched_group_barrier(0x100, R, 0);  // DS read: the first half
+#pragma unroll
+        for (int u = 1; u < U; ++u)
+#pragma unroll
+          for (int k = 0; k < NM; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, (R + NM - 1) / NM, 0);  // DS read
+          }
+#pragma unroll
+        for (int k = 0; k < NM; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x200, (DSW + NM - 1) / NM, 0);  // DS write
+          __builtin_amdgcn_sched_group_barrier(0x020, (VM + NM - 1) / NM, 0);   // VMEM read
         }
       }
     }
