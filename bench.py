@@ -31,6 +31,7 @@ Also reported on the same line:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -75,6 +76,9 @@ def parse_args() -> argparse.Namespace:
                     help="run only the HBM streaming probe (practical read / copy bandwidth)")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the forward GEMM on packed codes at large-K shapes")
+    ap.add_argument("--immediate-updates", action="store_true",
+                    help="--train-only: update each ratchet layer inside backward instead of "
+                         "batching the updates after it (A/B runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the decode bench and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=64)
@@ -660,7 +664,8 @@ TRAIN_1B = dict(model="ratchet-gpt-1B", vocab=8192, block=1024, batch=8, n_layer
                 n_embd=2048, ffn=5632, max_code=3, codes="septenary")
 
 
-def train_bench(shape: dict, steps: int, warmup: int, device, graph: bool):
+def train_bench(shape: dict, steps: int, warmup: int, device, graph: bool,
+                defer_updates: bool = True):
     """Training tokens/s of a ratchet transformer (int8 + int8_backward, fused update every
     step, AdamW on the float parameters, Zipf(1.1) token ids), sustained: syncs only at both
     ends of the timed steps. ``graph``: the step is captured once as a HIP graph and
@@ -677,6 +682,9 @@ def train_bench(shape: dict, steps: int, warmup: int, device, graph: bool):
                          n_head=shape["n_head"], n_embd=shape["n_embd"],
                          ffn_hidden=shape["ffn"], matmul_mode="int8", int8_backward=True)
     model = build_seeded_model(config, max_code=shape["max_code"], seed=1337).to(device).train()
+    # the layers' fused updates batched after backward (a few launches for the whole model);
+    # defer_updates=False keeps one update launch per layer inside backward (A/B runs)
+    model.defer_ratchet_updates(defer_updates)
     # capturable (device-side step count) in both modes: the same AdamW arithmetic, so the
     # eager and graph runs of the same steps end at the same loss; torch's fused AdamW (one
     # kernel for every parameter; the same update as the reference's foreach AdamW up to
@@ -810,29 +818,69 @@ def update_1b_bench(device, iters: int) -> dict:
                              1.0, counts.data_ptr(), row_rms.data_ptr(), None, flag.data_ptr(),
                              None, None, k, stream)
 
-        sweep()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
-            sweep()
-        e1.record()
-        torch.cuda.synchronize()
-        sweep_s = e0.elapsed_time(e1) * 1e-3 / iters
+        # the batched form the training step takes (RatchetGPT.defer_ratchet_updates): one
+        # rk_ratchet_update_multi launch per gradient source and row-length class
+        groups: dict = {}
+        for packed, grad, nsplit, n, k, row_rms in layers:
+            src = nat.RK_BF16 if grad.dtype == torch.bfloat16 else nat.RK_UPDATE_SRC_SPLITS
+            chunks = (k + 511) // 512
+            groups.setdefault((src, 4 if chunks <= 4 else 12, nsplit == 1), []).append(
+                (packed, grad, nsplit, n, k, row_rms))
+        tables = []
+        for (src, _, _), group in groups.items():
+            entries = (nat.UpdateLayer * len(group))()
+            row = 0
+            for d, (packed, grad, nsplit, n, k, row_rms) in zip(entries, group):
+                d.packed, d.g = packed.data_ptr(), grad.data_ptr()
+                d.counts, d.row_rms, d.nonfinite = (counts.data_ptr(), row_rms.data_ptr(),
+                                                    flag.data_ptr())
+                d.ldp, d.ldg, d.rows, d.K, d.row_begin = k, k, n, k, row
+                d.max_code, d.threshold, d.nsplit = mc, 8, nsplit
+                d.low, d.high, d.eps, d.beta1, d.beta2 = 0.5, 1.5, 1e-8, 0.0, 1.0
+                row += n
+            host = torch.frombuffer(bytearray(ctypes.string_at(ctypes.addressof(entries),
+                                                               ctypes.sizeof(entries))),
+                                    dtype=torch.uint8)
+            tables.append((src, len(group), host, host.to(device)))
+
+        def batched():
+            for src, count, host, dev in tables:
+                nat.call("rk_ratchet_update_multi", host.data_ptr(), dev.data_ptr(), count, src,
+                         stream)
+
+        def timed(fn) -> float:
+            fn()
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(iters):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e-3 / iters
+
+        sweep_s = timed(sweep)
+        batched_s = timed(batched)
         alg = sum(n * k * (2 + (2 if g.dtype == torch.bfloat16 else 4 * nsp)) + 4 * n
                   for _, g, nsp, n, k, _ in layers)
-        del layers
+        del layers, tables
         torch.cuda.empty_cache()
-        return {"alg_bytes": alg, "ms": round(sweep_s * 1e3, 3),
-                "GB_s": round(alg / sweep_s / 1e9, 1),
-                "frac_hbm": round(alg / sweep_s / PEAK_HBM_BPS, 4)}
+
+        def rate(sec: float) -> dict:
+            return {"ms": round(sec * 1e3, 3), "GB_s": round(alg / sec / 1e9, 1),
+                    "frac_hbm": round(alg / sec / PEAK_HBM_BPS, 4)}
+
+        return {"alg_bytes": alg, "launches": len(groups), **rate(batched_s),
+                "per_layer": {"launches": len(shapes), **rate(sweep_s)}}
 
     step = run(False)
     partials = run(True)
     return {"workload": "fused update of every 1B ratchet layer from what its backward hands "
-                        "it (bf16 gradient at one split, float32 split partials otherwise)",
-            "weights": sum(n * k for n, k in shapes), "launches": len(shapes), **step,
+                        "it (bf16 gradient at one split, float32 split partials otherwise), "
+                        "batched per gradient source and row length (rk_ratchet_update_multi); "
+                        "per_layer: one launch per layer",
+            "weights": sum(n * k for n, k in shapes), **step,
             "all_partials": {"workload": "every layer from float32 split partials", **partials}}
 
 
@@ -1163,10 +1211,12 @@ def main() -> int:
         shape = TRAIN_25M if args.train_only == "25m" else TRAIN_1B
         log(f"training only: {shape['model']}, warmup={args.warmup} steps={args.steps}")
         tok_s, step_s, loss = train_bench(shape, args.steps, args.warmup, device,
-                                          graph=not args.no_graph)
+                                          graph=not args.no_graph,
+                                          defer_updates=not args.immediate_updates)
         print(json.dumps({"model": shape["model"], "tokens_per_s": round(tok_s, 1),
                           "ms_per_step": round(step_s * 1e3, 3), "loss": round(loss, 5),
-                          "steps": args.steps, "graph": not args.no_graph}), flush=True)
+                          "steps": args.steps, "graph": not args.no_graph,
+                          "deferred_updates": not args.immediate_updates}), flush=True)
         return 0
     log(f"op bench: M={M_TOK} K={K_IN} N={N_OUT} warmup={args.warmup} steps={args.steps}")
     step_s, eager_s, layer, x, g = op_bench(args, device)

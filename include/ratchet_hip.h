@@ -384,6 +384,40 @@ int rk_ratchet_update_partials(uint8_t* packed, int64_t ldp, const float* partia
                                void* stream);
 
 /*
+ * One layer of rk_ratchet_update_multi. Device addresses are 64-bit integers (0 = absent
+ * for the optional outputs rms_ema, counts, row_rms, grad_scale, nonfinite). g is the
+ * layer's gradient [rows, K] (row stride ldg, dtype given by the call's src) or, for
+ * src == RK_UPDATE_SRC_SPLITS, its float32 split partials [nsplit, rows, K] (split stride
+ * rows * K). row_begin is the layer's first row in the call's concatenated row space:
+ * layer i starts where layer i - 1 ends (row_begin[0] == 0). 160 bytes, 8-byte aligned.
+ */
+typedef struct rk_update_layer {
+  uint64_t packed, g, counts, row_rms, rms_ema, grad_scale, nonfinite, reserved0;
+  int64_t ldp, ldg, rows, K, row_begin, reserved1;
+  int32_t max_code, threshold, nsplit, reserved2;
+  float low, high, eps, beta1, beta2, reserved3[3];
+} rk_update_layer;
+
+enum { RK_UPDATE_SRC_SPLITS = 2 };
+
+/*
+ * The fused normalize + update of rk_ratchet_update_grad (src RK_F32 / RK_BF16) or
+ * rk_ratchet_update_partials (src RK_UPDATE_SRC_SPLITS) for several layers in one launch:
+ * every layer's state, counts, row_rms, rms_ema, grad_scale and nonfinite are bit-identical
+ * to what that layer's own call gives (the same row code; counts add into the layer's
+ * counts). table_host and table_dev hold the same nlayers entries, in host and device
+ * memory: the host copy is validated and sizes the launch, the kernel reads the device
+ * copy (which must stay unchanged until the launch has run; under graph capture, for as
+ * long as the graph is replayed). Layers must not share packed state or outputs. The
+ * rms means are not written (rk_row_rms_means takes them from row_rms).
+ * Replaces: the per-layer fused update of the backward pass, _capture_weight_gradient
+ *           ratchet.py:487-537 called from the tile loop 148-169, run for every layer of the
+ *           model (model.py:252-273 collects its statistics) in one pass over their state.
+ */
+int rk_ratchet_update_multi(const rk_update_layer* table_host, const rk_update_layer* table_dev,
+                            int nlayers, int src, void* stream);
+
+/*
  * Means of segments of a row-rms buffer: means[s] = mean of row_rms[offsets[s] ..
  * offsets[s + 1]) for s < nseg (offsets: nseg + 1 device int64, non-decreasing; an empty
  * segment gives NaN), each summed in the order the update entry points use for their

@@ -703,6 +703,68 @@ Tensor normalize_rows(const Tensor& g_in, double eps, const OptTensor& rms_ema, 
   return z;
 }
 
+// Several layers' fused updates in one launch. table_host (CPU) and table_dev (on the
+// layers' device) hold the same rk_update_layer entries; `written` lists every tensor the
+// launch writes (each layer's packed state, counts, row_rms, rms_ema, grad_scale, nonfinite),
+// and every address the table writes through is checked to lie inside one of them.
+void update_multi(const Tensor& table_host, const Tensor& table_dev, int64_t src,
+                  at::TensorList written) {
+  constexpr int64_t kEntry = sizeof(rk_update_layer);
+  TORCH_CHECK(table_host.device().is_cpu() && table_host.scalar_type() == at::kByte &&
+                  table_host.is_contiguous(),
+              "table_host must be a contiguous CPU uint8 tensor");
+  require_gpu(table_dev, "the multi-layer ratchet update");
+  TORCH_CHECK(table_dev.scalar_type() == at::kByte && table_dev.is_contiguous() &&
+                  table_dev.numel() == table_host.numel(),
+              "table_dev must be a contiguous uint8 tensor the size of table_host");
+  TORCH_CHECK(table_host.numel() > 0 && table_host.numel() % kEntry == 0,
+              "the tables must hold whole rk_update_layer entries");
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(table_dev.data_ptr()) % 16 == 0,
+              "table_dev must be 16-byte aligned");
+  const int64_t n = table_host.numel() / kEntry;
+  TORCH_CHECK(n <= 0x7fffffff, "too many layers");
+  std::vector<std::pair<uintptr_t, uintptr_t>> ranges;
+  for (const Tensor& t : written) {
+    TORCH_CHECK(t.device() == table_dev.device(),
+                "written tensors must be on the device of table_dev");
+    const uintptr_t b = reinterpret_cast<uintptr_t>(t.data_ptr());
+    ranges.emplace_back(b, b + static_cast<uintptr_t>(t.numel() * t.element_size()));
+  }
+  std::sort(ranges.begin(), ranges.end());
+  auto covered = [&](uint64_t p, int64_t bytes) {
+    if (p == 0 || bytes <= 0) return true;
+    auto it = std::upper_bound(ranges.begin(), ranges.end(),
+                               std::make_pair(static_cast<uintptr_t>(p), UINTPTR_MAX));
+    while (it != ranges.begin()) {
+      --it;
+      if (it->first <= p && p + static_cast<uint64_t>(bytes) <= it->second) return true;
+    }
+    return false;
+  };
+  const auto* tab = reinterpret_cast<const rk_update_layer*>(table_host.data_ptr());
+  for (int64_t i = 0; i < n; ++i) {
+    const rk_update_layer& d = tab[i];
+    if (d.rows <= 0) continue;
+    TORCH_CHECK(covered(d.packed, (d.rows - 1) * d.ldp + d.K), "layer ", i,
+                ": its packed state is not among the written tensors");
+    TORCH_CHECK(covered(d.counts, 32), "layer ", i, ": counts not among the written tensors");
+    TORCH_CHECK(covered(d.row_rms, d.rows * 4), "layer ", i,
+                ": row_rms not among the written tensors");
+    TORCH_CHECK(covered(d.rms_ema, d.rows * 4), "layer ", i,
+                ": rms_ema not among the written tensors");
+    TORCH_CHECK(covered(d.grad_scale, d.rows * 4), "layer ", i,
+                ": grad_scale not among the written tensors");
+    TORCH_CHECK(covered(d.nonfinite, 4), "layer ", i,
+                ": nonfinite not among the written tensors");
+  }
+  const c10::DeviceGuard guard(table_dev.device());
+  check_status(rk_ratchet_update_multi(tab,
+                                       reinterpret_cast<const rk_update_layer*>(table_dev.data_ptr()),
+                                       static_cast<int>(n), static_cast<int>(src),
+                                       stream_of(table_dev)),
+               "rk_ratchet_update_multi");
+}
+
 void pressure_leak(Tensor& packed, int64_t max_code) {
   require_gpu(packed, "the pressure leak");
   TORCH_CHECK(packed.scalar_type() == at::kByte && packed.is_contiguous(),
@@ -1041,6 +1103,7 @@ TORCH_LIBRARY(ratchet, m) {
       "float low, float high, float eps, Tensor(b!)? rms_ema, float beta, Tensor(c!) counts, "
       "Tensor(d!)? row_rms, Tensor(e!)? grad_scale, Tensor(f!)? nonfinite, "
       "Tensor(g!)? rms_mean, Tensor(h!)? grad_out) -> ()");
+  m.def("update_multi(Tensor table_host, Tensor table_dev, int src, Tensor(a!)[] written) -> ()");
   m.def("normalize_rows(Tensor g, float eps, Tensor(a!)? rms_ema, float beta) -> Tensor");
   m.def("pressure_leak(Tensor(a!) packed, int max_code) -> ()");
   m.def("validate_state(Tensor packed, int max_code, Tensor? scale) -> Tensor");
@@ -1083,6 +1146,7 @@ TORCH_LIBRARY_IMPL(ratchet, CUDA, m) {
   m.impl("update_from_z", &update_from_z);
   m.impl("update_from_grad", &update_from_grad);
   m.impl("update_from_partials", &update_from_partials);
+  m.impl("update_multi", &update_multi);
   m.impl("normalize_rows", &normalize_rows);
   m.impl("pressure_leak", &pressure_leak);
   m.impl("validate_state", &validate_state);

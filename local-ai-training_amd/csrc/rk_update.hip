@@ -108,6 +108,129 @@ __global__ __launch_bounds__(256) void ratchet_update_grad_kernel(GradUpdateArgs
   flush_counts(cnt, a.counts);
 }
 
+// ---------------------------------------------------------------------------
+// Several layers in one launch (rk_ratchet_update_multi). The layers' rows form one row
+// space; wavefront w takes the contiguous rows [w R, (w + 1) R) and walks the layer table
+// forward as it crosses layer boundaries, each row through update_row with that layer's
+// arguments (the same code as the per-layer kernel, so the same results). Move counts add
+// up per wavefront and go to a layer's counters, four 64-bit atomics, when the wavefront
+// leaves the layer.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void flush_wave_counts(MoveCounts& cnt, int64_t* counts) {
+  const int p = wave_sum_int(cnt.pos), n = wave_sum_int(cnt.neg);
+  const int bp = wave_sum_int(cnt.bpos), bn = wave_sum_int(cnt.bneg);
+  if ((threadIdx.x & 63) == 0 && counts) {
+    unsigned long long* c = reinterpret_cast<unsigned long long*>(counts);
+    if (p) atomicAdd(c + 0, static_cast<unsigned long long>(p));
+    if (n) atomicAdd(c + 1, static_cast<unsigned long long>(n));
+    if (bp) atomicAdd(c + 2, static_cast<unsigned long long>(bp));
+    if (bn) atomicAdd(c + 3, static_cast<unsigned long long>(bn));
+  }
+  cnt = MoveCounts{};
+}
+
+// A table entry read into wave-uniform registers: the entry's address is the same for every
+// lane, but the compiler does not know the loaded words are, so each goes through
+// readfirstlane (a descriptor or row bound left in vector registers would turn every buffer
+// access of the row into a waterfall loop).
+__device__ __forceinline__ rk_update_layer load_layer(const rk_update_layer* p) {
+  static_assert(sizeof(rk_update_layer) % 16 == 0, "16-byte table entries");
+  rk_update_layer d;
+  const uint4* src = reinterpret_cast<const uint4*>(p);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&d);
+#pragma unroll
+  for (int i = 0; i < static_cast<int>(sizeof(rk_update_layer) / 16); ++i) {
+    const uint4 v = src[i];
+    dst[4 * i + 0] = __builtin_amdgcn_readfirstlane(v.x);
+    dst[4 * i + 1] = __builtin_amdgcn_readfirstlane(v.y);
+    dst[4 * i + 2] = __builtin_amdgcn_readfirstlane(v.z);
+    dst[4 * i + 3] = __builtin_amdgcn_readfirstlane(v.w);
+  }
+  return d;
+}
+
+__device__ __forceinline__ int64_t uniform_row_begin(const rk_update_layer* p) {
+  const int64_t v = p->row_begin;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <int DT>
+__device__ __forceinline__ GradUpdateArgs layer_args(const rk_update_layer& d) {
+  constexpr int V = DT == RK_F32 ? 4 : 8;
+  GradUpdateArgs a{};
+  a.packed = reinterpret_cast<uint8_t*>(d.packed);
+  a.ldp = d.ldp;
+  if constexpr (DT == SRC_SPLITS) {
+    a.part = reinterpret_cast<const float*>(d.g);
+    a.nsplit = d.nsplit;
+    a.part_stride = d.rows * d.K;
+    a.vec_p = (d.packed % 8) == 0 && (d.ldp % 8) == 0;
+  } else {
+    a.g = reinterpret_cast<const void*>(d.g);
+    a.ldg = d.ldg;
+    a.vec_g = (d.g % 16) == 0 && (d.ldg % V) == 0 && (d.K % V) == 0;
+    a.vec_p = (d.packed % V) == 0 && (d.ldp % V) == 0 && (d.K % V) == 0;
+  }
+  a.rows = d.rows;
+  a.K = d.K;
+  a.mc = d.max_code;
+  a.T = d.threshold;
+  a.low = d.low;
+  a.high = d.high;
+  a.eps = d.eps;
+  a.rms_ema = reinterpret_cast<float*>(d.rms_ema);
+  a.beta1 = d.beta1;
+  a.beta2 = d.beta2;
+  a.counts = reinterpret_cast<int64_t*>(d.counts);
+  a.row_rms = reinterpret_cast<float*>(d.row_rms);
+  a.grad_scale = reinterpret_cast<float*>(d.grad_scale);
+  a.nonfinite = reinterpret_cast<int32_t*>(d.nonfinite);
+  return a;
+}
+
+template <int DT, int NC, bool ONE_SPLIT>
+__global__ __launch_bounds__(256) void ratchet_update_multi_kernel(const rk_update_layer* tab,
+                                                                   int nlayers, int64_t total_rows,
+                                                                   int64_t rows_per_wave) {
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 +
+                    __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  int64_t r = w * rows_per_wave;
+  const int64_t r_end = r + rows_per_wave < total_rows ? r + rows_per_wave : total_rows;
+  if (r >= r_end) return;
+  // the last layer whose rows start at or before r (an empty layer shares its row_begin with
+  // the next one and is passed over)
+  int lo = 0, hi = nlayers - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (uniform_row_begin(tab + mid) <= r) lo = mid;
+    else hi = mid - 1;
+  }
+  int l = lo;
+  rk_update_layer d = load_layer(tab + l);
+  GradUpdateArgs a = layer_args<DT>(d);
+  int64_t lbeg = d.row_begin, lend = lbeg + d.rows;
+  MoveCounts cnt;
+  for (; r < r_end; ++r) {
+    if (r >= lend) {
+      flush_wave_counts(cnt, a.counts);
+      do {
+        ++l;
+        d = load_layer(tab + l);
+        lbeg = d.row_begin;
+        lend = lbeg + d.rows;
+      } while (r >= lend);
+      a = layer_args<DT>(d);
+    }
+    // K opaque per row, as in ratchet_update_grad_kernel
+    int64_t K = a.K;
+    asm volatile("" : "+s"(K));
+    update_row<DT, NC, false, ONE_SPLIT>(a, r - lbeg, K, cnt);
+  }
+  flush_wave_counts(cnt, a.counts);
+}
+
 static unsigned row_grid(int64_t rows) {
   // Enough blocks to fill 256 CUs several times over; rows beyond that loop.
   const int64_t want = (rows + 3) / 4;
@@ -158,9 +281,110 @@ static int launch_grad_kernel(const GradUpdateArgs& a, int g_dtype, hipStream_t 
   return launch_status(ZONLY ? "normalize_rows" : "ratchet_update_grad");
 }
 
+// Grid of the multi-layer update: as many blocks as stay resident (the kernel's occupancy
+// times the device's CUs), each wavefront a contiguous share of the rows.
+template <int DT, int NC, bool ONE_SPLIT>
+static void launch_multi(const rk_update_layer* tab, int nl, int64_t total, hipStream_t s) {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, ratchet_update_multi_kernel<DT, NC, ONE_SPLIT>, 256, 0) != hipSuccess || n < 1)
+      n = 1;
+    return n;
+  }();
+  // the device's CU count, looked up once per device (the attribute query is a driver call)
+  static int cu_cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int cus = __atomic_load_n(&cu_cache[dev], __ATOMIC_RELAXED);
+  if (cus < 1) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+    __atomic_store_n(&cu_cache[dev], cus, __ATOMIC_RELAXED);
+  }
+  const int64_t want = (total + 3) / 4;
+  const int64_t cap = static_cast<int64_t>(per_cu) * cus;
+  const int64_t blocks = want < cap ? want : cap;
+  const int64_t rpw = (total + 4 * blocks - 1) / (4 * blocks);
+  ratchet_update_multi_kernel<DT, NC, ONE_SPLIT>
+      <<<static_cast<unsigned>(blocks), 256, 0, s>>>(tab, nl, total, rpw);
+}
+
+template <int DT>
+static void launch_multi_nc(const rk_update_layer* tab, int nl, int64_t total, int64_t kmax,
+                            bool one_split, hipStream_t s) {
+  constexpr int V = DT == RK_F32 ? 4 : 8;
+  const int64_t nchunks = (kmax + 64 * V - 1) / (64 * V);
+  if constexpr (DT == RK_F32) {
+    if (nchunks <= 2) launch_multi<DT, 2, false>(tab, nl, total, s);
+    else if (nchunks <= 8) launch_multi<DT, 8, false>(tab, nl, total, s);
+    else launch_multi<DT, 0, false>(tab, nl, total, s);
+  } else if constexpr (DT == RK_BF16) {
+    if (nchunks <= 1) launch_multi<DT, 1, false>(tab, nl, total, s);
+    else if (nchunks <= 4) launch_multi<DT, 4, false>(tab, nl, total, s);
+    else if (nchunks <= 12) launch_multi<DT, 12, false>(tab, nl, total, s);
+    else launch_multi<DT, 0, false>(tab, nl, total, s);
+  } else {
+    if (one_split) {
+      if (nchunks <= 1) launch_multi<DT, 1, true>(tab, nl, total, s);
+      else if (nchunks <= 4) launch_multi<DT, 4, true>(tab, nl, total, s);
+      else if (nchunks <= 12) launch_multi<DT, 12, true>(tab, nl, total, s);
+      else launch_multi<DT, 0, false>(tab, nl, total, s);
+    } else {
+      if (nchunks <= 1) launch_multi<DT, 1, false>(tab, nl, total, s);
+      else if (nchunks <= 4) launch_multi<DT, 4, false>(tab, nl, total, s);
+      else if (nchunks <= 12) launch_multi<DT, 12, false>(tab, nl, total, s);
+      else launch_multi<DT, 0, false>(tab, nl, total, s);
+    }
+  }
+}
+
 }  // namespace rk
 
 using namespace rk;
+
+extern "C" int rk_ratchet_update_multi(const rk_update_layer* table_host,
+                                       const rk_update_layer* table_dev, int nlayers, int src,
+                                       void* stream) {
+  clear_error();
+  static_assert(sizeof(rk_update_layer) == 160, "rk_update_layer layout");
+  if (nlayers < 1) return fail(RK_ERR_ARG, "nlayers must be positive");
+  if (!table_host || !table_dev) return fail(RK_ERR_ARG, "null layer table");
+  if (src != RK_F32 && src != RK_BF16 && src != RK_UPDATE_SRC_SPLITS)
+    return fail(RK_ERR_ARG, "unsupported gradient source");
+  int64_t total = 0, kmax = 0;
+  bool one_split = true;
+  for (int i = 0; i < nlayers; ++i) {
+    const rk_update_layer& d = table_host[i];
+    if (d.row_begin != total)
+      return fail(RK_ERR_ARG, "layer %d: row_begin %lld where its rows start at %lld", i,
+                  static_cast<long long>(d.row_begin), static_cast<long long>(total));
+    if (int st = check_update_common(reinterpret_cast<const uint8_t*>(d.packed), d.ldp, d.rows,
+                                     d.K, d.max_code, d.threshold, d.low, d.high)) {
+      char msg[256];
+      snprintf(msg, sizeof msg, "%s", rk_last_error());
+      return fail(st, "layer %d: %s", i, msg);
+    }
+    if (!(d.eps > 0.0f)) return fail(RK_ERR_ARG, "layer %d: eps must be positive", i);
+    if (d.rows > 0 && !d.g) return fail(RK_ERR_ARG, "layer %d: null gradient", i);
+    if (src == RK_UPDATE_SRC_SPLITS) {
+      if (d.nsplit < 1 || d.nsplit > 64) return fail(RK_ERR_ARG, "layer %d: nsplit must be in 1..64", i);
+      if (d.K % 8 != 0 || d.g % 16 != 0)
+        return fail(RK_ERR_UNSUPPORTED, "layer %d: partials need K %% 8 == 0 and 16-byte alignment", i);
+      if (d.nsplit != 1) one_split = false;
+    } else if (d.ldg < d.K) {
+      return fail(RK_ERR_ARG, "layer %d: ldg < K", i);
+    }
+    if (d.rows > 0 && d.K > kmax) kmax = d.K;
+    total += d.rows;
+  }
+  if (total == 0) return RK_OK;
+  hipStream_t s = as_stream(stream);
+  if (src == RK_F32) launch_multi_nc<RK_F32>(table_dev, nlayers, total, kmax, false, s);
+  else if (src == RK_BF16) launch_multi_nc<RK_BF16>(table_dev, nlayers, total, kmax, false, s);
+  else launch_multi_nc<SRC_SPLITS>(table_dev, nlayers, total, kmax, one_split, s);
+  return launch_status("ratchet_update_multi");
+}
 
 extern "C" int rk_ratchet_update(uint8_t* packed, int64_t ldp, const float* z, int64_t ldz,
                                  int64_t rows, int64_t K, int max_code, int threshold,

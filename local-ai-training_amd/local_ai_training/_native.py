@@ -24,11 +24,30 @@ RK_BF16 = 1
 RK_I8 = 2
 RK_F32_AS_BF16 = 3
 
+RK_UPDATE_SRC_SPLITS = 2  # rk_ratchet_update_multi: the gradient as float32 split partials
+
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _u64 = ctypes.c_uint64
 _f32 = ctypes.c_float
 _p = ctypes.c_void_p
+
+
+class UpdateLayer(ctypes.Structure):
+    """One entry of rk_ratchet_update_multi's layer table (rk_update_layer, 160 bytes):
+    device addresses as integers (0 = absent), strides and sizes in elements."""
+
+    _fields_ = [
+        ("packed", _u64), ("g", _u64), ("counts", _u64), ("row_rms", _u64),
+        ("rms_ema", _u64), ("grad_scale", _u64), ("nonfinite", _u64), ("reserved0", _u64),
+        ("ldp", _i64), ("ldg", _i64), ("rows", _i64), ("K", _i64), ("row_begin", _i64),
+        ("reserved1", _i64),
+        ("max_code", ctypes.c_int32), ("threshold", ctypes.c_int32), ("nsplit", ctypes.c_int32),
+        ("reserved2", ctypes.c_int32),
+        ("low", _f32), ("high", _f32), ("eps", _f32), ("beta1", _f32), ("beta2", _f32),
+        ("reserved3", _f32 * 3),
+    ]
+
 
 # name -> argument types (all return int status, except where noted)
 SIGNATURES: dict[str, list] = {
@@ -69,6 +88,7 @@ SIGNATURES: dict[str, list] = {
                                _f32, _p, _f32, _f32, _p, _p, _p, _p, _p, _p],
     "rk_ratchet_update_partials": [_p, _i64, _p, _i32, _i64, _i64, _i32, _i32, _f32, _f32,
                                    _f32, _p, _f32, _f32, _p, _p, _p, _p, _p, _p, _i64, _p],
+    "rk_ratchet_update_multi": [_p, _p, _i32, _i32, _p],
     "rk_normalize_rows": [_p, _i32, _i64, _i64, _i64, _f32, _p, _f32, _f32, _p, _i64, _p, _p],
     "rk_pressure_leak": [_p, _i64, _i32, _p],
     "rk_validate_state": [_p, _i64, _i32, _p, _i64, _p, _p],

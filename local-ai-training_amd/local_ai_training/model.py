@@ -29,7 +29,7 @@ from .int8_fused import (
     FusedRMSNormQuantizeResidualFn,
     FusedTransposeQuantizeFn,
 )
-from .ratchet import DiscreteRatchetLinear, RatchetEmbedding, RatchetUpdateStats
+from .ratchet import DiscreteRatchetLinear, RatchetEmbedding, RatchetUpdateStats, UpdateQueue
 
 
 @dataclass(frozen=True)
@@ -582,7 +582,32 @@ class RatchetGPT(nn.Module):
             m._rms_slot = rms[bounds[i]:bounds[i + 1]]
             m._rms_slot_bounds = torch.tensor([0, sizes[i]], dtype=torch.int64, device=device)
 
+    def defer_ratchet_updates(self, enabled: bool = True) -> None:
+        """Batch the ratchet layers' fused updates: backward queues each layer's update
+        instead of launching it, and the next ``ratchet_update()`` (or
+        ``flush_ratchet_updates()``, ``discard_pending_gradients()``, or a queued layer's
+        next forward) runs them together, a few launches for the whole model. States, move
+        counts, row rms and EMA after ``ratchet_update()`` are bit-identical to the
+        per-layer updates; between backward and that call the layers hold their pre-update
+        states. Layers that need a trainable-scale gradient from backward, or keep their
+        weight gradient, still update inside backward."""
+        queue = UpdateQueue() if enabled else None
+        old = getattr(self, "_update_queue", None)
+        if old is not None:
+            old.flush()
+        for m in self.modules():
+            if isinstance(m, DiscreteRatchetLinear):
+                m._update_queue = queue
+        self._update_queue = queue
+
+    def flush_ratchet_updates(self) -> None:
+        """Run the updates backward queued (``defer_ratchet_updates``), if any."""
+        queue = getattr(self, "_update_queue", None)
+        if queue is not None:
+            queue.flush()
+
     def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
+        self.flush_ratchet_updates()
         layers = [m for m in self.modules() if isinstance(m, DiscreteRatchetLinear)]
         buf = getattr(self, "_count_slots", None)
         shared = (buf is not None and buf.shape[0] == len(layers)
@@ -636,6 +661,7 @@ class RatchetGPT(nn.Module):
         return aggregated.materialize() if validate else aggregated
 
     def discard_pending_gradients(self) -> None:
+        self.flush_ratchet_updates()
         for module in self.modules():
             if isinstance(module, DiscreteRatchetLinear):
                 module.discard_pending_gradient()

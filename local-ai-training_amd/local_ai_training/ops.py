@@ -115,7 +115,7 @@ def _register_fakes() -> None:
         return g.new_empty((g.shape[1], x.shape[1]), dtype=torch.bfloat16)
 
     for name in ("grad_weight_partials", "grad_weight_partials_x", "update_from_z",
-                 "update_from_grad", "update_from_partials", "pressure_leak"):
+                 "update_from_grad", "update_from_partials", "update_multi", "pressure_leak"):
         fake(f"ratchet::{name}")(lambda *args, **kwargs: None)
 
     @fake("ratchet::normalize_rows")
@@ -195,7 +195,8 @@ OPERATORS = (
     "dequant_bf16",
     "transpose_bf16", "dequant_transpose_bf16", "grad_weight_splits", "grad_weight",
     "grad_weight_x", "grad_weight_partials", "grad_weight_partials_x", "update_from_z",
-    "update_from_grad", "update_from_partials", "normalize_rows", "pressure_leak",
+    "update_from_grad", "update_from_partials", "update_multi", "normalize_rows",
+    "pressure_leak",
     "validate_state", "rmsnorm_quantize", "gelu_quantize", "transpose_quantize",
     "rmsnorm_backward", "gelu_backward", "embedding_backward", "quantize_rows_parts",
     "grad_weight_partials_parts", "cross_entropy_forward",

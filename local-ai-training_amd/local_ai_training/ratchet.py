@@ -54,6 +54,7 @@ from .int8_matmul import (
     transpose_bf16,
     unpack_transpose,
 )
+from . import _native
 from .ops import ratchet as _ops
 
 
@@ -430,6 +431,9 @@ class _RatchetMatmul(torch.autograd.Function):
                     inputs_t = transpose_bf16(x_direct)
                 grad_weight = grad_t @ inputs_t.t()
         if side is not None:
+            # joined here even when the update is queued: left to run ahead, grad_weight's
+            # backlog on the side stream slows the next layers' backward (1B step measured
+            # 0.6 ms slower)
             torch.cuda.current_stream(partials.device).wait_stream(side)
             partials.record_stream(torch.cuda.current_stream(partials.device))
         if partials is not None:
@@ -521,6 +525,129 @@ def _gradient_parts(ctx, layer, grads) -> list[Tensor] | None:
     if not grad_weight_parts_supported(parts, ctx.saved_tensors[0]):
         return None
     return parts
+
+
+class UpdateQueue:
+    """Fused updates that backward queued instead of launching one per layer, run together
+    by ``flush``: the queued layers of one gradient source (a bf16 or float32 gradient, or
+    float32 split partials) and row-length class go to one ``rk_ratchet_update_multi``
+    launch, which runs each row through the per-layer update's code (bit-identical states,
+    counts, row rms, EMA and non-finite flags). The layer tables live on the device and are
+    kept while the layers' buffers stay where they are, so a replayed graph reuses them with
+    no host work; a table that would have to be built during graph capture is not (the
+    group's layers are then updated one launch each)."""
+
+    def __init__(self) -> None:
+        self._entries: list[tuple] = []
+        self._tables: dict[tuple, tuple[Tensor, Tensor]] = {}
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    def push(self, layer: "DiscreteRatchetLinear", gradient: Tensor, from_partials: bool,
+             counts: Tensor, row_rms: Tensor, nonfinite: Tensor) -> None:
+        layer._queued = True
+        self._entries.append((layer, gradient, from_partials, counts, row_rms, nonfinite))
+
+    @staticmethod
+    def _source(gradient: Tensor, from_partials: bool) -> tuple[int, Tensor, int]:
+        """(source code, the [rows, K] gradient or [nsplit, rows, K] partials, nsplit)."""
+        if from_partials and gradient.dtype == torch.bfloat16:
+            return _native.RK_BF16, gradient[0], 1  # one split, written as the gradient
+        if from_partials:
+            return _native.RK_UPDATE_SRC_SPLITS, gradient, gradient.shape[0]
+        if gradient.dtype == torch.bfloat16:
+            return _native.RK_BF16, gradient, 1
+        return _native.RK_F32, gradient, 1
+
+    @staticmethod
+    def _chunk_class(src: int, k: int) -> int:
+        """The update kernel's register-resident chunk count for rows of k elements."""
+        if src == _native.RK_F32:
+            chunks = (k + 255) // 256
+            return 2 if chunks <= 2 else (8 if chunks <= 8 else 0)
+        chunks = (k + 511) // 512
+        return 1 if chunks <= 1 else (4 if chunks <= 4 else (12 if chunks <= 12 else 0))
+
+    def flush(self) -> None:
+        if not self._entries:
+            return
+        entries, self._entries = self._entries, []
+        device = entries[0][1].device
+        main = torch.cuda.current_stream(device)
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        side = _SIDE_STREAMS.get(index)
+        if side is not None:
+            # grad_weight may still be running on the side stream: its workspaces are
+            # complete only after this join (backward left it to the queue)
+            main.wait_stream(side)
+        groups: dict[tuple, list] = {}
+        for entry in entries:
+            layer, gradient, from_partials = entry[0], entry[1], entry[2]
+            src, g, nsplit = self._source(gradient, from_partials)
+            if g.dtype == torch.float32 and src != _native.RK_UPDATE_SRC_SPLITS:
+                g = g.contiguous()
+            key = (src, self._chunk_class(src, layer.in_features), nsplit == 1)
+            groups.setdefault(key, []).append((layer, g, nsplit) + tuple(entry[3:]))
+        for (src, _, _), group in groups.items():
+            self._launch(src, group, device)
+        for entry in entries:
+            entry[0]._queued = False
+
+    def _launch(self, src: int, group: list, device: torch.device) -> None:
+        key = tuple((layer.packed.data_ptr(), g.data_ptr(), tuple(g.shape), tuple(g.stride()),
+                     counts.data_ptr(), row_rms.data_ptr(), nonfinite.data_ptr(),
+                     layer._ema_ptr(), layer._rule_key())
+                    for layer, g, nsplit, counts, row_rms, nonfinite in group) + (src,)
+        tables = self._tables.get(key)
+        if tables is None:
+            if torch.cuda.is_current_stream_capturing():
+                # building a table here would record a host-to-device copy: update the
+                # group's layers one launch each instead
+                for layer, g, nsplit, counts, row_rms, nonfinite in group:
+                    layer._launch_update(g, counts, row_rms, None, nonfinite,
+                                         from_partials=src == _native.RK_UPDATE_SRC_SPLITS,
+                                         defer_mean=True, count_generation=False)
+                return
+            tables = self._build(src, group, device)
+            self._tables[key] = tables
+        written = []
+        for layer, g, nsplit, counts, row_rms, nonfinite in group:
+            written += [layer.packed, counts, row_rms, nonfinite]
+            if layer._ema_ptr():
+                written.append(layer.rms_ema)
+        _ops().update_multi(tables[0], tables[1], src, written)
+
+    @staticmethod
+    def _build(src: int, group: list, device: torch.device) -> tuple[Tensor, Tensor]:
+        import ctypes
+
+        entries = (_native.UpdateLayer * len(group))()
+        row = 0
+        for d, (layer, g, nsplit, counts, row_rms, nonfinite) in zip(entries, group):
+            rows, k = layer.out_features, layer.in_features
+            d.packed = layer.packed.data_ptr()
+            d.g = g.data_ptr()
+            d.counts = counts.data_ptr()
+            d.row_rms = row_rms.data_ptr()
+            d.rms_ema = layer._ema_ptr()
+            d.grad_scale = 0
+            d.nonfinite = nonfinite.data_ptr()
+            d.ldp = layer.packed.stride(0)
+            d.ldg = g.stride(-2)
+            d.rows, d.K, d.row_begin = rows, k, row
+            d.max_code, d.threshold, d.nsplit = layer.max_code, layer.pressure_threshold, nsplit
+            beta = layer.rms_ema_beta
+            d.low, d.high, d.eps = layer.bucket_low, layer.bucket_high, layer.eps
+            # beta2 = 1 - beta in float32, as the per-layer operator computes it
+            d.beta1 = beta
+            d.beta2 = float(torch.tensor(1.0, dtype=torch.float32)
+                            - torch.tensor(beta, dtype=torch.float32))
+            row += rows
+        host = torch.frombuffer(bytearray(ctypes.string_at(ctypes.addressof(entries),
+                                                           ctypes.sizeof(entries))),
+                                dtype=torch.uint8)
+        return host, host.to(device)
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -651,6 +778,11 @@ class DiscreteRatchetLinear(nn.Module):
         # model (``row_rms_means``) instead of one per layer
         self._rms_slot: Tensor | None = None
         self._rms_slot_bounds: Tensor | None = None
+        # a model that batches its layers' fused updates hands every layer one UpdateQueue:
+        # backward then queues this layer's update there, and the queue runs it together
+        # with the others (before the layer's next forward or statistics at the latest)
+        self._update_queue: UpdateQueue | None = None
+        self._queued = False
         self._reset_pending_stats()
 
     # -- state ----------------------------------------------------------------
@@ -733,6 +865,8 @@ class DiscreteRatchetLinear(nn.Module):
         shapes allow, the same float32 add). ``split`` > 1: return
         ``output.chunk(split, dim=-1)``; on the fused int8-backward path the chunks'
         gradients are then read in place rather than concatenated (the same results)."""
+        if self._queued:
+            self._update_queue.flush()  # this forward reads the updated state
         if self.matmul_mode != "fp32" or self.fuse_backward_update:
             return _RatchetMatmul.apply(inputs, inputs_int8, inputs_scale, self.packed,
                                         self.scale, self, out_dtype, residual, split)
@@ -775,7 +909,8 @@ class DiscreteRatchetLinear(nn.Module):
 
     def _launch_update(self, gradient: Tensor, counts: Tensor, row_rms: Tensor | None,
                        grad_scale: Tensor | None, nonfinite: Tensor | None, *,
-                       from_partials: bool = False, defer_mean: bool = False) -> None:
+                       from_partials: bool = False, defer_mean: bool = False,
+                       count_generation: bool = True) -> None:
         """One update launch from a weight gradient [N, K], or (``from_partials``) from the
         grad_weight GEMM's float32 split partials [nsplit, N, K], reduced inside the update
         with the same arithmetic. With ``keep_weight_gradient`` set, the bf16 gradient the
@@ -808,7 +943,27 @@ class DiscreteRatchetLinear(nn.Module):
             _ops().update_from_grad(self.packed, gradient, *rule)
             self.last_weight_gradient = gradient if self.keep_weight_gradient else None
         self._last_rms_mean = rms_mean
-        self._generation += 1
+        if count_generation:
+            self._generation += 1
+
+    def _ema_ptr(self) -> int:
+        """Device address of the per-row rms EMA, 0 without one."""
+        ema = getattr(self, "rms_ema", None) if self.rms_ema_beta > 0.0 else None
+        return 0 if ema is None else ema.data_ptr()
+
+    def _rule_key(self) -> tuple:
+        return (self.max_code, self.pressure_threshold, self.bucket_low, self.bucket_high,
+                self.eps, self.rms_ema_beta)
+
+    def _will_queue(self, want_grad_scale: bool, device: torch.device) -> bool:
+        """Whether the fused update of this backward goes to the model's queue: a queue is
+        attached, no trainable-scale gradient is wanted (backward must return it), no copy
+        of the gradient is kept, and the row rms go to the model's buffer."""
+        slot = self._rms_slot
+        return (self._update_queue is not None and not want_grad_scale
+                and not self.keep_weight_gradient and device.type == "cuda"
+                and slot is not None and slot.device == device
+                and None not in self._pending_rms_means)
 
     def _fused_update(self, grad_weight: Tensor, *, want_grad_scale: bool,
                       from_partials: bool = False) -> Tensor | None:
@@ -816,6 +971,15 @@ class DiscreteRatchetLinear(nn.Module):
         ``grad_weight`` is the gradient, or its split partials with ``from_partials``."""
         if grad_weight.shape[-2:] != (self.out_features, self.in_features):
             raise ValueError("fused gradient shape mismatch")
+        if self._will_queue(want_grad_scale, grad_weight.device):
+            self._update_queue.push(self, grad_weight, from_partials, self._counts(),
+                                    self._rms_slot, self._nonfinite_flag())
+            self._pending_stats_total_weights += self.out_features * self.in_features
+            self._pending_rms_means.append(None)
+            self._last_rms_mean = None
+            self.last_weight_gradient = None
+            self._generation += 1
+            return None
         slot = self._rms_slot
         defer = (slot is not None and slot.device == grad_weight.device
                  and None not in self._pending_rms_means)
@@ -916,6 +1080,8 @@ class DiscreteRatchetLinear(nn.Module):
             raise FloatingPointError("ratchet gradient contains NaN or Inf")
 
     def ratchet_update(self, *, validate: bool = True) -> RatchetUpdateStats:
+        if self._queued:
+            self._update_queue.flush()
         if self.fuse_backward_update:
             if validate:
                 self.check_finite_gradients()
@@ -964,6 +1130,9 @@ class DiscreteRatchetLinear(nn.Module):
         return stats.materialize() if validate else stats
 
     def discard_pending_gradient(self) -> None:
+        if self._queued:
+            # a queued fused update is applied, as the reference applied it inside backward
+            self._update_queue.flush()
         self._pending_weight_gradient = None
         self._effective_weight = None
 

@@ -23,6 +23,7 @@ MUTATED = {
                          "rms_mean"},
     "update_from_partials": {"packed", "rms_ema", "counts", "row_rms", "grad_scale",
                              "nonfinite", "rms_mean", "grad_out"},
+    "update_multi": {"written"},
     "normalize_rows": {"rms_ema"},
     "pressure_leak": {"packed"},
     "quantize_rows": {"x_bf16"},
