@@ -606,7 +606,8 @@ STEP_CLASSES = [
     ("fused ratchet update", r"ratchet_update|row_rms_(segment_)?mean"),
     ("prologue backward (RMSNorm/GELU)", r"rmsnorm_bwd|rmsnorm_gw_reduce|gelu_bwd"),
     ("attention (HIP forward, torch memory-efficient backward)", r"attn|fmha|flash|bwd_preprocess|bwd_postprocess"),
-    ("bf16 GEMM (hipBLASLt, lm_head grad_input)", r"Cijk_|gemm"),
+    ("bf16 grad_input (lm_head, MFMA on packed codes)", r"grad_input_bf16_kernel|effective_fragments"),
+    ("bf16 GEMM (hipBLASLt)", r"Cijk_|gemm"),
     ("effective bf16 weights", r"effective_bf16"),
     ("optimizer (AdamW)", r"multi_tensor|adam"),
     ("loss (cross-entropy) / reductions", r"xent|reduce|softmax|nll|cross_entropy"),

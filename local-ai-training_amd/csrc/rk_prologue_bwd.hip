@@ -13,9 +13,9 @@
 //   the hardware exp2 and reciprocal (absolute error < 3e-7, see tanh_fast).
 //
 // Both are HBM-bound streams. The RMSNorm kernel keeps a whole row in registers (one
-// wavefront per row, 4 columns per lane per 256-column chunk, K <= 4096), so x and
-// grad_y are read once, dx is written once, and grad_w is accumulated per lane over
-// the block's rows. Each block writes its grad_w partial; a second kernel sums the
+// wavefront per row up to 1024 columns, 2 or 4 wavefronts per row up to 4096; 4 columns
+// per lane per 256-column chunk), so x and grad_y are read once, dx is written once, and
+// grad_w is accumulated per lane over the block's rows. Each block writes its grad_w partial; a second kernel sums the
 // partials in block order, so grad_w is reproducible run to run (no float atomics).
 #include "rk_common.h"
 
@@ -104,15 +104,15 @@ struct NormBwdArgs {
   int64_t lda;
 };
 
-// One row's x, grad_y and (float32 x with a residual gradient) the residual gradient, all
-// requested before any is used.
+// One row's x, grad_y and (float32 x with a residual gradient) the residual gradient from
+// column c0 on, all requested before any is used.
 template <int GDT, int XDT, int NC>
 __device__ __forceinline__ void norm_load_row(const NormBwdArgs& a, int64_t row, int lane,
-                                              float (&xv)[NC][kBwdV], float (&gv)[NC][kBwdV],
-                                              float (&av)[NC][kBwdV]) {
+                                              int64_t c0, float (&xv)[NC][kBwdV],
+                                              float (&gv)[NC][kBwdV], float (&av)[NC][kBwdV]) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+    const int64_t e0 = c0 + c * kBwdSpan + lane * kBwdV;
     const int n = quad_valid(a.K, e0);
     load4<XDT>(a.x, row * a.ldx + e0, n, a.vec, xv[c]);
     load4<GDT>(a.gy, row * a.ldg + e0, n, a.vec, gv[c]);
@@ -122,14 +122,23 @@ __device__ __forceinline__ void norm_load_row(const NormBwdArgs& a, int64_t row,
   }
 }
 
-// One block = 4 wavefronts = rows [blockIdx.x * rows_per_block, +rows_per_block); wave w
-// takes rows w, w + 4, ... of that range. PREFETCH issues the next row's loads before
-// the current row's reductions (small NC only: it doubles the row registers).
-template <int GDT, int XDT, int NC, bool PREFETCH>
+// One block = 4 wavefronts over rows [blockIdx.x * rows_per_block, +rows_per_block). P
+// wavefronts share a row (P = 1, 2 or 4), each holding NC 256-column chunks of it: wave w
+// takes column slice w % P of rows w / P, w / P + 4 / P, ... With P > 1 the slices' sums of
+// squares and of grad_y * w * x meet in LDS (one barrier per row step; the slices are added
+// in slice order) and every slice finishes its own columns. Long rows so keep NC <= 4: the
+// next row's loads are issued before the current row's reductions (PREFETCH) without
+// lowering the occupancy, and there are enough rows in flight per CU to stream HBM.
+template <int GDT, int XDT, int NC, bool PREFETCH, int P>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
-  __shared__ __attribute__((aligned(16))) float red[4][NC * kBwdSpan];
+  constexpr int G = 4 / P;                 // rows per block step
+  constexpr int COLS = P * NC * kBwdSpan;  // columns one row step covers
+  __shared__ __attribute__((aligned(16))) float red[G][COLS];
+  __shared__ float sums[2][4][2];          // [step parity][wave] (sum x*x, sum g*w*x)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
+  const int slice = wave % P, grp = wave / P;
+  const int64_t c0 = static_cast<int64_t>(slice) * NC * kBwdSpan;  // the slice's first column
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * a.rows_per_block;
   const int64_t r1 = r0 + a.rows_per_block < a.M ? r0 + a.rows_per_block : a.M;
   const float kf = static_cast<float>(a.K);
@@ -138,61 +147,84 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
   int nv[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    const int64_t e0 = c * kBwdSpan + lane * kBwdV;
+    const int64_t e0 = c0 + c * kBwdSpan + lane * kBwdV;
     nv[c] = quad_valid(a.K, e0);
     load4<RK_F32>(a.w, e0, nv[c], a.vec, wv[c]);
 #pragma unroll
     for (int i = 0; i < kBwdV; ++i) gw[c][i] = 0.0f;
   }
 
-  int64_t row = r0 + wave;
+  // the same step count in every wavefront of the block (the LDS exchange has a barrier)
+  const int steps = static_cast<int>((r1 - r0 + G - 1) / G);
+  int64_t row = r0 + grp;
   float xv[NC][kBwdV], gv[NC][kBwdV], av[NC][kBwdV];
-  if (row < r1) norm_load_row<GDT, XDT, NC>(a, row, lane, xv, gv, av);
-  while (row < r1) {
-    const int64_t next = row + 4;
+  if (row < r1) norm_load_row<GDT, XDT, NC>(a, row, lane, c0, xv, gv, av);
+  for (int st = 0; st < steps; ++st) {
+    const bool valid = row < r1;  // uniform in the wavefront
+    const int64_t next = row + G;
     float xn[NC][kBwdV], gn[NC][kBwdV], an[NC][kBwdV];
     if constexpr (PREFETCH) {
-      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xn, gn, an);
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, c0, xn, gn, an);
     }
     float sxx = 0.0f, sgx = 0.0f;
+    if (valid) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
-      for (int i = 0; i < kBwdV; ++i) {
-        sxx = sxx + xv[c][i] * xv[c][i];
-        sgx = sgx + (gv[c][i] * wv[c][i]) * xv[c][i];
-      }
+        for (int i = 0; i < kBwdV; ++i) {
+          sxx = sxx + xv[c][i] * xv[c][i];
+          sgx = sgx + (gv[c][i] * wv[c][i]) * xv[c][i];
+        }
+    }
     sxx = wave_sum_butterfly(sxx);
     sgx = wave_sum_butterfly(sgx);
-    const float rs = 1.0f / sqrtf(sxx / kf + a.eps);
-    const float dvar = sgx * -0.5f * (rs * rs * rs);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      float dx[kBwdV];
-#pragma unroll
-      for (int i = 0; i < kBwdV; ++i) {
-        dx[i] = (gv[c][i] * wv[c][i]) * rs + dvar * 2.0f * xv[c][i] / kf;
-        gw[c][i] = gw[c][i] + gv[c][i] * xv[c][i] * rs;
+    if constexpr (P > 1) {
+      // two parity buffers: a slot is rewritten two steps later, after the next step's
+      // barrier, which every wavefront reaches only once it has read this step's sums
+      if (lane == 0) {
+        sums[st & 1][wave][0] = sxx;
+        sums[st & 1][wave][1] = sgx;
       }
-      const int64_t e0 = c * kBwdSpan + lane * kBwdV;
-      if constexpr (XDT == RK_F32) {
-        if (a.add && nv[c] > 0) {
-          // the residual stream's gradient joins here: one float32 add of the two
-          // contributions, the add autograd performs where x feeds both paths
+      __syncthreads();
+      sxx = sums[st & 1][grp * P][0];
+      sgx = sums[st & 1][grp * P][1];
 #pragma unroll
-          for (int i = 0; i < kBwdV; ++i) dx[i] = round_bf16(dx[i]) + av[c][i];
-          float* p = static_cast<float*>(a.gx) + row * a.ldgx + e0;
-          if (a.vec && nv[c] == 4) {
-            *reinterpret_cast<float4*>(p) = make_float4(dx[0], dx[1], dx[2], dx[3]);
-          } else {
+      for (int q = 1; q < P; ++q) {
+        sxx = sxx + sums[st & 1][grp * P + q][0];
+        sgx = sgx + sums[st & 1][grp * P + q][1];
+      }
+    }
+    if (valid) {
+      const float rs = 1.0f / sqrtf(sxx / kf + a.eps);
+      const float dvar = sgx * -0.5f * (rs * rs * rs);
 #pragma unroll
-            for (int i = 0; i < kBwdV; ++i)
-              if (i < nv[c]) p[i] = dx[i];
-          }
-          continue;
+      for (int c = 0; c < NC; ++c) {
+        float dx[kBwdV];
+#pragma unroll
+        for (int i = 0; i < kBwdV; ++i) {
+          dx[i] = (gv[c][i] * wv[c][i]) * rs + dvar * 2.0f * xv[c][i] / kf;
+          gw[c][i] = gw[c][i] + gv[c][i] * xv[c][i] * rs;
         }
+        const int64_t e0 = c0 + c * kBwdSpan + lane * kBwdV;
+        if constexpr (XDT == RK_F32) {
+          if (a.add && nv[c] > 0) {
+            // the residual stream's gradient joins here: one float32 add of the two
+            // contributions, the add autograd performs where x feeds both paths
+#pragma unroll
+            for (int i = 0; i < kBwdV; ++i) dx[i] = round_bf16(dx[i]) + av[c][i];
+            float* p = static_cast<float*>(a.gx) + row * a.ldgx + e0;
+            if (a.vec && nv[c] == 4) {
+              *reinterpret_cast<float4*>(p) = make_float4(dx[0], dx[1], dx[2], dx[3]);
+            } else {
+#pragma unroll
+              for (int i = 0; i < kBwdV; ++i)
+                if (i < nv[c]) p[i] = dx[i];
+            }
+            continue;
+          }
+        }
+        if (nv[c] > 0) store4_bf16<XDT>(a.gx, row * a.ldgx + e0, nv[c], a.vec, dx);
       }
-      if (nv[c] > 0) store4_bf16<XDT>(a.gx, row * a.ldgx + e0, nv[c], a.vec, dx);
     }
     if constexpr (PREFETCH) {
 #pragma unroll
@@ -204,20 +236,24 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(NormBwdArgs a) {
           av[c][i] = an[c][i];
         }
     } else {
-      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, xv, gv, av);
+      if (next < r1) norm_load_row<GDT, XDT, NC>(a, next, lane, c0, xv, gv, av);
     }
     row = next;
   }
 
-  // Block partial: the four waves' column sums, added in wave order.
+  // Block partial: the row groups' column sums, added in group order.
 #pragma unroll
   for (int c = 0; c < NC; ++c)
-    *reinterpret_cast<float4*>(&red[wave][c * kBwdSpan + lane * kBwdV]) =
+    *reinterpret_cast<float4*>(&red[grp][c0 + c * kBwdSpan + lane * kBwdV]) =
         make_float4(gw[c][0], gw[c][1], gw[c][2], gw[c][3]);
   __syncthreads();
   float* out = a.part + static_cast<int64_t>(blockIdx.x) * a.K;
-  for (int64_t col = threadIdx.x; col < a.K; col += 256)
-    out[col] = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
+  for (int64_t col = threadIdx.x; col < a.K; col += 256) {
+    float t = red[0][col];
+#pragma unroll
+    for (int q = 1; q < G; ++q) t = t + red[q][col];
+    out[col] = t;
+  }
 }
 
 // grad_w[k] = sum of part[p][k] over p: 16 columns x 16 part-groups per block; group g
@@ -331,20 +367,18 @@ bool vec4_ok(const void* p, int dt, int64_t ld, int64_t K) {
   return (reinterpret_cast<uintptr_t>(p) % align) == 0 && ld % 4 == 0 && K % 4 == 0;
 }
 
-template <int GDT, int XDT, int NC>
-void launch_norm_nc(const NormBwdArgs& a, dim3 grid, hipStream_t st) {
-  constexpr bool kPrefetch = NC <= 4;
-  rmsnorm_bwd_kernel<GDT, XDT, NC, kPrefetch><<<grid, dim3(256), 0, st>>>(a);
-}
-
+// Rows of up to 512 columns: one wavefront per row; longer rows: 2 or 4 wavefronts per row
+// with at most 2 chunks each up to 2048 columns, 4 beyond. (K = 2048 with one wavefront per
+// row and 8 chunks held 253 VGPRs, so no prefetch and one wavefront per SIMD: 80 us for
+// 8192 rows of float32 x, grad_y and residual gradient, 3.4 TB/s.)
 template <int GDT, int XDT>
 int launch_norm(const NormBwdArgs& a, dim3 grid, hipStream_t st) {
   const int64_t nc = (a.K + kBwdSpan - 1) / kBwdSpan;
-  if (nc <= 1) launch_norm_nc<GDT, XDT, 1>(a, grid, st);
-  else if (nc <= 2) launch_norm_nc<GDT, XDT, 2>(a, grid, st);
-  else if (nc <= 4) launch_norm_nc<GDT, XDT, 4>(a, grid, st);
-  else if (nc <= 8) launch_norm_nc<GDT, XDT, 8>(a, grid, st);
-  else launch_norm_nc<GDT, XDT, 16>(a, grid, st);
+  if (nc <= 1) rmsnorm_bwd_kernel<GDT, XDT, 1, true, 1><<<grid, dim3(256), 0, st>>>(a);
+  else if (nc <= 2) rmsnorm_bwd_kernel<GDT, XDT, 2, true, 1><<<grid, dim3(256), 0, st>>>(a);
+  else if (nc <= 4) rmsnorm_bwd_kernel<GDT, XDT, 2, true, 2><<<grid, dim3(256), 0, st>>>(a);
+  else if (nc <= 8) rmsnorm_bwd_kernel<GDT, XDT, 2, true, 4><<<grid, dim3(256), 0, st>>>(a);
+  else rmsnorm_bwd_kernel<GDT, XDT, 4, true, 4><<<grid, dim3(256), 0, st>>>(a);
   return launch_status("rmsnorm_backward");
 }
 
