@@ -50,7 +50,7 @@ struct GwArgs {
   uint16_t* out;    // one split: the bf16 gradient [N, K] (row stride ldo) written directly
   int64_t ldo;
   int64_t M, N, K;
-  int64_t m_chunk;  // tokens per split, a multiple of GW_BM
+  int64_t m_chunk;  // tokens per split, a multiple of the block's tokens per step
   int nsplit;
   // fused update (rk_grad_weight_update): the update's arguments over these partials, the
   // arrival counters (one per FEAT-row block, then one for the layer) and the arrivals that
@@ -75,20 +75,26 @@ __device__ __forceinline__ uint32_t gw_pack_bf16x2(float lo, float hi) {
 }
 
 // Block configurations: FEAT x FEAT output tiles (n x k) over WN x WK wavefronts, each a
-// (FEAT / WN) x (FEAT / WK) wave tile of 32 x 32 MFMA blocks; staged LDS rows of FEAT bf16
-// features plus 64 bytes (the pitch keeps consecutive token rows 16 banks apart).
-//  * 128 x 128, 2 x 2 waves: the op shape and small layers;
+// (FEAT / WN) x (FEAT / WK) wave tile of 32 x 32 MFMA blocks, times TG token groups; staged
+// LDS rows of FEAT bf16 features plus 64 bytes (the pitch keeps consecutive token rows 16
+// banks apart). With TG = 2 a pipeline step stages 2 x 32 tokens once for two sets of
+// WN x WK wavefronts, each set contracting its own 32 tokens; the second set's sums are
+// added to the first's through LDS at the end (one fixed add per output), so the block
+// covers twice the tokens per split with the same MFMAs per wavefront between barriers.
+//  * 128 x 128, 2 x 2 waves x 2 token groups: the op shape and small layers (one 8-wave
+//    block per CU: half the split partials of two 4-wave blocks, and each staged tile -
+//    its loads, its int8 -> bf16 conversion, its LDS writes - serves 8 wavefronts);
 //  * 256 x 256, 2 x 4 waves: large layers. A 128 x 128 bf16 tile fetches 64 bytes of g and
 //    X per token step for 1 MFLOP, about the whole L2 bandwidth at the bf16 MFMA peak; the
 //    large tile halves the bytes per FLOP.
-template <int FEAT_, int WN_, int WK_>
+template <int FEAT_, int WN_, int WK_, int TG_ = 1>
 struct GwCfg {
-  static constexpr int FEAT = FEAT_, WN = WN_, WK = WK_;
-  static constexpr int THREADS = 64 * WN * WK;
+  static constexpr int FEAT = FEAT_, WN = WN_, WK = WK_, TG = TG_;
+  static constexpr int THREADS = 64 * WN * WK * TG;
   static constexpr int PITCH = FEAT * 2 + 64;
   static constexpr int MI = FEAT / WN / 32, NJ = FEAT / WK / 32;
 };
-using GwSmall = GwCfg<128, 2, 2>;
+using GwSmall = GwCfg<128, 2, 2, 2>;
 using GwBig = GwCfg<256, 2, 4>;
 
 // A [BM tokens][FEAT features] tile of an operand with ES-byte elements is read as
@@ -160,10 +166,11 @@ void grad_weight_partial_kernel(GwArgs a) {
   constexpr int XE = XK == GW_X_Q8 ? 1 : (XK == GW_X_BF16 ? 2 : 4);  // X element bytes
   constexpr int FEAT = CFG::FEAT, THREADS = CFG::THREADS, PITCH = CFG::PITCH;
   constexpr int MI = CFG::MI, NJ = CFG::NJ;
-  using GP = GwPieces<GE, BM, FEAT, THREADS>;
-  using XP = GwPieces<XE, BM, FEAT, THREADS>;
+  constexpr int SB = BM * CFG::TG;  // tokens per pipeline step (all token groups)
+  using GP = GwPieces<GE, SB, FEAT, THREADS>;
+  using XP = GwPieces<XE, SB, FEAT, THREADS>;
   constexpr int GV = GP::kPerThread, XV = XP::kPerThread;
-  constexpr int TILE = BM * PITCH;  // one staged operand tile
+  constexpr int TILE = SB * PITCH;  // one staged operand tile
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * TILE];
 
   const int64_t tiles_k = (a.K + FEAT - 1) / FEAT;
@@ -176,11 +183,12 @@ void grad_weight_partial_kernel(GwArgs a) {
   const int64_t n0 = (t / tiles_k) * FEAT, k0 = (t % tiles_k) * FEAT;
   const int64_t m_begin = split * a.m_chunk;
   const int64_t m_end = min(a.M, m_begin + a.m_chunk);
-  const int steps = m_end > m_begin ? static_cast<int>((m_end - m_begin + BM - 1) / BM) : 0;
+  const int steps = m_end > m_begin ? static_cast<int>((m_end - m_begin + SB - 1) / SB) : 0;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave % CFG::WN, wk = wave / CFG::WN;
+  const int tg = wave / (CFG::WN * CFG::WK), wl = wave % (CFG::WN * CFG::WK);  // token group
+  const int wn = wl % CFG::WN, wk = wl / CFG::WN;
   const int nw0 = wn * (FEAT / CFG::WN), kw0 = wk * (FEAT / CFG::WK);  // wave tile origin
 
   // Buffer descriptors over this block's token range. num_records ends at the last valid
@@ -220,8 +228,8 @@ void grad_weight_partial_kernel(GwArgs a) {
     x_lds[j] = TILE + XP::row(c) * PITCH + XP::col(c) * 2;
     s_voff[j] = XP::row(c) * 4;
   }
-  const int g_step = BM * static_cast<int>(a.ldg) * GE;
-  const int x_step = BM * static_cast<int>(a.ldx) * XE;
+  const int g_step = SB * static_cast<int>(a.ldg) * GE;
+  const int x_step = SB * static_cast<int>(a.ldx) * XE;
 
   auto load_slot = [&](GwSlot<GV, XV>& r, int step) {
 #pragma unroll
@@ -236,7 +244,7 @@ void grad_weight_partial_kernel(GwArgs a) {
 #pragma unroll
       for (int j = 0; j < XV; ++j)
         r.s[j] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, s_voff[j], step * BM * 4, 0));
+            float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, s_voff[j], step * SB * 4, 0));
     }
   };
   // `tile` is the g tile of one LDS buffer; the X tile follows it.
@@ -326,10 +334,10 @@ void grad_weight_partial_kernel(GwArgs a) {
         for (int u = 0; u < U; ++u) {
 #pragma unroll
           for (int i = 0; i < MI; ++i)
-            fa[u][i] = tr16_fragment<PITCH>(gt, 16 * u, nw0 + 32 * i, lane);
+            fa[u][i] = tr16_fragment<PITCH>(gt, BM * tg + 16 * u, nw0 + 32 * i, lane);
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
-            fb[u][j] = tr16_fragment<PITCH>(xt, 16 * u, kw0 + 32 * j, lane);
+            fb[u][j] = tr16_fragment<PITCH>(xt, BM * tg + 16 * u, kw0 + 32 * j, lane);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -359,12 +367,49 @@ void grad_weight_partial_kernel(GwArgs a) {
     }
   }
 
+  if constexpr (CFG::TG == 2) {
+    // token group 1 hands its sums to group 0 through the (now idle) LDS tiles: float4
+    // (i, j, e / 4) of lane l of wave tile wl at float4 index (wl (MI NJ 4) + (i NJ + j) 4 +
+    // e / 4) 64 + l, so each write and read instruction covers 1 KB of consecutive words
+    static_assert(4 * MI * NJ * 16 * 64 * 4 <= 2 * 2 * TILE, "exchange fits the LDS tiles");
+    float4* xch = reinterpret_cast<float4*>(smem) + wl * (MI * NJ * 4 * 64) + lane;
+    __syncthreads();  // every wavefront's last fragment reads are done
+    if (tg == 1) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            xch[((i * NJ + j) * 4 + q) * 64] = make_float4(
+                acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    }
+    __syncthreads();
+    if (tg == 0) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 o = xch[((i * NJ + j) * 4 + q) * 64];
+            acc[i][j][4 * q] = acc[i][j][4 * q] + o.x;
+            acc[i][j][4 * q + 1] = acc[i][j][4 * q + 1] + o.y;
+            acc[i][j][4 * q + 2] = acc[i][j][4 * q + 2] + o.z;
+            acc[i][j][4 * q + 3] = acc[i][j][4 * q + 3] + o.w;
+          }
+    }
+  }
+  // token group 0 holds the block's sums; every wavefront stays for the fused update
+  const bool owner = tg == 0;
+
   // Partial sums: acc[i][j][e] is C[n][k] with k = k0 + kw0 + 32 j + lane % 32 and
   // n = n0 + nw0 + 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4.
   const int lk = lane & 31, lh = lane >> 5;
   if constexpr (BF16OUT) {
     // one split: the sum is complete; round it as grad_weight_reduce_kernel does (the same
     // packed conversion) and store the bf16 gradient, half the bytes of a float32 partial
+    if (!owner) return;
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -380,17 +425,19 @@ void grad_weight_partial_kernel(GwArgs a) {
     return;
   }
   float* out = a.part + static_cast<int64_t>(split) * a.N * a.K;
+  if (owner) {
 #pragma unroll
-  for (int i = 0; i < MI; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const int64_t k = k0 + kw0 + 32 * j + lk;
+      for (int j = 0; j < NJ; ++j) {
+        const int64_t k = k0 + kw0 + 32 * j + lk;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t n = n0 + nw0 + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (n < a.N && k < a.K) out[n * a.K + k] = acc[i][j][e];
+        for (int e = 0; e < 16; ++e) {
+          const int64_t n = n0 + nw0 + 32 * i + 8 * (e >> 2) + 4 * lh + (e & 3);
+          if (n < a.N && k < a.K) out[n * a.K + k] = acc[i][j][e];
+        }
       }
-    }
+  }
 
   if constexpr (UNC >= 0) {
     __shared__ int finisher;
@@ -505,10 +552,11 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
     if (ldg < part_cols) return fail(RK_ERR_ARG, "leading dimension too small");
   }
   const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
-  const int64_t chunk = ((M + nsplit - 1) / nsplit + GW_BM - 1) / GW_BM * GW_BM;
+  const int64_t sb = GW_BM * (big ? GwBig::TG : GwSmall::TG);  // tokens per pipeline step
+  const int64_t chunk = ((M + nsplit - 1) / nsplit + sb - 1) / sb * sb;
   // Buffer offsets are 32-bit: the furthest load of a block (ring padding and prefetch
   // included) must stay below 2^31 bytes from the block's first row.
-  const int64_t reach = chunk + (2 * kGwMaxRing + 1) * GW_BM;
+  const int64_t reach = chunk + (2 * kGwMaxRing + 1) * sb;
   if (reach * ldg * ge >= (int64_t{1} << 31) || reach * ldx * xe >= (int64_t{1} << 31))
     return fail(RK_ERR_UNSUPPORTED,
                 "grad_weight token range too large for 32-bit offsets; raise nsplit");
@@ -524,7 +572,7 @@ int grad_weight_launch(const void* g, int g_dtype, int64_t ldg, const void* x, i
   a.M = M;
   a.N = N;
   a.K = K;
-  a.m_chunk = chunk > 0 ? chunk : GW_BM;
+  a.m_chunk = chunk > 0 ? chunk : sb;
   a.nsplit = nsplit;
   a.nparts = nparts;
   a.part_cols = part_cols;
@@ -637,11 +685,11 @@ extern "C" int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K) {
   const bool big = gw_big_tiles(N, K);
   const int64_t feat = big ? GwBig::FEAT : GwSmall::FEAT;
   const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
-  // small tiles: about two 4-wave blocks per CU. Large tiles: one split while the tiles
+  // small tiles: about one 8-wave block per CU. Large tiles: one split while the tiles
   // alone occupy half the CUs (each further split adds 4 B per weight of partials that
   // the update reads back, which costs more than the idle CUs: measured at the 1B
   // shapes), else about one 8-wave block per CU.
-  int64_t splits = big ? (tiles >= 128 ? 1 : (256 + tiles - 1) / tiles) : (512 + tiles - 1) / tiles;
+  int64_t splits = big ? (tiles >= 128 ? 1 : (256 + tiles - 1) / tiles) : (256 + tiles - 1) / tiles;
   const int64_t max_by_m = (M + 511) / 512;         // at least 512 tokens per split
   if (splits > max_by_m) splits = max_by_m;
   if (splits > 64) splits = 64;
