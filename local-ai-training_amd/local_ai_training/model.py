@@ -631,11 +631,21 @@ class RatchetGPT(nn.Module):
             slot_means = _ratchet_ops().row_rms_means(rms, self._rms_offsets)
             for i, m in enumerate(layers):
                 m._rms_slot_mean = slot_means[i]
-        updates = [m.ratchet_update(validate=validate) for m in layers]
+        if shared:
+            # one copy of every layer's slot for their stats to own (one launch, where a
+            # clone per layer was one small copy each)
+            snapshot = buf.clone()
+            for i, m in enumerate(layers):
+                m._counts_snapshot = snapshot[i]
+        try:
+            updates = [m.ratchet_update(validate=validate) for m in layers]
+        finally:
+            for m in layers:
+                m._counts_snapshot = None
         if shared:
             # the layers' counts live in one buffer: one reduction for the four totals,
             # then the buffer is cleared for the next step
-            totals = buf.sum(dim=0)
+            totals = snapshot.sum(dim=0)
             moves = (totals[0], totals[1], totals[2], totals[3])
             buf.zero_()
             for m in layers:

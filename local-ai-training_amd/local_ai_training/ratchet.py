@@ -772,6 +772,9 @@ class DiscreteRatchetLinear(nn.Module):
         # holds counts a layer-level ratchet_update consumed
         self._counts_slot: Tensor | None = None
         self._slot_dirty = False
+        # the model's copy of every slot, taken once for all its layers before their
+        # ratchet_update: this layer's stats then own a row of it instead of a clone each
+        self._counts_snapshot: Tensor | None = None
         # likewise an [out_features] view of one row-rms buffer for all its layers, with
         # this layer's [2] int64 segment bounds [0, out_features): the first fused update of
         # a step writes its row rms there and leaves the mean to one launch for the whole
@@ -1092,8 +1095,12 @@ class DiscreteRatchetLinear(nn.Module):
             else:
                 # the model's shared count slot is cleared by its sum and reused next step:
                 # the stats own a copy (32 bytes), as the reference's per-layer stats own
-                # their tensors
-                own = counts.clone() if counts is self._counts_slot else counts
+                # their tensors - a row of the model's one copy of all slots when it made one
+                if counts is self._counts_slot:
+                    snap = self._counts_snapshot
+                    own = snap if snap is not None else counts.clone()
+                else:
+                    own = counts
                 pos, neg, bpos, bneg = own[0], own[1], own[2], own[3]
             stats = RatchetUpdateStats(
                 total_weights=self._pending_stats_total_weights,
@@ -1108,6 +1115,7 @@ class DiscreteRatchetLinear(nn.Module):
             nonfinite = self._nonfinite
             if counts is not None and counts is self._counts_slot:
                 self._slot_dirty = True  # cleared by the model's sum, or before next use
+            self._counts_snapshot = None
             self._reset_pending_stats()
             self._nonfinite = nonfinite
         elif self.matmul_mode != "fp32":
