@@ -685,11 +685,13 @@ extern "C" int rk_grad_weight_splits(int64_t M, int64_t N, int64_t K) {
   const bool big = gw_big_tiles(N, K);
   const int64_t feat = big ? GwBig::FEAT : GwSmall::FEAT;
   const int64_t tiles = ((N + feat - 1) / feat) * ((K + feat - 1) / feat);
-  // small tiles: about one 8-wave block per CU. Large tiles: one split while the tiles
-  // alone occupy half the CUs (each further split adds 4 B per weight of partials that
-  // the update reads back, which costs more than the idle CUs: measured at the 1B
+  // small tiles: at most one 8-wave block per CU (their LDS and registers allow no
+  // second), so the splits never make a second, mostly idle round of blocks (48 tiles x 6
+  // splits = 288 blocks took twice the time of 5 splits). Large tiles: one split while the
+  // tiles alone occupy half the CUs (each further split adds 4 B per weight of partials
+  // that the update reads back, which costs more than the idle CUs: measured at the 1B
   // shapes), else about one 8-wave block per CU.
-  int64_t splits = big ? (tiles >= 128 ? 1 : (256 + tiles - 1) / tiles) : (256 + tiles - 1) / tiles;
+  int64_t splits = big ? (tiles >= 128 ? 1 : (256 + tiles - 1) / tiles) : 256 / tiles;
   const int64_t max_by_m = (M + 511) / 512;         // at least 512 tokens per split
   if (splits > max_by_m) splits = max_by_m;
   if (splits > 64) splits = 64;
