@@ -193,13 +193,20 @@ __device__ __forceinline__ void transform_chunk(const QuantArgs& a, int64_t e0, 
   }
 }
 
-template <int DT, int SRC, bool SR, int NC, bool VEC>
+// P wavefronts per row (1, or 4: one row per block, wavefront w holding chunks w NC ..
+// w NC + NC - 1 in registers, the partial absmax of each met in LDS). The max is exact in
+// any order, so P changes no result.
+template <int DT, int SRC, bool SR, int NC, bool VEC, int P = 1>
 __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
+  static_assert(P == 1 || (P == 4 && NC > 0 && SRC != SRC_RMSNORM),
+                "row slices: register-resident rows, one row per block, no row norm");
   constexpr int V = Vec<DT>::N;
   constexpr int SPAN = kWave * V;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= a.M) return;
+  const int slice = P == 1 ? 0 : static_cast<int>(threadIdx.x >> 6);
+  const int64_t row = P == 1 ? static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)
+                             : static_cast<int64_t>(blockIdx.x);
+  if (row >= a.M) return;  // with P == 4 the whole block returns together
   const int64_t lane0 = static_cast<int64_t>(lane) * V;
   const int64_t nchunks = (a.K + SPAN - 1) / SPAN;
   int8_t* qrow = a.q + row * a.ldq;
@@ -219,12 +226,13 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
       static_cast<uint32_t>(a.row_offset + row) * static_cast<uint32_t>(a.K);
 
   if constexpr (NC > 0) {
-    // Register-resident row: one HBM read.
+    // Register-resident row (or row slice): one HBM read.
+    const int c0 = slice * NC;  // this wavefront's first chunk
     float xr[NC][V];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t e0 = c * SPAN + lane0;
-      if (c < nchunks && (!VEC || e0 < a.K)) {
+      const int64_t e0 = (c0 + c) * SPAN + lane0;
+      if (c0 + c < nchunks && (!VEC || e0 < a.K)) {
         load_chunk<DT, SRC, VEC>(a, row, e0, xr[c]);
         if (xbrow && e0 < a.K) store_bf16_chunk<DT>(xbrow, e0, a.K, xr[c]);
       } else {
@@ -245,21 +253,28 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t e0 = c * SPAN + lane0;
-      if (c < nchunks && e0 < a.K) {
+      const int64_t e0 = (c0 + c) * SPAN + lane0;
+      if (c0 + c < nchunks && e0 < a.K) {
         transform_chunk<DT, SRC, VEC>(a, e0, xr[c], row_factor);
 #pragma unroll
         for (int i = 0; i < V; ++i) amax = fmaxf(amax, fabsf(xr[c][i]));
       }
     }
     amax = wave_max(amax);
+    if constexpr (P > 1) {
+      __shared__ float slice_max[P];
+      if (lane == 0) slice_max[slice] = amax;
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < P; ++w) amax = fmaxf(amax, slice_max[w]);
+    }
     const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
     const float r = 1.0f / s;
-    if (lane == 0) a.scale[row] = s;
+    if (lane == 0 && slice == 0) a.scale[row] = s;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int64_t e0 = c * SPAN + lane0;
-      if (c < nchunks && e0 < a.K)
+      const int64_t e0 = (c0 + c) * SPAN + lane0;
+      if (c0 + c < nchunks && e0 < a.K)
         quant_store_chunk<DT, SR, VEC>(a, ctr_row, key, e0, xr[c], s, r, qrow, vec_store);
     }
   } else {
@@ -302,12 +317,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(QuantArgs a) {
   }
 }
 
-template <int DT, int SRC, bool SR, int NC>
+template <int DT, int SRC, bool SR, int NC, int P = 1>
 static void launch_quant_nc(const QuantArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   if (a.vec_ok) {
-    quant_rows_kernel<DT, SRC, SR, NC, true><<<grid, block, 0, stream>>>(a);
+    quant_rows_kernel<DT, SRC, SR, NC, true, P><<<grid, block, 0, stream>>>(a);
   } else {
-    quant_rows_kernel<DT, SRC, SR, NC, false><<<grid, block, 0, stream>>>(a);
+    quant_rows_kernel<DT, SRC, SR, NC, false, P><<<grid, block, 0, stream>>>(a);
   }
 }
 
@@ -337,6 +352,17 @@ static int launch_quant(const QuantArgs& a, hipStream_t stream) {
       if (nchunks <= kMaxChunks) {
         // e.g. the 1B model's 5632- and 6144-wide bf16 rows (GELU and plain prologues)
         launch_quant_nc<DT, SRC, SR, kMaxChunks>(a, grid, block, stream);
+        return launch_status("quantize_rows");
+      }
+    } else if constexpr (SRC != SRC_RMSNORM) {
+      if (nchunks <= 16 && a.M <= (int64_t{1} << 23)) {  // one block per row: grid in range
+        // stochastic bf16 rows of up to 16 chunks: the four wavefronts of a block share
+        // one row, 2-4 chunks each in registers (the 1B qkv and expansion gradients, 6144
+        // and 5632 wide, were re-read by the streaming form)
+        const dim3 rows(static_cast<unsigned>(a.M));
+        if (nchunks <= 8) launch_quant_nc<DT, SRC, SR, 2, 4>(a, rows, block, stream);
+        else if (nchunks <= 12) launch_quant_nc<DT, SRC, SR, 3, 4>(a, rows, block, stream);
+        else launch_quant_nc<DT, SRC, SR, 4, 4>(a, rows, block, stream);
         return launch_status("quantize_rows");
       }
     }
