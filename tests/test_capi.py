@@ -85,3 +85,40 @@ def test_attention_forward_rejects_before_device_work(lib):
     assert lib.rk_attention_forward(*args, i64(1), i64(1), i64(0), i64(64),
                                     ctypes.c_float(0.125), None, i64(0), i64(0), i64(64),
                                     None, None) == 0
+
+
+def _update_table(rows_list, k=512, nsplit=1, g=1 << 12):
+    """rk_update_layer entries with fake (never dereferenced) device addresses."""
+    table = (nat.UpdateLayer * len(rows_list))()
+    begin = 0
+    for entry, rows in zip(table, rows_list):
+        entry.packed, entry.g, entry.nonfinite = 1 << 12, g, 1 << 12
+        entry.ldp, entry.ldg, entry.rows, entry.K, entry.row_begin = k, k, rows, k, begin
+        entry.max_code, entry.threshold, entry.nsplit = 2, 8, nsplit
+        entry.low, entry.high, entry.eps, entry.beta1, entry.beta2 = 0.5, 1.5, 1e-8, 0.0, 1.0
+        begin += rows
+    return table
+
+
+def test_multi_layer_update_validates_its_table_on_the_host(lib):
+    """rk_ratchet_update_multi checks every entry of the host copy before any launch: the
+    rows must follow each other, the rule and the split layout must be valid; a table of
+    empty layers launches nothing."""
+    dev = ctypes.c_void_p(1 << 12)  # the device copy: never read when the call fails
+    call = lambda t, src=nat.RK_BF16, n=None: lib.rk_ratchet_update_multi(  # noqa: E731
+        ctypes.addressof(t), dev, len(t) if n is None else n, src, None)
+    table = _update_table([64, 32])
+    assert call(table, n=0) == 1 and b"nlayers" in lib.rk_last_error()
+    assert call(table, src=7) == 1 and b"gradient source" in lib.rk_last_error()
+    table[1].row_begin = 1
+    assert call(table) == 1 and b"row_begin" in lib.rk_last_error()
+    table = _update_table([64, 32])
+    table[0].max_code = 9
+    assert call(table) == 1 and b"layer 0" in lib.rk_last_error()
+    table = _update_table([64, 32], nsplit=65)
+    assert call(table, src=nat.RK_UPDATE_SRC_SPLITS) == 1 and b"nsplit" in lib.rk_last_error()
+    table = _update_table([64], k=500, nsplit=2)
+    assert call(table, src=nat.RK_UPDATE_SRC_SPLITS) == 3  # partials need K % 8 == 0
+    table = _update_table([64], g=0)
+    assert call(table) == 1 and b"null gradient" in lib.rk_last_error()
+    assert call(_update_table([0, 0])) == 0  # no rows: nothing to launch
