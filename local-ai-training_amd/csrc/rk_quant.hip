@@ -344,25 +344,25 @@ static int launch_quant(const QuantArgs& a, hipStream_t stream) {
   } else if (nchunks <= 4) {
     launch_quant_nc<DT, SRC, SR, 4>(a, grid, block, stream);
   } else {
+    if constexpr (SRC != SRC_RMSNORM) {
+      if (nchunks <= 16 && a.M <= (int64_t{1} << 23)) {  // one block per row: grid in range
+        // rows of 5 to 16 chunks: the four wavefronts of a block share one row, 2-4 chunks
+        // each in registers (one wavefront holding 8 or 12 chunks ran at 2-3 wavefronts
+        // per SIMD, or for stochastic bf16 rows kept them in scratch)
+        const dim3 rows(static_cast<unsigned>(a.M));
+        if (nchunks <= 8) launch_quant_nc<DT, SRC, SR, 2, 4>(a, rows, block, stream);
+        else if (nchunks <= 12) launch_quant_nc<DT, SRC, SR, 3, 4>(a, rows, block, stream);
+        else launch_quant_nc<DT, SRC, SR, 4, 4>(a, rows, block, stream);
+        return launch_status("quantize_rows");
+      }
+    }
     if constexpr (kLongRows) {
       if (nchunks <= 8) {
         launch_quant_nc<DT, SRC, SR, 8>(a, grid, block, stream);
         return launch_status("quantize_rows");
       }
       if (nchunks <= kMaxChunks) {
-        // e.g. the 1B model's 5632- and 6144-wide bf16 rows (GELU and plain prologues)
         launch_quant_nc<DT, SRC, SR, kMaxChunks>(a, grid, block, stream);
-        return launch_status("quantize_rows");
-      }
-    } else if constexpr (SRC != SRC_RMSNORM) {
-      if (nchunks <= 16 && a.M <= (int64_t{1} << 23)) {  // one block per row: grid in range
-        // stochastic bf16 rows of up to 16 chunks: the four wavefronts of a block share
-        // one row, 2-4 chunks each in registers (the 1B qkv and expansion gradients, 6144
-        // and 5632 wide, were re-read by the streaming form)
-        const dim3 rows(static_cast<unsigned>(a.M));
-        if (nchunks <= 8) launch_quant_nc<DT, SRC, SR, 2, 4>(a, rows, block, stream);
-        else if (nchunks <= 12) launch_quant_nc<DT, SRC, SR, 3, 4>(a, rows, block, stream);
-        else launch_quant_nc<DT, SRC, SR, 4, 4>(a, rows, block, stream);
         return launch_status("quantize_rows");
       }
     }
