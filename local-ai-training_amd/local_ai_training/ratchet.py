@@ -821,13 +821,25 @@ class DiscreteRatchetLinear(nn.Module):
         return (self.packed.numel() * self.packed.element_size()
                 + self.scale.numel() * self.scale.element_size())
 
+    def _apply_queued_update(self) -> None:
+        """Runs the update queue if it holds this layer's update from the last backward, so
+        a read of the state sees it applied (the reference updates inside backward)."""
+        if self._queued:
+            self._update_queue.flush()
+
     @property
     def code(self) -> Tensor:
+        self._apply_queued_update()
         return unpack_code_pressure(self.packed, self.max_code)[0]
 
     @property
     def pressure(self) -> Tensor:
+        self._apply_queued_update()
         return unpack_code_pressure(self.packed, self.max_code)[1]
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        self._apply_queued_update()
+        super()._save_to_state_dict(destination, prefix, keep_vars)
 
     @property
     def scale(self) -> Tensor:

@@ -217,3 +217,29 @@ def test_deferred_update_is_applied_before_the_layer_runs_again(cuda):
     assert not any(m._queued for m in layers)
     assert sum(not torch.equal(m.packed, p) for m, p in zip(layers, before)) > 0
     model.ratchet_update(validate=True)
+
+
+def test_reading_the_state_applies_a_queued_update(cuda):
+    # state_dict() and the code / pressure views flush the queue: after backward they show
+    # the updated state, as with updates inside backward
+    data = batches(cuda, 1)[0]
+    x, y = data[:, :-1], data[:, 1:]
+    states = []
+    for deferred in (False, True):
+        model = build_seeded_model(tiny_config(), max_code=2, seed=21).to(cuda).train()
+        model.defer_ratchet_updates(deferred)
+        torch.manual_seed(8)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            _, loss = model(x, y)
+        loss.backward()
+        layers = ratchet_layers(model)
+        if deferred:
+            assert all(m._queued for m in layers)
+            codes = layers[0].code  # flushes the whole queue
+            assert not any(m._queued for m in layers)
+            assert torch.equal(codes, states[0][1])
+        sd = {k: v.clone() for k, v in model.state_dict().items() if k.endswith("packed")}
+        states.append((sd, layers[0].code.clone()))
+        model.ratchet_update(validate=True)
+    assert states[0][0].keys() == states[1][0].keys()
+    assert all(torch.equal(states[0][0][k], states[1][0][k]) for k in states[0][0])
