@@ -13,7 +13,7 @@
 //   decode_gemv_kernel  (expand)   RMSNorm+quant prologue, tanh-GELU epilogue
 //   decode_gemv_kernel  (contract) per-token quant prologue, residual-add epilogue
 //
-// decode_gemv_kernel: a block owns 16 weight rows (n) and all M token rows. It requests
+// decode_gemv_kernel: a block owns 16 (or 32) weight rows (n) and up to 16 token rows. It requests
 // the activation rows first and then its packed code pieces (one 16-byte piece per
 // lane per 64-wide k-block, every k-block of the wave's K range at once), so the
 // prologue runs while the codes are still in flight. The prologue quantizes the M
@@ -132,15 +132,21 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
   for (int c = 0; c < NCH; ++c) {
     const int e0 = c * SPAN + lane * V;
     if (e0 < K) {
-      uint32_t word = 0;
+      // the reciprocal fast path for the lane's four values, redone through
+      // round_quotient (which divides where needed) only when one lies within the
+      // margin of a rounding boundary
+      bool exact = false;
+      float t[V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        float t = round_quotient<false>(xr[c][i], s, r, 0.0f);
-        t = fminf(fmaxf(t, -127.0f), 127.0f);
-        word |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(t))))
-                << (8 * i);
+      for (int i = 0; i < V; ++i) t[i] = round_fast<false>(xr[c][i], r, 0.0f, exact);
+      if (exact) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) t[i] = round_quotient<false>(xr[c][i], s, r, 0.0f);
       }
-      *reinterpret_cast<uint32_t*>(dst + e0) = word;
+      int qi[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) qi[i] = static_cast<int>(fminf(fmaxf(t[i], -127.0f), 127.0f));
+      *reinterpret_cast<uint32_t*>(dst + e0) = pack_bytes4(qi[0], qi[1], qi[2], qi[3]);
     }
   }
 }
@@ -148,7 +154,11 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
 // MM: capacity in token rows; WV: wavefronts (K is split across them, and the prologue
 // rows: wavefront w quantizes rows w, w + WV, ...); KBW: k-blocks a wavefront holds in
 // registers (>= ceil(K / 64 / WV)); NCH: 256-element chunks of a register-resident row
-// (>= ceil(K / 256)). Both are checked on the host.
+// (>= ceil(K / 256)). Both are checked on the host. NT: 16-row output tiles per workgroup,
+// all behind one prologue (the next tile's codes are requested before the current tile's
+// MFMAs). Token rows: blockIdx.y selects rows blockIdx.y * MM onward, so that more token
+// rows than MM, or a grid of twice the workgroups with half the prologue rows each, run
+// as several row groups over the same codes.
 //
 // Load order: the activation rows (and RMSNorm weight) are requested first, then the
 // packed codes, so the prologue waits only for the small activation loads while the
@@ -156,10 +166,22 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
 // wavefront both are preloaded when they fit the register budget (NCH <= 8).
 // (16-row variants with 512 threads and short K: 4 waves per SIMD, two workgroups per
 // CU; with 1024 threads: 4 waves per SIMD, one workgroup)
-template <int PRO, int EPI, int YDT, int MM, int WV, int KBW, int NCH>
-__global__ __launch_bounds__(64 * WV, (MM == 16 && (NCH <= 8 || WV == 16)) ? 4 : 1)
+template <int PRO, int EPI, int YDT, int MM, int WV, int KBW, int NCH, int NT = 1>
+__global__ __launch_bounds__(64 * WV, (MM >= 8 && (NCH <= 8 || WV == 16)) ? 4 : 1)
 void decode_gemv_kernel(DecodeGemvArgs a) {
   constexpr int NB = 16, KB = 64;
+  if (blockIdx.y > 0) {  // this workgroup's token rows (uniform)
+    const int mb = static_cast<int>(blockIdx.y) * MM;
+    if constexpr (PRO == DEC_PRO_INT8) {
+      a.xq += mb * a.ldxq;
+      a.xs += mb;
+    } else {
+      a.x += mb * a.ldx;
+    }
+    a.y = static_cast<char*>(a.y) + mb * a.ldy * (YDT == RK_BF16 ? 2 : 4);
+    a.M -= mb;
+  }
+  if (a.M > MM) a.M = MM;
   constexpr int RPW = (MM + WV - 1) / WV;                 // prologue rows per wavefront
   constexpr bool PRE = RPW == 1 || NCH <= 8;              // all prologue rows preloaded
   // RMSNorm weight: preloaded per wavefront with one prologue row; with two it is
@@ -181,18 +203,21 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int M = a.M, K = a.K;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * NB;
+  int64_t n0 = static_cast<int64_t>(blockIdx.x) * NT * NB;
 
   // 0. epilogue operands (wavefront 0 writes the outputs): row scales and, for the
   //    residual add, the rows being added to; requested first, needed last
   const int em = r16 < M ? r16 : M - 1;
-  const int64_t en = n0 + 4 * g4;
   float4 rs4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), old = rs4;
-  if (wave == 0) {
-    rs4 = *reinterpret_cast<const float4*>(a.rs + en);
-    if constexpr (EPI == DEC_EPI_ADD)
-      old = *reinterpret_cast<const float4*>(static_cast<const float*>(a.y) + em * a.ldy + en);
-  }
+  auto load_epilogue = [&](int64_t tile_n0) {
+    if (wave == 0) {
+      const int64_t en = tile_n0 + 4 * g4;
+      rs4 = *reinterpret_cast<const float4*>(a.rs + en);
+      if constexpr (EPI == DEC_EPI_ADD)
+        old = *reinterpret_cast<const float4*>(static_cast<const float*>(a.y) + em * a.ldy + en);
+    }
+  };
+  load_epilogue(n0);
 
   // 1. activation rows of the prologue (the first row only when they do not all fit)
   float xr[PRO == DEC_PRO_INT8 ? 1 : XR][NCH][4];
@@ -230,23 +255,26 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   // keep the activation loads ahead of the code loads in the instruction stream
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. this wavefront's packed code pieces, every k-block of its range at once
-  //    (positions past the range re-load its last k-block; their MFMAs are skipped)
-  const __amdgpu_buffer_rsrc_t b_rsrc =
-      make_buffer(a.packed + n0 * a.ldp, (NB - 1) * a.ldp + K);
+  // 2. this wavefront's packed code pieces of a 16-row tile, every k-block of its range at
+  //    once (positions past the range re-load its last k-block; their MFMAs are skipped)
   const int b_voff = r16 * static_cast<int>(a.ldp) + 16 * g4;
   const int nkb = K / KB;
   const int per = (nkb + WV - 1) / WV;
   const int kb_begin = wave * per;
   const int kb_cnt = nkb - kb_begin < per ? (nkb - kb_begin > 0 ? nkb - kb_begin : 0) : per;
   const int kb_last = kb_cnt > 0 ? kb_begin + kb_cnt - 1 : 0;
-  dec_u32x4 bw[KBW];
+  auto load_codes = [&](int64_t tile_n0, dec_u32x4 (&bw)[KBW]) {
+    const __amdgpu_buffer_rsrc_t b_rsrc =
+        make_buffer(a.packed + tile_n0 * a.ldp, (NB - 1) * a.ldp + K);
 #pragma unroll
-  for (int j = 0; j < KBW; ++j) {
-    const int kb = kb_begin + j < kb_last ? kb_begin + j : kb_last;
-    bw[j] = __builtin_bit_cast(
-        dec_u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, b_voff, kb * KB, 0));
-  }
+    for (int j = 0; j < KBW; ++j) {
+      const int kb = kb_begin + j < kb_last ? kb_begin + j : kb_last;
+      bw[j] = __builtin_bit_cast(
+          dec_u32x4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, b_voff, kb * KB, 0));
+    }
+  };
+  dec_u32x4 bw[KBW], bn[KBW];
+  load_codes(n0, bw);
 
   // 3. prologue: int8 rows (or quantized activation rows) and their scales into LDS
   if constexpr (PRO == DEC_PRO_INT8) {
@@ -278,59 +306,73 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   }
   __syncthreads();
 
-  // 4. MFMA over the wavefront's k-blocks (token rows past M read row MM-1: their
-  //    results are never stored)
+  // 4. per tile: MFMA over the wavefront's k-blocks (token rows past M read row MM-1: their
+  //    results are never stored), the next tile's codes requested first; the wavefronts'
+  //    sums meet in LDS and wavefront 0 writes the tile
   const int8_t* arow = qa + (r16 < MM ? r16 : MM - 1) * KP + 16 * g4;
-  dec_v4i acc = dec_v4i{0, 0, 0, 0};
+  auto tile = [&](dec_u32x4 (&cur)[KBW], dec_u32x4 (&nxt)[KBW], int t) {
+    if (t + 1 < NT) load_codes(n0 + NB, nxt);
+    dec_v4i acc = dec_v4i{0, 0, 0, 0};
 #pragma unroll
-  for (int j = 0; j < KBW; ++j) {
-    if (j < kb_cnt) {
-      dec_u32x4 v = bw[j];
-      v.x = decode4(v.x, a.mc4);
-      v.y = decode4(v.y, a.mc4);
-      v.z = decode4(v.z, a.mc4);
-      v.w = decode4(v.w, a.mc4);
-      const dec_v4i av = *reinterpret_cast<const dec_v4i*>(arow + (kb_begin + j) * KB);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(dec_v4i, v), av, acc, 0, 0,
-                                                  0);
+    for (int j = 0; j < KBW; ++j) {
+      if (j < kb_cnt) {
+        dec_u32x4 v = cur[j];
+        v.x = decode4(v.x, a.mc4);
+        v.y = decode4(v.y, a.mc4);
+        v.z = decode4(v.z, a.mc4);
+        v.w = decode4(v.w, a.mc4);
+        const dec_v4i av = *reinterpret_cast<const dec_v4i*>(arow + (kb_begin + j) * KB);
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(dec_v4i, v), av, acc, 0,
+                                                    0, 0);
+      }
     }
-  }
-  red[wave][lane] = acc;
-  __syncthreads();
-  if (wave != 0) return;
-  dec_v4i sum = red[0][lane];
+    red[wave][lane] = acc;
+    __syncthreads();
+    const int m = r16;
+    if (wave == 0 && m < M) {
+      dec_v4i sum = red[0][lane];
 #pragma unroll
-  for (int w = 1; w < WV; ++w) {
-    const dec_v4i t = red[w][lane];
-    sum = dec_v4i{sum[0] + t[0], sum[1] + t[1], sum[2] + t[2], sum[3] + t[3]};
-  }
-
-  // 5. epilogue: lane holds out[m = r16][n0 + 4*g4 + 0..3]
-  const int m = r16;
-  if (m >= M) return;
-  const int64_t n = en;
-  const float lsm = sc[m];
-  const float v0 = static_cast<float>(sum[0]) * lsm * rs4.x;
-  const float v1 = static_cast<float>(sum[1]) * lsm * rs4.y;
-  const float v2 = static_cast<float>(sum[2]) * lsm * rs4.z;
-  const float v3 = static_cast<float>(sum[3]) * lsm * rs4.w;
-  const uint32_t lo = dec_pack_bf16x2(v0, v1), hi = dec_pack_bf16x2(v2, v3);
-  if constexpr (EPI == DEC_EPI_STORE && YDT == RK_BF16) {
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + m * a.ldy + n) = make_uint2(lo, hi);
-  } else {
-    float f[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
-                  __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
-    float* yrow = static_cast<float*>(a.y) + m * a.ldy + n;
-    if constexpr (EPI == DEC_EPI_GELU) {
+      for (int w = 1; w < WV; ++w) {
+        const dec_v4i q = red[w][lane];
+        sum = dec_v4i{sum[0] + q[0], sum[1] + q[1], sum[2] + q[2], sum[3] + q[3]};
+      }
+      // 5. epilogue: lane holds out[m = r16][n0 + 4*g4 + 0..3]
+      const int64_t n = n0 + 4 * g4;
+      const float lsm = sc[m];
+      const float v0 = static_cast<float>(sum[0]) * lsm * rs4.x;
+      const float v1 = static_cast<float>(sum[1]) * lsm * rs4.y;
+      const float v2 = static_cast<float>(sum[2]) * lsm * rs4.z;
+      const float v3 = static_cast<float>(sum[3]) * lsm * rs4.w;
+      const uint32_t lo = dec_pack_bf16x2(v0, v1), hi = dec_pack_bf16x2(v2, v3);
+      if constexpr (EPI == DEC_EPI_STORE && YDT == RK_BF16) {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.y) + m * a.ldy + n) =
+            make_uint2(lo, hi);
+      } else {
+        float f[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u),
+                      __uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+        float* yrow = static_cast<float*>(a.y) + m * a.ldy + n;
+        if constexpr (EPI == DEC_EPI_GELU) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) f[r] = gelu_tanh(f[r]);
-    } else if constexpr (EPI == DEC_EPI_ADD) {
-      f[0] = old.x + f[0];
-      f[1] = old.y + f[1];
-      f[2] = old.z + f[2];
-      f[3] = old.w + f[3];
+          for (int r = 0; r < 4; ++r) f[r] = gelu_tanh(f[r]);
+        } else if constexpr (EPI == DEC_EPI_ADD) {
+          f[0] = old.x + f[0];
+          f[1] = old.y + f[1];
+          f[2] = old.z + f[2];
+          f[3] = old.w + f[3];
+        }
+        *reinterpret_cast<float4*>(yrow) = make_float4(f[0], f[1], f[2], f[3]);
+      }
     }
-    *reinterpret_cast<float4*>(yrow) = make_float4(f[0], f[1], f[2], f[3]);
+    n0 += NB;
+    if (t + 1 < NT) {
+      load_epilogue(n0);
+      __syncthreads();  // every wavefront read red before the next tile overwrites it
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < NT; t += 2) {
+    tile(bw, bn, t);
+    if (t + 1 < NT) tile(bn, bw, t + 1);
   }
 }
 
@@ -350,13 +392,23 @@ static int launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
   } else if (a.M <= 4) {
     if (small_k) decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
     else decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 24, 24><<<grid, 256, 0, stream>>>(a);
+  } else if (small_k && a.N >= 4096 && a.N % 32 == 0) {
+    // wide layers: two 16-row tiles behind one 16-row prologue (the prologue's VALU work,
+    // repeated by every workgroup, outweighs a second tile's code loads and MFMAs)
+    const dim3 grid2(static_cast<unsigned>(a.N / 32));
+    decode_gemv_kernel<PRO, EPI, YDT, 16, 8, 4, 8, 2><<<grid2, 512, 0, stream>>>(a);
   } else if (small_k) {
-    decode_gemv_kernel<PRO, EPI, YDT, 16, 8, 4, 8><<<grid, 512, 0, stream>>>(a);
+    // narrow layers (N / 16 workgroups would leave CUs idle): groups of 8 token rows, one
+    // prologue row per wavefront, twice the workgroups over the same codes
+    const dim3 grid8(static_cast<unsigned>(a.N / 16), static_cast<unsigned>((a.M + 7) / 8));
+    decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 4, 8><<<grid8, 512, 0, stream>>>(a);
   } else if constexpr (PRO == DEC_PRO_RMSNORM) {
     decode_gemv_kernel<PRO, EPI, YDT, 16, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
   } else {
-    // long rows without a norm weight: one preloaded row per wavefront (16 wavefronts)
-    decode_gemv_kernel<PRO, EPI, YDT, 16, 16, 6, 24><<<grid, 1024, 0, stream>>>(a);
+    // long rows without a norm weight: groups of 8 token rows, one preloaded row per
+    // wavefront
+    const dim3 grid8(static_cast<unsigned>(a.N / 16), static_cast<unsigned>((a.M + 7) / 8));
+    decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 12, 24><<<grid8, 512, 0, stream>>>(a);
   }
   return launch_status("decode_gemv");
 }

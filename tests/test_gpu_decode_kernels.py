@@ -57,10 +57,14 @@ def _gemv(layer, out, prologue, epilogue, x=None, xq=None, xs=None, w=None, eps=
 
 # (1, 5632, 2048) and (1, 6144, 32): one token row over rows longer than 2048, the
 # 8-wavefront split of K (the batch-1 contraction of the 1B model); (16, 2048, 6144) and
-# (16, 2048, 8192): the 1B qkv and lm_head at batch 16
+# (16, 2048, 8192): the 1B qkv and lm_head at batch 16 (two 16-row tiles per workgroup,
+# as (12, 1024, 4096) with fewer token rows); (16, 2048, 2048), (16, 5632, 2048),
+# (13, 2048, 2048), (9, 5632, 2048), (11, 6144, 32): groups of 8 token rows (the last one
+# partial)
 SHAPES = [(1, 2048, 6144), (1, 64, 16), (3, 2048, 5632), (4, 5632, 2048), (5, 320, 48),
           (16, 2048, 2048), (16, 5632, 2048), (11, 6144, 32), (1, 2048, 8192),
-          (1, 5632, 2048), (1, 6144, 32), (16, 2048, 6144), (16, 2048, 8192)]
+          (1, 5632, 2048), (1, 6144, 32), (16, 2048, 6144), (16, 2048, 8192),
+          (12, 1024, 4096), (13, 2048, 2048), (9, 5632, 2048)]
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
@@ -95,7 +99,7 @@ def test_int8_prologue_and_residual_add_match_the_packed_gemm(cuda, m, k, n):
 
 @pytest.mark.parametrize("m,k,n", [(1, 2048, 6144), (4, 2048, 2048), (16, 2048, 5632),
                                    (7, 512, 128), (2, 5632, 64), (1, 5632, 64),
-                                   (1, 6144, 128)])
+                                   (1, 6144, 128), (10, 6144, 64), (14, 2048, 4096)])
 def test_rmsnorm_prologue_equals_rmsnorm_quantize_then_gemm(cuda, m, k, n):
     gen = torch.Generator().manual_seed(m + k + 5 * n)
     x = (torch.randn(m, k, generator=gen) * 2.0).to(cuda)
@@ -112,7 +116,8 @@ def test_rmsnorm_prologue_equals_rmsnorm_quantize_then_gemm(cuda, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 2048, 5632), (16, 2048, 5632), (3, 640, 96),
-                                   (1, 5632, 128), (1, 6144, 64)])
+                                   (1, 5632, 128), (1, 6144, 64), (6, 1024, 4096),
+                                   (15, 2048, 96)])
 def test_gelu_epilogue_feeds_the_same_quantization_as_gelu_quantize(cuda, m, k, n):
     # expand GEMV with the GELU epilogue, then a plain quant of its float32 rows, must give
     # the q, s that rk_gelu_quantize computes from the GEMM's widened output
