@@ -395,8 +395,8 @@ static int launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
   } else if (small_k && a.N >= 4096 && a.N % 32 == 0) {
     // wide layers: two 16-row tiles behind one 16-row prologue (the prologue's VALU work,
     // repeated by every workgroup, outweighs a second tile's code loads and MFMAs)
-    const dim3 grid2(static_cast<unsigned>(a.N / 32));
-    decode_gemv_kernel<PRO, EPI, YDT, 16, 8, 4, 8, 2><<<grid2, 512, 0, stream>>>(a);
+    const dim3 grid2(static_cast<unsigned>(a.N / 32), static_cast<unsigned>((a.M + 7) / 8));
+    decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 4, 8, 2><<<grid2, 512, 0, stream>>>(a);
   } else if (small_k) {
     // narrow layers (N / 16 workgroups would leave CUs idle): groups of 8 token rows, one
     // prologue row per wavefront, twice the workgroups over the same codes
@@ -462,6 +462,44 @@ __device__ __forceinline__ void dec_store(void* base, int64_t idx, const float* 
   }
 }
 
+// One position's E cache elements as loaded: float32 as is; bf16 as the raw 16-bit words
+// (two per VGPR), widened where they are used, which halves the registers a loaded
+// batch holds.
+template <int CDT, int E>
+struct KvPiece {
+  float v[E];
+  __device__ __forceinline__ void load(const void* base, int64_t idx) {
+    dec_load<CDT, E>(base, idx, v);
+  }
+  __device__ __forceinline__ float operator[](int e) const { return v[e]; }
+};
+
+template <int E>
+struct KvPiece<RK_BF16, E> {
+  static_assert(E % 4 == 0, "whole 8-byte words");
+  uint32_t w[E / 2];
+  __device__ __forceinline__ void load(const void* base, int64_t idx) {
+    const uint16_t* p = static_cast<const uint16_t*>(base) + idx;
+    if constexpr (E % 8 == 0) {
+#pragma unroll
+      for (int c = 0; c < E / 8; ++c) {
+        const uint4 r = *reinterpret_cast<const uint4*>(p + 8 * c);
+        w[4 * c] = r.x;
+        w[4 * c + 1] = r.y;
+        w[4 * c + 2] = r.z;
+        w[4 * c + 3] = r.w;
+      }
+    } else {
+      const uint2 r = *reinterpret_cast<const uint2*>(p);
+      w[0] = r.x;
+      w[1] = r.y;
+    }
+  }
+  __device__ __forceinline__ float operator[](int e) const {
+    return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  }
+};
+
 // Merge (m2, l2, o2) into (m, l, o): both are softmax states over disjoint position
 // sets; an empty state has m = -inf, l = 0, o = 0.
 template <int E>
@@ -509,16 +547,17 @@ __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs
   // batch's loads are in flight while this one is reduced. Loads are unconditional
   // (positions past the split re-read position j0; position p takes the step's k, v
   // from registers), so waits count only the older batch.
-  auto load = [&](int jb, float (&kk)[U][E], float (&vv)[U][E]) {
+  using Piece = KvPiece<CDT, E>;
+  auto load = [&](int jb, Piece (&kk)[U], Piece (&vv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = jb + 16 * u;
       const int64_t off = cbase + static_cast<int64_t>(j < j1 ? j : j0) * a.sl;
-      dec_load<CDT, E>(a.kc, off, kk[u]);
-      dec_load<CDT, E>(a.vc, off, vv[u]);
+      kk[u].load(a.kc, off);
+      vv[u].load(a.vc, off);
     }
   };
-  auto reduce = [&](int jb, const float (&kk)[U][E], const float (&vv)[U][E]) {
+  auto reduce = [&](int jb, const Piece (&kk)[U], const Piece (&vv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = jb + 16 * u;
@@ -542,7 +581,7 @@ __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs
     }
   };
   {
-    float ka[U][E], va[U][E], kb[U][E], vb[U][E];
+    Piece ka[U], va[U], kb[U], vb[U];
     int jb = j0 + wave * 4 + grp;
     load(jb, ka, va);
     while (jb < j1) {
