@@ -82,6 +82,34 @@ __device__ __forceinline__ void dec_load_row(const float* row, int K, int lane,
   }
 }
 
+// Chunks c0 .. c0 + NC - 1 of a register-resident row (zeros past K) -> int8 values in
+// LDS at dst (the row's start): x / s rounded to nearest even, through the reciprocal
+// fast path for the lane's four values, redone through round_quotient (which divides
+// where needed) only when one lies within the margin of a rounding boundary.
+template <int NC>
+__device__ __forceinline__ void dec_store_q(const float (&xr)[NC][4], int c0, int lane, int K,
+                                            float s, float r, int8_t* dst) {
+  constexpr int V = 4, SPAN = kWave * V;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int e0 = (c0 + c) * SPAN + lane * V;
+    if (e0 < K) {
+      bool exact = false;
+      float t[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) t[i] = round_fast<false>(xr[c][i], r, 0.0f, exact);
+      if (exact) {
+#pragma unroll
+        for (int i = 0; i < V; ++i) t[i] = round_quotient<false>(xr[c][i], s, r, 0.0f);
+      }
+      int qi[V];
+#pragma unroll
+      for (int i = 0; i < V; ++i) qi[i] = static_cast<int>(fminf(fmaxf(t[i], -127.0f), 127.0f));
+      *reinterpret_cast<uint32_t*>(dst + e0) = pack_bytes4(qi[0], qi[1], qi[2], qi[3]);
+    }
+  }
+}
+
 // Register-resident row -> int8 row in LDS + its scale, with quant_rows_kernel's
 // arithmetic for an f32 row: the per-lane sum of squares in chunk order, the xor
 // butterfly, x * rsqrt-factor * w, the absmax scale and round_quotient. WREG: the
@@ -128,27 +156,7 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
   const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
   const float r = 1.0f / s;
   if (lane == 0) *s_out = s;
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int e0 = c * SPAN + lane * V;
-    if (e0 < K) {
-      // the reciprocal fast path for the lane's four values, redone through
-      // round_quotient (which divides where needed) only when one lies within the
-      // margin of a rounding boundary
-      bool exact = false;
-      float t[V];
-#pragma unroll
-      for (int i = 0; i < V; ++i) t[i] = round_fast<false>(xr[c][i], r, 0.0f, exact);
-      if (exact) {
-#pragma unroll
-        for (int i = 0; i < V; ++i) t[i] = round_quotient<false>(xr[c][i], s, r, 0.0f);
-      }
-      int qi[V];
-#pragma unroll
-      for (int i = 0; i < V; ++i) qi[i] = static_cast<int>(fminf(fmaxf(t[i], -127.0f), 127.0f));
-      *reinterpret_cast<uint32_t*>(dst + e0) = pack_bytes4(qi[0], qi[1], qi[2], qi[3]);
-    }
-  }
+  dec_store_q<NCH>(xr, 0, lane, K, s, r, dst);
 }
 
 // MM: capacity in token rows; WV: wavefronts (K is split across them, and the prologue
@@ -158,7 +166,10 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
 // all behind one prologue (the next tile's codes are requested before the current tile's
 // MFMAs). Token rows: blockIdx.y selects rows blockIdx.y * MM onward, so that more token
 // rows than MM, or a grid of twice the workgroups with half the prologue rows each, run
-// as several row groups over the same codes.
+// as several row groups over the same codes. RS (plain prologue only): wavefronts per
+// prologue row, each holding NCH / RS of its chunks; the slices' absmax values meet in LDS
+// (a max, so the scale is the one a whole-row wavefront computes) and each wavefront
+// quantizes its own slice.
 //
 // Load order: the activation rows (and RMSNorm weight) are requested first, then the
 // packed codes, so the prologue waits only for the small activation loads while the
@@ -166,10 +177,13 @@ __device__ __forceinline__ void dec_quant_row(const DecodeGemvArgs& a, int lane,
 // wavefront both are preloaded when they fit the register budget (NCH <= 8).
 // (16-row variants with 512 threads and short K: 4 waves per SIMD, two workgroups per
 // CU; with 1024 threads: 4 waves per SIMD, one workgroup)
-template <int PRO, int EPI, int YDT, int MM, int WV, int KBW, int NCH, int NT = 1>
+template <int PRO, int EPI, int YDT, int MM, int WV, int KBW, int NCH, int NT = 1, int RS = 1>
 __global__ __launch_bounds__(64 * WV, (MM >= 8 && (NCH <= 8 || WV == 16)) ? 4 : 1)
 void decode_gemv_kernel(DecodeGemvArgs a) {
   constexpr int NB = 16, KB = 64;
+  static_assert(RS == 1 || (PRO == DEC_PRO_PLAIN && MM * RS == WV && NCH % RS == 0),
+                "row slices: plain prologue, one slice per wavefront");
+  constexpr int NCHL = NCH / RS;  // row chunks a wavefront holds
   if (blockIdx.y > 0) {  // this workgroup's token rows (uniform)
     const int mb = static_cast<int>(blockIdx.y) * MM;
     if constexpr (PRO == DEC_PRO_INT8) {
@@ -196,6 +210,7 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   __shared__ __align__(16) int8_t qa[MM * KP];
   __shared__ __align__(16) float wsh[WLDS ? NCH * 256 : 4];
   __shared__ float sc[MM];
+  __shared__ float part[RS > 1 ? MM : 1][RS];  // slice absmax values
   __shared__ dec_v4i red[WV][kWave];
   // wave index made scalar: the code loads' k offset is then an SGPR (a value the
   // compiler takes as divergent would turn each buffer load into a waterfall loop)
@@ -220,12 +235,25 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   load_epilogue(n0);
 
   // 1. activation rows of the prologue (the first row only when they do not all fit)
-  float xr[PRO == DEC_PRO_INT8 ? 1 : XR][NCH][4];
+  float xr[PRO == DEC_PRO_INT8 ? 1 : XR][NCHL][4];
   float wr[NCH][4];  // RMSNorm weight (unread by the other prologues)
   dec_u32x4 xq_r[PRO == DEC_PRO_INT8 ? IPT : 1];
   int xq_lds[PRO == DEC_PRO_INT8 ? IPT : 1];
   const int pieces = K / 16;
-  if constexpr (PRO == DEC_PRO_INT8) {
+  const int srow = wave / RS, slice = wave - srow * RS;  // row slice (RS > 1)
+  if constexpr (RS > 1) {
+    const float* row = a.x + (srow < M ? srow : M - 1) * a.ldx;
+#pragma unroll
+    for (int c = 0; c < NCHL; ++c) {
+      const int e0 = (slice * NCHL + c) * kWave * 4 + lane * 4;
+      const bool in = e0 < K;
+      const float4 t = *reinterpret_cast<const float4*>(row + (in ? e0 : K - 4));
+      xr[0][c][0] = in ? t.x : 0.0f;
+      xr[0][c][1] = in ? t.y : 0.0f;
+      xr[0][c][2] = in ? t.z : 0.0f;
+      xr[0][c][3] = in ? t.w : 0.0f;
+    }
+  } else if constexpr (PRO == DEC_PRO_INT8) {
     // pieces past the M rows re-load piece 0 of row 0 (and store it back unchanged)
 #pragma unroll
     for (int i = 0; i < IPT; ++i) {
@@ -277,7 +305,25 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   load_codes(n0, bw);
 
   // 3. prologue: int8 rows (or quantized activation rows) and their scales into LDS
-  if constexpr (PRO == DEC_PRO_INT8) {
+  if constexpr (RS > 1) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCHL; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(xr[0][c][i]));  // zeros past K
+    amax = wave_max(amax);
+    if (lane == 0) part[srow][slice] = amax;
+    __syncthreads();
+    amax = part[srow][0];
+#pragma unroll
+    for (int j = 1; j < RS; ++j) amax = fmaxf(amax, part[srow][j]);
+    const float s = fmaxf(amax / 127.0f, 1.17549435e-38f);
+    const float r = 1.0f / s;
+    if (srow < M) {
+      if (slice == 0 && lane == 0) sc[srow] = s;
+      dec_store_q<NCHL>(xr[0], slice * NCHL, lane, K, s, r, qa + srow * KP);
+    }
+  } else if constexpr (PRO == DEC_PRO_INT8) {
 #pragma unroll
     for (int i = 0; i < IPT; ++i) *reinterpret_cast<dec_u32x4*>(qa + xq_lds[i]) = xq_r[i];
     if (tid < M) sc[tid] = a.xs[tid];
@@ -379,35 +425,49 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
 template <int PRO, int EPI, int YDT>
 static int launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(a.N / 16));
-  // Register and LDS footprints sized to K: rows of up to 2048 keep 8 chunks and 8
-  // k-blocks per wavefront; longer rows (<= 6144) hold 24 + 24. Up to 16 token rows run
-  // 8 wavefronts (two prologue rows each); with short rows two such workgroups fit a CU
-  // (registers and LDS), so grids of up to 512 workgroups run in one round.
+  // Register and LDS footprints sized to K: rows of up to 2048 keep 8 chunks, longer rows
+  // (<= 6144) 24. Plain prologue rows (no norm weight, whose sum of squares fixes the
+  // order of a row's reduction) are sliced over several wavefronts.
+  constexpr bool kPlain = PRO == DEC_PRO_PLAIN;
   const bool small_k = a.K <= 2048;
+  const dim3 grid8(static_cast<unsigned>(a.N / 16), static_cast<unsigned>((a.M + 7) / 8));
   if (a.M <= 1) {
     // one token row; long rows split K over 8 wavefronts (twice the code loads in flight
     // per CU: 14.7 -> 12.5 us for N 2048 x K 5632), short ones over 4 (8 were slower)
-    if (small_k) decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
-    else decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
+    if (small_k) {
+      if constexpr (kPlain)
+        decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8, 1, 4><<<grid, 256, 0, stream>>>(a);
+      else
+        decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
+    } else {
+      if constexpr (kPlain)
+        decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24, 1, 8><<<grid, 512, 0, stream>>>(a);
+      else
+        decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
+    }
   } else if (a.M <= 4) {
     if (small_k) decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
     else decode_gemv_kernel<PRO, EPI, YDT, 4, 4, 24, 24><<<grid, 256, 0, stream>>>(a);
   } else if (small_k && a.N >= 4096 && a.N % 32 == 0) {
-    // wide layers: two 16-row tiles behind one 16-row prologue (the prologue's VALU work,
-    // repeated by every workgroup, outweighs a second tile's code loads and MFMAs)
+    // wide layers: two 16-row tiles behind one prologue (the prologue's VALU work, repeated
+    // by every workgroup, outweighs a second tile's code loads and MFMAs), token rows in
+    // groups of 8
     const dim3 grid2(static_cast<unsigned>(a.N / 32), static_cast<unsigned>((a.M + 7) / 8));
     decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 4, 8, 2><<<grid2, 512, 0, stream>>>(a);
   } else if (small_k) {
-    // narrow layers (N / 16 workgroups would leave CUs idle): groups of 8 token rows, one
-    // prologue row per wavefront, twice the workgroups over the same codes
-    const dim3 grid8(static_cast<unsigned>(a.N / 16), static_cast<unsigned>((a.M + 7) / 8));
-    decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 4, 8><<<grid8, 512, 0, stream>>>(a);
+    // narrow layers (N / 16 workgroups would leave CUs idle): groups of 8 token rows, twice
+    // the workgroups over the same codes
+    if constexpr (kPlain)
+      decode_gemv_kernel<PRO, EPI, YDT, 8, 16, 2, 8, 1, 2><<<grid8, 1024, 0, stream>>>(a);
+    else
+      decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 4, 8><<<grid8, 512, 0, stream>>>(a);
   } else if constexpr (PRO == DEC_PRO_RMSNORM) {
     decode_gemv_kernel<PRO, EPI, YDT, 16, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
+  } else if constexpr (kPlain) {
+    // long plain rows: groups of 8 token rows, two wavefronts per row
+    decode_gemv_kernel<PRO, EPI, YDT, 8, 16, 6, 24, 1, 2><<<grid8, 1024, 0, stream>>>(a);
   } else {
-    // long rows without a norm weight: groups of 8 token rows, one preloaded row per
-    // wavefront
-    const dim3 grid8(static_cast<unsigned>(a.N / 16), static_cast<unsigned>((a.M + 7) / 8));
+    // long int8 rows: groups of 8 token rows
     decode_gemv_kernel<PRO, EPI, YDT, 8, 8, 12, 24><<<grid8, 512, 0, stream>>>(a);
   }
   return launch_status("decode_gemv");
