@@ -558,7 +558,44 @@ struct KvPiece<RK_BF16, E> {
   __device__ __forceinline__ float operator[](int e) const {
     return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
   }
+  __device__ __forceinline__ void store(void* base, int64_t idx) const {
+    uint16_t* p = static_cast<uint16_t*>(base) + idx;
+    if constexpr (E % 8 == 0) {
+#pragma unroll
+      for (int c = 0; c < E / 8; ++c)
+        *reinterpret_cast<uint4*>(p + 8 * c) =
+            make_uint4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
+    } else {
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    }
+  }
 };
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane row of the wavefront, every lane ending with its row's total, in
+// DPP moves: lane i adds lane 15-i, then 7-i within its half-row, then its quad partners
+// i^2 and i^1. Each step adds a symmetric pair (a + b on one lane, b + a on the other),
+// so all 16 lanes hold the same bits.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp_mov<0x140>(v);  // row_mirror
+  v = v + dpp_mov<0x141>(v);  // row_half_mirror
+  v = v + dpp_mov<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v = v + dpp_mov<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  return v;
+}
+
+typedef __bf16 dec_bf16x2v __attribute__((ext_vector_type(2)));
+
+// a.bf16[0] * b.bf16[0] + a.bf16[1] * b.bf16[1] + c (v_dot2c_f32_bf16; the products of two
+// bf16 values are exact in float32)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2v, a),
+                                         __builtin_bit_cast(dec_bf16x2v, b), c, false);
+}
 
 // Merge (m2, l2, o2) into (m, l, o): both are softmax states over disjoint position
 // sets; an empty state has m = -inf, l = 0, o = 0.
@@ -594,10 +631,20 @@ __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs
 
   const int64_t row = static_cast<int64_t>(b) * a.ldqkv + static_cast<int64_t>(h) * D + gl * E;
   const int64_t C = static_cast<int64_t>(a.H) * D;
+  // bf16 projections over a bf16 cache: q and the keys stay packed and meet in bf16 dot
+  // products (float32 accumulation), and a batch of positions shares one softmax rescale
+  constexpr bool kDot2 = QDT == RK_BF16 && CDT == RK_BF16;
   float qv[E], kn[E], vn[E];
-  dec_load<QDT, E>(a.qkv, row, qv);
-  dec_load<QDT, E>(a.qkv, row + C, kn);
-  dec_load<QDT, E>(a.qkv, row + 2 * C, vn);
+  KvPiece<RK_BF16, E> qp, knp, vnp;
+  if constexpr (kDot2) {
+    qp.load(a.qkv, row);
+    knp.load(a.qkv, row + C);
+    vnp.load(a.qkv, row + 2 * C);
+  } else {
+    dec_load<QDT, E>(a.qkv, row, qv);
+    dec_load<QDT, E>(a.qkv, row + C, kn);
+    dec_load<QDT, E>(a.qkv, row + 2 * C, vn);
+  }
   const int64_t cbase = static_cast<int64_t>(b) * a.sb + static_cast<int64_t>(h) * a.sh + gl * E;
 
   float m = -INFINITY, l = 0.0f, o[E];
@@ -617,7 +664,51 @@ __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs
       vv[u].load(a.vc, off);
     }
   };
+  auto reduce_dot2 = [&](int jb, const Piece (&kk)[U], const Piece (&vv)[U]) {
+    if constexpr (kDot2) {
+      // the batch's U scores (independent bf16 dot products, each summed over its 16
+      // lanes), then one rescale; positions past the split score -inf (weight 0), and the
+      // batch's first position is inside it, so the new maximum is finite
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool cur = jb + 16 * u == p;
+        float d = 0.0f;
+#pragma unroll
+        for (int w = 0; w < E / 2; ++w) d = dot2_bf16(qp.w[w], cur ? knp.w[w] : kk[u].w[w], d);
+        sc[u] = d;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) sc[u] = row16_sum(sc[u]);
+      float mn = m;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        sc[u] = jb + 16 * u < j1 ? sc[u] * a.scale : -INFINITY;
+        mn = fmaxf(mn, sc[u]);
+      }
+      const float c = expf(m - mn);  // 0 while m is -inf
+      float pj[U], psum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        pj[u] = expf(sc[u] - mn);
+        psum = psum + pj[u];
+      }
+      l = l * c + psum;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        float t = o[e] * c;
+#pragma unroll
+        for (int u = 0; u < U; ++u) t = t + pj[u] * (jb + 16 * u == p ? vnp[e] : vv[u][e]);
+        o[e] = t;
+      }
+      m = mn;
+    }
+  };
   auto reduce = [&](int jb, const Piece (&kk)[U], const Piece (&vv)[U]) {
+    if constexpr (kDot2) {
+      reduce_dot2(jb, kk, vv);
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = jb + 16 * u;
@@ -674,8 +765,13 @@ __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs
   // the split holding p appends the step's k, v (its loop read them from registers, and
   // no other workgroup reads position p)
   if (j0 <= p && p < j1 && tid < 16) {
-    dec_store<CDT, E>(a.kc, cbase + p * a.sl, kn);
-    dec_store<CDT, E>(a.vc, cbase + p * a.sl, vn);
+    if constexpr (kDot2) {
+      knp.store(a.kc, cbase + p * a.sl);
+      vnp.store(a.vc, cbase + p * a.sl);
+    } else {
+      dec_store<CDT, E>(a.kc, cbase + p * a.sl, kn);
+      dec_store<CDT, E>(a.vc, cbase + p * a.sl, vn);
+    }
   }
   __syncthreads();
   if (tid >= 16) return;
