@@ -614,9 +614,9 @@ __device__ __forceinline__ void dec_merge(float& m, float& l, float* o, float m2
 
 // grid (nsplit, H, B), 256 threads. 16 lanes share one position (E = D / 16 elements
 // each); a wavefront takes 4 positions per pass, the block 16, unrolled by U.
-template <int QDT, int CDT, int E>
+template <int QDT, int CDT, int E, int U>
 __global__ __launch_bounds__(256) void decode_attn_partial_kernel(DecodeAttnArgs a) {
-  constexpr int D = 16 * E, U = 4;
+  constexpr int D = 16 * E;
   __shared__ float sm[4], sl[4];
   __shared__ float so[4][D];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -853,8 +853,14 @@ __global__ __launch_bounds__(256) void decode_attn_combine_kernel(DecodeAttnArgs
 
 template <int QDT, int CDT, int E>
 static int launch_decode_attention(const DecodeAttnArgs& a, hipStream_t stream) {
-  decode_attn_partial_kernel<QDT, CDT, E>
-      <<<dim3(a.nsplit, a.H, a.B), 256, 0, stream>>>(a);
+  // splits of up to 32 positions (few sequence-head pairs) take batches of 2 positions per
+  // lane group, one batch per block; longer splits 4 (measured on the 1B model: batch 1
+  // 0.886 -> 0.878 ms per step with 2, batch 16 1.630 -> 1.647 with 2 and 1.638 with 8)
+  const dim3 grid(a.nsplit, a.H, a.B);
+  if (a.L <= 32 * a.nsplit)
+    decode_attn_partial_kernel<QDT, CDT, E, 2><<<grid, 256, 0, stream>>>(a);
+  else
+    decode_attn_partial_kernel<QDT, CDT, E, 4><<<grid, 256, 0, stream>>>(a);
   if (int st = launch_status("decode_attention")) return st;
   decode_attn_combine_kernel<E><<<dim3(a.H, a.B), 256, 0, stream>>>(a);
   return launch_status("decode_attention");
