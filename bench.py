@@ -1022,17 +1022,20 @@ def decode_bench(args, device) -> dict:
         tokens = torch.from_numpy(ids.astype(np.int64)).to(device)
         cache = model.new_cache(batch, dtype=torch.bfloat16)
         logits = model.prefill(tokens, cache)
-        graph = DecodeGraph(model, cache)
-        nxt = logits.argmax(-1, keepdim=True)
+        # the greedy graph picks each step's argmax into its token buffer and advances the
+        # position itself
+        graph = DecodeGraph(model, cache, greedy=True)
+        first = logits.argmax(-1, keepdim=True)
 
         def run(count):
-            nonlocal nxt
             for _ in range(count):
-                nxt = graph.step(nxt).argmax(-1, keepdim=True)
+                graph.next_greedy()
 
+        graph.tokens.copy_(first)
         run(min(args.warmup, steps))
         cache.length = prompt_len  # rewind: the timed steps rewrite the same positions
         cache.pos.fill_(prompt_len)
+        graph.tokens.copy_(first)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         run(steps)
@@ -1045,7 +1048,7 @@ def decode_bench(args, device) -> dict:
         chain = gemv_chain(model, batch, device, args.kernel_iters)
         entry = {"tokens_per_s": round(batch / step_s, 1), "ms_per_step": round(step_s * 1e3, 4),
                  "path": "fused" if fused_decode_supported(model, cache) else "modules",
-                 "launches_per_step": 6 * d["n_layer"] + 3,
+                 "launches_per_step": 6 * d["n_layer"] + 3,  # + embed, lm_head, greedy pick
                  "weight_GB_s": round(weight_bytes / step_s / 1e9, 1),
                  "step_bytes": weight_bytes + kv_bytes,
                  "step_frac_hbm": round((weight_bytes + kv_bytes) / step_s / PEAK_HBM_BPS, 4),

@@ -602,6 +602,14 @@ int rk_decode_embed(const int64_t* tokens, int64_t B, const float* table, int64_
                     int64_t C, const float* pos_table, int64_t n_pos, const int64_t* pos,
                     float* hidden, int64_t ldh, void* stream);
 
+/* Greedy pick and cache advance of one decode step, in one launch: tokens[b * ld_tokens]
+ * (int64) = the argmax of logits row b (float32 [B, V], row stride ldl): the first index
+ * of the largest value, a NaN ranking above every number, as torch.argmax; then, when pos
+ * is not null, *pos += 1. Replaces: torch.argmax(next_logits, dim=-1) at temperature 0
+ * (generate.py:188-189) and the window's growth by the picked token (generate.py:200). */
+int rk_decode_greedy(const float* logits, int64_t ldl, int64_t B, int64_t V, int64_t* tokens,
+                     int64_t ld_tokens, int64_t* pos, void* stream);
+
 /*
  * Token cross-entropy, mean over the rows whose target is not ignore_index: per row of
  * logits [M, V] (float32 / bfloat16, row stride ldl, 16-byte aligned rows, V a multiple of

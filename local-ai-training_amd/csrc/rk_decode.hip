@@ -888,6 +888,58 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(const int64_t* tokens
     out[c] = ok ? table[t * C + c] + pos_table[p * C + c] : __uint_as_float(0x7fc00000u);
 }
 
+// (v, i) ranks above (best, bi): the larger value, a NaN above every number, and among
+// equal values (or NaNs) the smaller index, which makes the pick torch.argmax's.
+__device__ __forceinline__ bool greedy_better(float v, int i, float best, int bi) {
+  const bool vn = v != v, bn = best != best;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > best || (v == best && i < bi);
+}
+
+// grid B, 256 threads: tokens[b * ldt] = the argmax of logits row b; block 0 then adds one
+// to *pos (no kernel of the step reads pos after this one).
+__global__ __launch_bounds__(256) void decode_greedy_kernel(const float* logits, int64_t ldl,
+                                                            int V, int64_t* tokens, int64_t ldt,
+                                                            int64_t* pos) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const float* row = logits + b * ldl;
+  float best = -INFINITY;
+  int bi = V;  // no index yet: any value, -inf included, ranks above it
+  for (int i = tid; i < V; i += 256) {
+    const float v = row[i];
+    if (greedy_better(v, i, best, bi)) {
+      best = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v = __shfl_xor(best, off, kWave);
+    const int i = __shfl_xor(bi, off, kWave);
+    if (greedy_better(v, i, best, bi)) {
+      best = v;
+      bi = i;
+    }
+  }
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+      if (greedy_better(sv[w], si[w], best, bi)) {
+        best = sv[w];
+        bi = si[w];
+      }
+    tokens[b * ldt] = bi;
+    if (pos != nullptr && b == 0) *pos = *pos + 1;
+  }
+}
+
 // Splits per (sequence, head), at least 16 positions per split, at most kDecMaxSplits.
 // Workgroups in all: about 512 for few (sequence, head) pairs, where the combine's
 // per-pair merge over the splits is on the critical path, and about 2048 for many, where
@@ -1063,4 +1115,17 @@ extern "C" int rk_decode_embed(const int64_t* tokens, int64_t B, const float* ta
   decode_embed_kernel<<<dim3(static_cast<unsigned>(B)), 256, 0, as_stream(stream)>>>(
       tokens, table, vocab, C, pos_table, n_pos, pos, hidden, ldh);
   return launch_status("decode_embed");
+}
+
+extern "C" int rk_decode_greedy(const float* logits, int64_t ldl, int64_t B, int64_t V,
+                                int64_t* tokens, int64_t ld_tokens, int64_t* pos, void* stream) {
+  clear_error();
+  if (B < 0 || V <= 0 || V > (int64_t{1} << 30)) return fail(RK_ERR_ARG, "invalid greedy shape");
+  if (B == 0) return RK_OK;
+  if (B > 65535) return fail(RK_ERR_ARG, "greedy grid too large");
+  if (!logits || !tokens) return fail(RK_ERR_ARG, "null greedy operand");
+  if (ldl < V || ld_tokens < 1) return fail(RK_ERR_ARG, "leading dimension too small");
+  decode_greedy_kernel<<<dim3(static_cast<unsigned>(B)), 256, 0, as_stream(stream)>>>(
+      logits, ldl, static_cast<int>(V), tokens, ld_tokens, pos);
+  return launch_status("decode_greedy");
 }

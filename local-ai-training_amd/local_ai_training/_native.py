@@ -112,6 +112,7 @@ SIGNATURES: dict[str, list] = {
     "rk_decode_attention": [_p, _i32, _i64, _p, _p, _i32, _i64, _i64, _i64, _p, _i64, _i64,
                             _i64, _i64, _f32, _p, _i64, _p, _i64, _p],
     "rk_decode_embed": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p],
+    "rk_decode_greedy": [_p, _i64, _i64, _i64, _p, _i64, _p, _p],
     "rk_hbm_stream": [_p, _p, _i64, _i32, _i32, _i32, _p],
     "rk_embedding_backward_workspace": [_i64, _i64, _i64],
     "rk_embedding_backward": [_p, _i32, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64,

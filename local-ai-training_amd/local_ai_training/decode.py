@@ -73,6 +73,24 @@ def decode_attention(qkv: Tensor, keys: Tensor, values: Tensor, pos: Tensor, n_h
     return out
 
 
+def decode_greedy(logits: Tensor, tokens: Tensor, pos: Tensor | None = None) -> Tensor:
+    """tokens[b, 0] = argmax of logits row b (torch.argmax's pick: the first largest value,
+    NaN above every number), then ``pos += 1`` when `pos` is given: the greedy choice of
+    ``generate.py:188-189`` and the window's growth by that token (``generate.py:200``) in
+    one launch (``rk_decode_greedy``). `logits` float32 with unit column stride, `tokens`
+    int64 [B, 1]."""
+    if logits.dtype != torch.float32 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("decode_greedy expects float32 logits [B, V] with unit column stride")
+    if tokens.dtype != torch.long or tokens.shape[0] != logits.shape[0]:
+        raise ValueError("decode_greedy expects int64 tokens with one row per logits row")
+    if pos is not None and (pos.dtype != torch.long or pos.numel() != 1):
+        raise ValueError("decode_greedy expects a one-element int64 position")
+    nat.call("rk_decode_greedy", logits.data_ptr(), logits.stride(0), logits.shape[0],
+             logits.shape[1], tokens.data_ptr(), tokens.stride(0), nat.ptr(pos),
+             nat.stream_handle(logits.device))
+    return tokens
+
+
 def attention_workspace_floats(batch: int, n_head: int, head: int, max_len: int) -> int:
     splits = int(nat.load_library().rk_decode_attention_splits(batch, n_head, max_len))
     return batch * n_head * splits * (head + 4)

@@ -67,6 +67,19 @@ def test_zero_sized_calls_are_no_ops(lib):
     assert lib.rk_pressure_leak(None, 0, 2, None) == 0
 
 
+def test_decode_greedy_validates_on_the_host(lib):
+    i64 = ctypes.c_int64
+    assert lib.rk_decode_greedy(None, i64(8), i64(0), i64(8), None, i64(1), None, None) == 0
+    assert lib.rk_decode_greedy(None, i64(8), i64(2), i64(0), None, i64(1), None, None) == 1
+    assert b"invalid greedy shape" in lib.rk_last_error()
+    assert lib.rk_decode_greedy(None, i64(8), i64(2), i64(8), None, i64(1), None, None) == 1
+    assert b"null greedy operand" in lib.rk_last_error()
+    buf = (ctypes.c_float * 16)()
+    out = (ctypes.c_int64 * 2)()
+    assert lib.rk_decode_greedy(buf, i64(4), i64(2), i64(8), out, i64(1), None, None) == 1
+    assert b"leading dimension" in lib.rk_last_error()
+
+
 def test_attention_forward_rejects_before_device_work(lib):
     """Head sizes other than 64 / 128 and unaligned strides return a status, no launch."""
     i64 = ctypes.c_int64

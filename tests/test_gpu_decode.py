@@ -198,6 +198,33 @@ def test_fused_decode_graph_replays_equal_eager_steps(cuda, batch):
     assert torch.equal(graphed.keys[1], eager.keys[1])
 
 
+@pytest.mark.parametrize("batch", [1, 16])
+def test_greedy_decode_graph_chains_the_eager_greedy_steps(cuda, batch):
+    # the greedy graph's replays (argmax into its token buffer, position advance inside the
+    # graph) against eager steps fed their own argmax: the same logits, picks and caches
+    model = _fused_model(cuda)
+    gen = torch.Generator().manual_seed(60 + batch)
+    prompt = torch.randint(0, 256, (batch, 7), generator=gen).to(cuda)
+    eager = model.new_cache(batch, dtype=torch.bfloat16)
+    graphed = model.new_cache(batch, dtype=torch.bfloat16)
+    first = model.prefill(prompt, eager).argmax(-1, keepdim=True)
+    model.prefill(prompt, graphed)
+    graph = DecodeGraph(model, graphed, greedy=True)
+    graph.tokens.copy_(first)
+    nxt = first
+    for step in range(20):
+        want = model.decode_step(nxt, eager)
+        nxt = want.argmax(-1, keepdim=True)
+        picks = graph.next_greedy()
+        torch.cuda.synchronize()
+        assert torch.equal(graph.logits, want), step
+        assert torch.equal(picks, nxt), step
+        assert int(graphed.pos) == int(eager.pos) == graphed.length == eager.length
+    assert torch.equal(graphed.keys[1], eager.keys[1])
+    with pytest.raises(RuntimeError, match="next_greedy"):
+        graph.step(nxt)
+
+
 def test_fused_generate_is_graph_independent(cuda):
     model = _fused_model(cuda)
     vocabulary = tuple(chr(0x100 + i) for i in range(256))

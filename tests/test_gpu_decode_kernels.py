@@ -28,6 +28,7 @@ from local_ai_training.decode import (
     PRO_RMSNORM,
     attention_workspace_floats,
     decode_attention,
+    decode_greedy,
 )
 from local_ai_training.int8_matmul import packed_int8_mm, quantize_rows
 from oracle import gemm as ogemm
@@ -169,7 +170,8 @@ def _attention_case(cuda, batch, heads, head, max_len, pos, cache_dtype, seed):
 
 @pytest.mark.parametrize("batch,heads,head,max_len,pos", [
     (1, 16, 128, 1024, 1023), (1, 16, 128, 1024, 0), (1, 16, 128, 1024, 600),
-    (16, 16, 128, 1024, 959), (3, 4, 64, 64, 17), (2, 2, 256, 48, 47), (5, 8, 64, 100, 1)])
+    (16, 16, 128, 1024, 959), (3, 4, 64, 64, 17), (2, 2, 256, 48, 47), (5, 8, 64, 100, 1),
+    (8, 16, 64, 200, 150), (16, 8, 128, 64, 0)])
 @pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
 def test_decode_attention_matches_float64_softmax(cuda, batch, heads, head, max_len, pos,
                                                   cache_dtype):
@@ -201,13 +203,14 @@ def test_decode_attention_matches_float64_softmax(cuda, batch, heads, head, max_
     assert float(err.max()) <= 2e-5
 
 
-def test_decode_attention_out_of_range_position_touches_nothing(cuda):
-    qkv, keys, values = _attention_case(cuda, 2, 4, 64, 32, 0, torch.bfloat16, seed=3)
+@pytest.mark.parametrize("batch,heads", [(2, 4), (16, 8)])
+def test_decode_attention_out_of_range_position_touches_nothing(cuda, batch, heads):
+    qkv, keys, values = _attention_case(cuda, batch, heads, 64, 32, 0, torch.bfloat16, seed=3)
     keys_before, values_before = keys.clone(), values.clone()
-    work = torch.zeros(attention_workspace_floats(2, 4, 64, 32), dtype=torch.float32,
+    work = torch.zeros(attention_workspace_floats(batch, heads, 64, 32), dtype=torch.float32,
                        device=cuda)
-    out = torch.empty(2, 256, dtype=torch.float32, device=cuda)
-    decode_attention(qkv, keys, values, torch.tensor([32], device=cuda), 4, work, out)
+    out = torch.empty(batch, heads * 64, dtype=torch.float32, device=cuda)
+    decode_attention(qkv, keys, values, torch.tensor([32], device=cuda), heads, work, out)
     torch.cuda.synchronize()
     assert torch.equal(keys, keys_before) and torch.equal(values, values_before)
     assert bool(torch.isnan(out).all())
@@ -219,6 +222,35 @@ def test_decode_attention_rejects_a_short_workspace(cuda):
     out = torch.empty(1, 256, dtype=torch.float32, device=cuda)
     with pytest.raises(nat.NativeError, match="workspace too small"):
         decode_attention(qkv, keys, values, torch.tensor([0], device=cuda), 4, work, out)
+
+
+@pytest.mark.parametrize("batch,vocab,pad", [(1, 8192, 0), (16, 8192, 0), (5, 1000, 24),
+                                             (3, 1, 3)])
+def test_decode_greedy_picks_the_first_argmax_and_advances(cuda, batch, vocab, pad):
+    gen = torch.Generator().manual_seed(batch * 7 + vocab)
+    rows = torch.randn(batch, vocab + pad, generator=gen)
+    rows[:, vocab:] = 1e30  # padding past V is never read
+    if vocab > 10:
+        rows[0, 3] = rows[0, 7] = rows[0, :vocab].max() + 1.0  # a tie: the first index
+        if batch > 1:
+            rows[1, vocab - 2] = float("nan")  # a NaN ranks above every number
+            rows[1, 5] = float("inf")
+        if batch > 2:
+            rows[2, :vocab] = float("-inf")  # all -inf: index 0
+        if batch > 3:
+            rows[3, 9] = rows[3, 4] = float("nan")  # the first NaN
+    logits = rows.to(cuda)[:, :vocab]
+    tokens = torch.full((batch, 2), -5, dtype=torch.long, device=cuda)
+    pos = torch.tensor([41], dtype=torch.long, device=cuda)
+    decode_greedy(logits, tokens[:, :1], pos)
+    torch.cuda.synchronize()
+    want = np.argmax(rows[:, :vocab].numpy(), axis=1)  # numpy: first max, NaN above all
+    assert torch.equal(torch.argmax(rows[:, :vocab], dim=-1), torch.from_numpy(want))
+    assert np.array_equal(tokens[:, 0].cpu().numpy(), want)
+    assert bool((tokens[:, 1] == -5).all()) and int(pos) == 42
+    decode_greedy(logits, tokens[:, 1:], None)  # no position: only the picks
+    torch.cuda.synchronize()
+    assert np.array_equal(tokens[:, 1].cpu().numpy(), want) and int(pos) == 42
 
 
 def test_decode_embed_is_the_table_row_plus_the_position_row(cuda):
