@@ -896,33 +896,61 @@ __device__ __forceinline__ bool greedy_better(float v, int i, float best, int bi
   return v > best || (v == best && i < bi);
 }
 
-// grid B, 256 threads: tokens[b * ldt] = the argmax of logits row b; block 0 then adds one
-// to *pos (no kernel of the step reads pos after this one).
-__global__ __launch_bounds__(256) void decode_greedy_kernel(const float* logits, int64_t ldl,
-                                                            int V, int64_t* tokens, int64_t ldt,
-                                                            int64_t* pos) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
+// grid B, 1024 threads: tokens[b * ldt] = the argmax of logits row b; block 0 then adds
+// one to *pos (no kernel of the step reads pos after this one). Each thread issues all its
+// loads of a pass before comparing (VEC: float4 pieces of 16-byte aligned rows).
+template <bool VEC>
+__global__ __launch_bounds__(1024) void decode_greedy_kernel(const float* logits, int64_t ldl,
+                                                             int V, int64_t* tokens,
+                                                             int64_t ldt, int64_t* pos) {
+  constexpr int NT = 1024, UN = 4;
+  __shared__ float sv[NT / kWave];
+  __shared__ int si[NT / kWave];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const float* row = logits + b * ldl;
   float best = -INFINITY;
   int bi = V;  // no index yet: any value, -inf included, ranks above it
-  for (int i = tid; i < V; i += 256) {
-    const float v = row[i];
+  auto take = [&](float v, int i) {
     if (greedy_better(v, i, best, bi)) {
       best = v;
       bi = i;
+    }
+  };
+  if constexpr (VEC) {
+    for (int base = 4 * tid; base < V; base += 4 * NT * UN) {
+      float4 t[UN];
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int i = base + 4 * NT * u;
+        t[u] = i < V ? *reinterpret_cast<const float4*>(row + i)
+                     : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      }
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int i = base + 4 * NT * u;
+        if (i < V) {
+          take(t[u].x, i);
+          take(t[u].y, i + 1);
+          take(t[u].z, i + 2);
+          take(t[u].w, i + 3);
+        }
+      }
+    }
+  } else {
+    for (int base = tid; base < V; base += NT * UN) {
+      float t[UN];
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int i = base + NT * u;
+        t[u] = i < V ? row[i] : -INFINITY;
+      }
+#pragma unroll
+      for (int u = 0; u < UN; ++u)
+        if (base + NT * u < V) take(t[u], base + NT * u);
     }
   }
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float v = __shfl_xor(best, off, kWave);
-    const int i = __shfl_xor(bi, off, kWave);
-    if (greedy_better(v, i, best, bi)) {
-      best = v;
-      bi = i;
-    }
-  }
+  for (int off = 32; off >= 1; off >>= 1) take(__shfl_xor(best, off, kWave), __shfl_xor(bi, off, kWave));
   if (lane == 0) {
     sv[wave] = best;
     si[wave] = bi;
@@ -930,11 +958,7 @@ __global__ __launch_bounds__(256) void decode_greedy_kernel(const float* logits,
   __syncthreads();
   if (tid == 0) {
 #pragma unroll
-    for (int w = 1; w < 4; ++w)
-      if (greedy_better(sv[w], si[w], best, bi)) {
-        best = sv[w];
-        bi = si[w];
-      }
+    for (int w = 1; w < NT / kWave; ++w) take(sv[w], si[w]);
     tokens[b * ldt] = bi;
     if (pos != nullptr && b == 0) *pos = *pos + 1;
   }
@@ -1125,7 +1149,12 @@ extern "C" int rk_decode_greedy(const float* logits, int64_t ldl, int64_t B, int
   if (B > 65535) return fail(RK_ERR_ARG, "greedy grid too large");
   if (!logits || !tokens) return fail(RK_ERR_ARG, "null greedy operand");
   if (ldl < V || ld_tokens < 1) return fail(RK_ERR_ARG, "leading dimension too small");
-  decode_greedy_kernel<<<dim3(static_cast<unsigned>(B)), 256, 0, as_stream(stream)>>>(
-      logits, ldl, static_cast<int>(V), tokens, ld_tokens, pos);
+  const dim3 grid(static_cast<unsigned>(B));
+  if (aligned16(logits) && V % 4 == 0 && ldl % 4 == 0)
+    decode_greedy_kernel<true><<<grid, 1024, 0, as_stream(stream)>>>(
+        logits, ldl, static_cast<int>(V), tokens, ld_tokens, pos);
+  else
+    decode_greedy_kernel<false><<<grid, 1024, 0, as_stream(stream)>>>(
+        logits, ldl, static_cast<int>(V), tokens, ld_tokens, pos);
   return launch_status("decode_greedy");
 }

@@ -224,8 +224,9 @@ def test_decode_attention_rejects_a_short_workspace(cuda):
         decode_attention(qkv, keys, values, torch.tensor([0], device=cuda), 4, work, out)
 
 
+# (5, 1000, 24): float4 pieces of padded rows; (4, 1001, 0) and (3, 1, 3): scalar loads
 @pytest.mark.parametrize("batch,vocab,pad", [(1, 8192, 0), (16, 8192, 0), (5, 1000, 24),
-                                             (3, 1, 3)])
+                                             (4, 1001, 0), (3, 1, 3), (2, 70000, 0)])
 def test_decode_greedy_picks_the_first_argmax_and_advances(cuda, batch, vocab, pad):
     gen = torch.Generator().manual_seed(batch * 7 + vocab)
     rows = torch.randn(batch, vocab + pad, generator=gen)
