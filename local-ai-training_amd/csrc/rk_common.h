@@ -125,29 +125,55 @@ __device__ __forceinline__ float tanh_fast(float u) {
 // Wavefront reductions (xor butterfly; every lane ends with the same value).
 // The float sum's association order is fixed: offsets 32, 16, 8, 4, 2, 1 with
 // v = v + v[lane ^ offset].
+//
+// The partner values move without the LDS crossbar: v_permlane32_swap / v_permlane16_swap
+// of a register with itself leave, in their two results, a lane's own value and its
+// lane ^ 32 (^ 16) partner's (which of the two is which depends on the half, and the sum
+// or max does not care: a + b and b + a are the same bits); DPP row_ror:8 gives lane ^ 8
+// inside a 16-lane row; lane ^ 4 is the half-row mirror (7 - i) of the quad-reversed
+// register (i ^ 3); quad_perm gives ^ 2 and ^ 1.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
+}
+
+// op(v, v[lane ^ off]) for off = 32, 16, 8, 4, 2, 1 on the raw 32-bit values
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_butterfly(T v, Op op) {
+  auto bits = [](T x) { return __builtin_bit_cast(uint32_t, x); };
+  auto val = [](uint32_t x) { return __builtin_bit_cast(T, x); };
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(bits(v), bits(v), false, false);
+    v = op(val(r[0]), val(r[1]));
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(bits(v), bits(v), false, false);
+    v = op(val(r[0]), val(r[1]));
+  }
+  v = op(v, val(dpp_u32<0x128>(bits(v))));                    // row_ror:8   -> lane ^ 8
+  v = op(v, val(dpp_u32<0x141>(dpp_u32<0x1b>(bits(v)))));     // half-row mirror of quad
+                                                              // reversal  -> lane ^ 4
+  v = op(v, val(dpp_u32<0x4e>(bits(v))));                     // quad_perm -> lane ^ 2
+  v = op(v, val(dpp_u32<0xb1>(bits(v))));                     // quad_perm -> lane ^ 1
   return v;
+}
+
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+  return wave_butterfly(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+  return wave_butterfly(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 __device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  return wave_butterfly(v, [](int a, int b) { return a + b; });
 }
 
 __device__ __forceinline__ int wave_or_int(int v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v |= __shfl_xor(v, off, kWave);
-  return v;
+  return wave_butterfly(v, [](int a, int b) { return a | b; });
 }
 
 // ---------------------------------------------------------------------------
