@@ -181,8 +181,9 @@ template <int PRO, int EPI, int YDT, int MM, int WV, int KBW, int NCH, int NT = 
 __global__ __launch_bounds__(64 * WV, (MM >= 8 && (NCH <= 8 || WV == 16)) ? 4 : 1)
 void decode_gemv_kernel(DecodeGemvArgs a) {
   constexpr int NB = 16, KB = 64;
-  static_assert(RS == 1 || (PRO == DEC_PRO_PLAIN && MM * RS == WV && NCH % RS == 0),
-                "row slices: plain prologue, one slice per wavefront");
+  static_assert(RS == 1 || (PRO != DEC_PRO_INT8 && MM * RS == WV && NCH % RS == 0),
+                "row slices: float prologue rows, one slice per wavefront");
+  constexpr bool kSlicedNorm = RS > 1 && PRO == DEC_PRO_RMSNORM;
   constexpr int NCHL = NCH / RS;  // row chunks a wavefront holds
   if (blockIdx.y > 0) {  // this workgroup's token rows (uniform)
     const int mb = static_cast<int>(blockIdx.y) * MM;
@@ -211,6 +212,7 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   __shared__ __align__(16) float wsh[WLDS ? NCH * 256 : 4];
   __shared__ float sc[MM];
   __shared__ float part[RS > 1 ? MM : 1][RS];  // slice absmax values
+  __shared__ float rfac[kSlicedNorm ? MM : 1];  // RMSNorm factors of sliced rows
   __shared__ dec_v4i red[WV][kWave];
   // wave index made scalar: the code loads' k offset is then an SGPR (a value the
   // compiler takes as divergent would turn each buffer load into a waterfall loop)
@@ -241,8 +243,15 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
   int xq_lds[PRO == DEC_PRO_INT8 ? IPT : 1];
   const int pieces = K / 16;
   const int srow = wave / RS, slice = wave - srow * RS;  // row slice (RS > 1)
+  // sliced RMSNorm rows: the first slice's wavefront also holds the whole row, whose sum of
+  // squares it takes in the unsliced order; every slice holds its piece of the norm weight
+  float xf[kSlicedNorm ? NCH : 1][4];
+  float wsl[kSlicedNorm ? NCHL : 1][4];
   if constexpr (RS > 1) {
     const float* row = a.x + (srow < M ? srow : M - 1) * a.ldx;
+    if constexpr (kSlicedNorm) {
+      if (slice == 0) dec_load_row<NCH>(row, K, lane, xf);
+    }
 #pragma unroll
     for (int c = 0; c < NCHL; ++c) {
       const int e0 = (slice * NCHL + c) * kWave * 4 + lane * 4;
@@ -252,6 +261,13 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
       xr[0][c][1] = in ? t.y : 0.0f;
       xr[0][c][2] = in ? t.z : 0.0f;
       xr[0][c][3] = in ? t.w : 0.0f;
+      if constexpr (kSlicedNorm) {
+        const float4 w = *reinterpret_cast<const float4*>(a.w + (in ? e0 : K - 4));
+        wsl[c][0] = in ? w.x : 0.0f;
+        wsl[c][1] = in ? w.y : 0.0f;
+        wsl[c][2] = in ? w.z : 0.0f;
+        wsl[c][3] = in ? w.w : 0.0f;
+      }
     }
   } else if constexpr (PRO == DEC_PRO_INT8) {
     // pieces past the M rows re-load piece 0 of row 0 (and store it back unchanged)
@@ -306,6 +322,25 @@ void decode_gemv_kernel(DecodeGemvArgs a) {
 
   // 3. prologue: int8 rows (or quantized activation rows) and their scales into LDS
   if constexpr (RS > 1) {
+    if constexpr (kSlicedNorm) {
+      // dec_quant_row's factor: the per-lane sum of squares in chunk order over the whole
+      // row, the xor butterfly, 1 / sqrt(mean + eps); then (x * factor) * w per slice
+      if (slice == 0) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc = acc + xf[c][i] * xf[c][i];
+        acc = wave_sum_butterfly(acc);
+        if (lane == 0) rfac[srow] = 1.0f / sqrtf(acc / static_cast<float>(K) + a.eps);
+      }
+      __syncthreads();
+      const float rf = rfac[srow];
+#pragma unroll
+      for (int c = 0; c < NCHL; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xr[0][c][i] = xr[0][c][i] * rf * wsl[c][i];
+    }
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCHL; ++c)
@@ -434,13 +469,16 @@ static int launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
   if (a.M <= 1) {
     // one token row; long rows split K over 8 wavefronts (twice the code loads in flight
     // per CU: 14.7 -> 12.5 us for N 2048 x K 5632), short ones over 4 (8 were slower)
+    // (float rows sliced over all the wavefronts: plain ones by absmax alone, RMSNorm ones
+    // after the first wavefront's whole-row sum of squares)
+    constexpr bool kSlice1 = PRO != DEC_PRO_INT8;
     if (small_k) {
-      if constexpr (kPlain)
+      if constexpr (kSlice1)
         decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8, 1, 4><<<grid, 256, 0, stream>>>(a);
       else
         decode_gemv_kernel<PRO, EPI, YDT, 1, 4, 8, 8><<<grid, 256, 0, stream>>>(a);
     } else {
-      if constexpr (kPlain)
+      if constexpr (kSlice1)
         decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24, 1, 8><<<grid, 512, 0, stream>>>(a);
       else
         decode_gemv_kernel<PRO, EPI, YDT, 1, 8, 12, 24><<<grid, 512, 0, stream>>>(a);
