@@ -368,6 +368,10 @@ class _RatchetMatmul(torch.autograd.Function):
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 partials = split_weight_gradient(g_w)
+                if partials is not None and layer._pending_counts is None:
+                    # the update's zeroed move counters, made here behind grad_weight rather
+                    # than on the main stream after the join (the update's critical path)
+                    layer._counts().record_stream(main)
             if partials is None:
                 main.wait_stream(side)
                 side = None
