@@ -254,16 +254,19 @@ def test_decode_greedy_picks_the_first_argmax_and_advances(cuda, batch, vocab, p
     assert np.array_equal(tokens[:, 1].cpu().numpy(), want) and int(pos) == 42
 
 
-def test_decode_embed_is_the_table_row_plus_the_position_row(cuda):
+# width 256: float4 pieces; 250: rows not 16-byte aligned, one element per thread; 4100:
+# more than one pass of pieces per thread
+@pytest.mark.parametrize("width", [256, 250, 4100])
+def test_decode_embed_is_the_table_row_plus_the_position_row(cuda, width):
     gen = torch.Generator().manual_seed(2)
-    table = torch.randn(300, 256, generator=gen).to(cuda)
-    positions = torch.randn(64, 256, generator=gen).to(cuda)
+    table = torch.randn(300, width, generator=gen).to(cuda)
+    positions = torch.randn(64, width, generator=gen).to(cuda)
     tokens = torch.tensor([5, 299, 0, 17], device=cuda)
-    hidden = torch.empty(4, 256, device=cuda)
+    hidden = torch.empty(4, width, device=cuda)
     for p in (0, 63, 64):
         pos = torch.tensor([p], device=cuda)
-        nat.call("rk_decode_embed", tokens.data_ptr(), 4, table.data_ptr(), 300, 256,
-                 positions.data_ptr(), 64, pos.data_ptr(), hidden.data_ptr(), 256,
+        nat.call("rk_decode_embed", tokens.data_ptr(), 4, table.data_ptr(), 300, width,
+                 positions.data_ptr(), 64, pos.data_ptr(), hidden.data_ptr(), width,
                  nat.stream_handle(cuda))
         torch.cuda.synchronize()
         if p < 64:
@@ -271,8 +274,8 @@ def test_decode_embed_is_the_table_row_plus_the_position_row(cuda):
         else:
             assert bool(torch.isnan(hidden).all())
     bad = torch.tensor([300], device=cuda)
-    nat.call("rk_decode_embed", bad.data_ptr(), 1, table.data_ptr(), 300, 256,
+    nat.call("rk_decode_embed", bad.data_ptr(), 1, table.data_ptr(), 300, width,
              positions.data_ptr(), 64, torch.tensor([0], device=cuda).data_ptr(),
-             hidden.data_ptr(), 256, nat.stream_handle(cuda))
+             hidden.data_ptr(), width, nat.stream_handle(cuda))
     torch.cuda.synchronize()
     assert bool(torch.isnan(hidden[0]).all())
